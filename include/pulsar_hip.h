@@ -1,0 +1,132 @@
+/*
+ * pulsar_hip.h — C ABI of libpulsar_hip.so, the MI355X (gfx950) implementation of
+ * Pulsar's KV-cache self-speculative decode path.
+ *
+ * Conventions
+ *   - Every entry returns an int status (PULSAR_OK = 0). On failure
+ *     pulsar_last_error() returns a thread-local message; no C++ exception crosses
+ *     the boundary.
+ *   - Pointers are device pointers unless the name says host_. The caller allocates
+ *     every input and output (the library keeps no allocation across calls except
+ *     inside an engine handle).
+ *   - Work is enqueued on the given HIP stream; no entry synchronises the host unless
+ *     documented. Kernels launched here are capturable in a HIP graph.
+ *   - dtype selects the element type of activation tensors: PULSAR_F32 or PULSAR_BF16
+ *     (bf16 as raw 16-bit words, round-to-nearest-even). The reference op surface is
+ *     bf16-only; fp32 instantiations are extra.
+ *
+ * Each op entry cites the reference binding it replaces
+ * (csrc/pulsar_cuda.cpp = pybind module, csrc/kernels.cu = CUDA kernels).
+ */
+#ifndef PULSAR_HIP_H_
+#define PULSAR_HIP_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PULSAR_OK 0
+#define PULSAR_ERR_INVALID 1     /* bad shape, dtype or argument (reference: TORCH_CHECK) */
+#define PULSAR_ERR_HIP 2         /* HIP runtime or launch error */
+#define PULSAR_ERR_UNSUPPORTED 3 /* configuration this build does not implement */
+
+#define PULSAR_F32 0
+#define PULSAR_BF16 1
+
+/* Thread-local message of the last failing call on this thread. */
+const char* pulsar_last_error(void);
+/* ABI version of this header (bumped on any signature change). */
+int pulsar_abi_version(void);
+
+/* ---------------------------------------------------------------------------------
+ * Op surface of the reference's pulsar_cuda module
+ * ------------------------------------------------------------------------------- */
+
+/* rmsnorm_forward(x, weight, eps) -> (y, rsqrt)
+ * Replaces csrc/pulsar_cuda.cpp:202 / csrc/kernels.cu:224-266.
+ * x, y: [rows, dim] contiguous; w: fp32 [dim]; rsqrt_out: fp32 [rows] (nullable). */
+int pulsar_rmsnorm_forward(const void* x, const float* w, void* y, float* rsqrt_out,
+                           int64_t rows, int64_t dim, float eps, int dtype,
+                           hipStream_t stream);
+
+/* rope_forward(qk, cos, sin) -> out, rotate-half with fp32 tables.
+ * Replaces csrc/pulsar_cuda.cpp:211 / csrc/kernels.cu:935-965.
+ * x, y: contiguous [rows, head_dim] where row = ((b*H)+h)*T + t; table row t = row % T;
+ * cos, sin: fp32 [T, head_dim/2]. */
+int pulsar_rope_forward(const void* x, void* y, const float* cos, const float* sin,
+                        int64_t rows, int64_t T, int64_t head_dim, int dtype,
+                        hipStream_t stream);
+
+/* qk_rmsnorm_rope_forward(x, weight, cos, sin, T, eps) -> (y, rsqrt)
+ * Replaces csrc/pulsar_cuda.cpp:225-226 / csrc/kernels.cu:2716-2765.
+ * x: [B,H,T,64] with element strides (sB, sH, sT, 1); w: fp32 [H,64];
+ * cos, sin: fp32 [T,32]; y: contiguous [B,H,T,64]; rsqrt_out: fp32 [B*H*T] (nullable).
+ * head_dim must be 64 (error message contains "head_dim == 64"). */
+int pulsar_qk_rmsnorm_rope_forward(const void* x, int64_t sB, int64_t sH, int64_t sT,
+                                   int64_t B, int64_t H, int64_t T, int64_t head_dim,
+                                   const float* w, const float* cos, const float* sin,
+                                   void* y, float* rsqrt_out, float eps, int dtype,
+                                   hipStream_t stream);
+
+/* fused_attn_gate_forward(attn_out, gate_logits) -> out
+ * Replaces csrc/pulsar_cuda.cpp:230-231 / csrc/kernels.cu:2930-2958.
+ * attn: contiguous [B,H,T,64]; gate_logits: fp32 [B,T,H]; out: [B,T,H*64]. */
+int pulsar_fused_attn_gate_forward(const void* attn, const float* gate_logits, void* out,
+                                   int64_t B, int64_t H, int64_t T, int64_t head_dim,
+                                   int dtype, hipStream_t stream);
+
+/* causal_depthwise_conv1d_k4_forward(x, weight) -> y = x + sum_k w[:,k] x[t-k]
+ * Replaces csrc/pulsar_cuda.cpp:274-276 / csrc/kernels.cu:3653-3691.
+ * x, y: contiguous [B,T,D]; w: fp32 [D,4]. */
+int pulsar_causal_conv1d_k4_forward(const void* x, const float* w, void* y, int64_t B,
+                                    int64_t T, int64_t D, int dtype, hipStream_t stream);
+
+/* fused_swiglu_forward(gu, d_ff) -> silu(gu[..,:d_ff]) * gu[..,d_ff:]
+ * Replaces csrc/pulsar_cuda.cpp:209 / csrc/kernels.cu:825-863.
+ * gu: contiguous [rows, 2*d_ff]; out: [rows, d_ff]. */
+int pulsar_fused_swiglu_forward(const void* gu, void* out, int64_t rows, int64_t d_ff,
+                                int dtype, hipStream_t stream);
+
+/* moe_router_topk_forward(logits, expert_bias, top_k, z_loss_weight)
+ *   -> (topk_idx int64 [N,K], topk_weights bf16 [N,K], z_loss fp32 [], probs_mean fp32 [E])
+ * Replaces csrc/pulsar_cuda.cpp:255-266 / csrc/kernels.cu:2417-2491.
+ * Centred-sigmoid scores, top-K of score+bias (ties to the lower index), weights
+ * s/(sum s + 1e-6). z_loss = w_z * mean(logsumexp(centred)^2) (0 when w_z <= 0),
+ * probs_mean = mean sigmoid score; both reduced deterministically. E <= 32, K <= 8. */
+int pulsar_moe_router_topk_forward(const void* logits, int logits_dtype, const float* bias,
+                                   int64_t* topk_idx, uint16_t* topk_w_bf16, float* z_loss,
+                                   float* probs_mean, int64_t N, int64_t E, int64_t K,
+                                   float z_loss_weight, hipStream_t stream);
+
+/* moe_dispatch_forward(x, topk_idx, token_to_slot, E, C, expert_counts) -> [E,C,D]
+ * Replaces csrc/pulsar_cuda.cpp:213-215 / csrc/kernels.cu:1548-1605.
+ * Slots >= count[e] (or all unused slots when expert_counts is NULL) are zeroed. */
+int pulsar_moe_dispatch_forward(const void* x, const int64_t* topk_idx, const int32_t* slots,
+                                const int64_t* expert_counts, void* expert_inputs, int64_t N,
+                                int64_t D, int64_t K, int64_t E, int64_t C, int dtype,
+                                hipStream_t stream);
+
+/* moe_combine_forward(expert_outputs, topk_idx, topk_weights, token_to_slot, shared_out)
+ *   out[t] = shared[t] + sum_k w[t,k] * expert_out[e,slot]   (fp32 accumulate)
+ * Replaces csrc/pulsar_cuda.cpp:217-219 / csrc/kernels.cu:1633-1664.
+ * shared_out nullable; weights are bf16 words. */
+int pulsar_moe_combine_forward(const void* expert_outputs, const int64_t* topk_idx,
+                               const uint16_t* topk_w_bf16, const int32_t* slots,
+                               const void* shared_out, void* out, int64_t N, int64_t D,
+                               int64_t K, int64_t E, int64_t C, int dtype, hipStream_t stream);
+
+/* moe_slots_from_order(flat_e, order, E, C) -> (slots int32 [M], counts int64 [E])
+ * Replaces csrc/pulsar_cuda.cpp:235-236 / csrc/kernels.cu:3058-3095.
+ * slot = rank of the assignment within its expert in `order`, -1 when >= C. */
+int pulsar_moe_slots_from_order(const int64_t* flat_e, const int64_t* order, int32_t* slots,
+                                int64_t* counts, int64_t M, int64_t E, int64_t C,
+                                hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PULSAR_HIP_H_ */

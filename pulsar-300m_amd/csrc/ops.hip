@@ -1,0 +1,510 @@
+// Op surface of the reference's pulsar_cuda module, written for gfx950 (wave64).
+//
+// Each kernel is one pass over its tensors with 128-bit loads where the row length
+// allows; reductions are wave64 shuffles. Every entry validates shapes on the host and
+// returns a status code instead of throwing.
+#include <string>
+
+#include "common.h"
+#include "../../include/pulsar_hip.h"
+
+namespace pulsar {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm over rows: one block per row, fp32 statistics.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const T* __restrict__ x,
+                                                      const float* __restrict__ w,
+                                                      T* __restrict__ y,
+                                                      float* __restrict__ rsq, int dim,
+                                                      float eps) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * dim;
+  T* yr = y + row * dim;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+    float v = to_f(xr[i]);
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+  if (threadIdx.x == 0 && rsq) rsq[row] = inv;
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) yr[i] = from_f<T>(to_f(xr[i]) * inv * w[i]);
+}
+
+// ---------------------------------------------------------------------------
+// RoPE (rotate-half) on contiguous rows of head_dim; table row = row % T.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void rope_kernel(const T* __restrict__ x, T* __restrict__ y,
+                            const float* __restrict__ cs, const float* __restrict__ sn,
+                            int64_t rows, int64_t T_, int hd) {
+  const int half = hd / 2;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = idx / half;
+  const int i = (int)(idx % half);
+  if (row >= rows) return;
+  const int64_t t = row % T_;
+  const float c = cs[t * half + i], s = sn[t * half + i];
+  const float a = to_f(x[row * hd + i]), b = to_f(x[row * hd + i + half]);
+  y[row * hd + i] = from_f<T>(a * c - b * s);
+  y[row * hd + i + half] = from_f<T>(b * c + a * s);
+}
+
+// ---------------------------------------------------------------------------
+// QK RMSNorm + RoPE: one wave per 64-element head vector; lane i pairs with lane i^32.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(
+    const T* __restrict__ x, int64_t sB, int64_t sH, int64_t sT, int H, int T_,
+    int64_t nvec, const float* __restrict__ w, const float* __restrict__ cs,
+    const float* __restrict__ sn, T* __restrict__ y, float* __restrict__ rsq, float eps) {
+  const int64_t v = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (v >= nvec) return;
+  const int lane = threadIdx.x & 63;
+  const int t = (int)(v % T_);
+  const int h = (int)((v / T_) % H);
+  const int64_t b = v / ((int64_t)T_ * H);
+  const float xv = to_f(x[b * sB + h * sH + (int64_t)t * sT + lane]);
+  const float ss = wave_sum(xv * xv);
+  const float inv = 1.0f / sqrtf(ss / 64.0f + eps);
+  if (lane == 0 && rsq) rsq[v] = inv;
+  const float n = xv * inv * w[h * 64 + lane];
+  const float partner = __shfl_xor(n, 32, 64);
+  const int j = lane & 31;
+  const float c = cs[t * 32 + j], s = sn[t * 32 + j];
+  const float out = (lane < 32) ? (n * c - partner * s) : (n * c + partner * s);
+  y[v * 64 + lane] = from_f<T>(out);
+}
+
+// ---------------------------------------------------------------------------
+// Attention gate + [B,H,T,D] -> [B,T,H*D] transpose.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void attn_gate_kernel(const T* __restrict__ a, const float* __restrict__ gl,
+                                 T* __restrict__ out, int H, int T_, int hd, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int d = (int)(idx % hd);
+  const int64_t hv = idx / hd;  // (b, t, h) in output order
+  const int h = (int)(hv % H);
+  const int t = (int)((hv / H) % T_);
+  const int64_t b = hv / ((int64_t)H * T_);
+  const float g = sigmoidf_(gl[hv]);
+  out[idx] = from_f<T>(to_f(a[((b * H + h) * T_ + t) * hd + d]) * g);
+}
+
+// ---------------------------------------------------------------------------
+// Causal depthwise conv k=4 with residual, fp32 arithmetic.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void conv_k4_kernel(const T* __restrict__ x, const float* __restrict__ w,
+                               T* __restrict__ y, int64_t T_, int64_t D, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int64_t d = idx % D;
+  const int64_t t = (idx / D) % T_;
+  const float x0 = to_f(x[idx]);
+  const float x1 = t >= 1 ? to_f(x[idx - D]) : 0.f;
+  const float x2 = t >= 2 ? to_f(x[idx - 2 * D]) : 0.f;
+  const float x3 = t >= 3 ? to_f(x[idx - 3 * D]) : 0.f;
+  const float* wd = w + d * 4;
+  y[idx] = from_f<T>(x0 + (wd[0] * x0 + wd[1] * x1 + wd[2] * x2 + wd[3] * x3));
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU: silu(gate) * up in fp32.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void swiglu_kernel(const T* __restrict__ gu, T* __restrict__ out, int64_t dff,
+                              int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int64_t r = idx / dff, c = idx % dff;
+  const float g = to_f(gu[r * 2 * dff + c]);
+  const float u = to_f(gu[r * 2 * dff + dff + c]);
+  out[idx] = from_f<T>(g * sigmoidf_(g) * u);
+}
+
+// ---------------------------------------------------------------------------
+// Router top-k: one lane per token. Scores in registers (E <= 32).
+// ---------------------------------------------------------------------------
+template <typename L>
+__device__ __forceinline__ void router_scores(const L* lt, const float* bias, int E, float* c,
+                                              float* s, float* b) {
+  float sum = 0.f;
+  for (int e = 0; e < E; ++e) {
+    c[e] = to_f(lt[e]);
+    sum += c[e];
+  }
+  const float mean = sum / (float)E;
+  for (int e = 0; e < E; ++e) {
+    c[e] = c[e] - mean;
+    s[e] = sigmoidf_(c[e]);
+    b[e] = s[e] + bias[e];
+  }
+}
+
+template <typename L>
+__global__ void router_topk_kernel(const L* __restrict__ logits, const float* __restrict__ bias,
+                                   int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out,
+                                   int64_t N, int E, int K) {
+  const int64_t tok = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tok >= N) return;
+  float c[32], s[32], b[32];
+  router_scores(logits + tok * E, bias, E, c, s, b);
+  int bi[8];
+  float bv[8];
+  for (int k = 0; k < K; ++k) {
+    bi[k] = -1;
+    bv[k] = -INFINITY;
+  }
+  for (int e = 0; e < E; ++e) {
+    const float v = b[e];
+    if (v > bv[K - 1]) {
+      int p = K - 1;
+      while (p > 0 && v > bv[p - 1]) {
+        bv[p] = bv[p - 1];
+        bi[p] = bi[p - 1];
+        --p;
+      }
+      bv[p] = v;
+      bi[p] = e;
+    }
+  }
+  float tot = 0.f;
+  for (int k = 0; k < K; ++k) tot += s[bi[k]];
+  tot += 1e-6f;
+  for (int k = 0; k < K; ++k) {
+    idx_out[tok * K + k] = bi[k];
+    w_out[tok * K + k] = f2bf(s[bi[k]] / tot).u;
+  }
+}
+
+// Deterministic z-loss and probs_mean: one block loops over all tokens.
+template <typename L>
+__global__ void __launch_bounds__(256) router_stats_kernel(const L* __restrict__ logits,
+                                                           const float* __restrict__ bias,
+                                                           float* __restrict__ z_loss,
+                                                           float* __restrict__ probs_mean,
+                                                           int64_t N, int E, float zw) {
+  __shared__ float red[16];
+  float c[32], s[32], b[32];
+  float pm[32];
+  for (int e = 0; e < E; ++e) pm[e] = 0.f;
+  float zsum = 0.f;
+  for (int64_t t = threadIdx.x; t < N; t += blockDim.x) {
+    router_scores(logits + t * E, bias, E, c, s, b);
+    float mx = -INFINITY;
+    for (int e = 0; e < E; ++e) mx = fmaxf(mx, c[e]);
+    float se = 0.f;
+    for (int e = 0; e < E; ++e) {
+      se += expf(c[e] - mx);
+      pm[e] += s[e];
+    }
+    const float lse = mx + logf(se);
+    zsum += lse * lse;
+  }
+  const float inv_n = N > 0 ? 1.0f / (float)N : 0.f;
+  const float zt = block_sum(zsum, red);
+  if (threadIdx.x == 0) z_loss[0] = zw > 0.f ? zw * zt * inv_n : 0.f;
+  for (int e = 0; e < E; ++e) {
+    const float v = block_sum(pm[e], red);
+    if (threadIdx.x == 0) probs_mean[e] = v * inv_n;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MoE dispatch / combine / slots.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void moe_zero_kernel(T* __restrict__ buf, const int64_t* __restrict__ counts, int C,
+                                int64_t D) {
+  const int e = blockIdx.y;
+  int64_t start = 0;
+  if (counts) {
+    const int64_t n = counts[e];
+    start = n < 0 ? 0 : (n > C ? C : n);
+  }
+  const int64_t len = (C - start) * D;
+  T* base = buf + ((int64_t)e * C + start) * D;
+  T zero = from_f<T>(0.f);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+       i += (int64_t)gridDim.x * blockDim.x)
+    base[i] = zero;
+}
+
+template <typename T>
+__global__ void moe_dispatch_kernel(const T* __restrict__ x, const int64_t* __restrict__ idx,
+                                    const int32_t* __restrict__ slots, T* __restrict__ dst,
+                                    int64_t D, int K, int E, int C) {
+  const int64_t tok = blockIdx.x;
+  for (int k = 0; k < K; ++k) {
+    const int slot = slots[tok * K + k];
+    const int64_t e = idx[tok * K + k];
+    if (slot < 0 || slot >= C || e < 0 || e >= E) continue;
+    T* d = dst + (e * C + slot) * D;
+    for (int64_t i = threadIdx.x; i < D; i += blockDim.x) d[i] = x[tok * D + i];
+  }
+}
+
+template <typename T>
+__global__ void moe_combine_kernel(const T* __restrict__ eo, const int64_t* __restrict__ idx,
+                                   const uint16_t* __restrict__ wts,
+                                   const int32_t* __restrict__ slots,
+                                   const T* __restrict__ shared, T* __restrict__ out,
+                                   int64_t D, int K, int E, int C) {
+  const int64_t tok = blockIdx.x;
+  for (int64_t i = threadIdx.x; i < D; i += blockDim.x) {
+    float acc = shared ? to_f(shared[tok * D + i]) : 0.f;
+    for (int k = 0; k < K; ++k) {
+      const int slot = slots[tok * K + k];
+      const int64_t e = idx[tok * K + k];
+      if (slot < 0 || slot >= C || e < 0 || e >= E) continue;
+      bf16 wb;
+      wb.u = wts[tok * K + k];
+      acc += bf2f(wb) * to_f(eo[(e * C + slot) * D + i]);
+    }
+    out[tok * D + i] = from_f<T>(acc);
+  }
+}
+
+__global__ void slots_count_kernel(const int64_t* __restrict__ flat_e, int64_t* __restrict__ counts,
+                                   int64_t M, int E) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M) return;
+  const int64_t e = flat_e[i];
+  if (e >= 0 && e < E) atomicAdd(reinterpret_cast<unsigned long long*>(&counts[e]), 1ull);
+}
+
+__global__ void slots_assign_kernel(const int64_t* __restrict__ flat_e,
+                                    const int64_t* __restrict__ order,
+                                    const int64_t* __restrict__ counts, int32_t* __restrict__ slots,
+                                    int64_t M, int E, int C) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M) return;
+  const int64_t orig = order[i];
+  const int64_t e = flat_e[orig];
+  int64_t start = 0;
+  for (int j = 0; j < E && j < e; ++j) start += counts[j];
+  const int64_t rank = i - start;
+  slots[orig] = (e >= 0 && e < E && rank >= 0 && rank < C) ? (int32_t)rank : -1;
+}
+
+__global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+inline unsigned blocks_for(int64_t n, int threads) {
+  return (unsigned)((n + threads - 1) / threads);
+}
+
+template <typename F>
+int dispatch_dtype(int dtype, F&& f) {
+  if (dtype == PULSAR_F32) return f(float{});
+  if (dtype == PULSAR_BF16) return f(bf16{});
+  return fail(PULSAR_ERR_INVALID, "dtype must be PULSAR_F32 or PULSAR_BF16");
+}
+
+}  // namespace pulsar
+
+using namespace pulsar;
+
+extern "C" {
+
+const char* pulsar_last_error(void) { return g_last_error.c_str(); }
+
+int pulsar_abi_version(void) { return 1; }
+
+int pulsar_rmsnorm_forward(const void* x, const float* w, void* y, float* rsqrt_out,
+                           int64_t rows, int64_t dim, float eps, int dtype,
+                           hipStream_t stream) {
+  PULSAR_REQUIRE(rows >= 0 && dim > 0, "rmsnorm: rows >= 0 and dim > 0 required");
+  if (rows == 0) return PULSAR_OK;
+  PULSAR_REQUIRE(x && w && y, "rmsnorm: null pointer");
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    rmsnorm_kernel<T><<<(unsigned)rows, 256, 0, stream>>>((const T*)x, w, (T*)y, rsqrt_out,
+                                                          (int)dim, eps);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_rope_forward(const void* x, void* y, const float* cos, const float* sin,
+                        int64_t rows, int64_t T, int64_t head_dim, int dtype,
+                        hipStream_t stream) {
+  PULSAR_REQUIRE(head_dim > 0 && head_dim % 2 == 0, "rope: head_dim must be even");
+  PULSAR_REQUIRE(T > 0 || rows == 0, "rope: T must be positive");
+  if (rows == 0) return PULSAR_OK;
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T_ = decltype(tag);
+    const int64_t n = rows * (head_dim / 2);
+    rope_kernel<T_><<<blocks_for(n, 256), 256, 0, stream>>>((const T_*)x, (T_*)y, cos, sin, rows,
+                                                            T, (int)head_dim);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_qk_rmsnorm_rope_forward(const void* x, int64_t sB, int64_t sH, int64_t sT,
+                                   int64_t B, int64_t H, int64_t T, int64_t head_dim,
+                                   const float* w, const float* cos, const float* sin,
+                                   void* y, float* rsqrt_out, float eps, int dtype,
+                                   hipStream_t stream) {
+  if (head_dim != 64)
+    return fail(PULSAR_ERR_INVALID,
+                "qk_rmsnorm_rope requires head_dim == 64, got " + std::to_string(head_dim));
+  const int64_t nvec = B * H * T;
+  if (nvec == 0) return PULSAR_OK;
+  PULSAR_REQUIRE(T > 0 && H > 0, "qk_rmsnorm_rope: H and T must be positive");
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T_ = decltype(tag);
+    qk_norm_rope_kernel<T_><<<blocks_for(nvec, 4), 256, 0, stream>>>(
+        (const T_*)x, sB, sH, sT, (int)H, (int)T, nvec, w, cos, sin, (T_*)y, rsqrt_out, eps);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_fused_attn_gate_forward(const void* attn, const float* gate_logits, void* out,
+                                   int64_t B, int64_t H, int64_t T, int64_t head_dim,
+                                   int dtype, hipStream_t stream) {
+  if (head_dim != 64)
+    return fail(PULSAR_ERR_INVALID,
+                "fused_attn_gate requires head_dim == 64, got " + std::to_string(head_dim));
+  const int64_t total = B * H * T * head_dim;
+  if (total == 0) return PULSAR_OK;
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T_ = decltype(tag);
+    attn_gate_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>(
+        (const T_*)attn, gate_logits, (T_*)out, (int)H, (int)T, (int)head_dim, total);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_causal_conv1d_k4_forward(const void* x, const float* w, void* y, int64_t B,
+                                    int64_t T, int64_t D, int dtype, hipStream_t stream) {
+  PULSAR_REQUIRE(B >= 0 && T >= 0 && D > 0, "conv1d_k4: bad shape");
+  const int64_t total = B * T * D;
+  if (total == 0) return PULSAR_OK;
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T_ = decltype(tag);
+    conv_k4_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>((const T_*)x, w, (T_*)y, T,
+                                                                   D, total);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_fused_swiglu_forward(const void* gu, void* out, int64_t rows, int64_t d_ff,
+                                int dtype, hipStream_t stream) {
+  PULSAR_REQUIRE(rows >= 0 && d_ff > 0, "swiglu: bad shape");
+  const int64_t total = rows * d_ff;
+  if (total == 0) return PULSAR_OK;
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T_ = decltype(tag);
+    swiglu_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>((const T_*)gu, (T_*)out, d_ff,
+                                                                  total);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_moe_router_topk_forward(const void* logits, int logits_dtype, const float* bias,
+                                   int64_t* topk_idx, uint16_t* topk_w_bf16, float* z_loss,
+                                   float* probs_mean, int64_t N, int64_t E, int64_t K,
+                                   float z_loss_weight, hipStream_t stream) {
+  if (E < 1 || E > 32)
+    return fail(PULSAR_ERR_INVALID,
+                "moe_router_topk_forward supports E <= 32, got " + std::to_string(E));
+  if (K < 1 || K > 8 || K > E)
+    return fail(PULSAR_ERR_INVALID,
+                "top_k must be in [1, min(8, E)], got " + std::to_string(K));
+  PULSAR_REQUIRE(N >= 0, "router: N must be >= 0");
+  return dispatch_dtype(logits_dtype, [&](auto tag) {
+    using L = decltype(tag);
+    if (N > 0)
+      router_topk_kernel<L><<<blocks_for(N, 128), 128, 0, stream>>>(
+          (const L*)logits, bias, topk_idx, topk_w_bf16, N, (int)E, (int)K);
+    PULSAR_LAUNCH_CHECK();
+    if (z_loss && probs_mean) {
+      router_stats_kernel<L><<<1, 256, 0, stream>>>((const L*)logits, bias, z_loss, probs_mean,
+                                                    N, (int)E, z_loss_weight);
+      PULSAR_LAUNCH_CHECK();
+    }
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_moe_dispatch_forward(const void* x, const int64_t* topk_idx, const int32_t* slots,
+                                const int64_t* expert_counts, void* expert_inputs, int64_t N,
+                                int64_t D, int64_t K, int64_t E, int64_t C, int dtype,
+                                hipStream_t stream) {
+  if (D % 8 != 0)
+    return fail(PULSAR_ERR_INVALID,
+                "D must be a multiple of 8 for vectorised dispatch, got " + std::to_string(D));
+  PULSAR_REQUIRE(N >= 0 && K >= 0 && E > 0 && C >= 0, "dispatch: bad shape");
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    if (C > 0) {
+      dim3 g(64, (unsigned)E);
+      moe_zero_kernel<T><<<g, 256, 0, stream>>>((T*)expert_inputs, expert_counts, (int)C, D);
+      PULSAR_LAUNCH_CHECK();
+    }
+    if (N > 0 && K > 0 && C > 0) {
+      moe_dispatch_kernel<T><<<(unsigned)N, 128, 0, stream>>>(
+          (const T*)x, topk_idx, slots, (T*)expert_inputs, D, (int)K, (int)E, (int)C);
+      PULSAR_LAUNCH_CHECK();
+    }
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_moe_combine_forward(const void* expert_outputs, const int64_t* topk_idx,
+                               const uint16_t* topk_w_bf16, const int32_t* slots,
+                               const void* shared_out, void* out, int64_t N, int64_t D,
+                               int64_t K, int64_t E, int64_t C, int dtype, hipStream_t stream) {
+  PULSAR_REQUIRE(N >= 0 && D > 0 && K >= 0, "combine: bad shape");
+  if (N == 0) return PULSAR_OK;
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    moe_combine_kernel<T><<<(unsigned)N, 128, 0, stream>>>(
+        (const T*)expert_outputs, topk_idx, topk_w_bf16, slots, (const T*)shared_out, (T*)out, D,
+        (int)K, (int)E, (int)C);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  });
+}
+
+int pulsar_moe_slots_from_order(const int64_t* flat_e, const int64_t* order, int32_t* slots,
+                                int64_t* counts, int64_t M, int64_t E, int64_t C,
+                                hipStream_t stream) {
+  PULSAR_REQUIRE(E > 0 && E <= 1024 && M >= 0, "slots_from_order: bad shape");
+  fill_i64_kernel<<<blocks_for(E, 64), 64, 0, stream>>>(counts, E, 0);
+  PULSAR_LAUNCH_CHECK();
+  if (M == 0) return PULSAR_OK;
+  slots_count_kernel<<<blocks_for(M, 256), 256, 0, stream>>>(flat_e, counts, M, (int)E);
+  PULSAR_LAUNCH_CHECK();
+  slots_assign_kernel<<<blocks_for(M, 256), 256, 0, stream>>>(flat_e, order, counts, slots, M,
+                                                              (int)E, (int)C);
+  PULSAR_LAUNCH_CHECK();
+  return PULSAR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,215 @@
+"""Write golden vectors for the decode path by running the reference itself on the CPU.
+
+Run in the development container only (the reference tree is not present on GPU machines):
+
+    python tests/golden/make_golden.py [--ref /root/reference] [--skip-full]
+
+It imports the reference's ``src/model.py`` and ``src/infer.py`` unchanged, loads the
+synthetic weights of ``pulsar_engine.weights.synthetic_state`` into
+``PulsarForCausalLM``, casts with ``to_training_precision`` as ``load_inference_model``
+does (``src/infer.py:808-810``), and drives ``PulsarInferenceEngine`` through a
+duck-typed tokenizer that maps prompts to fixed id lists (the pattern of the
+reference's ``tests/test_model.py:518-526``). Only inputs and outputs are stored.
+
+Outputs (``tests/golden/*.npz`` plus ``index.json``):
+
+* ``tiny_<dtype>.npz`` — tiny config, 24-token prompt: prefill logits, per-pulse decode
+  logits and hidden states of the first decode steps, and generated id streams for greedy
+  (penalty 1.15 and 10), plain vs self-speculative, and a seeded sampled run.
+* ``full_fp32.npz`` — full-size fp32 model, 128-token prompt: prefill logits, the three
+  pulse logits of the first decode step, 64-token greedy self-speculative stream with
+  per-step top-5 ids/logits of the draft (pulse 0) and verify (pulse 2) passes, and a
+  penalty-10 greedy stream whose tokens are not dominated by the self-logit.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(REPO, "pulsar-300m_amd"))
+
+from pulsar_engine import weights as W  # noqa: E402
+from pulsar_engine.config import PulsarConfig, tiny_config  # noqa: E402
+
+
+class IdTokenizer:
+    """Duck-typed tokenizer: prompt strings are keys into a table of id lists."""
+
+    unk_token_id = None
+
+    def __init__(self, table: dict):
+        self.table = table
+
+    def encode(self, prompt, return_tensors=None):
+        return torch.tensor([self.table[prompt]], dtype=torch.long)
+
+    def decode(self, ids, skip_special_tokens=False):
+        return "".join(f"<{int(i)}>" for i in ids)
+
+    def convert_tokens_to_ids(self, tok):
+        # Ids of data/pulsar_tokenizer/tokenizer.json added_tokens; "</s>" is absent.
+        return {"<|endoftext|>": 0, "<|im_end|>": 2}.get(tok)
+
+
+def parse_ids(pieces):
+    return [int(p.strip("<>")) for p in pieces]
+
+
+def build_reference(ref_root: str, cfg: PulsarConfig, state: dict, dtype):
+    if ref_root not in sys.path:
+        sys.path.insert(0, ref_root)
+    # Keep the reference from importing this repository's pulsar_cuda package; instead
+    # emulate the drop-in being importable. On CPU tensors every pulsar_cuda call site is
+    # gated on x.is_cuda, so the one effect is that RoPE receives fp32 cos/sin tables
+    # (src/model.py:557), which is the configuration the HIP path reproduces.
+    sys.modules.setdefault("pulsar_cuda", None)
+    import src.model as ref_model  # noqa: E402
+    ref_model.HAS_PULSAR_CUDA = True
+    from src.infer import PulsarInferenceEngine  # noqa: E402
+    from src.model import PulsarConfig as RefConfig, PulsarForCausalLM  # noqa: E402
+
+    rcfg = RefConfig(**cfg.to_dict())
+    model = PulsarForCausalLM(rcfg)
+    sd = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in state.items()}
+    sd["lm_head.weight"] = sd["tok_emb.weight"]
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    bad = [k for k in missing if not any(s in k for s in ("counts", "pulse_counts"))]
+    assert not bad and not unexpected, (bad, unexpected)
+    model.to_training_precision(dtype)
+    return PulsarInferenceEngine(model, device="cpu", dtype=dtype)
+
+
+def record_passes(engine):
+    """Wrap decode_pulse_pass / prefill to capture their outputs."""
+    log = {"passes": [], "prefill": []}
+    orig_pass = engine.decode_pulse_pass
+    orig_prefill = engine.prefill
+
+    def pass_wrap(token_id, pos, kv_cache, pulse_idx, h_pulse_prev=None, h_0_norm_cached=None):
+        out = orig_pass(token_id, pos, kv_cache, pulse_idx, h_pulse_prev=h_pulse_prev,
+                        h_0_norm_cached=h_0_norm_cached)
+        log["passes"].append((int(token_id), int(pos), int(pulse_idx),
+                              out[0].detach().float().clone(), out[1].detach().float().clone()))
+        return out
+
+    def prefill_wrap(input_ids, kv_cache):
+        out = orig_prefill(input_ids, kv_cache)
+        log["prefill"].append(out.detach().float().clone())
+        return out
+
+    engine.decode_pulse_pass = pass_wrap
+    engine.prefill = prefill_wrap
+    return log
+
+
+def run(engine, tok, prompt_key, n, temperature, top_p, rp, speculative, seed=None):
+    if seed is not None:
+        torch.manual_seed(seed)
+    gen = (engine.self_speculative_stream_generate if speculative else engine.stream_generate)
+    return parse_ids(gen(tok, prompt_key, max_new_tokens=n, temperature=temperature,
+                         top_p=top_p, repetition_penalty=rp))
+
+
+def tiny_goldens(ref_root: str, dtype, tag: str, out_dir: str) -> dict:
+    cfg = tiny_config()
+    state = W.synthetic_state(cfg, seed=0)
+    prompt = W.uniform_ids(0, "tiny_prompt", 24, cfg.vocab_size).tolist()
+    tok = IdTokenizer({"p": prompt})
+    eng = build_reference(ref_root, cfg, state, dtype)
+    out = {"prompt": np.array(prompt, dtype=np.int64)}
+
+    log = record_passes(eng)
+    ids = run(eng, tok, "p", 6, 0.0, 1.0, 1.15, speculative=False)
+    out["greedy_plain_ids"] = np.array(ids, dtype=np.int64)
+    out["prefill_logits"] = log["prefill"][0].numpy().reshape(-1)
+    out["pass_token"] = np.array([p[0] for p in log["passes"]], dtype=np.int64)
+    out["pass_pos"] = np.array([p[1] for p in log["passes"]], dtype=np.int64)
+    out["pass_pulse"] = np.array([p[2] for p in log["passes"]], dtype=np.int64)
+    out["pass_logits"] = np.stack([p[3].numpy().reshape(-1) for p in log["passes"]])
+    out["pass_hidden"] = np.stack([p[4].numpy().reshape(-1) for p in log["passes"]])
+
+    eng = build_reference(ref_root, cfg, state, dtype)
+    out["greedy_spec_ids"] = np.array(run(eng, tok, "p", 20, 0.0, 1.0, 1.15, True), dtype=np.int64)
+    out["greedy_rp10_plain_ids"] = np.array(run(eng, tok, "p", 20, 0.0, 1.0, 10.0, False), dtype=np.int64)
+    out["greedy_rp10_spec_ids"] = np.array(run(eng, tok, "p", 20, 0.0, 1.0, 10.0, True), dtype=np.int64)
+    out["sampled_spec_ids"] = np.array(run(eng, tok, "p", 20, 0.8, 0.95, 1.15, True, seed=1234),
+                                       dtype=np.int64)
+    out["sampled_rp10_spec_ids"] = np.array(run(eng, tok, "p", 20, 1.0, 0.9, 10.0, True, seed=99),
+                                            dtype=np.int64)
+    path = os.path.join(out_dir, f"tiny_{tag}.npz")
+    np.savez_compressed(path, **out)
+    return {"file": os.path.basename(path), "config": cfg.to_dict(), "seed": 0,
+            "weights_sha256": W.state_digest(state), "dtype": tag}
+
+
+def full_goldens(ref_root: str, out_dir: str) -> dict:
+    cfg = PulsarConfig()
+    t0 = time.time()
+    state = W.synthetic_state(cfg, seed=0)
+    digest = W.state_digest(state)
+    prompt = W.uniform_ids(0, "prompt", 128, cfg.vocab_size).tolist()
+    tok = IdTokenizer({"p": prompt})
+    eng = build_reference(ref_root, cfg, state, torch.float32)
+    print(f"[golden] full model built in {time.time() - t0:.1f}s", flush=True)
+    out = {"prompt": np.array(prompt, dtype=np.int64)}
+
+    log = record_passes(eng)
+    ids = run(eng, tok, "p", 64, 0.0, 1.0, 1.15, speculative=True)
+    out["greedy_spec_ids"] = np.array(ids, dtype=np.int64)
+    out["prefill_logits"] = log["prefill"][0].numpy().reshape(-1)
+    first = [p for p in log["passes"] if p[1] == len(prompt)]
+    out["step0_pass_logits"] = np.stack([p[3].numpy().reshape(-1) for p in first[:3]])
+    draft = [p for p in log["passes"] if p[2] == 0]
+    verify = [p for p in log["passes"] if p[2] == 2]
+    top = lambda ps: [torch.topk(p[3].reshape(-1), 5) for p in ps]  # noqa: E731
+    out["pulse0_top5_ids"] = np.stack([t.indices.numpy() for t in top(draft)])
+    out["pulse0_top5_vals"] = np.stack([t.values.numpy() for t in top(draft)])
+    out["pulse2_top5_ids"] = np.stack([t.indices.numpy() for t in top(verify)])
+    out["pulse2_top5_vals"] = np.stack([t.values.numpy() for t in top(verify)])
+    out["pulse_pos"] = np.array([p[1] for p in verify], dtype=np.int64)
+    print(f"[golden] full greedy stream done at {time.time() - t0:.1f}s", flush=True)
+
+    eng = build_reference(ref_root, cfg, state, torch.float32)
+    log = record_passes(eng)
+    ids = run(eng, tok, "p", 32, 0.0, 1.0, 10.0, speculative=True)
+    out["greedy_rp10_spec_ids"] = np.array(ids, dtype=np.int64)
+    verify = [p for p in log["passes"] if p[2] == 2]
+    out["rp10_pulse2_top5_vals"] = np.stack([torch.topk(p[3].reshape(-1), 5).values.numpy()
+                                             for p in verify])
+    print(f"[golden] full rp10 stream done at {time.time() - t0:.1f}s", flush=True)
+    path = os.path.join(out_dir, "full_fp32.npz")
+    np.savez_compressed(path, **out)
+    return {"file": os.path.basename(path), "config": cfg.to_dict(), "seed": 0,
+            "weights_sha256": digest, "dtype": "fp32"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--ref", default="/root/reference")
+    ap.add_argument("--out", default=HERE)
+    ap.add_argument("--skip-full", action="store_true")
+    args = ap.parse_args()
+    torch.set_num_threads(max(1, min(8, os.cpu_count() or 1)))
+    index = {"generator": "tests/golden/make_golden.py", "torch": torch.__version__,
+             "rope_tables": "fp32 (reference HAS_PULSAR_CUDA=True, CPU tensors)",
+             "numpy": np.__version__, "stop_ids": [0, 2], "entries": []}
+    index["entries"].append(tiny_goldens(args.ref, torch.float32, "fp32", args.out))
+    index["entries"].append(tiny_goldens(args.ref, torch.bfloat16, "bf16", args.out))
+    if not args.skip_full:
+        index["entries"].append(full_goldens(args.ref, args.out))
+    with open(os.path.join(args.out, "index.json"), "w") as f:
+        json.dump(index, f, indent=1)
+    print("[golden] wrote", [e["file"] for e in index["entries"]])
+
+
+if __name__ == "__main__":
+    main()
