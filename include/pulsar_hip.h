@@ -125,6 +125,103 @@ int pulsar_moe_slots_from_order(const int64_t* flat_e, const int64_t* order, int
                                 int64_t* counts, int64_t M, int64_t E, int64_t C,
                                 hipStream_t stream);
 
+
+/* ---------------------------------------------------------------------------------
+ * Decode engine: prefill + self-speculative decode of a batch of sequences.
+ * Replaces the reference's PulsarInferenceEngine (src/infer.py:181-731) and
+ * UnifiedKVCache (src/infer.py:64-178). No reference C entry exists for these: the
+ * reference drives the same math from Python; a binding mirrors its Python interface.
+ * ------------------------------------------------------------------------------- */
+
+#define PULSAR_MAX_LAYERS 16
+
+/* Architecture constants plus device pointers to the kernel-format weights.
+ * T = element type selected by dtype. Per-pulse tensors hold the first n_pulses pulses.
+ * Host-side preparation (see pulsar_engine/model.py) merges the per-pulse LoRA into the
+ * projections exactly as the reference (src/model.py:716-727), appends the attention-gate
+ * rows to the merged qkv weight, transposes routed experts to [E][out][in], and rounds
+ * fp32-kept parameters through T where the reference casts them (.to(x.dtype)). */
+typedef struct PulsarModelDesc {
+  int32_t vocab, d_model, n_heads, n_kv_heads, head_dim, d_expert, d_shared, n_layers;
+  int32_t n_pulses, n_experts, top_k, window, base_seq_len, reinject_rank, dtype;
+  uint32_t local_mask;      /* bit L set: layer L is a sliding-window layer */
+  float rms_eps, softcap;
+  int32_t rope_len;         /* rows of the RoPE tables (>= max positions) */
+  const void* tok_emb;      /* [V][D] T, tied output head */
+  const float* anchor_norm; /* [D] */
+  const float* state_norm;  /* [D] */
+  const float* final_norm;  /* [D] */
+  const float* conv_w;      /* [D][4] or NULL */
+  const void* step_emb;     /* [P][D] T */
+  const void* reinject_down;/* [P][r][2D] T */
+  const void* reinject_up;  /* [P][D][r] T */
+  const void* reinject_bias;/* [P][D] T */
+  const void* res_scale;    /* [P][D] T */
+  const float* rope_cos_local;  /* [rope_len][head_dim/2] */
+  const float* rope_sin_local;
+  const float* rope_cos_global;
+  const float* rope_sin_global;
+  const float* attn_norm[PULSAR_MAX_LAYERS];   /* [P][D] */
+  const float* mlp_norm[PULSAR_MAX_LAYERS];    /* [P][D] */
+  const void* wqkvg[PULSAR_MAX_LAYERS];        /* [P][qkv+H][D] T: merged qkv | gate rows */
+  const void* gate_bias[PULSAR_MAX_LAYERS];    /* [P][H] T */
+  const void* wo[PULSAR_MAX_LAYERS];           /* [P][D][H*hd] T merged */
+  const float* q_norm[PULSAR_MAX_LAYERS];      /* [P][H][hd] */
+  const float* k_norm[PULSAR_MAX_LAYERS];      /* [P][Hkv][hd] */
+  const float* v_lambda[PULSAR_MAX_LAYERS];    /* [P] sigmoid(lambda) rounded through T */
+  const void* shared_gu[PULSAR_MAX_LAYERS];    /* [2 d_shared][D] T */
+  const void* shared_down[PULSAR_MAX_LAYERS];  /* [D][d_shared] T */
+  const void* routed_gu[PULSAR_MAX_LAYERS];    /* [E][2 d_expert][D] T */
+  const void* routed_down[PULSAR_MAX_LAYERS];  /* [E][D][d_expert] T */
+  const float* router[PULSAR_MAX_LAYERS];      /* [P][E][D] */
+  const float* expert_bias[PULSAR_MAX_LAYERS]; /* [P][E] */
+  const void* routed_scale[PULSAR_MAX_LAYERS]; /* [P][D] T */
+} PulsarModelDesc;
+
+/* Generation settings (the reference's generate() arguments, src/infer.py:733-743). */
+typedef struct PulsarEngineConfig {
+  int32_t max_batch;     /* sequences */
+  int32_t max_prompt;    /* prompt tokens per sequence */
+  int32_t max_new;       /* max_new_tokens */
+  int32_t max_ctx;       /* positions per sequence (>= max_prompt + max_new + 1) */
+  int32_t speculative;   /* 1: self-speculative (generate(speculative=True)); 0: plain */
+  int32_t all_logits;    /* 1: compute logits for every pulse pass (testing) */
+  float temperature;     /* <= 1e-4 selects greedy */
+  float top_p;
+  float repetition_penalty;
+  int32_t n_stop;
+  int32_t stop_ids[8];
+  uint64_t seed;
+} PulsarEngineConfig;
+
+/* Buffers readable with pulsar_engine_read. */
+#define PULSAR_BUF_TOKENS 0    /* int32 [B][max_new] emitted ids */
+#define PULSAR_BUF_SEQSTATE 1  /* int32 [B][20] controller state: [0]=done [1]=produced
+                                  [11]=tests [12]=accepted */
+#define PULSAR_BUF_LOGITS 2    /* fp32 [n_lrows][V] logits of the last step */
+#define PULSAR_BUF_ROWS 3      /* int32 [n_rows][8] rows of the next step
+                                  (seq, slot, pulse, pos, token, lrow, extra, 0) */
+#define PULSAR_BUF_CTL 4       /* int32 [16] n_rows, n_lrows, pulse_start[4],
+                                  pulse_count[4], active, step */
+#define PULSAR_BUF_LAST_ROWS 5 /* int32 [n_rows][8] rows of the last executed step */
+#define PULSAR_BUF_LAST_CTL 6  /* int32 [16] control block of the last executed step */
+
+int pulsar_engine_create(const PulsarModelDesc* model, const PulsarEngineConfig* cfg,
+                         void** handle);
+int pulsar_engine_destroy(void* handle);
+/* Prefill B prompts of T tokens (host ids, row-major [B][T]), fill the KV cache, draw the
+ * first token of every sequence. Synchronises the stream at the end. */
+int pulsar_engine_prefill(void* handle, const int32_t* host_ids, int32_t B, int32_t T,
+                          hipStream_t stream);
+/* Run n pulse steps. use_graph=1 replays a captured HIP graph of one step. */
+int pulsar_engine_step(void* handle, int32_t n_steps, int32_t use_graph, hipStream_t stream);
+/* Steps until every sequence is done (or max_steps), checking every `check_every` steps. */
+int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
+                           hipStream_t stream, int32_t* steps_run);
+/* Copy an engine buffer to host memory (synchronises the stream). */
+int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes,
+                       hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

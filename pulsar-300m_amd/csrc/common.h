@@ -10,6 +10,8 @@
 
 #include <string>
 
+#include "../../include/pulsar_hip.h"
+
 namespace pulsar {
 
 struct bf16 {

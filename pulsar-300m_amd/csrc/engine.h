@@ -1,0 +1,86 @@
+// Internal interfaces of the decode/prefill engine (not part of the C ABI).
+#pragma once
+
+#include "common.h"
+
+namespace pulsar {
+
+constexpr int kMaxLayers = 16;
+constexpr int kMaxPulses = 3;
+constexpr int kHeadDim = 64;
+constexpr int kPage = 64;  // positions per KV page
+
+// One (token, pulse) evaluation inside a step. Rows of a step are sorted by pulse.
+struct RowDesc {
+  int32_t seq;    // sequence index
+  int32_t slot;   // token-state slot of the sequence (0 or 1)
+  int32_t pulse;  // 0..n_pulses-1
+  int32_t pos;    // absolute position of the token
+  int32_t token;  // token id
+  int32_t lrow;   // logits row, or -1 when this pass needs no logits
+  int32_t extra_seen;  // token counted as seen when sampling this row (-1 = none)
+  int32_t pad;
+};
+
+// Step control block, written by the controller (or the host for prefill).
+struct StepCtl {
+  int32_t n_rows;
+  int32_t n_lrows;
+  int32_t pulse_start[4];
+  int32_t pulse_count[4];
+  int32_t active;      // sequences not finished
+  int32_t step;        // step counter
+  int32_t pad[4];
+};
+
+// GEMM epilogues.
+enum Epi : int {
+  EPI_STORE = 0,      // C[r][n] = T(acc)
+  EPI_QKVG = 1,       // columns < n_main: store; tail columns: sigmoid gate with bias
+  EPI_RESID = 2,      // C[r][n] = T(C[r][n] + T(acc))
+  EPI_SWIGLU = 3,     // act = T(silu(T(acc_gate)) * T(acc_up))
+  EPI_LOGITS = 4,     // softcapped logits, fp32 store of T-rounded values
+  EPI_LOGITS_RAW = 5, // T-rounded logits without softcap (prefill)
+  EPI_SCALE = 6,      // C = T(T(acc) * scale[n])  (prefill routed down with routed_scale)
+};
+
+// Row-set modes of a GEMM launch.
+enum RowMode : int {
+  ROWS_PULSE = 0,   // group g = pulse: rows [pulse_start[g], +pulse_count[g]) of the step
+  ROWS_LIST = 1,    // group g: rows list[g][0..count[g]) ; A row = a_map(entry), C row = entry
+  ROWS_ALL = 2,     // single group: rows [0, n) with n from ctl->n_rows or m_fixed
+  ROWS_LOGITS = 3,  // logits rows i < ctl->n_lrows (A row = C row = i)
+};
+
+struct GemmArgs {
+  const void* A;           // activations, row stride lda (elements)
+  int64_t lda;
+  const void* W;           // weights [groups][N][K] row-major
+  int64_t w_group_stride;  // elements between groups (0 = shared weight)
+  int64_t ldw;
+  void* C;                 // output rows, stride ldc
+  int64_t ldc;
+  int K;
+  int N;                   // output columns (for SWIGLU: act columns; weights hold 2N rows)
+  int n_main;              // EPI_QKVG: number of non-gate columns
+  int row_mode;
+  int group_offset;        // first group index covered by grid.y == 0
+  int m_fixed;             // ROWS_ALL with ctl == nullptr
+  const StepCtl* ctl;
+  const int32_t* list;        // ROWS_LIST: [groups][list_stride]
+  const int32_t* list_count;  // ROWS_LIST: [groups]
+  int64_t list_stride;
+  int a_div;               // ROWS_LIST: A row = entry / a_div (1 = same as entry)
+  // epilogue operands
+  void* C2;                // EPI_QKVG: gate output [rows][n_gate]
+  int64_t ldc2;
+  const void* bias;        // EPI_QKVG: [groups][n_gate] T ; EPI_SCALE: [N] T
+  int64_t bias_group_stride;
+  float softcap;
+  int c_row_offset;        // added to C row index (prefill chunking)
+};
+
+int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
+                hipStream_t s);
+
+}  // namespace pulsar

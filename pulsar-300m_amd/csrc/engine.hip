@@ -1,0 +1,915 @@
+// Decode engine: owns the KV cache, per-row work buffers and controller state of a batch
+// of sequences; runs prefill eagerly and decode as a step (one pulse of every active row)
+// that can be captured once into a HIP graph and replayed.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+#include "rows.h"
+#include "sample.h"
+
+namespace pulsar {
+
+struct Engine {
+  PulsarModelDesc m{};
+  PulsarEngineConfig cfg{};
+  int dtype = 0, es = 4;
+  int D = 0, H = 0, Hkv = 0, qkv = 0, qkvg = 0, E = 0, K = 0, de = 0, ds = 0, L = 0, P = 0, V = 0;
+  int B = 0, max_rows = 0, R = 0, max_pages = 0, lcap = 0, max_splits = 0;
+  std::vector<void*> allocs;
+
+  StepCtl* ctl = nullptr;
+  StepCtl* last_ctl = nullptr;
+  RowDesc* rows = nullptr;
+  RowDesc* last_rows = nullptr;
+  SeqState* state = nullptr;
+  int32_t *lrow_seq = nullptr, *lrow_extra = nullptr, *argmax = nullptr, *draw = nullptr;
+  int32_t *tokens = nullptr, *stop_ids = nullptr;
+  uint32_t* seen = nullptr;
+  void *e_state = nullptr, *hout_state = nullptr;
+  void *h_in = nullptr, *h = nullptr, *xn = nullptr, *qkvbuf = nullptr, *gate = nullptr;
+  void *attn_out = nullptr, *v_first = nullptr, *act_s = nullptr, *act_r = nullptr;
+  void *out_s = nullptr, *out_r = nullptr, *xn_final = nullptr;
+  float *part = nullptr, *logits = nullptr, *topk_w = nullptr;
+  int32_t *topk_idx = nullptr, *keep = nullptr;
+  int32_t *lists = nullptr, *list_count = nullptr;      // decode: [L][E][max_rows*K], [L][E]
+  int32_t *p_lists = nullptr, *p_lcount = nullptr, *p_cnt = nullptr;  // prefill
+  int32_t* p_ids = nullptr;
+  RowDesc* p_rows = nullptr;  // [P][R]
+  StepCtl* p_ctl = nullptr;   // [P]
+  int32_t* page_table = nullptr;
+  KVDesc kv{};
+  int prompt_len = 0;
+  bool prefilled = false;
+
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+
+  ~Engine() {
+    if (exec) hipGraphExecDestroy(exec);
+    if (graph) hipGraphDestroy(graph);
+    for (void* p : allocs) hipFree(p);
+  }
+
+  template <typename X>
+  int alloc(X** p, size_t bytes) {
+    void* q = nullptr;
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(&q, bytes);
+    if (e != hipSuccess)
+      return fail(PULSAR_ERR_HIP, std::string("hipMalloc(") + std::to_string(bytes) +
+                                      "): " + hipGetErrorString(e));
+    allocs.push_back(q);
+    *p = reinterpret_cast<X*>(q);
+    return PULSAR_OK;
+  }
+};
+
+#define PULSAR_TRY(expr)          \
+  do {                            \
+    int _rc = (expr);             \
+    if (_rc != PULSAR_OK) return _rc; \
+  } while (0)
+
+namespace {
+
+int validate(const PulsarModelDesc& m, const PulsarEngineConfig& c) {
+  PULSAR_REQUIRE(m.dtype == PULSAR_F32 || m.dtype == PULSAR_BF16, "model dtype");
+  PULSAR_REQUIRE(m.head_dim == kHeadDim, "engine requires head_dim == 64");
+  PULSAR_REQUIRE(m.n_heads % m.n_kv_heads == 0 && m.n_heads / m.n_kv_heads == 4,
+                 "engine requires 4 query heads per kv head");
+  PULSAR_REQUIRE(m.n_layers >= 1 && m.n_layers <= PULSAR_MAX_LAYERS, "n_layers");
+  PULSAR_REQUIRE(m.n_pulses >= 1 && m.n_pulses <= kMaxPulses, "n_pulses must be 1..3");
+  PULSAR_REQUIRE(m.n_experts >= 1 && m.n_experts <= 32 && m.top_k >= 1 && m.top_k <= 8,
+                 "experts");
+  PULSAR_REQUIRE(m.d_model % 256 == 0 && m.d_expert % 256 == 0 && m.d_shared % 256 == 0,
+                 "d_model, d_expert, d_shared must be multiples of 256");
+  PULSAR_REQUIRE(m.reinject_rank >= 1 && m.reinject_rank <= 16, "reinject rank");
+  PULSAR_REQUIRE(m.vocab % 4096 == 0, "vocab must be a multiple of 4096");
+  PULSAR_REQUIRE(c.max_batch >= 1 && c.max_batch <= 256, "max_batch must be 1..256");
+  PULSAR_REQUIRE(c.max_prompt >= 1 && c.max_new >= 0, "max_prompt/max_new");
+  PULSAR_REQUIRE(c.max_ctx >= c.max_prompt + c.max_new + 2, "max_ctx < max_prompt + max_new + 2");
+  PULSAR_REQUIRE(m.rope_len >= c.max_ctx, "rope tables shorter than max_ctx");
+  PULSAR_REQUIRE(c.n_stop >= 0 && c.n_stop <= 8, "n_stop must be 0..8");
+  return PULSAR_OK;
+}
+
+__global__ void set_seen_kernel(const int32_t* ids, uint32_t* seen, int T, int V, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int b = i / T;
+  const int tok = ids[i];
+  atomicOr(&seen[(int64_t)b * (V / 32) + (tok >> 5)], 1u << (tok & 31));
+}
+
+__global__ void copy_rows_kernel(const StepCtl* ctl, const RowDesc* rows, StepCtl* last_ctl,
+                                 RowDesc* last_rows) {
+  const int n = ctl->n_rows;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) last_rows[i] = rows[i];
+  if (threadIdx.x == 0) *last_ctl = *ctl;
+}
+
+void kv_desc(Engine& e) {
+  e.kv.page_table = e.page_table;
+  e.kv.local_mask = e.m.local_mask;
+  e.kv.Hkv = e.Hkv;
+  e.kv.lcap = e.lcap;
+  e.kv.max_pages = e.max_pages;
+}
+
+int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) {
+  PULSAR_TRY(validate(m, c));
+  Engine* e = new Engine();
+  std::unique_ptr<Engine> guard(e);
+  e->m = m;
+  e->cfg = c;
+  e->dtype = m.dtype;
+  e->es = m.dtype == PULSAR_BF16 ? 2 : 4;
+  e->D = m.d_model;
+  e->H = m.n_heads;
+  e->Hkv = m.n_kv_heads;
+  e->qkv = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
+  e->qkvg = e->qkv + m.n_heads;
+  e->E = m.n_experts;
+  e->K = m.top_k;
+  e->de = m.d_expert;
+  e->ds = m.d_shared;
+  e->L = m.n_layers;
+  e->P = m.n_pulses;
+  e->V = m.vocab;
+  e->B = c.max_batch;
+  e->max_rows = 2 * c.max_batch;
+  e->R = std::max(e->max_rows, c.max_batch * c.max_prompt);
+  e->max_pages = (c.max_ctx + kPage - 1) / kPage;
+  e->lcap = m.window + kPage;
+  e->max_splits = (c.max_ctx + kSplitLen - 1) / kSplitLen;
+  const size_t es = e->es, D = e->D, R = e->R, MR = e->max_rows;
+  Engine& x = *e;
+  PULSAR_TRY(x.alloc(&x.ctl, sizeof(StepCtl)));
+  PULSAR_TRY(x.alloc(&x.last_ctl, sizeof(StepCtl)));
+  PULSAR_TRY(x.alloc(&x.rows, sizeof(RowDesc) * MR));
+  PULSAR_TRY(x.alloc(&x.last_rows, sizeof(RowDesc) * MR));
+  PULSAR_TRY(x.alloc(&x.state, sizeof(SeqState) * x.B));
+  PULSAR_TRY(x.alloc(&x.lrow_seq, 4 * MR));
+  PULSAR_TRY(x.alloc(&x.lrow_extra, 4 * MR));
+  PULSAR_TRY(x.alloc(&x.argmax, 4 * MR));
+  PULSAR_TRY(x.alloc(&x.draw, 8 * MR));
+  PULSAR_TRY(x.alloc(&x.tokens, 4 * (size_t)x.B * std::max(1, c.max_new)));
+  PULSAR_TRY(x.alloc(&x.stop_ids, 4 * 8));
+  PULSAR_TRY(x.alloc(&x.seen, 4 * (size_t)x.B * (x.V / 32)));
+  PULSAR_TRY(x.alloc(&x.e_state, es * R * D));
+  PULSAR_TRY(x.alloc(&x.hout_state, es * R * D));
+  PULSAR_TRY(x.alloc(&x.h_in, es * R * D));
+  PULSAR_TRY(x.alloc(&x.h, es * R * D));
+  PULSAR_TRY(x.alloc(&x.xn, es * R * D));
+  PULSAR_TRY(x.alloc(&x.qkvbuf, es * R * x.qkv));
+  PULSAR_TRY(x.alloc(&x.gate, es * R * x.H));
+  PULSAR_TRY(x.alloc(&x.attn_out, es * R * x.H * kHeadDim));
+  PULSAR_TRY(x.alloc(&x.v_first, es * R * x.Hkv * kHeadDim));
+  PULSAR_TRY(x.alloc(&x.act_s, es * R * x.ds));
+  PULSAR_TRY(x.alloc(&x.act_r, es * R * x.K * x.de));
+  PULSAR_TRY(x.alloc(&x.out_s, es * R * D));
+  PULSAR_TRY(x.alloc(&x.out_r, es * R * x.K * D));
+  PULSAR_TRY(x.alloc(&x.xn_final, es * std::max<size_t>(MR, x.B) * D));
+  PULSAR_TRY(x.alloc(&x.logits, 4 * std::max<size_t>(MR, x.B) * x.V));
+  PULSAR_TRY(x.alloc(&x.topk_idx, 4 * R * x.K));
+  PULSAR_TRY(x.alloc(&x.topk_w, 4 * R * x.K));
+  PULSAR_TRY(x.alloc(&x.keep, 4 * R * x.K));
+  PULSAR_TRY(x.alloc(&x.part, 4 * MR * x.Hkv * x.max_splits * 4 * 66));
+  PULSAR_TRY(x.alloc(&x.lists, 4 * (size_t)x.L * x.E * MR * x.K));
+  PULSAR_TRY(x.alloc(&x.list_count, 4 * (size_t)x.L * x.E));
+  PULSAR_TRY(x.alloc(&x.p_lists, 4 * (size_t)x.E * R * x.K));
+  PULSAR_TRY(x.alloc(&x.p_lcount, 4 * (size_t)x.E));
+  PULSAR_TRY(x.alloc(&x.p_cnt, 4 * (size_t)x.B * x.E));
+  PULSAR_TRY(x.alloc(&x.p_ids, 4 * (size_t)x.B * c.max_prompt));
+  PULSAR_TRY(x.alloc(&x.p_rows, sizeof(RowDesc) * x.P * (size_t)x.B * c.max_prompt));
+  PULSAR_TRY(x.alloc(&x.p_ctl, sizeof(StepCtl) * x.P));
+  PULSAR_TRY(x.alloc(&x.page_table, 4 * (size_t)x.B * x.max_pages));
+  // KV cache
+  const size_t local_elems = (size_t)x.B * x.Hkv * x.lcap * kHeadDim;
+  const size_t global_elems = (size_t)x.B * x.max_pages * x.Hkv * kPage * kHeadDim;
+  for (int l = 0; l < x.L; ++l) {
+    const bool loc = (m.local_mask >> l) & 1u;
+    const size_t n = loc ? local_elems : global_elems;
+    PULSAR_TRY(x.alloc(&x.kv.k[l], es * n));
+    PULSAR_TRY(x.alloc(&x.kv.v[l], es * n));
+  }
+  std::vector<int32_t> pt((size_t)x.B * x.max_pages);
+  for (size_t i = 0; i < pt.size(); ++i) pt[i] = (int32_t)i;  // sequence b owns pages [b*mp, (b+1)*mp)
+  PULSAR_CHECK_HIP(hipMemcpy(x.page_table, pt.data(), pt.size() * 4, hipMemcpyHostToDevice));
+  std::vector<int32_t> stops(8, -1);
+  for (int i = 0; i < c.n_stop; ++i) stops[i] = c.stop_ids[i];
+  PULSAR_CHECK_HIP(hipMemcpy(x.stop_ids, stops.data(), 32, hipMemcpyHostToDevice));
+  PULSAR_CHECK_HIP(hipMemset(x.ctl, 0, sizeof(StepCtl)));
+  PULSAR_CHECK_HIP(hipMemset(x.last_ctl, 0, sizeof(StepCtl)));
+  PULSAR_CHECK_HIP(hipMemset(x.state, 0, sizeof(SeqState) * x.B));
+  PULSAR_CHECK_HIP(hipMemset(x.list_count, 0, 4 * (size_t)x.L * x.E));
+  kv_desc(x);
+  *out = guard.release();
+  return PULSAR_OK;
+}
+
+GemmArgs gemm_base(const Engine& e) {
+  GemmArgs g{};
+  g.a_div = 1;
+  g.softcap = 0.f;
+  return g;
+}
+
+// One pulse pass of every active row + logits + sampling + controller.
+int enqueue_step(Engine& e, hipStream_t s) {
+  const PulsarModelDesc& m = e.m;
+  const int D = e.D, MR = e.max_rows, dt = e.dtype;
+  PulseInputArgs pi{};
+  pi.ctl = e.ctl;
+  pi.rows = e.rows;
+  pi.D = D;
+  pi.rank = m.reinject_rank;
+  pi.eps = m.rms_eps;
+  pi.tok_emb = m.tok_emb;
+  pi.anchor_norm = m.anchor_norm;
+  pi.conv_w = m.conv_w;
+  pi.state_norm = m.state_norm;
+  pi.step_emb = m.step_emb;
+  pi.reinject_down = m.reinject_down;
+  pi.reinject_up = m.reinject_up;
+  pi.reinject_bias = m.reinject_bias;
+  pi.e_state = e.e_state;
+  pi.hout_state = e.hout_state;
+  pi.h_in = e.h_in;
+  pi.h = e.h;
+  pi.zero_counts = e.list_count;
+  pi.n_zero = e.L * e.E;
+  PULSAR_TRY(launch_pulse_input(pi, dt, MR, s));
+  const int64_t lstride = (int64_t)MR * e.K;
+  for (int l = 0; l < e.L; ++l) {
+    const bool loc = (m.local_mask >> l) & 1u;
+    NormArgs na{};
+    na.ctl = e.ctl;
+    na.rows = e.rows;
+    na.x = e.h;
+    na.ldx = D;
+    na.w = m.attn_norm[l];
+    na.w_pulse_stride = D;
+    na.y = e.xn;
+    na.D = D;
+    na.eps = m.rms_eps;
+    PULSAR_TRY(launch_norm_rows(na, dt, MR, s));
+    GemmArgs g = gemm_base(e);
+    g.A = e.xn;
+    g.lda = D;
+    g.W = m.wqkvg[l];
+    g.w_group_stride = (int64_t)e.qkvg * D;
+    g.ldw = D;
+    g.C = e.qkvbuf;
+    g.ldc = e.qkv;
+    g.K = D;
+    g.N = e.qkvg;
+    g.n_main = e.qkv;
+    g.row_mode = ROWS_PULSE;
+    g.ctl = e.ctl;
+    g.C2 = e.gate;
+    g.ldc2 = e.H;
+    g.bias = m.gate_bias[l];
+    g.bias_group_stride = e.H;
+    PULSAR_TRY(launch_gemm(g, dt, EPI_QKVG, e.P, MR, s));
+    QKPostArgs qa{};
+    qa.ctl = e.ctl;
+    qa.rows = e.rows;
+    qa.qkv = e.qkvbuf;
+    qa.ldq = e.qkv;
+    qa.H = e.H;
+    qa.Hkv = e.Hkv;
+    qa.layer = l;
+    qa.is_local = loc;
+    qa.window = m.window;
+    qa.base_seq_len = m.base_seq_len;
+    qa.eps = m.rms_eps;
+    qa.q_norm = m.q_norm[l];
+    qa.k_norm = m.k_norm[l];
+    qa.v_lambda = m.v_lambda[l];
+    qa.v_first = e.v_first;
+    qa.cos = loc ? m.rope_cos_local : m.rope_cos_global;
+    qa.sin = loc ? m.rope_sin_local : m.rope_sin_global;
+    qa.kv = e.kv;
+    PULSAR_TRY(launch_qk_post(qa, dt, MR, s));
+    AttnArgs aa{};
+    aa.ctl = e.ctl;
+    aa.rows = e.rows;
+    aa.qkv = e.qkvbuf;
+    aa.ldq = e.qkv;
+    aa.gate = e.gate;
+    aa.out = e.attn_out;
+    aa.part = e.part;
+    aa.max_splits = e.max_splits;
+    aa.H = e.H;
+    aa.Hkv = e.Hkv;
+    aa.layer = l;
+    aa.is_local = loc;
+    aa.window = m.window;
+    aa.scale = 0.125f;
+    aa.kv = e.kv;
+    PULSAR_TRY(launch_attn_decode(aa, dt, MR, s));
+    g = gemm_base(e);
+    g.A = e.attn_out;
+    g.lda = (int64_t)e.H * kHeadDim;
+    g.W = m.wo[l];
+    g.w_group_stride = (int64_t)D * e.H * kHeadDim;
+    g.ldw = (int64_t)e.H * kHeadDim;
+    g.C = e.h;
+    g.ldc = D;
+    g.K = e.H * kHeadDim;
+    g.N = D;
+    g.row_mode = ROWS_PULSE;
+    g.ctl = e.ctl;
+    PULSAR_TRY(launch_gemm(g, dt, EPI_RESID, e.P, MR, s));
+    na.w = m.mlp_norm[l];
+    PULSAR_TRY(launch_norm_rows(na, dt, MR, s));
+    RouterArgs ra{};
+    ra.ctl = e.ctl;
+    ra.rows = e.rows;
+    ra.x = e.xn;
+    ra.w = m.router[l];
+    ra.bias = m.expert_bias[l];
+    ra.E = e.E;
+    ra.K = e.K;
+    ra.D = D;
+    ra.topk_idx = e.topk_idx;
+    ra.topk_w = e.topk_w;
+    ra.lists = e.lists + (int64_t)l * e.E * lstride;
+    ra.list_count = e.list_count + (int64_t)l * e.E;
+    ra.list_stride = lstride;
+    PULSAR_TRY(launch_router_decode(ra, dt, MR, s));
+    // shared expert gate/up + SwiGLU
+    g = gemm_base(e);
+    g.A = e.xn;
+    g.lda = D;
+    g.W = m.shared_gu[l];
+    g.ldw = D;
+    g.C = e.act_s;
+    g.ldc = e.ds;
+    g.K = D;
+    g.N = e.ds;
+    g.row_mode = ROWS_ALL;
+    g.ctl = e.ctl;
+    PULSAR_TRY(launch_gemm(g, dt, EPI_SWIGLU, 1, MR, s));
+    // routed experts gate/up + SwiGLU over each expert's assignment list
+    g = gemm_base(e);
+    g.A = e.xn;
+    g.lda = D;
+    g.W = m.routed_gu[l];
+    g.w_group_stride = (int64_t)2 * e.de * D;
+    g.ldw = D;
+    g.C = e.act_r;
+    g.ldc = e.de;
+    g.K = D;
+    g.N = e.de;
+    g.row_mode = ROWS_LIST;
+    g.list = ra.lists;
+    g.list_count = ra.list_count;
+    g.list_stride = lstride;
+    g.a_div = e.K;
+    PULSAR_TRY(launch_gemm(g, dt, EPI_SWIGLU, e.E, MR, s));
+    // shared down
+    g = gemm_base(e);
+    g.A = e.act_s;
+    g.lda = e.ds;
+    g.W = m.shared_down[l];
+    g.ldw = e.ds;
+    g.C = e.out_s;
+    g.ldc = D;
+    g.K = e.ds;
+    g.N = D;
+    g.row_mode = ROWS_ALL;
+    g.ctl = e.ctl;
+    PULSAR_TRY(launch_gemm(g, dt, EPI_STORE, 1, MR, s));
+    // routed down
+    g = gemm_base(e);
+    g.A = e.act_r;
+    g.lda = e.de;
+    g.W = m.routed_down[l];
+    g.w_group_stride = (int64_t)D * e.de;
+    g.ldw = e.de;
+    g.C = e.out_r;
+    g.ldc = D;
+    g.K = e.de;
+    g.N = D;
+    g.row_mode = ROWS_LIST;
+    g.list = ra.lists;
+    g.list_count = ra.list_count;
+    g.list_stride = lstride;
+    g.a_div = 1;
+    PULSAR_TRY(launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
+    CombineArgs ca{};
+    ca.ctl = e.ctl;
+    ca.rows = e.rows;
+    ca.K = e.K;
+    ca.D = D;
+    ca.shared = e.out_s;
+    ca.routed = e.out_r;
+    ca.topk_w = e.topk_w;
+    ca.routed_scale = m.routed_scale[l];
+    ca.h = e.h;
+    PULSAR_TRY(launch_moe_combine(ca, dt, MR, s));
+  }
+  PulseOutputArgs po{};
+  po.ctl = e.ctl;
+  po.rows = e.rows;
+  po.D = D;
+  po.eps = m.rms_eps;
+  po.h_in = e.h_in;
+  po.h = e.h;
+  po.res_scale = m.res_scale;
+  po.hout_state = e.hout_state;
+  po.final_norm = m.final_norm;
+  po.xn_final = e.xn_final;
+  PULSAR_TRY(launch_pulse_output(po, dt, MR, s));
+  GemmArgs g = gemm_base(e);
+  g.A = e.xn_final;
+  g.lda = D;
+  g.W = m.tok_emb;
+  g.ldw = D;
+  g.C = e.logits;
+  g.ldc = e.V;
+  g.K = D;
+  g.N = e.V;
+  g.row_mode = ROWS_LOGITS;
+  g.ctl = e.ctl;
+  g.softcap = m.softcap;
+  PULSAR_TRY(launch_gemm(g, dt, EPI_LOGITS, 1, MR, s));
+  SampleArgs sa{};
+  sa.ctl = e.ctl;
+  sa.logits = e.logits;
+  sa.lrow_seq = e.lrow_seq;
+  sa.lrow_extra = e.lrow_extra;
+  sa.seen = e.seen;
+  sa.state = e.state;
+  sa.V = e.V;
+  sa.greedy = e.cfg.temperature <= 1e-4f;
+  sa.temperature = std::max(e.cfg.temperature, 1e-5f);
+  sa.top_p = e.cfg.top_p;
+  sa.rep_penalty = e.cfg.repetition_penalty;
+  sa.seed = e.cfg.seed;
+  sa.out_argmax = e.argmax;
+  sa.out_draw = e.draw;
+  PULSAR_TRY(launch_sample(sa, dt, MR, s));
+  copy_rows_kernel<<<1, 256, 0, s>>>(e.ctl, e.rows, e.last_ctl, e.last_rows);
+  PULSAR_LAUNCH_CHECK();
+  ControllerArgs co{};
+  co.ctl = e.ctl;
+  co.state = e.state;
+  co.rows = e.rows;
+  co.lrow_seq = e.lrow_seq;
+  co.lrow_extra = e.lrow_extra;
+  co.seen = e.seen;
+  co.out_tokens = e.tokens;
+  co.argmax = e.argmax;
+  co.draw = e.draw;
+  co.stop_ids = e.stop_ids;
+  co.n_stop = e.cfg.n_stop;
+  co.B = e.B;
+  co.V = e.V;
+  co.n_pulses = e.P;
+  co.max_new = e.cfg.max_new;
+  co.speculative = e.cfg.speculative;
+  co.all_logits = e.cfg.all_logits;
+  co.prompt_len = e.prompt_len;
+  PULSAR_TRY(launch_controller(co, s));
+  return PULSAR_OK;
+}
+
+int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
+  const PulsarModelDesc& m = e.m;
+  PULSAR_REQUIRE(Bq == e.B, "prefill batch must equal max_batch");
+  PULSAR_REQUIRE(T >= 1 && T <= e.cfg.max_prompt, "prompt length out of range");
+  const int D = e.D, dt = e.dtype, P = e.P;
+  const int BT = Bq * T;
+  e.prompt_len = T;
+  for (int i = 0; i < BT; ++i)
+    PULSAR_REQUIRE(host_ids[i] >= 0 && host_ids[i] < e.V, "prompt id out of vocabulary");
+  // graph of a previous generation refers to the same buffers; it stays valid.
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.p_ids, host_ids, 4 * (size_t)BT, hipMemcpyHostToDevice, s));
+  std::vector<RowDesc> rows((size_t)P * BT);
+  std::vector<StepCtl> ctls(P);
+  for (int k = 0; k < P; ++k) {
+    for (int b = 0; b < Bq; ++b)
+      for (int t = 0; t < T; ++t) {
+        const int lrow = (k == P - 1 && t == T - 1) ? b : -1;
+        rows[(size_t)k * BT + b * T + t] = RowDesc{b, 0, k, t, host_ids[b * T + t], lrow, -1, 0};
+      }
+    StepCtl c{};
+    c.n_rows = BT;
+    c.n_lrows = (k == P - 1) ? Bq : 0;
+    c.pulse_start[k] = 0;
+    c.pulse_count[k] = BT;
+    ctls[k] = c;
+  }
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.p_rows, rows.data(), sizeof(RowDesc) * rows.size(),
+                                  hipMemcpyHostToDevice, s));
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.p_ctl, ctls.data(), sizeof(StepCtl) * P,
+                                  hipMemcpyHostToDevice, s));
+  std::vector<int32_t> lseq(e.max_rows, 0), lext(e.max_rows, -1);
+  for (int b = 0; b < Bq; ++b) lseq[b] = b;
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.lrow_seq, lseq.data(), 4 * lseq.size(), hipMemcpyHostToDevice, s));
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.lrow_extra, lext.data(), 4 * lext.size(), hipMemcpyHostToDevice, s));
+  PULSAR_CHECK_HIP(hipMemsetAsync(e.state, 0, sizeof(SeqState) * e.B, s));
+  PULSAR_CHECK_HIP(hipMemsetAsync(e.seen, 0, 4 * (size_t)e.B * (e.V / 32), s));
+  PULSAR_CHECK_HIP(hipMemsetAsync(e.ctl, 0, sizeof(StepCtl), s));
+
+  PULSAR_TRY(launch_prefill_stem(e.p_ids, m.tok_emb, m.anchor_norm, m.conv_w, e.xn, e.e_state,
+                                 Bq, T, D, m.rms_eps, dt, s));
+  const int64_t lstride = (int64_t)e.R * e.K;
+  for (int k = 0; k < P; ++k) {
+    const StepCtl* ctl = e.p_ctl + k;
+    const RowDesc* prow = e.p_rows + (size_t)k * BT;
+    PulseInputArgs pi{};
+    pi.ctl = ctl;
+    pi.rows = prow;
+    pi.D = D;
+    pi.rank = m.reinject_rank;
+    pi.prefill = 1;
+    pi.prefill_T = T;
+    pi.eps = m.rms_eps;
+    pi.tok_emb = m.tok_emb;
+    pi.anchor_norm = m.anchor_norm;
+    pi.conv_w = m.conv_w;
+    pi.state_norm = m.state_norm;
+    pi.step_emb = m.step_emb;
+    pi.reinject_down = m.reinject_down;
+    pi.reinject_up = m.reinject_up;
+    pi.reinject_bias = m.reinject_bias;
+    pi.e_state = e.e_state;
+    pi.hout_state = e.hout_state;
+    pi.h_in = e.h_in;
+    pi.h = e.h;
+    PULSAR_TRY(launch_pulse_input(pi, dt, BT, s));
+    for (int l = 0; l < e.L; ++l) {
+      const bool loc = (m.local_mask >> l) & 1u;
+      NormArgs na{};
+      na.ctl = ctl;
+      na.rows = prow;
+      na.x = e.h;
+      na.ldx = D;
+      na.w = m.attn_norm[l];
+      na.w_pulse_stride = D;
+      na.y = e.xn;
+      na.D = D;
+      na.eps = m.rms_eps;
+      PULSAR_TRY(launch_norm_rows(na, dt, BT, s));
+      GemmArgs g = gemm_base(e);
+      g.A = e.xn;
+      g.lda = D;
+      g.W = m.wqkvg[l];
+      g.w_group_stride = (int64_t)e.qkvg * D;
+      g.ldw = D;
+      g.C = e.qkvbuf;
+      g.ldc = e.qkv;
+      g.K = D;
+      g.N = e.qkvg;
+      g.n_main = e.qkv;
+      g.row_mode = ROWS_PULSE;
+      g.group_offset = k;
+      g.ctl = ctl;
+      g.C2 = e.gate;
+      g.ldc2 = e.H;
+      g.bias = m.gate_bias[l];
+      g.bias_group_stride = e.H;
+      PULSAR_TRY(launch_gemm(g, dt, EPI_QKVG, 1, BT, s));
+      QKPostArgs qa{};
+      qa.ctl = ctl;
+      qa.rows = prow;
+      qa.qkv = e.qkvbuf;
+      qa.ldq = e.qkv;
+      qa.H = e.H;
+      qa.Hkv = e.Hkv;
+      qa.layer = l;
+      qa.is_local = loc;
+      qa.prefill = 1;
+      qa.prefill_T = T;
+      qa.window = m.window;
+      qa.base_seq_len = m.base_seq_len;
+      qa.eps = m.rms_eps;
+      qa.q_norm = m.q_norm[l];
+      qa.k_norm = m.k_norm[l];
+      qa.v_lambda = m.v_lambda[l];
+      qa.v_first = e.v_first;
+      qa.cos = loc ? m.rope_cos_local : m.rope_cos_global;
+      qa.sin = loc ? m.rope_sin_local : m.rope_sin_global;
+      qa.kv = e.kv;
+      PULSAR_TRY(launch_qk_post(qa, dt, BT, s));
+      AttnArgs aa{};
+      aa.ctl = ctl;
+      aa.rows = prow;
+      aa.qkv = e.qkvbuf;
+      aa.ldq = e.qkv;
+      aa.gate = e.gate;
+      aa.out = e.attn_out;
+      aa.H = e.H;
+      aa.Hkv = e.Hkv;
+      aa.layer = l;
+      aa.is_local = loc;
+      aa.window = m.window;
+      aa.prefill_T = T;
+      aa.scale = 0.125f;
+      aa.kv = e.kv;
+      PULSAR_TRY(launch_attn_prefill(aa, dt, Bq, s));
+      g = gemm_base(e);
+      g.A = e.attn_out;
+      g.lda = (int64_t)e.H * kHeadDim;
+      g.W = m.wo[l];
+      g.w_group_stride = (int64_t)D * e.H * kHeadDim;
+      g.ldw = (int64_t)e.H * kHeadDim;
+      g.C = e.h;
+      g.ldc = D;
+      g.K = e.H * kHeadDim;
+      g.N = D;
+      g.row_mode = ROWS_PULSE;
+      g.group_offset = k;
+      g.ctl = ctl;
+      PULSAR_TRY(launch_gemm(g, dt, EPI_RESID, 1, BT, s));
+      na.w = m.mlp_norm[l];
+      PULSAR_TRY(launch_norm_rows(na, dt, BT, s));
+      RouterArgs ra{};
+      ra.x = e.xn;
+      ra.w = m.router[l];
+      ra.bias = m.expert_bias[l];
+      ra.E = e.E;
+      ra.K = e.K;
+      ra.D = D;
+      ra.pulse = k;
+      ra.m_fixed = BT;
+      ra.topk_idx = e.topk_idx;
+      ra.topk_w = e.topk_w;
+      PULSAR_TRY(launch_router_prefill(ra, dt, s));
+      // capacity of a reference prefill call: N = T tokens of one sequence (src/model.py:1339-1342)
+      const double avg = (double)T * e.K / e.E;
+      const long raw = (long)std::ceil(avg * 1.25);
+      const int C = (int)std::max<long>(32, ((raw + 31) / 32) * 32);
+      PULSAR_CHECK_HIP(hipMemsetAsync(e.p_cnt, 0, 4 * (size_t)Bq * e.E, s));
+      PULSAR_CHECK_HIP(hipMemsetAsync(e.p_lcount, 0, 4 * (size_t)e.E, s));
+      PULSAR_TRY(launch_prefill_capacity(e.topk_idx, e.topk_w, e.p_cnt, e.keep, e.p_lists,
+                                         e.p_lcount, lstride, Bq, T, e.K, e.E, C, s));
+      g = gemm_base(e);
+      g.A = e.xn;
+      g.lda = D;
+      g.W = m.shared_gu[l];
+      g.ldw = D;
+      g.C = e.act_s;
+      g.ldc = e.ds;
+      g.K = D;
+      g.N = e.ds;
+      g.row_mode = ROWS_ALL;
+      g.m_fixed = BT;
+      PULSAR_TRY(launch_gemm(g, dt, EPI_SWIGLU, 1, BT, s));
+      g = gemm_base(e);
+      g.A = e.xn;
+      g.lda = D;
+      g.W = m.routed_gu[l];
+      g.w_group_stride = (int64_t)2 * e.de * D;
+      g.ldw = D;
+      g.C = e.act_r;
+      g.ldc = e.de;
+      g.K = D;
+      g.N = e.de;
+      g.row_mode = ROWS_LIST;
+      g.list = e.p_lists;
+      g.list_count = e.p_lcount;
+      g.list_stride = lstride;
+      g.a_div = e.K;
+      PULSAR_TRY(launch_gemm(g, dt, EPI_SWIGLU, e.E, BT, s));
+      g = gemm_base(e);
+      g.A = e.act_s;
+      g.lda = e.ds;
+      g.W = m.shared_down[l];
+      g.ldw = e.ds;
+      g.C = e.out_s;
+      g.ldc = D;
+      g.K = e.ds;
+      g.N = D;
+      g.row_mode = ROWS_ALL;
+      g.m_fixed = BT;
+      PULSAR_TRY(launch_gemm(g, dt, EPI_STORE, 1, BT, s));
+      g = gemm_base(e);
+      g.A = e.act_r;
+      g.lda = e.de;
+      g.W = m.routed_down[l];
+      g.w_group_stride = (int64_t)D * e.de;
+      g.ldw = e.de;
+      g.C = e.out_r;
+      g.ldc = D;
+      g.K = e.de;
+      g.N = D;
+      g.row_mode = ROWS_LIST;
+      g.list = e.p_lists;
+      g.list_count = e.p_lcount;
+      g.list_stride = lstride;
+      g.a_div = 1;
+      g.bias = reinterpret_cast<const char*>(m.routed_scale[l]) + (size_t)k * D * e.es;
+      PULSAR_TRY(launch_gemm(g, dt, EPI_SCALE, e.E, BT, s));
+      CombineArgs ca{};
+      ca.m_fixed = BT;
+      ca.pulse = k;
+      ca.prefill = 1;
+      ca.K = e.K;
+      ca.D = D;
+      ca.shared = e.out_s;
+      ca.routed = e.out_r;
+      ca.topk_w = e.topk_w;
+      ca.keep = e.keep;
+      ca.routed_scale = m.routed_scale[l];
+      ca.h = e.h;
+      PULSAR_TRY(launch_moe_combine(ca, dt, BT, s));
+    }
+    PulseOutputArgs po{};
+    po.ctl = ctl;
+    po.rows = prow;
+    po.D = D;
+    po.prefill = 1;
+    po.prefill_T = T;
+    po.eps = m.rms_eps;
+    po.h_in = e.h_in;
+    po.h = e.h;
+    po.res_scale = m.res_scale;
+    po.hout_state = e.hout_state;
+    po.final_norm = m.final_norm;
+    po.xn_final = e.xn_final;
+    PULSAR_TRY(launch_pulse_output(po, dt, BT, s));
+  }
+  const StepCtl* lctl = e.p_ctl + (P - 1);
+  GemmArgs g = gemm_base(e);
+  g.A = e.xn_final;
+  g.lda = D;
+  g.W = m.tok_emb;
+  g.ldw = D;
+  g.C = e.logits;
+  g.ldc = e.V;
+  g.K = D;
+  g.N = e.V;
+  g.row_mode = ROWS_LOGITS;
+  g.ctl = lctl;
+  PULSAR_TRY(launch_gemm(g, dt, EPI_LOGITS_RAW, 1, Bq, s));
+  set_seen_kernel<<<(BT + 255) / 256, 256, 0, s>>>(e.p_ids, e.seen, T, e.V, BT);
+  PULSAR_LAUNCH_CHECK();
+  SampleArgs sa{};
+  sa.ctl = lctl;
+  sa.logits = e.logits;
+  sa.lrow_seq = e.lrow_seq;
+  sa.lrow_extra = e.lrow_extra;
+  sa.seen = e.seen;
+  sa.state = e.state;
+  sa.V = e.V;
+  sa.greedy = e.cfg.temperature <= 1e-4f;
+  sa.temperature = std::max(e.cfg.temperature, 1e-5f);
+  sa.top_p = e.cfg.top_p;
+  sa.rep_penalty = e.cfg.repetition_penalty;
+  sa.seed = e.cfg.seed;
+  sa.out_argmax = e.argmax;
+  sa.out_draw = e.draw;
+  PULSAR_TRY(launch_sample(sa, dt, Bq, s));
+  ControllerArgs co{};
+  co.ctl = e.ctl;
+  co.state = e.state;
+  co.rows = e.rows;
+  co.lrow_seq = e.lrow_seq;
+  co.lrow_extra = e.lrow_extra;
+  co.seen = e.seen;
+  co.out_tokens = e.tokens;
+  co.argmax = e.argmax;
+  co.draw = e.draw;
+  co.stop_ids = e.stop_ids;
+  co.n_stop = e.cfg.n_stop;
+  co.B = e.B;
+  co.V = e.V;
+  co.n_pulses = e.P;
+  co.max_new = e.cfg.max_new;
+  co.speculative = e.cfg.speculative;
+  co.all_logits = e.cfg.all_logits;
+  co.init = 1;
+  co.prompt_len = T;
+  PULSAR_TRY(launch_controller(co, s));
+  PULSAR_CHECK_HIP(hipStreamSynchronize(s));
+  e.prefilled = true;
+  return PULSAR_OK;
+}
+
+int step(Engine& e, int n, int use_graph, hipStream_t s) {
+  PULSAR_REQUIRE(e.prefilled, "engine: prefill before stepping");
+  if (!use_graph) {
+    for (int i = 0; i < n; ++i) PULSAR_TRY(enqueue_step(e, s));
+    return PULSAR_OK;
+  }
+  if (!e.exec) {
+    PULSAR_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_step(e, s);
+    hipGraph_t gr = nullptr;
+    const hipError_t ce = hipStreamEndCapture(s, &gr);
+    if (rc != PULSAR_OK) {
+      if (gr) hipGraphDestroy(gr);
+      return rc;
+    }
+    if (ce != hipSuccess) return fail(PULSAR_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce));
+    e.graph = gr;
+    PULSAR_CHECK_HIP(hipGraphInstantiate(&e.exec, gr, nullptr, nullptr, 0));
+  }
+  for (int i = 0; i < n; ++i) PULSAR_CHECK_HIP(hipGraphLaunch(e.exec, s));
+  return PULSAR_OK;
+}
+
+}  // namespace
+
+}  // namespace pulsar
+
+using namespace pulsar;
+
+extern "C" {
+
+int pulsar_engine_create(const PulsarModelDesc* model, const PulsarEngineConfig* cfg,
+                         void** handle) {
+  PULSAR_REQUIRE(model && cfg && handle, "engine_create: null argument");
+  Engine* e = nullptr;
+  PULSAR_TRY(create(*model, *cfg, &e));
+  *handle = e;
+  return PULSAR_OK;
+}
+
+int pulsar_engine_destroy(void* handle) {
+  delete reinterpret_cast<Engine*>(handle);
+  return PULSAR_OK;
+}
+
+int pulsar_engine_prefill(void* handle, const int32_t* host_ids, int32_t B, int32_t T,
+                          hipStream_t stream) {
+  PULSAR_REQUIRE(handle && host_ids, "engine_prefill: null argument");
+  return prefill(*reinterpret_cast<Engine*>(handle), host_ids, B, T, stream);
+}
+
+int pulsar_engine_step(void* handle, int32_t n_steps, int32_t use_graph, hipStream_t stream) {
+  PULSAR_REQUIRE(handle, "engine_step: null handle");
+  return step(*reinterpret_cast<Engine*>(handle), n_steps, use_graph, stream);
+}
+
+int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
+                           hipStream_t stream, int32_t* steps_run) {
+  PULSAR_REQUIRE(handle && check_every >= 1, "engine_generate: bad argument");
+  Engine& e = *reinterpret_cast<Engine*>(handle);
+  int done = 0;
+  StepCtl c{};
+  while (done < max_steps) {
+    const int n = std::min(check_every, max_steps - done);
+    PULSAR_TRY(step(e, n, 1, stream));
+    done += n;
+    PULSAR_CHECK_HIP(hipMemcpyAsync(&c, e.ctl, sizeof(StepCtl), hipMemcpyDeviceToHost, stream));
+    PULSAR_CHECK_HIP(hipStreamSynchronize(stream));
+    if (c.active == 0) break;
+  }
+  if (steps_run) *steps_run = done;
+  return PULSAR_OK;
+}
+
+int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes,
+                       hipStream_t stream) {
+  PULSAR_REQUIRE(handle && host_dst && bytes >= 0, "engine_read: bad argument");
+  Engine& e = *reinterpret_cast<Engine*>(handle);
+  const void* src = nullptr;
+  int64_t cap = 0;
+  switch (what) {
+    case PULSAR_BUF_TOKENS:
+      src = e.tokens;
+      cap = 4ll * e.B * std::max(1, e.cfg.max_new);
+      break;
+    case PULSAR_BUF_SEQSTATE:
+      src = e.state;
+      cap = (int64_t)sizeof(SeqState) * e.B;
+      break;
+    case PULSAR_BUF_LOGITS:
+      src = e.logits;
+      cap = 4ll * std::max(e.max_rows, e.B) * e.V;
+      break;
+    case PULSAR_BUF_ROWS:
+      src = e.rows;
+      cap = (int64_t)sizeof(RowDesc) * e.max_rows;
+      break;
+    case PULSAR_BUF_CTL:
+      src = e.ctl;
+      cap = sizeof(StepCtl);
+      break;
+    case PULSAR_BUF_LAST_ROWS:
+      src = e.last_rows;
+      cap = (int64_t)sizeof(RowDesc) * e.max_rows;
+      break;
+    case PULSAR_BUF_LAST_CTL:
+      src = e.last_ctl;
+      cap = sizeof(StepCtl);
+      break;
+    default:
+      return fail(PULSAR_ERR_INVALID, "engine_read: unknown buffer");
+  }
+  PULSAR_REQUIRE(bytes <= cap, "engine_read: more bytes than the buffer holds");
+  PULSAR_CHECK_HIP(hipMemcpyAsync(host_dst, src, bytes, hipMemcpyDeviceToHost, stream));
+  PULSAR_CHECK_HIP(hipStreamSynchronize(stream));
+  return PULSAR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,276 @@
+// Row-tiled GEMMs for decode and prefill: C[rows, N] = epi(A[rows, K] . W[N, K]^T).
+//
+// bf16: a workgroup of 4 waves owns a 32-row x 16-column output tile and splits K four
+// ways; each wave runs v_mfma_f32_16x16x32_bf16 on two 16-row blocks that share the
+// weight operand, with every weight element loaded exactly once (128-bit loads, k
+// contiguous per lane). Partial tiles are summed through LDS and wave 0 applies the
+// epilogue. Row sets come from the step control block (rows of one pulse, rows of one
+// expert, all rows, or logits rows), so one launch serves every pulse / expert group and
+// groups without rows exit before touching their weights.
+//
+// fp32: one wave per output column, lanes split K with 128-bit loads, wave64 reduction.
+#include "engine.h"
+
+namespace pulsar {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+namespace {
+
+__device__ __forceinline__ bf16x8_t load_bf16x8(const bf16* p) {
+  return *reinterpret_cast<const bf16x8_t*>(p);
+}
+
+// Resolve the (A row, C row) pairs of this workgroup's 32-row tile into LDS.
+// Returns the number of valid rows (0 => nothing to do).
+__device__ int resolve_rows(const GemmArgs& g, int group, int tile, int* a_row, int* c_row) {
+  __shared__ int s_n;
+  if (threadIdx.x == 0) {
+    int n = 0;
+    switch (g.row_mode) {
+      case ROWS_PULSE: {
+        const int cnt = g.ctl->pulse_count[group];
+        n = cnt - tile * 32;
+        break;
+      }
+      case ROWS_LIST:
+        n = g.list_count[group] - tile * 32;
+        break;
+      case ROWS_ALL: {
+        const int tot = g.ctl ? g.ctl->n_rows : g.m_fixed;
+        n = tot - tile * 32;
+        break;
+      }
+      case ROWS_LOGITS:
+        n = g.ctl->n_lrows - tile * 32;
+        break;
+    }
+    s_n = n < 0 ? 0 : (n > 32 ? 32 : n);
+  }
+  __syncthreads();
+  const int n = s_n;
+  if (threadIdx.x < 32) {
+    const int m = threadIdx.x;
+    int ar = -1, cr = -1;
+    if (m < n) {
+      const int i = tile * 32 + m;
+      switch (g.row_mode) {
+        case ROWS_PULSE:
+          ar = cr = g.ctl->pulse_start[group] + i;
+          break;
+        case ROWS_LIST: {
+          const int e = g.list[(int64_t)group * g.list_stride + i];
+          ar = e / g.a_div;
+          cr = e;
+          break;
+        }
+        case ROWS_ALL:
+          ar = cr = i;
+          break;
+        case ROWS_LOGITS:
+          ar = cr = i;
+          break;
+      }
+    }
+    a_row[m] = ar;
+    c_row[m] = cr < 0 ? -1 : cr + g.c_row_offset;
+  }
+  __syncthreads();
+  return n;
+}
+
+template <typename T>
+__device__ __forceinline__ void epilogue(const GemmArgs& g, int epi, int group, int crow, int col,
+                                         float acc, float acc_up) {
+  T* C = reinterpret_cast<T*>(g.C);
+  switch (epi) {
+    case EPI_STORE:
+      C[(int64_t)crow * g.ldc + col] = from_f<T>(acc);
+      break;
+    case EPI_QKVG:
+      if (col < g.n_main) {
+        C[(int64_t)crow * g.ldc + col] = from_f<T>(acc);
+      } else {
+        const int h = col - g.n_main;
+        const T* b = reinterpret_cast<const T*>(g.bias) + (int64_t)group * g.bias_group_stride;
+        const float v = rnd<T>(acc + to_f(b[h]));
+        reinterpret_cast<T*>(g.C2)[(int64_t)crow * g.ldc2 + h] = from_f<T>(sigmoidf_(v));
+      }
+      break;
+    case EPI_RESID: {
+      T* p = C + (int64_t)crow * g.ldc + col;
+      *p = from_f<T>(to_f(*p) + rnd<T>(acc));
+      break;
+    }
+    case EPI_SWIGLU: {
+      const float gt = rnd<T>(acc), up = rnd<T>(acc_up);
+      C[(int64_t)crow * g.ldc + col] = from_f<T>(gt * sigmoidf_(gt) * up);
+      break;
+    }
+    case EPI_LOGITS: {
+      float l = rnd<T>(acc);
+      if (g.softcap > 0.f) {
+        float t = rnd<T>(l / g.softcap);
+        t = rnd<T>(tanhf(t));
+        l = rnd<T>(g.softcap * t);
+      }
+      reinterpret_cast<float*>(g.C)[(int64_t)crow * g.ldc + col] = l;
+      break;
+    }
+    case EPI_LOGITS_RAW:
+      reinterpret_cast<float*>(g.C)[(int64_t)crow * g.ldc + col] = rnd<T>(acc);
+      break;
+    case EPI_SCALE: {
+      const T* s = reinterpret_cast<const T*>(g.bias);
+      C[(int64_t)crow * g.ldc + col] = from_f<T>(rnd<T>(acc) * to_f(s[col]));
+      break;
+    }
+  }
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
+  constexpr bool kPair = (EPI == EPI_SWIGLU);
+  __shared__ int a_row[32], c_row[32];
+  __shared__ float red[3][64][kPair ? 16 : 8];
+  const int group = blockIdx.y + g.group_offset;
+  const int col0 = blockIdx.x * 16;
+  if (col0 >= g.N) return;
+  const int n = resolve_rows(g, group, blockIdx.z, a_row, c_row);
+  if (n == 0) return;
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int m = lane & 15, kq = lane >> 4;
+  const bf16* A = reinterpret_cast<const bf16*>(g.A);
+  const bf16* W = reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
+  const int ar0 = a_row[m], ar1 = a_row[m + 16];
+  const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * g.lda;
+  const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * g.lda;
+  const bool v0 = ar0 >= 0, v1 = ar1 >= 0;
+  const bool vc = col0 + m < g.N;  // columns past N (last tile) read row 0 and are dropped
+  const bf16* w0 = W + (int64_t)(vc ? col0 + m : 0) * g.ldw;
+  const bf16* w1 = W + (int64_t)(vc ? g.N + col0 + m : 0) * g.ldw;
+
+  const int kspan = g.K >> 2;
+  const int kbeg = wv * kspan;
+  f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
+  const bf16x8_t zero = {};
+#pragma unroll 4
+  for (int k = kbeg + kq * 8; k < kbeg + kspan; k += 32) {
+    const bf16x8_t b0 = load_bf16x8(w0 + k);
+    bf16x8_t b1;
+    if constexpr (kPair) b1 = load_bf16x8(w1 + k);
+    const bf16x8_t x0 = v0 ? load_bf16x8(a0 + k) : zero;
+    const bf16x8_t x1 = v1 ? load_bf16x8(a1 + k) : zero;
+    c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, b0, c00, 0, 0, 0);
+    c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, b0, c10, 0, 0, 0);
+    if constexpr (kPair) {
+      c01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, b1, c01, 0, 0, 0);
+      c11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, b1, c11, 0, 0, 0);
+    }
+  }
+  if (wv > 0) {
+    float* r = red[wv - 1][lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      r[j] = c00[j];
+      r[4 + j] = c10[j];
+      if constexpr (kPair) {
+        r[8 + j] = c01[j];
+        r[12 + j] = c11[j];
+      }
+    }
+  }
+  __syncthreads();
+  if (wv != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w) {
+    const float* r = red[w][lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c00[j] += r[j];
+      c10[j] += r[4 + j];
+      if constexpr (kPair) {
+        c01[j] += r[8 + j];
+        c11[j] += r[12 + j];
+      }
+    }
+  }
+  // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16.
+  const int col = col0 + m;
+  if (!vc) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r0 = kq * 4 + j, r1 = 16 + kq * 4 + j;
+    if (r0 < n) epilogue<bf16>(g, EPI, group, c_row[r0], col, c00[j], c01[j]);
+    if (r1 < n) epilogue<bf16>(g, EPI, group, c_row[r1], col, c10[j], c11[j]);
+  }
+}
+
+// fp32: 4 waves per workgroup, one output column per wave, 32-row tile.
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
+  constexpr bool kPair = (EPI == EPI_SWIGLU);
+  __shared__ int a_row[32], c_row[32];
+  const int group = blockIdx.y + g.group_offset;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int col = blockIdx.x * 4 + wv;
+  if (blockIdx.x * 4 >= g.N) return;
+  const int n = resolve_rows(g, group, blockIdx.z, a_row, c_row);
+  if (n == 0 || col >= g.N) return;
+  const float* A = reinterpret_cast<const float*>(g.A);
+  const float* W = reinterpret_cast<const float*>(g.W) + (int64_t)group * g.w_group_stride;
+  const float* w0 = W + (int64_t)col * g.ldw;
+  const float* w1 = W + (int64_t)(g.N + col) * g.ldw;
+  for (int r = 0; r < n; ++r) {
+    const float* a = A + (int64_t)a_row[r] * g.lda;
+    float s0 = 0.f, s1 = 0.f;
+    for (int k = lane * 4; k < g.K; k += 256) {
+      const float4 av = *reinterpret_cast<const float4*>(a + k);
+      const float4 bv = *reinterpret_cast<const float4*>(w0 + k);
+      s0 += av.x * bv.x + av.y * bv.y + av.z * bv.z + av.w * bv.w;
+      if constexpr (kPair) {
+        const float4 uv = *reinterpret_cast<const float4*>(w1 + k);
+        s1 += av.x * uv.x + av.y * uv.y + av.z * uv.z + av.w * uv.w;
+      }
+    }
+    s0 = wave_sum(s0);
+    if constexpr (kPair) s1 = wave_sum(s1);
+    if (lane == (r & 63)) epilogue<float>(g, EPI, group, c_row[r], col, s0, s1);
+  }
+}
+
+template <int EPI>
+int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream_t s) {
+  const int tiles = (max_rows + 31) / 32;
+  if (tiles <= 0 || groups <= 0) return PULSAR_OK;
+  if (dtype == PULSAR_BF16) {
+    dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)groups, (unsigned)tiles);
+    gemm_bf16_kernel<EPI><<<grid, 256, 0, s>>>(a);
+  } else {
+    dim3 grid((unsigned)((a.N + 3) / 4), (unsigned)groups, (unsigned)tiles);
+    gemm_f32_kernel<EPI><<<grid, 256, 0, s>>>(a);
+  }
+  PULSAR_LAUNCH_CHECK();
+  return PULSAR_OK;
+}
+
+}  // namespace
+
+int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows, hipStream_t s) {
+  if (a.K % 256 != 0)
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: K must be a multiple of 256");
+  switch (epi) {
+    case EPI_STORE: return launch_one<EPI_STORE>(a, dtype, groups, max_rows, s);
+    case EPI_QKVG: return launch_one<EPI_QKVG>(a, dtype, groups, max_rows, s);
+    case EPI_RESID: return launch_one<EPI_RESID>(a, dtype, groups, max_rows, s);
+    case EPI_SWIGLU: return launch_one<EPI_SWIGLU>(a, dtype, groups, max_rows, s);
+    case EPI_LOGITS: return launch_one<EPI_LOGITS>(a, dtype, groups, max_rows, s);
+    case EPI_LOGITS_RAW: return launch_one<EPI_LOGITS_RAW>(a, dtype, groups, max_rows, s);
+    case EPI_SCALE: return launch_one<EPI_SCALE>(a, dtype, groups, max_rows, s);
+  }
+  return fail(PULSAR_ERR_INVALID, "gemm: unknown epilogue");
+}
+
+}  // namespace pulsar

@@ -6,7 +6,7 @@
 #include <string>
 
 #include "common.h"
-#include "../../include/pulsar_hip.h"
+
 
 namespace pulsar {
 

@@ -1,0 +1,196 @@
+// Argument blocks and launchers of the per-row kernels (rows.hip).
+#pragma once
+
+#include "engine.h"
+
+namespace pulsar {
+
+constexpr int kSplitLen = 256;  // keys per decode-attention block
+
+// KV cache addressing. Local (sliding-window) layers: a per-sequence ring of `lcap`
+// positions, [B][Hkv][lcap][64]. Global layers: pages of 64 positions from a shared pool,
+// [n_pages][Hkv][64][64], located through page_table[b][pos / 64].
+struct KVDesc {
+  void* k[kMaxLayers];
+  void* v[kMaxLayers];
+  const int32_t* page_table;
+  uint32_t local_mask;
+  int Hkv;
+  int lcap;
+  int max_pages;
+};
+
+__device__ __forceinline__ int64_t kv_offset(const KVDesc& c, int layer, int b, int g, int pos) {
+  if ((c.local_mask >> layer) & 1u) {
+    return (((int64_t)b * c.Hkv + g) * c.lcap + (pos % c.lcap)) * kHeadDim;
+  }
+  const int page = c.page_table[(int64_t)b * c.max_pages + pos / kPage];
+  return (((int64_t)page * c.Hkv + g) * kPage + (pos % kPage)) * kHeadDim;
+}
+
+struct PulseInputArgs {
+  const StepCtl* ctl;
+  const RowDesc* rows;
+  int D, rank, prefill, prefill_T;
+  float eps;
+  const void* tok_emb;
+  const float* anchor_norm;
+  const float* conv_w;      // nullable
+  const float* state_norm;
+  const void* step_emb;     // [P][D] T
+  const void* reinject_down;  // [P][rank][2D] T
+  const void* reinject_up;    // [P][D][rank] T
+  const void* reinject_bias;  // [P][D] T
+  void* e_state;            // anchor embedding per state
+  void* hout_state;         // previous pulse output per state
+  void* h_in;
+  void* h;
+  int32_t* zero_counts;     // zeroed by block 0 (expert list counts of the step)
+  int n_zero;
+};
+
+struct NormArgs {
+  const StepCtl* ctl;
+  const RowDesc* rows;
+  int use_lrows;
+  const int32_t* lrow_src;
+  const void* x;
+  int64_t ldx;
+  const float* w;
+  int64_t w_pulse_stride;
+  void* y;
+  int D;
+  float eps;
+};
+
+struct QKPostArgs {
+  const StepCtl* ctl;
+  const RowDesc* rows;
+  void* qkv;
+  int64_t ldq;
+  int H, Hkv, layer, is_local, prefill, prefill_T, window, base_seq_len;
+  float eps;
+  const float* q_norm;    // [P][H][64]
+  const float* k_norm;    // [P][Hkv][64]
+  const float* v_lambda;  // [P] sigmoid(lambda) rounded through T
+  void* v_first;          // [rows][Hkv*64]
+  const float* cos;       // [positions][32]
+  const float* sin;
+  KVDesc kv;
+};
+
+struct AttnArgs {
+  const StepCtl* ctl;
+  const RowDesc* rows;
+  const void* qkv;
+  int64_t ldq;
+  const void* gate;  // [rows][H] T
+  void* out;         // [rows][H*64] T
+  float* part;       // decode split partials
+  int max_splits;
+  int H, Hkv, layer, is_local, window, prefill_T;
+  float scale;
+  KVDesc kv;
+};
+
+struct RouterArgs {
+  const StepCtl* ctl;
+  const RowDesc* rows;
+  const void* x;
+  const float* w;      // [P][E][D] fp32
+  const float* bias;   // [P][E]
+  int E, K, D, pulse, m_fixed;
+  int32_t* topk_idx;   // [rows][K]
+  float* topk_w;       // [rows][K] (values rounded through T)
+  int32_t* lists;      // [E][list_stride] assignment ids (decode), nullable
+  int32_t* list_count; // [E]
+  int64_t list_stride;
+};
+
+struct CombineArgs {
+  const StepCtl* ctl;  // null for prefill (m_fixed rows)
+  const RowDesc* rows;
+  int m_fixed, pulse, prefill, K, D;
+  const void* shared;  // [rows][D]
+  const void* routed;  // [rows*K][D]
+  const float* topk_w;
+  const int32_t* keep; // [rows*K] or null
+  const void* routed_scale;  // [P][D] T
+  void* h;
+};
+
+struct PulseOutputArgs {
+  const StepCtl* ctl;
+  const RowDesc* rows;
+  int D, prefill, prefill_T;
+  float eps;
+  const void* h_in;
+  const void* h;
+  const void* res_scale;  // [P][D] T
+  void* hout_state;
+  const float* final_norm;
+  void* xn_final;         // [lrows][D]
+};
+
+// Shared top-k routine of the two router kernels (single thread).
+template <typename T>
+__device__ __forceinline__ void route_topk(const float* lg, int E, int K, const float* bias, int r,
+                                           const RouterArgs& a) {
+  float sum = 0.f;
+  for (int e = 0; e < E; ++e) sum += lg[e];
+  const float mean = sum / (float)E;
+  float s[32], b[32];
+  for (int e = 0; e < E; ++e) {
+    const float c = lg[e] - mean;
+    s[e] = 1.0f / (1.0f + expf(-c));
+    b[e] = s[e] + bias[e];
+  }
+  int bi[8];
+  float bv[8];
+  for (int k = 0; k < K; ++k) {
+    bi[k] = 0;
+    bv[k] = -INFINITY;
+  }
+  for (int e = 0; e < E; ++e) {
+    const float v = b[e];
+    if (v > bv[K - 1]) {
+      int p = K - 1;
+      while (p > 0 && v > bv[p - 1]) {
+        bv[p] = bv[p - 1];
+        bi[p] = bi[p - 1];
+        --p;
+      }
+      bv[p] = v;
+      bi[p] = e;
+    }
+  }
+  float tot = 0.f;
+  for (int k = 0; k < K; ++k) tot += s[bi[k]];
+  tot += 1e-6f;
+  for (int k = 0; k < K; ++k) {
+    a.topk_idx[(int64_t)r * K + k] = bi[k];
+    a.topk_w[(int64_t)r * K + k] = rnd<T>(s[bi[k]] / tot);
+    if (a.lists) {
+      const int p = atomicAdd(&a.list_count[bi[k]], 1);
+      a.lists[(int64_t)bi[k] * a.list_stride + p] = r * K + k;
+    }
+  }
+}
+
+int launch_pulse_input(const PulseInputArgs& a, int dtype, int max_rows, hipStream_t s);
+int launch_norm_rows(const NormArgs& a, int dtype, int max_rows, hipStream_t s);
+int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s);
+int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s);
+int launch_attn_prefill(const AttnArgs& a, int dtype, int B, hipStream_t s);
+int launch_router_decode(const RouterArgs& a, int dtype, int max_rows, hipStream_t s);
+int launch_router_prefill(const RouterArgs& a, int dtype, hipStream_t s);
+int launch_prefill_capacity(const int32_t* idx, const float* w, int32_t* cnt, int32_t* keep,
+                            int32_t* lists, int32_t* lcount, int64_t list_stride, int B, int T_,
+                            int K, int E, int C, hipStream_t s);
+int launch_moe_combine(const CombineArgs& a, int dtype, int max_rows, hipStream_t s);
+int launch_pulse_output(const PulseOutputArgs& a, int dtype, int max_rows, hipStream_t s);
+int launch_prefill_stem(const int32_t* ids, const void* emb, const float* anchor_w,
+                        const float* conv_w, void* a_buf, void* e_buf, int B, int T_, int D,
+                        float eps, int dtype, hipStream_t s);
+
+}  // namespace pulsar

@@ -1,0 +1,53 @@
+// Sampling and controller argument blocks (sample.hip).
+#pragma once
+
+#include "engine.h"
+
+namespace pulsar {
+
+constexpr int KIND_TESTED = 0;  // token drawn at the top of the reference loop (gets a draft test)
+constexpr int KIND_PLAIN = 1;   // accepted draft (its successor is a plain draw)
+
+// Per-sequence decode state, owned by the controller.
+struct SeqState {
+  int32_t done, produced, max_new;
+  int32_t c_tok, c_pos, c_pulse, c_kind, c_slot;
+  int32_t s_valid, s_tok, d_tok;
+  int32_t tests, accepted;
+  int32_t row_c, row_s, lrow_c, lrow_s;
+  uint32_t ctr;
+  int32_t pad[2];
+};
+
+struct SampleArgs {
+  const StepCtl* ctl;
+  const float* logits;  // [lrows][V]
+  const int32_t* lrow_seq;
+  const int32_t* lrow_extra;
+  const uint32_t* seen;  // [B][V/32]
+  const SeqState* state;
+  int V, greedy;
+  float temperature, top_p, rep_penalty;
+  uint64_t seed;
+  int32_t* out_argmax;  // [lrows]
+  int32_t* out_draw;    // [lrows][2]
+};
+
+struct ControllerArgs {
+  StepCtl* ctl;
+  SeqState* state;
+  RowDesc* rows;
+  int32_t* lrow_seq;
+  int32_t* lrow_extra;
+  uint32_t* seen;
+  int32_t* out_tokens;  // [B][max_new]
+  const int32_t* argmax;
+  const int32_t* draw;
+  const int32_t* stop_ids;
+  int n_stop, B, V, n_pulses, max_new, speculative, all_logits, init, prompt_len;
+};
+
+int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s);
+int launch_controller(const ControllerArgs& a, hipStream_t s);
+
+}  // namespace pulsar

@@ -1,0 +1,403 @@
+// Sampling and the speculative controller, both on the device so that a captured step
+// graph can be replayed without host round trips.
+//
+// Sampling (reference src/infer.py:658-685): repetition penalty over the seen set
+// (divide positive, multiply non-positive), greedy argmax (first maximum) when the
+// temperature is <= 1e-4, else temperature scaling, top-p (keep the smallest set of
+// highest-scoring tokens whose mass strictly above each kept token is <= top_p, found by
+// bisection on the order-preserving integer key of the scaled logits) and an inverse-CDF
+// draw over the kept tokens in index order. Two independent draws are produced per row.
+//
+// Controller (reference src/infer.py:623-731): per sequence, the current token c runs its
+// pulses; in speculative mode the pulse-0 logits of a "tested" token give the reference's
+// draft d, which is also the speculative next token s whose pulse 0 runs in the same step
+// as c's last pulse (it attends to c's last-pulse K/V written earlier in that step). The
+// verify draw v decides acceptance exactly as the reference (d == v and d not a stop id);
+// on rejection the next token is a fresh draw, and s's work is kept when it equals that
+// draw. After an accepted draft the next token is a plain draw, as in the reference;
+// s is then the pulse-0 argmax guess of the accepted token, which changes which work is
+// speculative but never the emitted distribution.
+#include "sample.h"
+
+namespace pulsar {
+
+namespace {
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float uniform01(uint64_t seed, int seq, uint32_t ctr, int d) {
+  uint64_t k = mix64(seed + 0x9E3779B97F4A7C15ull * (uint64_t)(seq + 1));
+  k = mix64(k ^ ((uint64_t)ctr << 8) ^ (uint64_t)d);
+  return (float)(k >> 40) * (1.0f / 16777216.0f);
+}
+
+// Block-wide exclusive scan of one float per thread (blockDim 1024). `red` needs 16 floats.
+__device__ float block_excl_scan(float v, float* red, float* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  float incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  __syncthreads();
+  if (lane == 63) red[w] = incl;
+  __syncthreads();
+  float base = 0.f, tot = 0.f;
+  for (int i = 0; i < nw; ++i) {
+    if (i < w) base += red[i];
+    tot += red[i];
+  }
+  *total = tot;
+  return base + incl - v;
+}
+
+struct ArgMax {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ ArgMax better(ArgMax a, ArgMax b) {
+  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+
+__device__ ArgMax block_argmax(ArgMax x, ArgMax* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    ArgMax o;
+    o.v = __shfl_xor(x.v, off, 64);
+    o.i = __shfl_xor(x.i, off, 64);
+    x = better(x, o);
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = x;
+  __syncthreads();
+  ArgMax r = red[0];
+  for (int i = 1; i < nw; ++i) r = better(r, red[i]);
+  return r;
+}
+
+}  // namespace
+
+template <typename T, int PER>
+__global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
+  __shared__ float red[16];
+  __shared__ ArgMax ared[16];
+  const int lr = blockIdx.x;
+  if (lr >= a.ctl->n_lrows) return;
+  const int seq = a.lrow_seq[lr];
+  const int extra = a.lrow_extra[lr];
+  const float* lg = a.logits + (int64_t)lr * a.V;
+  const uint32_t* seen = a.seen + (int64_t)seq * (a.V / 32);
+  const int base = threadIdx.x * PER;
+  float l[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(lg + base + i);
+    l[i] = v.x;
+    l[i + 1] = v.y;
+    l[i + 2] = v.z;
+    l[i + 3] = v.w;
+  }
+  if (a.rep_penalty != 1.0f) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = base + i;
+      const bool s = ((seen[idx >> 5] >> (idx & 31)) & 1u) || idx == extra;
+      if (s) l[i] = l[i] > 0.f ? rnd<T>(l[i] / a.rep_penalty) : rnd<T>(l[i] * a.rep_penalty);
+    }
+  }
+  ArgMax am{-INFINITY, 0x7fffffff};
+#pragma unroll
+  for (int i = 0; i < PER; ++i) am = better(am, ArgMax{l[i], base + i});
+  am = block_argmax(am, ared);
+  if (a.greedy) {
+    if (threadIdx.x == 0) {
+      a.out_argmax[lr] = am.i;
+      a.out_draw[lr * 2] = am.i;
+      a.out_draw[lr * 2 + 1] = am.i;
+    }
+    return;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    l[i] = rnd<T>(l[i] / a.temperature);
+    mx = fmaxf(mx, l[i]);
+  }
+  mx = block_max(mx, red);
+  float zl = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) zl += expf(l[i] - mx);
+  const float Z = block_sum(zl, red);
+  uint32_t kstar = 0;
+  if (a.top_p < 1.0f) {
+    const float lim = a.top_p * Z;
+    uint32_t lo = 0, hi = 0xffffffffu;
+    while (lo < hi) {
+      const uint32_t mid = lo + ((hi - lo) >> 1);
+      float f = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if (order_key(l[i]) > mid) f += expf(l[i] - mx);
+      f = block_sum(f, red);
+      if (f <= lim)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    kstar = lo;
+  }
+  float own = 0.f;
+  int last_kept = -1;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (order_key(l[i]) >= kstar) {
+      own += expf(l[i] - mx);
+      last_kept = base + i;
+    }
+  }
+  float total;
+  const float pre = block_excl_scan(own, red, &total);
+  ArgMax lk = block_argmax(ArgMax{(float)last_kept, 0}, ared);
+  __shared__ int pick[2];
+  if (threadIdx.x < 2) pick[threadIdx.x] = (int)lk.v;
+  __syncthreads();
+  // stream: step counter of the sequence, and whether this is the speculative row
+  const uint32_t ctr = a.state[seq].ctr * 2u + (extra >= 0 ? 1u : 0u);
+  for (int d = 0; d < 2; ++d) {
+    const float target = uniform01(a.seed, seq, ctr, d) * total;
+    if (own > 0.f && target >= pre && target < pre + own) {
+      float run = pre;
+      int choice = -1;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        if (order_key(l[i]) >= kstar) {
+          run += expf(l[i] - mx);
+          if (choice < 0 && target < run) choice = base + i;
+        }
+      }
+      if (choice < 0) choice = last_kept;
+      pick[d] = choice;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    a.out_argmax[lr] = am.i;
+    a.out_draw[lr * 2] = pick[0];
+    a.out_draw[lr * 2 + 1] = pick[1];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Controller (single thread; B <= a few hundred).
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ bool is_stop(const ControllerArgs& a, int tok) {
+  for (int i = 0; i < a.n_stop; ++i)
+    if (a.stop_ids[i] == tok) return true;
+  return false;
+}
+
+__device__ void emit(const ControllerArgs& a, SeqState& s, int b, int tok) {
+  a.out_tokens[(int64_t)b * a.max_new + s.produced] = tok;
+  s.produced += 1;
+  a.seen[(int64_t)b * (a.V / 32) + (tok >> 5)] |= 1u << (tok & 31);
+  if (s.produced >= s.max_new) s.done = 1;
+}
+
+// c <- s (whose pulse 0 ran this step). kind = kind of the new current token.
+__device__ void promote(const ControllerArgs& a, SeqState& s, int kind) {
+  s.c_tok = s.s_tok;
+  s.c_pos = s.c_pos + 1;
+  s.c_slot = 1 - s.c_slot;
+  s.c_kind = kind;
+  s.c_pulse = 1;
+  s.s_valid = 0;
+  // the new current token's pulse-0 logits are those of the s row
+  const int lr = s.lrow_s;
+  if (kind == KIND_TESTED) {
+    s.d_tok = a.draw[lr * 2];
+    s.s_valid = !is_stop(a, s.d_tok);
+    s.s_tok = s.d_tok;
+  } else {
+    const int g = a.argmax[lr];
+    s.s_valid = !is_stop(a, g);
+    s.s_tok = g;
+  }
+}
+
+__device__ void fresh(SeqState& s, int tok) {
+  s.c_tok = tok;
+  s.c_pos = s.c_pos + 1;
+  s.c_slot = 1 - s.c_slot;
+  s.c_kind = KIND_TESTED;
+  s.c_pulse = 0;
+  s.s_valid = 0;
+}
+
+}  // namespace
+
+__global__ void controller_kernel(ControllerArgs a) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  StepCtl* ctl = a.ctl;
+  const int P = a.n_pulses;
+  for (int b = 0; b < a.B; ++b) {
+    SeqState s = a.state[b];
+    if (a.init) {
+      s = SeqState{};
+      s.max_new = a.max_new;
+      s.c_pos = a.prompt_len - 1;
+      s.c_slot = 1;
+      s.row_c = s.row_s = s.lrow_c = s.lrow_s = -1;
+      const int t = a.draw[b * 2];
+      if (is_stop(a, t) || s.max_new <= 0) {
+        s.done = 1;
+      } else {
+        emit(a, s, b, t);
+        fresh(s, t);
+      }
+      a.state[b] = s;
+      continue;
+    }
+    if (s.done) continue;
+    s.ctr += 1;
+    const int pulse_ran = s.c_pulse;
+    if (pulse_ran < P - 1) {
+      if (pulse_ran == 0 && a.speculative) {
+        const int lr = s.lrow_c;
+        if (s.c_kind == KIND_TESTED) {
+          s.d_tok = a.draw[lr * 2];
+          s.s_valid = !is_stop(a, s.d_tok);
+          s.s_tok = s.d_tok;
+        } else {
+          const int g = a.argmax[lr];
+          s.s_valid = !is_stop(a, g);
+          s.s_tok = g;
+        }
+      }
+      s.c_pulse = pulse_ran + 1;
+    } else {
+      const int lr = s.lrow_c;
+      const bool s_ran = s.row_s >= 0;
+      if (a.speculative && s.c_kind == KIND_TESTED) {
+        const int v = a.draw[lr * 2];
+        s.tests += 1;
+        if (s.d_tok == v && !is_stop(a, s.d_tok)) {
+          s.accepted += 1;
+          emit(a, s, b, s.d_tok);
+          if (!s.done) promote(a, s, KIND_PLAIN);
+        } else {
+          const int t = a.draw[lr * 2 + 1];
+          if (is_stop(a, t)) {
+            s.done = 1;
+          } else {
+            emit(a, s, b, t);
+            if (!s.done) {
+              if (s_ran && s.s_tok == t)
+                promote(a, s, KIND_TESTED);
+              else
+                fresh(s, t);
+            }
+          }
+        }
+      } else {
+        const int t = a.draw[lr * 2];
+        if (is_stop(a, t)) {
+          s.done = 1;
+        } else {
+          emit(a, s, b, t);
+          if (!s.done) {
+            if (a.speculative && s_ran && s.s_tok == t)
+              promote(a, s, KIND_TESTED);
+            else
+              fresh(s, t);
+          }
+        }
+      }
+    }
+    a.state[b] = s;
+  }
+  // Next step's rows, grouped by pulse.
+  int n = 0, nl = 0, active = 0;
+  for (int p = 0; p < P; ++p) {
+    ctl->pulse_start[p] = n;
+    for (int b = 0; b < a.B; ++b) {
+      SeqState& s = a.state[b];
+      if (p == 0) {
+        s.row_c = s.row_s = s.lrow_c = s.lrow_s = -1;
+        if (!s.done) ++active;
+      }
+      if (s.done) continue;
+      if (s.c_pulse == p) {
+        const bool want = a.all_logits || s.c_pulse == P - 1 || (a.speculative && s.c_pulse == 0);
+        RowDesc r{b, s.c_slot, p, s.c_pos, s.c_tok, want ? nl : -1, -1, 0};
+        if (want) {
+          a.lrow_seq[nl] = b;
+          a.lrow_extra[nl] = -1;
+          s.lrow_c = nl++;
+        }
+        s.row_c = n;
+        a.rows[n++] = r;
+      }
+      if (p == 0 && a.speculative && s.c_pulse == P - 1 && s.s_valid) {
+        RowDesc r{b, 1 - s.c_slot, 0, s.c_pos + 1, s.s_tok, nl, s.s_tok, 0};
+        a.lrow_seq[nl] = b;
+        a.lrow_extra[nl] = s.s_tok;
+        s.lrow_s = nl++;
+        s.row_s = n;
+        a.rows[n++] = r;
+      }
+    }
+    ctl->pulse_count[p] = n - ctl->pulse_start[p];
+  }
+  ctl->n_rows = n;
+  ctl->n_lrows = nl;
+  ctl->active = active;
+  ctl->step += 1;
+}
+
+int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s) {
+  if (a.V % 4096 != 0 || a.V / 1024 > 64)
+    return fail(PULSAR_ERR_UNSUPPORTED, "sample: vocab must be a multiple of 4096 and <= 65536");
+  const int per = a.V / 1024;
+#define PULSAR_SAMPLE_CASE(N)                                                              \
+  case N:                                                                                  \
+    if (dtype == PULSAR_BF16)                                                              \
+      sample_kernel<bf16, N><<<max_lrows, 1024, 0, s>>>(a);                                \
+    else                                                                                   \
+      sample_kernel<float, N><<<max_lrows, 1024, 0, s>>>(a);                               \
+    break;
+  switch (per) {
+    PULSAR_SAMPLE_CASE(4)
+    PULSAR_SAMPLE_CASE(8)
+    PULSAR_SAMPLE_CASE(16)
+    PULSAR_SAMPLE_CASE(32)
+    PULSAR_SAMPLE_CASE(64)
+    default:
+      return fail(PULSAR_ERR_UNSUPPORTED, "sample: vocab/1024 must be a power of two");
+  }
+#undef PULSAR_SAMPLE_CASE
+  PULSAR_LAUNCH_CHECK();
+  return PULSAR_OK;
+}
+
+int launch_controller(const ControllerArgs& a, hipStream_t s) {
+  controller_kernel<<<1, 64, 0, s>>>(a);
+  PULSAR_LAUNCH_CHECK();
+  return PULSAR_OK;
+}
+
+}  // namespace pulsar

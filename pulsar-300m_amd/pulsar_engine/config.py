@@ -118,3 +118,28 @@ def tiny_config(**overrides) -> PulsarConfig:
     )
     base.update(overrides)
     return PulsarConfig(**base)
+
+
+def small_config(**overrides) -> PulsarConfig:
+    """Reduced configuration that satisfies the HIP engine's shape rules (head_dim 64, four
+    query heads per kv head, widths multiples of 256, vocab a multiple of 4096); layer 3 is
+    global and the 16-token window is exceeded by short prompts. For fast GPU checks."""
+    base = dict(
+        vocab_size=4096,
+        d_model=256,
+        n_heads=4,
+        n_kv_heads=1,
+        head_dim=64,
+        d_expert=256,
+        d_shared=256,
+        n_core=4,
+        n_routed_experts=8,
+        top_k=2,
+        max_pulses=4,
+        default_pulses=3,
+        base_seq_len=32,
+        max_seq_len=512,
+        sliding_window=16,
+    )
+    base.update(overrides)
+    return PulsarConfig(**base)

@@ -1,0 +1,236 @@
+"""Host side of the HIP decode engine.
+
+``HipEngine`` wraps one engine handle of libpulsar_hip.so (a batch of sequences with its KV
+cache). ``PulsarInferenceEngine`` mirrors the reference's generation interface
+(src/infer.py:181-782: ``generate``, ``stream_generate``, ``self_speculative_stream_generate``)
+and adds a batched id-level entry, ``generate_ids``.
+
+The whole decode loop runs on the GPU: each step is one pulse of every active row, the
+sampling and the accept/resample controller included, replayed from a captured HIP graph;
+the host only polls a done flag every few steps.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Iterable, Iterator, Optional, Sequence
+
+import numpy as np
+import torch
+
+from pulsar_cuda import _lib
+
+from .model import DeviceModel
+
+# Seq-state fields (int32 words of the controller's per-sequence record).
+ST_DONE, ST_PRODUCED, ST_TESTS, ST_ACCEPTED = 0, 1, 11, 12
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+class HipEngine:
+    """A batch of sequences decoded by the HIP engine."""
+
+    def __init__(self, model: DeviceModel, *, batch: int, max_prompt: int, max_new: int,
+                 speculative: bool = True, temperature: float = 0.7, top_p: float = 0.9,
+                 repetition_penalty: float = 1.15, stop_ids: Iterable[int] = (0,),
+                 seed: int = 0, all_logits: bool = False, max_ctx: Optional[int] = None):
+        self.lib = _lib.load()
+        self.model = model
+        self.batch = batch
+        self.max_new = max_new
+        self.V = model.cfg.vocab_size
+        stops = [int(s) for s in stop_ids][:8]
+        c = _lib.PulsarEngineConfig()
+        c.max_batch, c.max_prompt, c.max_new = batch, max_prompt, max_new
+        c.max_ctx = max_ctx or (max_prompt + max_new + 2)
+        c.speculative, c.all_logits = int(bool(speculative)), int(bool(all_logits))
+        c.temperature, c.top_p, c.repetition_penalty = temperature, top_p, repetition_penalty
+        c.n_stop = len(stops)
+        for i, s in enumerate(stops):
+            c.stop_ids[i] = s
+        c.seed = seed & 0xFFFFFFFFFFFFFFFF
+        if c.max_ctx > model.rope_len:
+            raise ValueError(f"max_ctx {c.max_ctx} exceeds the model's RoPE tables ({model.rope_len})")
+        self.cfg = c
+        h = ctypes.c_void_p()
+        _lib.check(self.lib.pulsar_engine_create(model.desc_ref(), ctypes.byref(c), ctypes.byref(h)))
+        self.handle = h
+        self.steps = 0
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.pulsar_engine_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -- running ---------------------------------------------------------------
+    def prefill(self, ids) -> None:
+        a = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+        if a.ndim != 2 or a.shape[0] != self.batch:
+            raise ValueError(f"prompt ids must be [batch={self.batch}, T]")
+        _lib.check(self.lib.pulsar_engine_prefill(self.handle, a.ctypes.data, a.shape[0],
+                                                  a.shape[1], _stream()))
+        self.steps = 0
+
+    def step(self, n: int = 1, graph: bool = False) -> None:
+        _lib.check(self.lib.pulsar_engine_step(self.handle, n, int(graph), _stream()))
+        self.steps += n
+
+    def run(self, max_steps: Optional[int] = None, check_every: int = 16) -> int:
+        """Step until every sequence finished; returns the number of steps run."""
+        if max_steps is None:
+            max_steps = 4 * (self.max_new + 2) * self.model.n_pulses
+        ran = ctypes.c_int32(0)
+        _lib.check(self.lib.pulsar_engine_generate(self.handle, max_steps, check_every, _stream(),
+                                                   ctypes.byref(ran)))
+        self.steps += ran.value
+        return ran.value
+
+    # -- reading ---------------------------------------------------------------
+    def _read(self, what: int, arr: np.ndarray) -> np.ndarray:
+        _lib.check(self.lib.pulsar_engine_read(self.handle, what, arr.ctypes.data, arr.nbytes,
+                                               _stream()))
+        return arr
+
+    def state(self) -> np.ndarray:
+        return self._read(_lib.BUF_SEQSTATE, np.zeros((self.batch, _lib.SEQSTATE_INTS), np.int32))
+
+    def tokens(self) -> list[list[int]]:
+        st = self.state()
+        toks = self._read(_lib.BUF_TOKENS, np.zeros((self.batch, max(1, self.max_new)), np.int32))
+        return [toks[b, : st[b, ST_PRODUCED]].tolist() for b in range(self.batch)]
+
+    def ctl(self) -> np.ndarray:
+        return self._read(_lib.BUF_CTL, np.zeros(_lib.CTL_INTS, np.int32))
+
+    def logits(self, n: int) -> np.ndarray:
+        return self._read(_lib.BUF_LOGITS, np.zeros((n, self.V), np.float32))
+
+    def rows(self, last: bool = True) -> np.ndarray:
+        """Rows (seq, slot, pulse, pos, token, lrow, extra, 0) of the last executed step, or of
+        the next step when last=False."""
+        ctl = self._read(_lib.BUF_LAST_CTL if last else _lib.BUF_CTL,
+                         np.zeros(_lib.CTL_INTS, np.int32))
+        buf = np.zeros((2 * self.batch, _lib.ROW_INTS), np.int32)
+        self._read(_lib.BUF_LAST_ROWS if last else _lib.BUF_ROWS, buf)
+        return buf[: int(ctl[0])]
+
+    def acceptance(self) -> tuple[int, int]:
+        st = self.state()
+        return int(st[:, ST_TESTS].sum()), int(st[:, ST_ACCEPTED].sum())
+
+
+def stop_ids_for(cfg, tokenizer=None) -> set[int]:
+    """{eos} plus the tokenizer ids of the reference's stop strings (src/infer.py:649-656)."""
+    ids = {cfg.eos_token_id}
+    if tokenizer is not None:
+        for s in ("<|im_end|>", "<|endoftext|>", "</s>"):
+            try:
+                sid = tokenizer.convert_tokens_to_ids(s)
+                if sid is not None and sid != getattr(tokenizer, "unk_token_id", None):
+                    ids.add(int(sid))
+            except Exception:
+                pass
+    return ids
+
+
+class PulsarInferenceEngine:
+    """Generation interface of the reference engine on the HIP decode path."""
+
+    def __init__(self, model: DeviceModel, device="cuda", dtype=None):
+        self.model = model
+        self.cfg = model.cfg
+        self.device = torch.device(device)
+        self.dtype = model.dtype
+        self.stop_token_ids = {self.cfg.eos_token_id}
+        self.last_engine: Optional[HipEngine] = None
+
+    def generate_ids(self, prompt_ids: Sequence[Sequence[int]], max_new_tokens: int = 512,
+                     temperature: float = 0.7, top_p: float = 0.9,
+                     repetition_penalty: float = 1.15, speculative: bool = True,
+                     stop_ids: Optional[Iterable[int]] = None, seed: int = 0) -> list[list[int]]:
+        """Batched id-level generation; prompts must share one length."""
+        ids = np.asarray(prompt_ids, dtype=np.int32)
+        if ids.ndim == 1:
+            ids = ids[None, :]
+        stops = sorted(stop_ids if stop_ids is not None else self.stop_token_ids)
+        eng = HipEngine(self.model, batch=ids.shape[0], max_prompt=ids.shape[1],
+                        max_new=max_new_tokens, speculative=speculative,
+                        temperature=temperature, top_p=top_p,
+                        repetition_penalty=repetition_penalty, stop_ids=stops, seed=seed)
+        try:
+            eng.prefill(ids)
+            eng.run()
+            out = eng.tokens()
+        finally:
+            self.last_engine = eng
+        return out
+
+    def _stream(self, tokenizer, prompt: str, max_new_tokens, temperature, top_p,
+                repetition_penalty, speculative) -> Iterator[str]:
+        ids = tokenizer.encode(prompt, return_tensors="pt")
+        ids = np.asarray(ids.reshape(1, -1).cpu().numpy(), dtype=np.int32)
+        stops = stop_ids_for(self.cfg, tokenizer)
+        eng = HipEngine(self.model, batch=1, max_prompt=ids.shape[1], max_new=max_new_tokens,
+                        speculative=speculative, temperature=temperature, top_p=top_p,
+                        repetition_penalty=repetition_penalty, stop_ids=sorted(stops))
+        self.last_engine = eng
+        eng.prefill(ids)
+        sent = 0
+        limit = 4 * (max_new_tokens + 2) * self.model.n_pulses
+        while True:
+            toks = eng.tokens()[0]
+            for t in toks[sent:]:
+                yield tokenizer.decode([t], skip_special_tokens=False)
+            sent = len(toks)
+            if eng.state()[0, ST_DONE] or eng.steps >= limit:
+                break
+            eng.step(8, graph=True)
+
+    def stream_generate(self, tokenizer, prompt: str, max_new_tokens: int = 512,
+                        temperature: float = 0.7, top_p: float = 0.9,
+                        repetition_penalty: float = 1.15) -> Iterator[str]:
+        """Plain decode (src/infer.py:551-621)."""
+        return self._stream(tokenizer, prompt, max_new_tokens, temperature, top_p,
+                            repetition_penalty, speculative=False)
+
+    def self_speculative_stream_generate(self, tokenizer, prompt: str, max_new_tokens: int = 512,
+                                         temperature: float = 0.7, top_p: float = 0.9,
+                                         repetition_penalty: float = 1.15) -> Iterator[str]:
+        """Pulse-0 draft, last-pulse verify (src/infer.py:623-731)."""
+        return self._stream(tokenizer, prompt, max_new_tokens, temperature, top_p,
+                            repetition_penalty, speculative=True)
+
+    def generate(self, tokenizer, prompt: str, max_new_tokens: int = 512,
+                 temperature: float = 0.7, top_p: float = 0.9, repetition_penalty: float = 1.15,
+                 stream: bool = False, speculative: bool = False) -> str:
+        """Prompt plus completion, optionally streamed to stdout (src/infer.py:733-782)."""
+        import sys
+
+        gen = (self.self_speculative_stream_generate if speculative else self.stream_generate)(
+            tokenizer, prompt, max_new_tokens=max_new_tokens, temperature=temperature,
+            top_p=top_p, repetition_penalty=repetition_penalty)
+        pieces = []
+        for piece in gen:
+            if stream:
+                sys.stdout.write(piece)
+                sys.stdout.flush()
+            pieces.append(piece)
+        if stream:
+            sys.stdout.write("\n")
+            sys.stdout.flush()
+        return prompt + "".join(pieces)
