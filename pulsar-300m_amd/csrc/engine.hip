@@ -46,10 +46,12 @@ struct Engine {
 
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
+  hipStream_t capture_stream = nullptr;  // graphs are captured here (never the legacy stream)
 
   ~Engine() {
     if (exec) hipGraphExecDestroy(exec);
     if (graph) hipGraphDestroy(graph);
+    if (capture_stream) hipStreamDestroy(capture_stream);
     for (void* p : allocs) hipFree(p);
   }
 
@@ -206,6 +208,7 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_CHECK_HIP(hipMemset(x.last_ctl, 0, sizeof(StepCtl)));
   PULSAR_CHECK_HIP(hipMemset(x.state, 0, sizeof(SeqState) * x.B));
   PULSAR_CHECK_HIP(hipMemset(x.list_count, 0, 4 * (size_t)x.L * x.E));
+  PULSAR_CHECK_HIP(hipStreamCreateWithFlags(&x.capture_stream, hipStreamNonBlocking));
   kv_desc(x);
   *out = guard.release();
   return PULSAR_OK;
@@ -801,10 +804,12 @@ int step(Engine& e, int n, int use_graph, hipStream_t s) {
     return PULSAR_OK;
   }
   if (!e.exec) {
-    PULSAR_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    const int rc = enqueue_step(e, s);
+    // Capture records work without running it; the graph is then launched on `s`.
+    hipStream_t cs = e.capture_stream;
+    PULSAR_CHECK_HIP(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_step(e, cs);
     hipGraph_t gr = nullptr;
-    const hipError_t ce = hipStreamEndCapture(s, &gr);
+    const hipError_t ce = hipStreamEndCapture(cs, &gr);
     if (rc != PULSAR_OK) {
       if (gr) hipGraphDestroy(gr);
       return rc;

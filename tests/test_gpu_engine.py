@@ -69,7 +69,8 @@ def _compare_passes(models, full_state, dtype, prompt, n_new, tol, rp=1.15):
     bad = [(k, e) for k, e in errs if e > tol]
     assert not bad, bad[:5]
     if dtype == torch.float32:
-        assert len(errs) == 1 + 3 * n_new, len(errs)
+        # the reference also runs the passes of the last emitted token; the engine stops
+        assert len(errs) == 1 + 3 * (n_new - 1), len(errs)
         assert eng.tokens()[0] == ref_ids
     else:
         # bf16 streams may part at a near-tie; passes are compared while they agree
