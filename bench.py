@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""Benchmark of the KV-cache self-speculative decode path on one MI355X.
+
+Workload (default): random-init Pulsar-283M in bf16 (weights N(0, 0.02), reference constant
+init elsewhere), batch 16, 2048-token uniform-random prompts, sampled self-speculative decode
+with temperature 0.8, top-p 0.95, repetition penalty 1.15 (the reference default), 256 new
+tokens per sequence, stop ids disabled so every sequence produces exactly 256 tokens.
+
+A step = one generation of the whole batch from the prefilled KV cache: rewind (redraw the
+first token from the saved prefill logits with a new seed) and decode until every sequence
+has its 256 tokens. Prefill runs once, untimed, and is reported separately.
+
+Prints one JSON line: value = accepted tokens/s over the K timed steps; roofline = the
+dominant kernel class measured with HIP events (eager profiled generation), against its
+algorithmic bytes; cpu_baseline = the oracle (PyTorch CPU restatement of the reference path)
+decoding one sequence of the same workload on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "pulsar-300m_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "accepted tokens/s at 1 GPU (batch 16, ctx 2k); % HBM roofline; acceptance rate"
+HBM_PEAK = 8.0e12
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def profile_generation(eng, cfg, es, seed):
+    """One eager generation with per-class HIP-event timing and algorithmic bytes."""
+    from pulsar_engine import traffic
+
+    eng.rewind(seed)
+    eng.profile(True)
+    totals = {c: 0.0 for c in traffic.CLASSES}
+    steps = 0
+    while not eng.state()[:, 0].all() and steps < 4 * (eng.max_new + 2) * 3:
+        eng.step(1)
+        steps += 1
+        rows = [(int(r[0]), int(r[2]), int(r[3])) for r in eng.rows(last=True)]
+        n_lrows = int(eng.last_ctl()[1])
+        b = traffic.step_bytes(cfg, es, rows, eng.expert_counts(), n_lrows)
+        for k, v in b.items():
+            totals[k] += v
+    prof = eng.profile_read()
+    eng.profile(False)
+    return prof, totals, steps
+
+
+def cpu_baseline(cfg, state, prompt, n_new, temperature, top_p, rp):
+    import torch
+
+    from oracle import pulsar_ref as R
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    eng = R.load_ref(cfg, state, torch.bfloat16, stop_ids=set())
+    torch.manual_seed(0)
+    gen = eng.self_speculative_ids(prompt, n_new, temperature, top_p, rp)
+    t0 = time.perf_counter()
+    first = next(gen)  # includes the prefill
+    t1 = time.perf_counter()
+    rest = list(gen)
+    t2 = time.perf_counter()
+    n = len(rest)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {
+        "value": round(n / (t2 - t1), 3) if n else None,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle (PyTorch CPU restatement of src/infer.py) in bf16, 1 sequence of the "
+                   f"workload: {len(prompt)}-token prompt prefilled in {t1 - t0:.1f}s (untimed), "
+                   f"then {n} self-speculative tokens after the first timed in {t2 - t1:.1f}s; "
+                   f"cpu '{model}', torch {torch.__version__}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--prompt-len", type=int, default=2048)
+    ap.add_argument("--new-tokens", type=int, default=256)
+    ap.add_argument("--temperature", type=float, default=0.8)
+    ap.add_argument("--top-p", type=float, default=0.95)
+    ap.add_argument("--repetition-penalty", type=float, default=1.15)
+    ap.add_argument("--plain", action="store_true", help="plain decode instead of self-speculative")
+    ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-new-tokens", type=int, default=12)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the decode path shards by sequence; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from pulsar_engine import traffic
+    from pulsar_engine import weights as W
+    from pulsar_engine.config import PulsarConfig
+    from pulsar_engine.engine import HipEngine
+    from pulsar_engine.model import DeviceModel
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    cfg = PulsarConfig()
+    B, T, N = args.batch, args.prompt_len, args.new_tokens
+    t0 = time.perf_counter()
+    state = W.synthetic_state(cfg, seed=0)
+    log(f"weights generated in {time.perf_counter() - t0:.1f}s")
+    model = DeviceModel(cfg, state, torch.bfloat16, rope_len=max(cfg.max_seq_len, T + N + 8))
+    es = 2
+    prompts = np.stack([W.uniform_ids(0, f"bench_prompt_{b}", T, cfg.vocab_size) for b in range(B)])
+    eng = HipEngine(model, batch=B, max_prompt=T, max_new=N, speculative=not args.plain,
+                    temperature=args.temperature, top_p=args.top_p,
+                    repetition_penalty=args.repetition_penalty, stop_ids=[], seed=1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.prefill(prompts)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {B}x{T} in {prefill_s:.3f}s")
+
+    def generation(seed: int) -> tuple[int, int, int, int]:
+        eng.rewind(seed)
+        steps = eng.run(check_every=16)
+        st = eng.state()
+        return steps, int(st[:, 1].sum()), int(st[:, 11].sum()), int(st[:, 12].sum())
+
+    for w in range(args.warmup):
+        generation(1000 + w)
+        log(f"warmup {w + 1}/{args.warmup} done")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    produced = tests = accepted = graph_steps = 0
+    for k in range(args.steps):
+        s, p, t, a = generation(2000 + k)
+        produced += p
+        tests += t
+        accepted += a
+        graph_steps += s
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    value = produced / elapsed
+    log(f"timed {args.steps} generations: {produced} tokens in {elapsed:.3f}s, "
+        f"{graph_steps} pulse steps, acceptance {accepted}/{tests}")
+
+    roofline = None
+    step_frac = None
+    prof_detail = None
+    if not args.no_profile:
+        prof, bytes_by_class, psteps = profile_generation(eng, cfg, es, 3000)
+        tot_ms = sum(v[0] for v in prof.values())
+        dom = max(prof, key=lambda k: prof[k][0])
+        ms, n = prof[dom]
+        per_launch = bytes_by_class[dom] / max(n, 1)
+        avg_s = ms / max(n, 1) / 1e3
+        achieved = per_launch / avg_s
+        roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                    "kernel": dom, "bytes_per_launch": int(per_launch),
+                    "avg_launch_us": round(avg_s * 1e6, 2)}
+        all_bytes = sum(bytes_by_class.values())
+        # whole-generation algorithmic bytes against the graph-replayed generation time
+        step_frac = (all_bytes / (elapsed / args.steps)) / HBM_PEAK
+        prof_detail = {k: {"ms": round(v[0], 3), "launches": v[1],
+                           "GB_per_s": round(bytes_by_class[k] / max(v[0], 1e-9) / 1e6, 1)}
+                       for k, v in prof.items() if v[1]}
+        log(f"profiled eager generation: {psteps} steps, {tot_ms:.1f} ms kernel time, "
+            f"dominant {dom} {ms:.1f} ms")
+        log("per-class: " + json.dumps(prof_detail))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg, state, prompts[0], args.cpu_new_tokens, args.temperature,
+                           args.top_p, args.repetition_penalty)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights (N(0,0.02)), uniform random prompt ids",
+        "config": {
+            "workload": f"Pulsar-283M bf16, batch {B}, {T}-token prompts, sampled "
+                        f"{'plain' if args.plain else 'self-speculative'} decode of {N} tokens",
+            "batch": B, "prompt_len": T, "new_tokens": N, "temperature": args.temperature,
+            "top_p": args.top_p, "repetition_penalty": args.repetition_penalty,
+            "schedule": "plain" if args.plain else
+                        "exact self-speculative (pulse-0 draft pipelined with the verify pulse)",
+            "stop_ids": "disabled",
+        },
+        "acceptance_rate": round(accepted / tests, 4) if tests else None,
+        "prefill_s": round(prefill_s, 3),
+        "hbm_roofline_frac_generation": round(step_frac, 4) if step_frac is not None else None,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernel_profile": prof_detail,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -205,6 +205,13 @@ typedef struct PulsarEngineConfig {
                                   pulse_count[4], active, step */
 #define PULSAR_BUF_LAST_ROWS 5 /* int32 [n_rows][8] rows of the last executed step */
 #define PULSAR_BUF_LAST_CTL 6  /* int32 [16] control block of the last executed step */
+#define PULSAR_BUF_EXPERT_COUNTS 7 /* int32 [n_layers][E] rows routed to each expert, last step */
+
+/* Kernel classes of the per-class timing (pulsar_engine_profile_read). */
+#define PULSAR_PROF_CLASSES 16
+/* 0 pulse input, 1 rmsnorm, 2 qkv+gate GEMM, 3 qk-norm/rope/KV write, 4 attention,
+ * 5 wo GEMM, 6 router, 7 shared gate/up, 8 routed gate/up, 9 shared down, 10 routed down,
+ * 11 MoE combine, 12 pulse output, 13 lm_head, 14 sampling, 15 controller */
 
 int pulsar_engine_create(const PulsarModelDesc* model, const PulsarEngineConfig* cfg,
                          void** handle);
@@ -218,6 +225,14 @@ int pulsar_engine_step(void* handle, int32_t n_steps, int32_t use_graph, hipStre
 /* Steps until every sequence is done (or max_steps), checking every `check_every` steps. */
 int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
                            hipStream_t stream, int32_t* steps_run);
+/* Restart decoding from the prefilled cache with a new sampling seed: the first token is
+ * drawn again from the saved prefill logits. Synchronises the stream. */
+int pulsar_engine_rewind(void* handle, uint64_t seed, hipStream_t stream);
+/* Enable (1) or disable (0) per-class event timing; steps then run eagerly (no graph) with
+ * a HIP event pair around every kernel launch. Enabling resets the counters. */
+int pulsar_engine_profile(void* handle, int32_t enable);
+/* Accumulated milliseconds and launch counts per class, [PULSAR_PROF_CLASSES] each. */
+int pulsar_engine_profile_read(void* handle, double* host_ms, int64_t* host_launches);
 /* Copy an engine buffer to host memory (synchronises the stream). */
 int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes,
                        hipStream_t stream);

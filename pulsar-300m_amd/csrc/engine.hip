@@ -2,6 +2,7 @@
 // of sequences; runs prefill eagerly and decode as a step (one pulse of every active row)
 // that can be captured once into a HIP graph and replayed.
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -33,6 +34,15 @@ struct Engine {
   void *attn_out = nullptr, *v_first = nullptr, *act_s = nullptr, *act_r = nullptr;
   void *out_s = nullptr, *out_r = nullptr, *xn_final = nullptr;
   float *part = nullptr, *logits = nullptr, *topk_w = nullptr;
+  float* plogits = nullptr;   // prefill logits [B][V], kept for rewind
+  uint64_t* d_seed = nullptr;
+  // per-kernel-class event timing of eager steps
+  bool prof_on = false;
+  std::vector<hipEvent_t> ev_pool;
+  int ev_used = 0;
+  std::vector<std::array<int, 3>> spans;  // (class, start event, end event)
+  double prof_ms[PULSAR_PROF_CLASSES] = {};
+  int64_t prof_n[PULSAR_PROF_CLASSES] = {};
   int32_t *topk_idx = nullptr, *keep = nullptr;
   int32_t *lists = nullptr, *list_count = nullptr;      // decode: [L][E][max_rows*K], [L][E]
   int32_t *p_lists = nullptr, *p_lcount = nullptr, *p_cnt = nullptr;  // prefill
@@ -52,6 +62,7 @@ struct Engine {
     if (exec) hipGraphExecDestroy(exec);
     if (graph) hipGraphDestroy(graph);
     if (capture_stream) hipStreamDestroy(capture_stream);
+    for (hipEvent_t ev : ev_pool) hipEventDestroy(ev);
     for (void* p : allocs) hipFree(p);
   }
 
@@ -121,6 +132,49 @@ void kv_desc(Engine& e) {
   e.kv.max_pages = e.max_pages;
 }
 
+int prof_mark(Engine& e, hipStream_t s) {
+  if (!e.prof_on) return -1;
+  if (e.ev_used == (int)e.ev_pool.size()) {
+    hipEvent_t ev;
+    if (hipEventCreate(&ev) != hipSuccess) return -1;
+    e.ev_pool.push_back(ev);
+  }
+  const int i = e.ev_used++;
+  if (hipEventRecord(e.ev_pool[i], s) != hipSuccess) return -1;
+  return i;
+}
+
+void prof_span(Engine& e, int cls, int a, int b) {
+  if (a >= 0 && b >= 0) e.spans.push_back({cls, a, b});
+}
+
+int prof_collect(Engine& e, hipStream_t s) {
+  if (!e.prof_on) return PULSAR_OK;
+  PULSAR_CHECK_HIP(hipStreamSynchronize(s));
+  for (const auto& sp : e.spans) {
+    float ms = 0.f;
+    PULSAR_CHECK_HIP(hipEventElapsedTime(&ms, e.ev_pool[sp[1]], e.ev_pool[sp[2]]));
+    e.prof_ms[sp[0]] += ms;
+    e.prof_n[sp[0]] += 1;
+  }
+  e.spans.clear();
+  e.ev_used = 0;
+  return PULSAR_OK;
+}
+
+#define PULSAR_TIMED(cls, expr)          \
+  do {                                   \
+    const int _a = prof_mark(e, s);      \
+    PULSAR_TRY(expr);                    \
+    prof_span(e, (cls), _a, prof_mark(e, s)); \
+  } while (0)
+
+enum ProfClass {
+  PC_INPUT = 0, PC_NORM, PC_QKVG, PC_QKPOST, PC_ATTN, PC_WO, PC_ROUTER, PC_SHARED_GU,
+  PC_ROUTED_GU, PC_SHARED_DOWN, PC_ROUTED_DOWN, PC_COMBINE, PC_OUTPUT, PC_LMHEAD, PC_SAMPLE,
+  PC_CONTROL
+};
+
 int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) {
   PULSAR_TRY(validate(m, c));
   Engine* e = new Engine();
@@ -145,7 +199,9 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   e->max_rows = 2 * c.max_batch;
   e->R = std::max(e->max_rows, c.max_batch * c.max_prompt);
   e->max_pages = (c.max_ctx + kPage - 1) / kPage;
-  e->lcap = m.window + kPage;
+  // ring capacity: the prompt's last `window` positions stay intact while max_new tokens
+  // (+1 speculative) are appended, so a rewound decode sees the prefill state unchanged
+  e->lcap = m.window + c.max_new + kPage;
   e->max_splits = (c.max_ctx + kSplitLen - 1) / kSplitLen;
   const size_t es = e->es, D = e->D, R = e->R, MR = e->max_rows;
   Engine& x = *e;
@@ -176,6 +232,8 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.out_r, es * R * x.K * D));
   PULSAR_TRY(x.alloc(&x.xn_final, es * std::max<size_t>(MR, x.B) * D));
   PULSAR_TRY(x.alloc(&x.logits, 4 * std::max<size_t>(MR, x.B) * x.V));
+  PULSAR_TRY(x.alloc(&x.plogits, 4 * (size_t)x.B * x.V));
+  PULSAR_TRY(x.alloc(&x.d_seed, 8));
   PULSAR_TRY(x.alloc(&x.topk_idx, 4 * R * x.K));
   PULSAR_TRY(x.alloc(&x.topk_w, 4 * R * x.K));
   PULSAR_TRY(x.alloc(&x.keep, 4 * R * x.K));
@@ -245,7 +303,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   pi.h = e.h;
   pi.zero_counts = e.list_count;
   pi.n_zero = e.L * e.E;
-  PULSAR_TRY(launch_pulse_input(pi, dt, MR, s));
+  PULSAR_TIMED(PC_INPUT, launch_pulse_input(pi, dt, MR, s));
   const int64_t lstride = (int64_t)MR * e.K;
   for (int l = 0; l < e.L; ++l) {
     const bool loc = (m.local_mask >> l) & 1u;
@@ -259,7 +317,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     na.y = e.xn;
     na.D = D;
     na.eps = m.rms_eps;
-    PULSAR_TRY(launch_norm_rows(na, dt, MR, s));
+    PULSAR_TIMED(PC_NORM, launch_norm_rows(na, dt, MR, s));
     GemmArgs g = gemm_base(e);
     g.A = e.xn;
     g.lda = D;
@@ -277,7 +335,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.ldc2 = e.H;
     g.bias = m.gate_bias[l];
     g.bias_group_stride = e.H;
-    PULSAR_TRY(launch_gemm(g, dt, EPI_QKVG, e.P, MR, s));
+    PULSAR_TIMED(PC_QKVG, launch_gemm(g, dt, EPI_QKVG, e.P, MR, s));
     QKPostArgs qa{};
     qa.ctl = e.ctl;
     qa.rows = e.rows;
@@ -297,7 +355,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     qa.cos = loc ? m.rope_cos_local : m.rope_cos_global;
     qa.sin = loc ? m.rope_sin_local : m.rope_sin_global;
     qa.kv = e.kv;
-    PULSAR_TRY(launch_qk_post(qa, dt, MR, s));
+    PULSAR_TIMED(PC_QKPOST, launch_qk_post(qa, dt, MR, s));
     AttnArgs aa{};
     aa.ctl = e.ctl;
     aa.rows = e.rows;
@@ -314,7 +372,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     aa.window = m.window;
     aa.scale = 0.125f;
     aa.kv = e.kv;
-    PULSAR_TRY(launch_attn_decode(aa, dt, MR, s));
+    PULSAR_TIMED(PC_ATTN, launch_attn_decode(aa, dt, MR, s));
     g = gemm_base(e);
     g.A = e.attn_out;
     g.lda = (int64_t)e.H * kHeadDim;
@@ -327,9 +385,9 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.N = D;
     g.row_mode = ROWS_PULSE;
     g.ctl = e.ctl;
-    PULSAR_TRY(launch_gemm(g, dt, EPI_RESID, e.P, MR, s));
+    PULSAR_TIMED(PC_WO, launch_gemm(g, dt, EPI_RESID, e.P, MR, s));
     na.w = m.mlp_norm[l];
-    PULSAR_TRY(launch_norm_rows(na, dt, MR, s));
+    PULSAR_TIMED(PC_NORM, launch_norm_rows(na, dt, MR, s));
     RouterArgs ra{};
     ra.ctl = e.ctl;
     ra.rows = e.rows;
@@ -344,7 +402,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     ra.lists = e.lists + (int64_t)l * e.E * lstride;
     ra.list_count = e.list_count + (int64_t)l * e.E;
     ra.list_stride = lstride;
-    PULSAR_TRY(launch_router_decode(ra, dt, MR, s));
+    PULSAR_TIMED(PC_ROUTER, launch_router_decode(ra, dt, MR, s));
     // shared expert gate/up + SwiGLU
     g = gemm_base(e);
     g.A = e.xn;
@@ -357,7 +415,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.N = e.ds;
     g.row_mode = ROWS_ALL;
     g.ctl = e.ctl;
-    PULSAR_TRY(launch_gemm(g, dt, EPI_SWIGLU, 1, MR, s));
+    PULSAR_TIMED(PC_SHARED_GU, launch_gemm(g, dt, EPI_SWIGLU, 1, MR, s));
     // routed experts gate/up + SwiGLU over each expert's assignment list
     g = gemm_base(e);
     g.A = e.xn;
@@ -374,7 +432,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.list_count = ra.list_count;
     g.list_stride = lstride;
     g.a_div = e.K;
-    PULSAR_TRY(launch_gemm(g, dt, EPI_SWIGLU, e.E, MR, s));
+    PULSAR_TIMED(PC_ROUTED_GU, launch_gemm(g, dt, EPI_SWIGLU, e.E, MR, s));
     // shared down
     g = gemm_base(e);
     g.A = e.act_s;
@@ -387,7 +445,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.N = D;
     g.row_mode = ROWS_ALL;
     g.ctl = e.ctl;
-    PULSAR_TRY(launch_gemm(g, dt, EPI_STORE, 1, MR, s));
+    PULSAR_TIMED(PC_SHARED_DOWN, launch_gemm(g, dt, EPI_STORE, 1, MR, s));
     // routed down
     g = gemm_base(e);
     g.A = e.act_r;
@@ -404,7 +462,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.list_count = ra.list_count;
     g.list_stride = lstride;
     g.a_div = 1;
-    PULSAR_TRY(launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
+    PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
     CombineArgs ca{};
     ca.ctl = e.ctl;
     ca.rows = e.rows;
@@ -415,7 +473,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     ca.topk_w = e.topk_w;
     ca.routed_scale = m.routed_scale[l];
     ca.h = e.h;
-    PULSAR_TRY(launch_moe_combine(ca, dt, MR, s));
+    PULSAR_TIMED(PC_COMBINE, launch_moe_combine(ca, dt, MR, s));
   }
   PulseOutputArgs po{};
   po.ctl = e.ctl;
@@ -428,7 +486,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   po.hout_state = e.hout_state;
   po.final_norm = m.final_norm;
   po.xn_final = e.xn_final;
-  PULSAR_TRY(launch_pulse_output(po, dt, MR, s));
+  PULSAR_TIMED(PC_OUTPUT, launch_pulse_output(po, dt, MR, s));
   GemmArgs g = gemm_base(e);
   g.A = e.xn_final;
   g.lda = D;
@@ -441,7 +499,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   g.row_mode = ROWS_LOGITS;
   g.ctl = e.ctl;
   g.softcap = m.softcap;
-  PULSAR_TRY(launch_gemm(g, dt, EPI_LOGITS, 1, MR, s));
+  PULSAR_TIMED(PC_LMHEAD, launch_gemm(g, dt, EPI_LOGITS, 1, MR, s));
   SampleArgs sa{};
   sa.ctl = e.ctl;
   sa.logits = e.logits;
@@ -454,10 +512,11 @@ int enqueue_step(Engine& e, hipStream_t s) {
   sa.temperature = std::max(e.cfg.temperature, 1e-5f);
   sa.top_p = e.cfg.top_p;
   sa.rep_penalty = e.cfg.repetition_penalty;
-  sa.seed = e.cfg.seed;
+  sa.seed = e.d_seed;
   sa.out_argmax = e.argmax;
   sa.out_draw = e.draw;
-  PULSAR_TRY(launch_sample(sa, dt, MR, s));
+  PULSAR_TIMED(PC_SAMPLE, launch_sample(sa, dt, MR, s));
+  const int _pc = prof_mark(e, s);
   copy_rows_kernel<<<1, 256, 0, s>>>(e.ctl, e.rows, e.last_ctl, e.last_rows);
   PULSAR_LAUNCH_CHECK();
   ControllerArgs co{};
@@ -480,6 +539,63 @@ int enqueue_step(Engine& e, hipStream_t s) {
   co.all_logits = e.cfg.all_logits;
   co.prompt_len = e.prompt_len;
   PULSAR_TRY(launch_controller(co, s));
+  prof_span(e, PC_CONTROL, _pc, prof_mark(e, s));
+  return PULSAR_OK;
+}
+
+// Draw the first token of every sequence from the prefill logits and (re)initialise the
+// controller state; the KV cache of the prompt is left as prefill wrote it.
+int first_token(Engine& e, uint64_t seed, hipStream_t s) {
+  const int T = e.prompt_len, BT = e.B * T;
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.d_seed, &seed, 8, hipMemcpyHostToDevice, s));
+  PULSAR_CHECK_HIP(hipMemsetAsync(e.state, 0, sizeof(SeqState) * e.B, s));
+  PULSAR_CHECK_HIP(hipMemsetAsync(e.seen, 0, 4 * (size_t)e.B * (e.V / 32), s));
+  set_seen_kernel<<<(BT + 255) / 256, 256, 0, s>>>(e.p_ids, e.seen, T, e.V, BT);
+  PULSAR_LAUNCH_CHECK();
+  const StepCtl* lctl = e.p_ctl + (e.P - 1);
+  SampleArgs sa{};
+  sa.ctl = lctl;
+  sa.logits = e.plogits;
+  sa.lrow_seq = e.lrow_seq;
+  sa.lrow_extra = e.lrow_extra;
+  sa.seen = e.seen;
+  sa.state = e.state;
+  sa.V = e.V;
+  sa.greedy = e.cfg.temperature <= 1e-4f;
+  sa.temperature = std::max(e.cfg.temperature, 1e-5f);
+  sa.top_p = e.cfg.top_p;
+  sa.rep_penalty = e.cfg.repetition_penalty;
+  sa.seed = e.d_seed;
+  sa.out_argmax = e.argmax;
+  sa.out_draw = e.draw;
+  std::vector<int32_t> lseq(e.max_rows, 0), lext(e.max_rows, -1);
+  for (int b = 0; b < e.B; ++b) lseq[b] = b;
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.lrow_seq, lseq.data(), 4 * lseq.size(), hipMemcpyHostToDevice, s));
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.lrow_extra, lext.data(), 4 * lext.size(), hipMemcpyHostToDevice, s));
+  PULSAR_TRY(launch_sample(sa, e.dtype, e.B, s));
+  ControllerArgs co{};
+  co.ctl = e.ctl;
+  co.state = e.state;
+  co.rows = e.rows;
+  co.lrow_seq = e.lrow_seq;
+  co.lrow_extra = e.lrow_extra;
+  co.seen = e.seen;
+  co.out_tokens = e.tokens;
+  co.argmax = e.argmax;
+  co.draw = e.draw;
+  co.stop_ids = e.stop_ids;
+  co.n_stop = e.cfg.n_stop;
+  co.B = e.B;
+  co.V = e.V;
+  co.n_pulses = e.P;
+  co.max_new = e.cfg.max_new;
+  co.speculative = e.cfg.speculative;
+  co.all_logits = e.cfg.all_logits;
+  co.init = 1;
+  co.prompt_len = T;
+  PULSAR_TRY(launch_controller(co, s));
+  // host vectors above are read by the async copies: finish before they go out of scope
+  PULSAR_CHECK_HIP(hipStreamSynchronize(s));
   return PULSAR_OK;
 }
 
@@ -513,12 +629,6 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
                                   hipMemcpyHostToDevice, s));
   PULSAR_CHECK_HIP(hipMemcpyAsync(e.p_ctl, ctls.data(), sizeof(StepCtl) * P,
                                   hipMemcpyHostToDevice, s));
-  std::vector<int32_t> lseq(e.max_rows, 0), lext(e.max_rows, -1);
-  for (int b = 0; b < Bq; ++b) lseq[b] = b;
-  PULSAR_CHECK_HIP(hipMemcpyAsync(e.lrow_seq, lseq.data(), 4 * lseq.size(), hipMemcpyHostToDevice, s));
-  PULSAR_CHECK_HIP(hipMemcpyAsync(e.lrow_extra, lext.data(), 4 * lext.size(), hipMemcpyHostToDevice, s));
-  PULSAR_CHECK_HIP(hipMemsetAsync(e.state, 0, sizeof(SeqState) * e.B, s));
-  PULSAR_CHECK_HIP(hipMemsetAsync(e.seen, 0, 4 * (size_t)e.B * (e.V / 32), s));
   PULSAR_CHECK_HIP(hipMemsetAsync(e.ctl, 0, sizeof(StepCtl), s));
 
   PULSAR_TRY(launch_prefill_stem(e.p_ids, m.tok_emb, m.anchor_norm, m.conv_w, e.xn, e.e_state,
@@ -746,52 +856,14 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   g.lda = D;
   g.W = m.tok_emb;
   g.ldw = D;
-  g.C = e.logits;
+  g.C = e.plogits;
   g.ldc = e.V;
   g.K = D;
   g.N = e.V;
   g.row_mode = ROWS_LOGITS;
   g.ctl = lctl;
   PULSAR_TRY(launch_gemm(g, dt, EPI_LOGITS_RAW, 1, Bq, s));
-  set_seen_kernel<<<(BT + 255) / 256, 256, 0, s>>>(e.p_ids, e.seen, T, e.V, BT);
-  PULSAR_LAUNCH_CHECK();
-  SampleArgs sa{};
-  sa.ctl = lctl;
-  sa.logits = e.logits;
-  sa.lrow_seq = e.lrow_seq;
-  sa.lrow_extra = e.lrow_extra;
-  sa.seen = e.seen;
-  sa.state = e.state;
-  sa.V = e.V;
-  sa.greedy = e.cfg.temperature <= 1e-4f;
-  sa.temperature = std::max(e.cfg.temperature, 1e-5f);
-  sa.top_p = e.cfg.top_p;
-  sa.rep_penalty = e.cfg.repetition_penalty;
-  sa.seed = e.cfg.seed;
-  sa.out_argmax = e.argmax;
-  sa.out_draw = e.draw;
-  PULSAR_TRY(launch_sample(sa, dt, Bq, s));
-  ControllerArgs co{};
-  co.ctl = e.ctl;
-  co.state = e.state;
-  co.rows = e.rows;
-  co.lrow_seq = e.lrow_seq;
-  co.lrow_extra = e.lrow_extra;
-  co.seen = e.seen;
-  co.out_tokens = e.tokens;
-  co.argmax = e.argmax;
-  co.draw = e.draw;
-  co.stop_ids = e.stop_ids;
-  co.n_stop = e.cfg.n_stop;
-  co.B = e.B;
-  co.V = e.V;
-  co.n_pulses = e.P;
-  co.max_new = e.cfg.max_new;
-  co.speculative = e.cfg.speculative;
-  co.all_logits = e.cfg.all_logits;
-  co.init = 1;
-  co.prompt_len = T;
-  PULSAR_TRY(launch_controller(co, s));
+  PULSAR_TRY(first_token(e, e.cfg.seed, s));
   PULSAR_CHECK_HIP(hipStreamSynchronize(s));
   e.prefilled = true;
   return PULSAR_OK;
@@ -799,8 +871,11 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
 
 int step(Engine& e, int n, int use_graph, hipStream_t s) {
   PULSAR_REQUIRE(e.prefilled, "engine: prefill before stepping");
-  if (!use_graph) {
-    for (int i = 0; i < n; ++i) PULSAR_TRY(enqueue_step(e, s));
+  if (!use_graph || e.prof_on) {
+    for (int i = 0; i < n; ++i) {
+      PULSAR_TRY(enqueue_step(e, s));
+      PULSAR_TRY(prof_collect(e, s));
+    }
     return PULSAR_OK;
   }
   if (!e.exec) {
@@ -873,6 +948,38 @@ int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
   return PULSAR_OK;
 }
 
+int pulsar_engine_rewind(void* handle, uint64_t seed, hipStream_t stream) {
+  PULSAR_REQUIRE(handle, "engine_rewind: null handle");
+  Engine& e = *reinterpret_cast<Engine*>(handle);
+  PULSAR_REQUIRE(e.prefilled, "engine_rewind: prefill first");
+  return first_token(e, seed, stream);
+}
+
+int pulsar_engine_profile(void* handle, int32_t enable) {
+  PULSAR_REQUIRE(handle, "engine_profile: null handle");
+  Engine& e = *reinterpret_cast<Engine*>(handle);
+  e.prof_on = enable != 0;
+  if (e.prof_on) {
+    for (int i = 0; i < PULSAR_PROF_CLASSES; ++i) {
+      e.prof_ms[i] = 0.0;
+      e.prof_n[i] = 0;
+    }
+    e.spans.clear();
+    e.ev_used = 0;
+  }
+  return PULSAR_OK;
+}
+
+int pulsar_engine_profile_read(void* handle, double* host_ms, int64_t* host_launches) {
+  PULSAR_REQUIRE(handle && host_ms && host_launches, "engine_profile_read: null argument");
+  Engine& e = *reinterpret_cast<Engine*>(handle);
+  for (int i = 0; i < PULSAR_PROF_CLASSES; ++i) {
+    host_ms[i] = e.prof_ms[i];
+    host_launches[i] = e.prof_n[i];
+  }
+  return PULSAR_OK;
+}
+
 int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes,
                        hipStream_t stream) {
   PULSAR_REQUIRE(handle && host_dst && bytes >= 0, "engine_read: bad argument");
@@ -907,6 +1014,10 @@ int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes
     case PULSAR_BUF_LAST_CTL:
       src = e.last_ctl;
       cap = sizeof(StepCtl);
+      break;
+    case PULSAR_BUF_EXPERT_COUNTS:
+      src = e.list_count;
+      cap = 4ll * e.L * e.E;
       break;
     default:
       return fail(PULSAR_ERR_INVALID, "engine_read: unknown buffer");

@@ -28,7 +28,7 @@ struct SampleArgs {
   const SeqState* state;
   int V, greedy;
   float temperature, top_p, rep_penalty;
-  uint64_t seed;
+  const uint64_t* seed;  // device word, so a captured graph follows re-seeding
   int32_t* out_argmax;  // [lrows]
   int32_t* out_draw;    // [lrows][2]
 };

@@ -177,7 +177,7 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
   // stream: step counter of the sequence, and whether this is the speculative row
   const uint32_t ctr = a.state[seq].ctr * 2u + (extra >= 0 ? 1u : 0u);
   for (int d = 0; d < 2; ++d) {
-    const float target = uniform01(a.seed, seq, ctr, d) * total;
+    const float target = uniform01(*a.seed, seq, ctr, d) * total;
     if (own > 0.f && target >= pre && target < pre + own) {
       float run = pre;
       int choice = -1;

@@ -19,9 +19,16 @@ BUF_ROWS = 3
 BUF_CTL = 4
 BUF_LAST_ROWS = 5
 BUF_LAST_CTL = 6
+BUF_EXPERT_COUNTS = 7
 SEQSTATE_INTS = 20
 ROW_INTS = 8
 CTL_INTS = 16
+PROF_CLASSES = 16
+PROF_NAMES = (
+    "pulse_input", "rmsnorm", "qkv_gate_gemm", "qk_post", "attention", "wo_gemm", "router",
+    "shared_gate_up", "routed_gate_up", "shared_down", "routed_down", "moe_combine",
+    "pulse_output", "lm_head", "sample", "controller",
+)
 
 _c_i32 = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -86,6 +93,9 @@ _PROTOS = {
     "pulsar_engine_step": [_vp, _c_i32, _c_i32, _vp],
     "pulsar_engine_generate": [_vp, _c_i32, _c_i32, _vp, ctypes.POINTER(_c_i32)],
     "pulsar_engine_read": [_vp, _c_i32, _vp, _c_i64, _vp],
+    "pulsar_engine_rewind": [_vp, ctypes.c_uint64, _vp],
+    "pulsar_engine_profile": [_vp, _c_i32],
+    "pulsar_engine_profile_read": [_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)],
 }
 
 EXPORTED = tuple(["pulsar_last_error", *_PROTOS])

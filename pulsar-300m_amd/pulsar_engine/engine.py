@@ -86,6 +86,21 @@ class HipEngine:
                                                   a.shape[1], _stream()))
         self.steps = 0
 
+    def rewind(self, seed: int) -> None:
+        """Restart decoding from the prefilled cache with a new sampling seed."""
+        _lib.check(self.lib.pulsar_engine_rewind(self.handle, seed & 0xFFFFFFFFFFFFFFFF, _stream()))
+        self.steps = 0
+
+    def profile(self, enable: bool) -> None:
+        """Per-kernel-class HIP-event timing; steps run eagerly while enabled."""
+        _lib.check(self.lib.pulsar_engine_profile(self.handle, int(bool(enable))))
+
+    def profile_read(self) -> dict:
+        ms = (ctypes.c_double * _lib.PROF_CLASSES)()
+        n = (ctypes.c_int64 * _lib.PROF_CLASSES)()
+        _lib.check(self.lib.pulsar_engine_profile_read(self.handle, ms, n))
+        return {name: (ms[i], n[i]) for i, name in enumerate(_lib.PROF_NAMES)}
+
     def step(self, n: int = 1, graph: bool = False) -> None:
         _lib.check(self.lib.pulsar_engine_step(self.handle, n, int(graph), _stream()))
         self.steps += n
@@ -115,7 +130,13 @@ class HipEngine:
         return [toks[b, : st[b, ST_PRODUCED]].tolist() for b in range(self.batch)]
 
     def ctl(self) -> np.ndarray:
+        """Control block of the next step: n_rows, n_lrows, pulse_start[4], pulse_count[4],
+        active sequences, step counter."""
         return self._read(_lib.BUF_CTL, np.zeros(_lib.CTL_INTS, np.int32))
+
+    def last_ctl(self) -> np.ndarray:
+        """Control block of the last executed step."""
+        return self._read(_lib.BUF_LAST_CTL, np.zeros(_lib.CTL_INTS, np.int32))
 
     def logits(self, n: int) -> np.ndarray:
         return self._read(_lib.BUF_LOGITS, np.zeros((n, self.V), np.float32))
@@ -128,6 +149,11 @@ class HipEngine:
         buf = np.zeros((2 * self.batch, _lib.ROW_INTS), np.int32)
         self._read(_lib.BUF_LAST_ROWS if last else _lib.BUF_ROWS, buf)
         return buf[: int(ctl[0])]
+
+    def expert_counts(self) -> np.ndarray:
+        """Rows routed to each expert in every layer during the last step, [layers, E]."""
+        c = self.model.cfg
+        return self._read(_lib.BUF_EXPERT_COUNTS, np.zeros((c.n_core, c.n_routed_experts), np.int32))
 
     def acceptance(self) -> tuple[int, int]:
         st = self.state()

@@ -1,0 +1,57 @@
+"""Algorithmic HBM bytes of a decode step, per kernel class.
+
+The figure the roofline fraction is quoted against: every weight byte a step must read once
+(per-pulse projection variants once per pulse present in the step, routed experts once per
+expert that received at least one row, the tied output head once when any row needs
+logits), the KV entries each row attends to, and the activations each kernel reads and
+writes. Caches and re-reads are not counted; measured HBM traffic is reported beside it.
+"""
+
+from __future__ import annotations
+
+from collections import defaultdict
+
+from .config import PulsarConfig
+
+CLASSES = (
+    "pulse_input", "rmsnorm", "qkv_gate_gemm", "qk_post", "attention", "wo_gemm", "router",
+    "shared_gate_up", "routed_gate_up", "shared_down", "routed_down", "moe_combine",
+    "pulse_output", "lm_head", "sample", "controller",
+)
+
+
+def step_bytes(cfg: PulsarConfig, es: int, rows, expert_counts, n_lrows: int) -> dict:
+    """rows: iterable of (seq, pulse, pos); expert_counts: [layers][E] rows per expert."""
+    D, H, Hk, hd = cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    E, K, de, ds, V = cfg.n_routed_experts, cfg.top_k, cfg.d_expert, cfg.d_shared, cfg.vocab_size
+    q_dim, qkv = cfg.q_dim, cfg.qkv_dim
+    rows = list(rows)
+    n = len(rows)
+    out: dict[str, float] = defaultdict(float)
+    if n == 0:
+        return out
+    pulses = {p for _, p, _ in rows}
+    npul = len(pulses)
+    r = cfg.reinject_gate_rank
+    out["pulse_input"] = n * D * es * 4 + npul * (3 * r * D + 2 * D) * es
+    for L in range(cfg.n_core):
+        local = cfg.is_local(L)
+        ctx = sum(min(pos + 1, cfg.sliding_window) if local else pos + 1 for _, _, pos in rows)
+        touched = int(sum(1 for c in expert_counts[L] if c > 0))
+        assigned = int(sum(expert_counts[L]))
+        out["rmsnorm"] += 2 * (n * D * es * 2 + npul * D * 4)
+        out["qkv_gate_gemm"] += npul * (qkv + H) * D * es + n * (D + qkv + H) * es
+        out["qk_post"] += n * (qkv * es * 2 + 2 * Hk * hd * es)
+        out["attention"] += ctx * Hk * hd * 2 * es + n * (q_dim + H + q_dim) * es
+        out["wo_gemm"] += npul * D * q_dim * es + n * (q_dim + 2 * D) * es
+        out["router"] += npul * E * D * 4 + n * D * es
+        out["shared_gate_up"] += 2 * ds * D * es + n * (D + ds) * es
+        out["routed_gate_up"] += touched * 2 * de * D * es + assigned * (D + de) * es
+        out["shared_down"] += D * ds * es + n * (ds + D) * es
+        out["routed_down"] += touched * D * de * es + assigned * (de + D) * es
+        out["moe_combine"] += n * (K + 3) * D * es
+    out["pulse_output"] = n * 3 * D * es + n_lrows * D * es
+    if n_lrows:
+        out["lm_head"] = V * D * es + n_lrows * (D * es + V * 4)
+        out["sample"] = n_lrows * V * 4
+    return out
