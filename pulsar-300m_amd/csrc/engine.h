@@ -78,6 +78,16 @@ struct GemmArgs {
   int64_t bias_group_stride;
   float softcap;
   int c_row_offset;        // added to C row index (prefill chunking)
+  // Optional extra group 0 computed over all rows with its own operands (the shared expert
+  // fused into the routed-expert launch); list groups then start at grid.y == 1.
+  int has_g0;
+  const void* A0;
+  int64_t lda0;
+  const void* W0;
+  int64_t ldw0;
+  void* C0;
+  int64_t ldc0;
+  int N0;
 };
 
 int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,

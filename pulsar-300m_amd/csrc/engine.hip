@@ -117,13 +117,6 @@ __global__ void set_seen_kernel(const int32_t* ids, uint32_t* seen, int T, int V
   atomicOr(&seen[(int64_t)b * (V / 32) + (tok >> 5)], 1u << (tok & 31));
 }
 
-__global__ void copy_rows_kernel(const StepCtl* ctl, const RowDesc* rows, StepCtl* last_ctl,
-                                 RowDesc* last_rows) {
-  const int n = ctl->n_rows;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) last_rows[i] = rows[i];
-  if (threadIdx.x == 0) *last_ctl = *ctl;
-}
-
 void kv_desc(Engine& e) {
   e.kv.page_table = e.page_table;
   e.kv.local_mask = e.m.local_mask;
@@ -280,6 +273,10 @@ GemmArgs gemm_base(const Engine& e) {
 }
 
 // One pulse pass of every active row + logits + sampling + controller.
+// Per layer: qkv+gate GEMM, qk-norm/RoPE/KV write, attention (+ split combine), wo GEMM with
+// residual, mlp-norm + router, shared+routed gate/up GEMM, shared+routed down GEMM, MoE
+// combine with residual and the next layer's attn-norm (the first layer's attn-norm is
+// fused into the pulse-input kernel).
 int enqueue_step(Engine& e, hipStream_t s) {
   const PulsarModelDesc& m = e.m;
   const int D = e.D, MR = e.max_rows, dt = e.dtype;
@@ -303,21 +300,12 @@ int enqueue_step(Engine& e, hipStream_t s) {
   pi.h = e.h;
   pi.zero_counts = e.list_count;
   pi.n_zero = e.L * e.E;
+  pi.norm_w = m.attn_norm[0];
+  pi.xn = e.xn;
   PULSAR_TIMED(PC_INPUT, launch_pulse_input(pi, dt, MR, s));
   const int64_t lstride = (int64_t)MR * e.K;
   for (int l = 0; l < e.L; ++l) {
     const bool loc = (m.local_mask >> l) & 1u;
-    NormArgs na{};
-    na.ctl = e.ctl;
-    na.rows = e.rows;
-    na.x = e.h;
-    na.ldx = D;
-    na.w = m.attn_norm[l];
-    na.w_pulse_stride = D;
-    na.y = e.xn;
-    na.D = D;
-    na.eps = m.rms_eps;
-    PULSAR_TIMED(PC_NORM, launch_norm_rows(na, dt, MR, s));
     GemmArgs g = gemm_base(e);
     g.A = e.xn;
     g.lda = D;
@@ -386,12 +374,10 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.row_mode = ROWS_PULSE;
     g.ctl = e.ctl;
     PULSAR_TIMED(PC_WO, launch_gemm(g, dt, EPI_RESID, e.P, MR, s));
-    na.w = m.mlp_norm[l];
-    PULSAR_TIMED(PC_NORM, launch_norm_rows(na, dt, MR, s));
     RouterArgs ra{};
     ra.ctl = e.ctl;
     ra.rows = e.rows;
-    ra.x = e.xn;
+    ra.x = e.h;
     ra.w = m.router[l];
     ra.bias = m.expert_bias[l];
     ra.E = e.E;
@@ -402,21 +388,11 @@ int enqueue_step(Engine& e, hipStream_t s) {
     ra.lists = e.lists + (int64_t)l * e.E * lstride;
     ra.list_count = e.list_count + (int64_t)l * e.E;
     ra.list_stride = lstride;
-    PULSAR_TIMED(PC_ROUTER, launch_router_decode(ra, dt, MR, s));
-    // shared expert gate/up + SwiGLU
-    g = gemm_base(e);
-    g.A = e.xn;
-    g.lda = D;
-    g.W = m.shared_gu[l];
-    g.ldw = D;
-    g.C = e.act_s;
-    g.ldc = e.ds;
-    g.K = D;
-    g.N = e.ds;
-    g.row_mode = ROWS_ALL;
-    g.ctl = e.ctl;
-    PULSAR_TIMED(PC_SHARED_GU, launch_gemm(g, dt, EPI_SWIGLU, 1, MR, s));
-    // routed experts gate/up + SwiGLU over each expert's assignment list
+    ra.norm_w = m.mlp_norm[l];
+    ra.xn = e.xn;
+    ra.eps = m.rms_eps;
+    PULSAR_TIMED(PC_ROUTER, launch_norm_router(ra, dt, MR, s));
+    // shared expert (group 0, all rows) + routed experts (assignment lists): gate/up + SwiGLU
     g = gemm_base(e);
     g.A = e.xn;
     g.lda = D;
@@ -432,21 +408,17 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.list_count = ra.list_count;
     g.list_stride = lstride;
     g.a_div = e.K;
-    PULSAR_TIMED(PC_ROUTED_GU, launch_gemm(g, dt, EPI_SWIGLU, e.E, MR, s));
-    // shared down
-    g = gemm_base(e);
-    g.A = e.act_s;
-    g.lda = e.ds;
-    g.W = m.shared_down[l];
-    g.ldw = e.ds;
-    g.C = e.out_s;
-    g.ldc = D;
-    g.K = e.ds;
-    g.N = D;
-    g.row_mode = ROWS_ALL;
     g.ctl = e.ctl;
-    PULSAR_TIMED(PC_SHARED_DOWN, launch_gemm(g, dt, EPI_STORE, 1, MR, s));
-    // routed down
+    g.has_g0 = 1;
+    g.A0 = e.xn;
+    g.lda0 = D;
+    g.W0 = m.shared_gu[l];
+    g.ldw0 = D;
+    g.C0 = e.act_s;
+    g.ldc0 = e.ds;
+    g.N0 = e.ds;
+    PULSAR_TIMED(PC_ROUTED_GU, launch_gemm(g, dt, EPI_SWIGLU, e.E, MR, s));
+    // shared + routed down projections
     g = gemm_base(e);
     g.A = e.act_r;
     g.lda = e.de;
@@ -462,7 +434,33 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.list_count = ra.list_count;
     g.list_stride = lstride;
     g.a_div = 1;
-    PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
+    g.ctl = e.ctl;
+    if (e.ds == e.de) {
+      g.has_g0 = 1;
+      g.A0 = e.act_s;
+      g.lda0 = e.ds;
+      g.W0 = m.shared_down[l];
+      g.ldw0 = e.ds;
+      g.C0 = e.out_s;
+      g.ldc0 = D;
+      g.N0 = D;
+      PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
+    } else {
+      // the fused launch shares K between groups; different widths take two launches
+      PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
+      GemmArgs gs = gemm_base(e);
+      gs.A = e.act_s;
+      gs.lda = e.ds;
+      gs.W = m.shared_down[l];
+      gs.ldw = e.ds;
+      gs.C = e.out_s;
+      gs.ldc = D;
+      gs.K = e.ds;
+      gs.N = D;
+      gs.row_mode = ROWS_ALL;
+      gs.ctl = e.ctl;
+      PULSAR_TIMED(PC_SHARED_DOWN, launch_gemm(gs, dt, EPI_STORE, 1, MR, s));
+    }
     CombineArgs ca{};
     ca.ctl = e.ctl;
     ca.rows = e.rows;
@@ -473,6 +471,9 @@ int enqueue_step(Engine& e, hipStream_t s) {
     ca.topk_w = e.topk_w;
     ca.routed_scale = m.routed_scale[l];
     ca.h = e.h;
+    ca.next_norm = l + 1 < e.L ? m.attn_norm[l + 1] : nullptr;
+    ca.xn = e.xn;
+    ca.eps = m.rms_eps;
     PULSAR_TIMED(PC_COMBINE, launch_moe_combine(ca, dt, MR, s));
   }
   PulseOutputArgs po{};
@@ -517,9 +518,9 @@ int enqueue_step(Engine& e, hipStream_t s) {
   sa.out_draw = e.draw;
   PULSAR_TIMED(PC_SAMPLE, launch_sample(sa, dt, MR, s));
   const int _pc = prof_mark(e, s);
-  copy_rows_kernel<<<1, 256, 0, s>>>(e.ctl, e.rows, e.last_ctl, e.last_rows);
-  PULSAR_LAUNCH_CHECK();
   ControllerArgs co{};
+  co.last_ctl = e.last_ctl;
+  co.last_rows = e.last_rows;
   co.ctl = e.ctl;
   co.state = e.state;
   co.rows = e.rows;
@@ -574,6 +575,8 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   PULSAR_CHECK_HIP(hipMemcpyAsync(e.lrow_extra, lext.data(), 4 * lext.size(), hipMemcpyHostToDevice, s));
   PULSAR_TRY(launch_sample(sa, e.dtype, e.B, s));
   ControllerArgs co{};
+  co.last_ctl = e.last_ctl;
+  co.last_rows = e.last_rows;
   co.ctl = e.ctl;
   co.state = e.state;
   co.rows = e.rows;
@@ -863,6 +866,9 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   g.row_mode = ROWS_LOGITS;
   g.ctl = lctl;
   PULSAR_TRY(launch_gemm(g, dt, EPI_LOGITS_RAW, 1, Bq, s));
+  // the prefill logits are also the readable "last logits" until the first step runs
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.logits, e.plogits, 4 * (size_t)Bq * e.V,
+                                  hipMemcpyDeviceToDevice, s));
   PULSAR_TRY(first_token(e, e.cfg.seed, s));
   PULSAR_CHECK_HIP(hipStreamSynchronize(s));
   e.prefilled = true;

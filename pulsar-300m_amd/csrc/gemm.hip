@@ -9,6 +9,8 @@
 // groups without rows exit before touching their weights.
 //
 // fp32: one wave per output column, lanes split K with 128-bit loads, wave64 reduction.
+#include <algorithm>
+
 #include "engine.h"
 
 namespace pulsar {
@@ -26,9 +28,10 @@ __device__ __forceinline__ bf16x8_t load_bf16x8(const bf16* p) {
 // Returns the number of valid rows (0 => nothing to do).
 __device__ int resolve_rows(const GemmArgs& g, int group, int tile, int* a_row, int* c_row) {
   __shared__ int s_n;
+  const int mode = (g.has_g0 && group < 0) ? ROWS_ALL : g.row_mode;
   if (threadIdx.x == 0) {
     int n = 0;
-    switch (g.row_mode) {
+    switch (mode) {
       case ROWS_PULSE: {
         const int cnt = g.ctl->pulse_count[group];
         n = cnt - tile * 32;
@@ -55,7 +58,7 @@ __device__ int resolve_rows(const GemmArgs& g, int group, int tile, int* a_row, 
     int ar = -1, cr = -1;
     if (m < n) {
       const int i = tile * 32 + m;
-      switch (g.row_mode) {
+      switch (mode) {
         case ROWS_PULSE:
           ar = cr = g.ctl->pulse_start[group] + i;
           break;
@@ -81,16 +84,16 @@ __device__ int resolve_rows(const GemmArgs& g, int group, int tile, int* a_row, 
 }
 
 template <typename T>
-__device__ __forceinline__ void epilogue(const GemmArgs& g, int epi, int group, int crow, int col,
-                                         float acc, float acc_up) {
-  T* C = reinterpret_cast<T*>(g.C);
+__device__ __forceinline__ void epilogue(const GemmArgs& g, int epi, int group, void* Cv,
+                                         int64_t ldc, int crow, int col, float acc, float acc_up) {
+  T* C = reinterpret_cast<T*>(Cv);
   switch (epi) {
     case EPI_STORE:
-      C[(int64_t)crow * g.ldc + col] = from_f<T>(acc);
+      C[(int64_t)crow * ldc + col] = from_f<T>(acc);
       break;
     case EPI_QKVG:
       if (col < g.n_main) {
-        C[(int64_t)crow * g.ldc + col] = from_f<T>(acc);
+        C[(int64_t)crow * ldc + col] = from_f<T>(acc);
       } else {
         const int h = col - g.n_main;
         const T* b = reinterpret_cast<const T*>(g.bias) + (int64_t)group * g.bias_group_stride;
@@ -99,13 +102,13 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, int epi, int group, 
       }
       break;
     case EPI_RESID: {
-      T* p = C + (int64_t)crow * g.ldc + col;
+      T* p = C + (int64_t)crow * ldc + col;
       *p = from_f<T>(to_f(*p) + rnd<T>(acc));
       break;
     }
     case EPI_SWIGLU: {
       const float gt = rnd<T>(acc), up = rnd<T>(acc_up);
-      C[(int64_t)crow * g.ldc + col] = from_f<T>(gt * sigmoidf_(gt) * up);
+      C[(int64_t)crow * ldc + col] = from_f<T>(gt * sigmoidf_(gt) * up);
       break;
     }
     case EPI_LOGITS: {
@@ -115,59 +118,106 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, int epi, int group, 
         t = rnd<T>(tanhf(t));
         l = rnd<T>(g.softcap * t);
       }
-      reinterpret_cast<float*>(g.C)[(int64_t)crow * g.ldc + col] = l;
+      reinterpret_cast<float*>(Cv)[(int64_t)crow * ldc + col] = l;
       break;
     }
     case EPI_LOGITS_RAW:
-      reinterpret_cast<float*>(g.C)[(int64_t)crow * g.ldc + col] = rnd<T>(acc);
+      reinterpret_cast<float*>(Cv)[(int64_t)crow * ldc + col] = rnd<T>(acc);
       break;
     case EPI_SCALE: {
       const T* s = reinterpret_cast<const T*>(g.bias);
-      C[(int64_t)crow * g.ldc + col] = from_f<T>(rnd<T>(acc) * to_f(s[col]));
+      C[(int64_t)crow * ldc + col] = from_f<T>(rnd<T>(acc) * to_f(s[col]));
       break;
     }
   }
 }
 
-template <int EPI>
+// Rows of group `group` in the row set: count and the (A row, C row) of entry i.
+__device__ __forceinline__ int group_count(const GemmArgs& g, int mode, int group) {
+  switch (mode) {
+    case ROWS_PULSE: return g.ctl->pulse_count[group];
+    case ROWS_LIST: return g.list_count[group];
+    case ROWS_ALL: return g.ctl ? g.ctl->n_rows : g.m_fixed;
+    default: return g.ctl->n_lrows;
+  }
+}
+
+__device__ __forceinline__ void entry_rows(const GemmArgs& g, int mode, int group, int i, int& ar,
+                                           int& cr) {
+  switch (mode) {
+    case ROWS_PULSE:
+      ar = cr = g.ctl->pulse_start[group] + i;
+      break;
+    case ROWS_LIST: {
+      const int e = g.list[(int64_t)group * g.list_stride + i];
+      ar = e / g.a_div;
+      cr = e;
+      break;
+    }
+    default:
+      ar = cr = i;
+      break;
+  }
+  cr += g.c_row_offset;
+}
+
+template <int EPI, int KITER>
 __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
-  __shared__ int a_row[32], c_row[32];
   __shared__ float red[3][64][kPair ? 16 : 8];
-  const int group = blockIdx.y + g.group_offset;
+  // grid.y == 0 is the optional all-rows group (group -1) when has_g0 is set
+  const int group = (int)blockIdx.y + g.group_offset - (g.has_g0 ? 1 : 0);
+  const bool g0 = group < 0;
+  const int mode = g0 ? ROWS_ALL : g.row_mode;
+  const int N = g0 ? g.N0 : g.N;
   const int col0 = blockIdx.x * 16;
-  if (col0 >= g.N) return;
-  const int n = resolve_rows(g, group, blockIdx.z, a_row, c_row);
-  if (n == 0) return;
+  if (col0 >= N) return;
+  const int tile0 = blockIdx.z * 32;
+  const int n = min(32, group_count(g, mode, group) - tile0);  // uniform per workgroup
+  if (n <= 0) return;
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = lane & 15, kq = lane >> 4;
-  const bf16* A = reinterpret_cast<const bf16*>(g.A);
-  const bf16* W = reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
-  const int ar0 = a_row[m], ar1 = a_row[m + 16];
-  const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * g.lda;
-  const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * g.lda;
-  const bool v0 = ar0 >= 0, v1 = ar1 >= 0;
-  const bool vc = col0 + m < g.N;  // columns past N (last tile) read row 0 and are dropped
-  const bf16* w0 = W + (int64_t)(vc ? col0 + m : 0) * g.ldw;
-  const bf16* w1 = W + (int64_t)(vc ? g.N + col0 + m : 0) * g.ldw;
+  const int64_t lda = g0 ? g.lda0 : g.lda, ldw = g0 ? g.ldw0 : g.ldw;
+  const bf16* W = g0 ? reinterpret_cast<const bf16*>(g.W0)
+                     : reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
+  const bool vc = col0 + m < N;  // columns past N (last tile) read row 0 and are dropped
+  const bf16* w0 = W + (int64_t)(vc ? col0 + m : 0) * ldw;
+  const bf16* w1 = W + (int64_t)(vc ? N + col0 + m : 0) * ldw;
 
-  const int kspan = g.K >> 2;
-  const int kbeg = wv * kspan;
-  f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
+  // Weight loads first: they depend only on the group, so their latency overlaps the row
+  // lookup below. Every load of this wave's K quarter is in flight before the first MFMA.
+  const int kb = wv * (KITER * 32) + kq * 8;
+  bf16x8_t bw[KITER], bu[KITER], xa[KITER], xb[KITER];
+#pragma unroll
+  for (int i = 0; i < KITER; ++i) {
+    bw[i] = load_bf16x8(w0 + kb + 32 * i);
+    if constexpr (kPair) bu[i] = load_bf16x8(w1 + kb + 32 * i);
+  }
+  const bool two = n > 16;  // second 16-row block present (uniform per workgroup)
+  int ar0 = -1, ar1 = -1, cdummy;
+  if (m < n) entry_rows(g, mode, group, tile0 + m, ar0, cdummy);
+  if (m + 16 < n) entry_rows(g, mode, group, tile0 + m + 16, ar1, cdummy);
+  const bf16* A = reinterpret_cast<const bf16*>(g0 ? g.A0 : g.A);
+  const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * lda;
+  const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * lda;
   const bf16x8_t zero = {};
-#pragma unroll 4
-  for (int k = kbeg + kq * 8; k < kbeg + kspan; k += 32) {
-    const bf16x8_t b0 = load_bf16x8(w0 + k);
-    bf16x8_t b1;
-    if constexpr (kPair) b1 = load_bf16x8(w1 + k);
-    const bf16x8_t x0 = v0 ? load_bf16x8(a0 + k) : zero;
-    const bf16x8_t x1 = v1 ? load_bf16x8(a1 + k) : zero;
-    c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, b0, c00, 0, 0, 0);
-    c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, b0, c10, 0, 0, 0);
-    if constexpr (kPair) {
-      c01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, b1, c01, 0, 0, 0);
-      c11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, b1, c11, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < KITER; ++i) {
+    xa[i] = ar0 >= 0 ? load_bf16x8(a0 + kb + 32 * i) : zero;
+    if (two) xb[i] = ar1 >= 0 ? load_bf16x8(a1 + kb + 32 * i) : zero;
+  }
+  f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
+#pragma unroll
+  for (int i = 0; i < KITER; ++i) {
+    c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[i], c00, 0, 0, 0);
+    if constexpr (kPair) c01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bu[i], c01, 0, 0, 0);
+  }
+  if (two) {
+#pragma unroll
+    for (int i = 0; i < KITER; ++i) {
+      c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[i], bw[i], c10, 0, 0, 0);
+      if constexpr (kPair) c11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[i], bu[i], c11, 0, 0, 0);
     }
   }
   if (wv > 0) {
@@ -200,11 +250,20 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
   // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16.
   const int col = col0 + m;
   if (!vc) return;
+  void* Cout = g0 ? g.C0 : g.C;
+  const int64_t ldc = g0 ? g.ldc0 : g.ldc;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r0 = kq * 4 + j, r1 = 16 + kq * 4 + j;
-    if (r0 < n) epilogue<bf16>(g, EPI, group, c_row[r0], col, c00[j], c01[j]);
-    if (r1 < n) epilogue<bf16>(g, EPI, group, c_row[r1], col, c10[j], c11[j]);
+    int ar, cr;
+    if (r0 < n) {
+      entry_rows(g, mode, group, tile0 + r0, ar, cr);
+      epilogue<bf16>(g, EPI, group, Cout, ldc, cr, col, c00[j], c01[j]);
+    }
+    if (r1 < n) {
+      entry_rows(g, mode, group, tile0 + r1, ar, cr);
+      epilogue<bf16>(g, EPI, group, Cout, ldc, cr, col, c10[j], c11[j]);
+    }
   }
 }
 
@@ -213,18 +272,24 @@ template <int EPI>
 __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
   __shared__ int a_row[32], c_row[32];
-  const int group = blockIdx.y + g.group_offset;
+  const int group = (int)blockIdx.y + g.group_offset - (g.has_g0 ? 1 : 0);
+  const bool g0 = group < 0;
+  const int N = g0 ? g.N0 : g.N;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int col = blockIdx.x * 4 + wv;
-  if (blockIdx.x * 4 >= g.N) return;
+  if (blockIdx.x * 4 >= N) return;
   const int n = resolve_rows(g, group, blockIdx.z, a_row, c_row);
-  if (n == 0 || col >= g.N) return;
-  const float* A = reinterpret_cast<const float*>(g.A);
-  const float* W = reinterpret_cast<const float*>(g.W) + (int64_t)group * g.w_group_stride;
-  const float* w0 = W + (int64_t)col * g.ldw;
-  const float* w1 = W + (int64_t)(g.N + col) * g.ldw;
+  if (n == 0 || col >= N) return;
+  const float* A = reinterpret_cast<const float*>(g0 ? g.A0 : g.A);
+  const int64_t lda = g0 ? g.lda0 : g.lda, ldw = g0 ? g.ldw0 : g.ldw;
+  const float* W = g0 ? reinterpret_cast<const float*>(g.W0)
+                      : reinterpret_cast<const float*>(g.W) + (int64_t)group * g.w_group_stride;
+  void* Cout = g0 ? g.C0 : g.C;
+  const int64_t ldc = g0 ? g.ldc0 : g.ldc;
+  const float* w0 = W + (int64_t)col * ldw;
+  const float* w1 = W + (int64_t)(N + col) * ldw;
   for (int r = 0; r < n; ++r) {
-    const float* a = A + (int64_t)a_row[r] * g.lda;
+    const float* a = A + (int64_t)a_row[r] * lda;
     float s0 = 0.f, s1 = 0.f;
     for (int k = lane * 4; k < g.K; k += 256) {
       const float4 av = *reinterpret_cast<const float4*>(a + k);
@@ -237,7 +302,7 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
     }
     s0 = wave_sum(s0);
     if constexpr (kPair) s1 = wave_sum(s1);
-    if (lane == (r & 63)) epilogue<float>(g, EPI, group, c_row[r], col, s0, s1);
+    if (lane == (r & 63)) epilogue<float>(g, EPI, group, Cout, ldc, c_row[r], col, s0, s1);
   }
 }
 
@@ -245,11 +310,19 @@ template <int EPI>
 int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream_t s) {
   const int tiles = (max_rows + 31) / 32;
   if (tiles <= 0 || groups <= 0) return PULSAR_OK;
+  const int gy = groups + (a.has_g0 ? 1 : 0);
+  const int nmax = a.has_g0 ? std::max(a.N, a.N0) : a.N;
   if (dtype == PULSAR_BF16) {
-    dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)groups, (unsigned)tiles);
-    gemm_bf16_kernel<EPI><<<grid, 256, 0, s>>>(a);
+    dim3 grid((unsigned)((nmax + 15) / 16), (unsigned)gy, (unsigned)tiles);
+    switch (a.K) {
+      case 256: gemm_bf16_kernel<EPI, 2><<<grid, 256, 0, s>>>(a); break;
+      case 512: gemm_bf16_kernel<EPI, 4><<<grid, 256, 0, s>>>(a); break;
+      case 1024: gemm_bf16_kernel<EPI, 8><<<grid, 256, 0, s>>>(a); break;
+      case 2048: gemm_bf16_kernel<EPI, 16><<<grid, 256, 0, s>>>(a); break;
+      default: return fail(PULSAR_ERR_UNSUPPORTED, "gemm: K must be 256, 512, 1024 or 2048");
+    }
   } else {
-    dim3 grid((unsigned)((a.N + 3) / 4), (unsigned)groups, (unsigned)tiles);
+    dim3 grid((unsigned)((nmax + 3) / 4), (unsigned)gy, (unsigned)tiles);
     gemm_f32_kernel<EPI><<<grid, 256, 0, s>>>(a);
   }
   PULSAR_LAUNCH_CHECK();

@@ -6,6 +6,8 @@
 namespace pulsar {
 
 constexpr int kSplitLen = 256;  // keys per decode-attention block
+constexpr int kMaxPer = 8;      // row elements per thread of a 256-thread block (D <= 2048)
+constexpr int kMaxRank = 16;    // re-injection gate rank bound
 
 // KV cache addressing. Local (sliding-window) layers: a per-sequence ring of `lcap`
 // positions, [B][Hkv][lcap][64]. Global layers: pages of 64 positions from a shared pool,
@@ -47,6 +49,8 @@ struct PulseInputArgs {
   void* h;
   int32_t* zero_counts;     // zeroed by block 0 (expert list counts of the step)
   int n_zero;
+  const float* norm_w;      // [P][D] attn_norm of the first layer (nullable)
+  void* xn;                 // normed h_in output when norm_w is set
 };
 
 struct NormArgs {
@@ -105,6 +109,9 @@ struct RouterArgs {
   int32_t* lists;      // [E][list_stride] assignment ids (decode), nullable
   int32_t* list_count; // [E]
   int64_t list_stride;
+  const float* norm_w; // norm_router: [P][D] mlp_norm weight
+  void* xn;            // norm_router: normed output [rows][D]
+  float eps;
 };
 
 struct CombineArgs {
@@ -117,6 +124,9 @@ struct CombineArgs {
   const int32_t* keep; // [rows*K] or null
   const void* routed_scale;  // [P][D] T
   void* h;
+  const float* next_norm;    // [P][D] attn_norm of the next layer (nullable)
+  void* xn;                  // normed h output when next_norm is set
+  float eps;
 };
 
 struct PulseOutputArgs {
@@ -183,6 +193,8 @@ int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s);
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s);
 int launch_attn_prefill(const AttnArgs& a, int dtype, int B, hipStream_t s);
 int launch_router_decode(const RouterArgs& a, int dtype, int max_rows, hipStream_t s);
+// mlp_norm + router fused: a.x = residual stream h, a.norm_w/a.xn the norm weight/output.
+int launch_norm_router(const RouterArgs& a, int dtype, int max_rows, hipStream_t s);
 int launch_router_prefill(const RouterArgs& a, int dtype, hipStream_t s);
 int launch_prefill_capacity(const int32_t* idx, const float* w, int32_t* cnt, int32_t* keep,
                             int32_t* lists, int32_t* lcount, int64_t list_stride, int B, int T_,

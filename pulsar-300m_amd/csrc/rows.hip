@@ -44,6 +44,29 @@ __device__ float row_inv_rms(const T* x, int D, float eps, float* red) {
   return 1.0f / sqrtf(ss / (float)D + eps);
 }
 
+// Store a row held as hv[c] (element threadIdx.x + 256c) into h_in and h, and, when w is
+// given, its RMSNorm T(w * (h * inv)) into xn.
+template <typename T, int NPER>
+__device__ void store_and_norm(const float* hv, T* h_in, T* h, const float* w, T* xn, int D,
+                               float eps, float* red) {
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NPER; ++c) {
+    const int i = threadIdx.x + c * 256;
+    if (h_in) h_in[i] = from_f<T>(hv[c]);
+    h[i] = from_f<T>(hv[c]);
+    ss += hv[c] * hv[c];
+  }
+  if (!w) return;
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+  for (int c = 0; c < NPER; ++c) {
+    const int i = threadIdx.x + c * 256;
+    xn[i] = from_f<T>(w[i] * (hv[c] * inv));
+  }
+}
+
 __device__ __forceinline__ float lerp_ref(float s, float e, float w) {
   // torch.lerp: start + w*(end-start) for |w| < 0.5, else end - (end-start)*(1-w)
   return fabsf(w) < 0.5f ? s + w * (e - s) : e - (e - s) * (1.0f - w);
@@ -55,7 +78,7 @@ __device__ __forceinline__ float lerp_ref(float s, float e, float w) {
 // Pulse input. pulse 0: stem (decode: embed, anchor norm, conv over one token) + step
 // embedding. pulse >= 1: rank-r re-injection gate on (anchor, state-normed previous pulse).
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int NPER>
 __global__ void __launch_bounds__(256) pulse_input_kernel(PulseInputArgs a) {
   __shared__ float red[16];
   __shared__ float gh[16];
@@ -71,25 +94,28 @@ __global__ void __launch_bounds__(256) pulse_input_kernel(PulseInputArgs a) {
   T* h_in = reinterpret_cast<T*>(a.h_in) + (int64_t)r * D;
   T* h = reinterpret_cast<T*>(a.h) + (int64_t)r * D;
   const T* step = reinterpret_cast<const T*>(a.step_emb) + (int64_t)rd.pulse * D;
+  float hv[NPER];
   if (rd.pulse == 0) {
     if (!a.prefill) {
       const T* x0 = reinterpret_cast<const T*>(a.tok_emb) + (int64_t)rd.token * D;
       const float inv = row_inv_rms(x0, D, a.eps, red);
-      for (int i = threadIdx.x; i < D; i += blockDim.x) {
+#pragma unroll
+      for (int c = 0; c < NPER; ++c) {
+        const int i = threadIdx.x + c * 256;
         float v = rnd<T>(ld(x0, i) * inv * a.anchor_norm[i]);
         if (a.conv_w) v = rnd<T>(v + a.conv_w[i * 4] * v);
         e[i] = from_f<T>(v);
-        const float hi = rnd<T>(v + ld(step, i));
-        h_in[i] = from_f<T>(hi);
-        h[i] = from_f<T>(hi);
+        hv[c] = rnd<T>(v + ld(step, i));
       }
     } else {
-      for (int i = threadIdx.x; i < D; i += blockDim.x) {
-        const float hi = rnd<T>(ld(e, i) + ld(step, i));
-        h_in[i] = from_f<T>(hi);
-        h[i] = from_f<T>(hi);
+#pragma unroll
+      for (int c = 0; c < NPER; ++c) {
+        const int i = threadIdx.x + c * 256;
+        hv[c] = rnd<T>(ld(e, i) + ld(step, i));
       }
     }
+    store_and_norm<T, NPER>(hv, h_in, h, a.norm_w ? a.norm_w + (int64_t)rd.pulse * D : nullptr,
+                      reinterpret_cast<T*>(a.xn) + (int64_t)r * D, D, a.eps, red);
     return;
   }
   // pulse >= 1
@@ -97,30 +123,57 @@ __global__ void __launch_bounds__(256) pulse_input_kernel(PulseInputArgs a) {
   const float inv = row_inv_rms(hp, D, a.eps, red);
   const int R = a.rank;
   const T* wd = reinterpret_cast<const T*>(a.reinject_down) + (int64_t)rd.pulse * R * 2 * D;
-  // g_hidden[j] = T(T(e . wd[j][:D]) + T(r . wd[j][D:]))
-  for (int j = 0; j < R; ++j) {
-    float se = 0.f, sr = 0.f;
-    for (int i = threadIdx.x; i < D; i += blockDim.x) {
-      const float rv = rnd<T>(ld(hp, i) * inv * a.state_norm[i]);
-      se += ld(e, i) * ld(wd, (int64_t)j * 2 * D + i);
-      sr += rv * ld(wd, (int64_t)j * 2 * D + D + i);
+  // g_hidden[j] = T(T(e . wd[j][:D]) + T(r . wd[j][D:])), all 2R partial sums in one pass
+  float pe[kMaxRank], pr[kMaxRank];
+#pragma unroll
+  for (int j = 0; j < kMaxRank; ++j) pe[j] = pr[j] = 0.f;
+#pragma unroll
+  for (int c = 0; c < NPER; ++c) {
+    const int i = threadIdx.x + c * 256;
+    const float ev = ld(e, i);
+    const float rv = rnd<T>(ld(hp, i) * inv * a.state_norm[i]);
+#pragma unroll
+    for (int j = 0; j < kMaxRank; ++j) {
+      if (j < R) {
+        pe[j] += ev * ld(wd, (int64_t)j * 2 * D + i);
+        pr[j] += rv * ld(wd, (int64_t)j * 2 * D + D + i);
+      }
     }
-    se = block_sum(se, red);
-    sr = block_sum(sr, red);
-    if (threadIdx.x == 0) gh[j] = rnd<T>(rnd<T>(se) + rnd<T>(sr));
+  }
+  __shared__ float gred[4][2 * kMaxRank];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < kMaxRank; ++j) {
+    if (j < R) {
+      const float x = wave_sum(pe[j]), y = wave_sum(pr[j]);
+      if (lane == 0) {
+        gred[wv][j] = x;
+        gred[wv][kMaxRank + j] = y;
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < R) {
+    const int j = threadIdx.x;
+    const float se = gred[0][j] + gred[1][j] + gred[2][j] + gred[3][j];
+    const float sr = gred[0][kMaxRank + j] + gred[1][kMaxRank + j] + gred[2][kMaxRank + j] +
+                     gred[3][kMaxRank + j];
+    gh[j] = rnd<T>(rnd<T>(se) + rnd<T>(sr));
   }
   __syncthreads();
   const T* wu = reinterpret_cast<const T*>(a.reinject_up) + (int64_t)rd.pulse * D * R;
   const T* bu = reinterpret_cast<const T*>(a.reinject_bias) + (int64_t)rd.pulse * D;
-  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+#pragma unroll
+  for (int c = 0; c < NPER; ++c) {
+    const int i = threadIdx.x + c * 256;
     float acc = 0.f;
     for (int j = 0; j < R; ++j) acc += gh[j] * ld(wu, (int64_t)i * R + j);
     const float mix = rnd<T>(sigmoidf_(rnd<T>(acc + ld(bu, i))));
     const float rv = rnd<T>(ld(hp, i) * inv * a.state_norm[i]);
-    const float hi = rnd<T>(rnd<T>(lerp_ref(rv, ld(e, i), mix)) + ld(step, i));
-    h_in[i] = from_f<T>(hi);
-    h[i] = from_f<T>(hi);
+    hv[c] = rnd<T>(rnd<T>(lerp_ref(rv, ld(e, i), mix)) + ld(step, i));
   }
+  store_and_norm<T, NPER>(hv, h_in, h, a.norm_w ? a.norm_w + (int64_t)rd.pulse * D : nullptr,
+                    reinterpret_cast<T*>(a.xn) + (int64_t)r * D, D, a.eps, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -237,13 +290,26 @@ __global__ void __launch_bounds__(256) qk_post_kernel(QKPostArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention, split over keys: block (row, kv head, split) handles 4 query heads
-// and up to 256 keys (64 per wave); writes (max, sum, acc[64]) partials per query head.
+// Decode attention, split over keys: block (row, kv head, split) serves the 4 query heads
+// of the group over up to 256 keys, 64 per wave. Lane l owns key group (l >> 3), i.e. keys
+// kbeg + (l >> 3) + 8i for i < 8, and dims 8*(l & 7) .. +8, so each K and V load is 128
+// contiguous bits and every 8 lanes read one 128-byte key row: the wave reads 1 KB of
+// contiguous cache per load instruction. Scores are reduced over the 8 lanes of a key
+// group, softmax statistics over the wave; partials (max, sum, acc[64]) per query head go
+// to `part` and the combine kernel merges the splits.
 // ---------------------------------------------------------------------------
 template <typename T>
+__device__ __forceinline__ void load8v(const T* p, float* o, bool valid) {
+  if (valid) {
+    load8(p, o);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = 0.f;
+  }
+}
+
+template <typename T>
 __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
-  __shared__ float qs[4][64];
-  __shared__ float ps[4][4][64];
   __shared__ float wm[4][4], wl[4][4];
   __shared__ float wacc[4][4][64];
   const int r = blockIdx.x;
@@ -256,72 +322,104 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   const int nsplit = (nkeys + kSplitLen - 1) / kSplitLen;
   if (s >= nsplit) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const T* q = reinterpret_cast<const T*>(a.qkv) + (int64_t)r * a.ldq + (g * 4) * 64;
-  qs[wv][lane] = ld(q, wv * 64 + lane);
-  __syncthreads();
+  const int kg = lane >> 3, dc = lane & 7;
+  // q of the 4 heads, this lane's 8 dims
+  const T* q = reinterpret_cast<const T*>(a.qkv) + (int64_t)r * a.ldq + (g * 4) * 64 + dc * 8;
+  float qv[4][8];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) load8(q + h * 64, qv[h]);
   const int kbeg = lo + s * kSplitLen + wv * 64;
-  const int key = kbeg + lane;
-  const bool valid = key <= pos;
   const T* Kc = reinterpret_cast<const T*>(a.kv.k[a.layer]);
   const T* Vc = reinterpret_cast<const T*>(a.kv.v[a.layer]);
-  float sc[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  if (valid) {
-    const T* kr = Kc + kv_offset(a.kv, a.layer, rd.seq, g, key);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float kf[8][8], vf[8][8];
+  bool valid[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      float kv[8];
-      load8(kr + c * 8, kv);
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-#pragma unroll
-        for (int h = 0; h < 4; ++h) acc[h] += qs[h][c * 8 + d] * kv[d];
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < 4; ++h) sc[h] = acc[h] * a.scale;
+  for (int i = 0; i < 8; ++i) {
+    const int key = kbeg + kg + 8 * i;
+    valid[i] = key <= pos;
+    const int64_t off = valid[i] ? kv_offset(a.kv, a.layer, rd.seq, g, key) + dc * 8 : 0;
+    load8v(Kc + off, kf[i], valid[i]);
+    load8v(Vc + off, vf[i], valid[i]);
   }
-  float m[4], l[4];
+  float sc[4][8];
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
-    m[h] = wave_max(sc[h]);
-    const float p = valid ? expf(sc[h] - m[h]) : 0.f;
-    l[h] = wave_sum(p);
-    ps[wv][h][lane] = p;
-  }
-  __syncthreads();
-  // P.V: lane = dim
-  float o[4] = {0.f, 0.f, 0.f, 0.f};
-  const int nk = min(64, pos - kbeg + 1);
-  for (int jj = 0; jj < nk; ++jj) {
-    const float vv = ld(Vc, kv_offset(a.kv, a.layer, rd.seq, g, kbeg + jj) + lane);
 #pragma unroll
-    for (int h = 0; h < 4; ++h) o[h] += ps[wv][h][jj] * vv;
+    for (int i = 0; i < 8; ++i) {
+      float acc = 0.f;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc += qv[h][d] * kf[i][d];
+      // sum the 8 dim chunks of this key
+      acc += __shfl_xor(acc, 1, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      acc += __shfl_xor(acc, 4, 64);
+      sc[h][i] = valid[i] ? acc * a.scale : -INFINITY;
+    }
+  }
+  float m[4], l[4], o[4][8];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sc[h][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    m[h] = mx;
+    float ls = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[h][d] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float p = valid[i] ? expf(sc[h][i] - mx) : 0.f;
+      ls += p;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) o[h][d] += p * vf[i][d];
+    }
+    // the 8 lanes of a key group hold the same scores: sum over key groups only
+    ls += __shfl_xor(ls, 8, 64);
+    ls += __shfl_xor(ls, 16, 64);
+    ls += __shfl_xor(ls, 32, 64);
+    l[h] = ls;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      float v = o[h][d];
+      v += __shfl_xor(v, 8, 64);
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      o[h][d] = v;
+    }
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) wacc[wv][h][dc * 8 + d] = o[h][d];
   }
   if (lane == 0) {
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      wm[wv][h] = nk > 0 ? m[h] : -INFINITY;
-      wl[wv][h] = nk > 0 ? l[h] : 0.f;
+      wm[wv][h] = m[h];
+      wl[wv][h] = l[h];
     }
   }
-#pragma unroll
-  for (int h = 0; h < 4; ++h) wacc[wv][h][lane] = o[h];
   __syncthreads();
-  // combine the 4 waves: wave wv finalises query head wv
-  const int h = wv;
+  // combine the 4 waves: thread (h = tid/64, d = tid%64)
+  const int h = wv, d = lane;
   float M = -INFINITY;
+#pragma unroll
   for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][h]);
   float L = 0.f, O = 0.f;
+#pragma unroll
   for (int w = 0; w < 4; ++w) {
     if (wm[w][h] == -INFINITY) continue;
     const float f = expf(wm[w][h] - M);
     L += wl[w][h] * f;
-    O += wacc[w][h][lane] * f;
+    O += wacc[w][h][d] * f;
   }
   float* out = a.part + ((((int64_t)r * a.Hkv + g) * a.max_splits + s) * 4 + h) * 66;
-  out[2 + lane] = O;
-  if (lane == 0) {
+  out[2 + d] = O;
+  if (d == 0) {
     out[0] = M;
     out[1] = L;
   }
@@ -478,6 +576,53 @@ __global__ void __launch_bounds__(256) router_decode_kernel(RouterArgs a) {
   route_topk<T>(lg, E, a.K, a.bias + (int64_t)pulse * E, r, a);
 }
 
+// mlp_norm + decode router in one pass over the residual row.
+template <typename T, int E, int NPER>
+__global__ void __launch_bounds__(256) norm_router_kernel(RouterArgs a) {
+  __shared__ float red[16];
+  __shared__ float part[4][E];
+  __shared__ float lg[32];
+  const int r = blockIdx.x;
+  if (r >= a.ctl->n_rows) return;
+  const int pulse = a.rows[r].pulse;
+  const int D = a.D;
+  const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)r * D;
+  const float* nw = a.norm_w + (int64_t)pulse * D;
+  const float* W = a.w + (int64_t)pulse * E * D;
+  float xv[NPER];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NPER; ++c) {
+    const int i = threadIdx.x + c * 256;
+    xv[c] = ld(x, i);
+    ss += xv[c] * xv[c];
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+  float acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  T* xn = reinterpret_cast<T*>(a.xn) + (int64_t)r * D;
+#pragma unroll
+  for (int c = 0; c < NPER; ++c) {
+    const int i = threadIdx.x + c * 256;
+    const float y = rnd<T>(nw[i] * (xv[c] * inv));
+    xn[i] = from_f<T>(y);
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] += y * W[(int64_t)e * D + i];
+  }
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float v = wave_sum(acc[e]);
+    if (lane == 0) part[wv][e] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  for (int e = 0; e < E; ++e) lg[e] = part[0][e] + part[1][e] + part[2][e] + part[3][e];
+  route_topk<T>(lg, E, a.K, a.bias + (int64_t)pulse * E, r, a);
+}
+
 // Prefill router: logits in the activation dtype with T-rounded weights.
 template <typename T>
 __global__ void __launch_bounds__(256) router_prefill_kernel(RouterArgs a) {
@@ -551,7 +696,7 @@ __global__ void prefill_slots_kernel(const int32_t* __restrict__ idx, const floa
 // decode: routed = sum_k T(out_k * w_k) in T, mlp = T(shared + T(routed * rs)), h += mlp.
 // prefill: routed = index_add of T(w_k * out_k) in T (dropped = 0), mlp = T(shared + routed).
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int NPER>
 __global__ void __launch_bounds__(256) moe_combine_rows_kernel(CombineArgs a) {
   const int r = blockIdx.x;
   const int n = a.ctl ? a.ctl->n_rows : a.m_fixed;
@@ -568,20 +713,26 @@ __global__ void __launch_bounds__(256) moe_combine_rows_kernel(CombineArgs a) {
   }
   const int pulse = a.ctl ? a.rows[r].pulse : a.pulse;
   const T* rs = reinterpret_cast<const T*>(a.routed_scale) + (int64_t)pulse * D;
-  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+  float hv[NPER];
+#pragma unroll
+  for (int c = 0; c < NPER; ++c) {
+    const int i = threadIdx.x + c * 256;
     float routed = 0.f, mlp;
     if (!a.prefill) {
       for (int k = 0; k < K; ++k) routed = rnd<T>(routed + rnd<T>(ld(ro, (int64_t)k * D + i) * w[k]));
       mlp = rnd<T>(ld(sh, i) + rnd<T>(routed * ld(rs, i)));
     } else {
       for (int k = 0; k < K; ++k) {
-        const float c = kept[k] ? rnd<T>(w[k] * ld(ro, (int64_t)k * D + i)) : 0.f;
-        routed = rnd<T>(routed + c);
+        const float cv = kept[k] ? rnd<T>(w[k] * ld(ro, (int64_t)k * D + i)) : 0.f;
+        routed = rnd<T>(routed + cv);
       }
       mlp = rnd<T>(ld(sh, i) + routed);
     }
-    h[i] = from_f<T>(ld(h, i) + mlp);
+    hv[c] = rnd<T>(ld(h, i) + mlp);
   }
+  __shared__ float red[16];
+  store_and_norm<T, NPER>(hv, (T*)nullptr, h, a.next_norm ? a.next_norm + (int64_t)pulse * D : nullptr,
+                    reinterpret_cast<T*>(a.xn) + (int64_t)r * D, D, a.eps, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -623,8 +774,32 @@ __global__ void __launch_bounds__(256) pulse_output_kernel(PulseOutputArgs a) {
     return PULSAR_OK;                                                         \
   } while (0)
 
+// Row kernels hold D/256 elements per thread in registers (D a multiple of 256, <= 2048).
+#define PULSAR_NPER_DISPATCH(D, KERNEL_T, grid, arg)                                         \
+  do {                                                                                       \
+    const int _nper = (D) / 256;                                                             \
+    if ((D) % 256 != 0 || _nper < 1 || _nper > kMaxPer)                                      \
+      return fail(PULSAR_ERR_UNSUPPORTED, "d_model must be a multiple of 256 up to 2048");   \
+    switch (_nper) {                                                                         \
+      case 1: KERNEL_T(1)<<<(grid), 256, 0, s>>>(arg); break;                                \
+      case 2: KERNEL_T(2)<<<(grid), 256, 0, s>>>(arg); break;                                \
+      case 4: KERNEL_T(4)<<<(grid), 256, 0, s>>>(arg); break;                                \
+      case 8: KERNEL_T(8)<<<(grid), 256, 0, s>>>(arg); break;                                \
+      default: return fail(PULSAR_ERR_UNSUPPORTED, "d_model/256 must be 1, 2, 4 or 8");      \
+    }                                                                                        \
+    PULSAR_LAUNCH_CHECK();                                                                   \
+    return PULSAR_OK;                                                                        \
+  } while (0)
+
 int launch_pulse_input(const PulseInputArgs& a, int dtype, int max_rows, hipStream_t s) {
-  PULSAR_DISPATCH(dtype, pulse_input_kernel, dim3(max_rows), 256, a);
+  if (dtype == PULSAR_BF16) {
+#define K_(N) pulse_input_kernel<bf16, N>
+    PULSAR_NPER_DISPATCH(a.D, K_, dim3(max_rows), a);
+#undef K_
+  }
+#define K_(N) pulse_input_kernel<float, N>
+  PULSAR_NPER_DISPATCH(a.D, K_, dim3(max_rows), a);
+#undef K_
 }
 int launch_norm_rows(const NormArgs& a, int dtype, int max_rows, hipStream_t s) {
   PULSAR_DISPATCH(dtype, norm_rows_kernel, dim3(max_rows), 256, a);
@@ -647,6 +822,28 @@ int launch_attn_prefill(const AttnArgs& a, int dtype, int B, hipStream_t s) {
 int launch_router_decode(const RouterArgs& a, int dtype, int max_rows, hipStream_t s) {
   PULSAR_DISPATCH(dtype, router_decode_kernel, dim3(max_rows), 256, a);
 }
+int launch_norm_router(const RouterArgs& a, int dtype, int max_rows, hipStream_t s) {
+  if (a.D > 256 * kMaxPer) return fail(PULSAR_ERR_UNSUPPORTED, "norm_router: d_model > 2048");
+#define PULSAR_NR_CASE(EV)                                                  \
+  if (a.E == EV) {                                                          \
+    if (dtype == PULSAR_BF16) {                                             \
+      PULSAR_NPER_DISPATCH(a.D, K_BF16_##EV, dim3(max_rows), a);            \
+    }                                                                       \
+    PULSAR_NPER_DISPATCH(a.D, K_F32_##EV, dim3(max_rows), a);               \
+  }
+#define K_BF16_16(N) norm_router_kernel<bf16, 16, N>
+#define K_F32_16(N) norm_router_kernel<float, 16, N>
+#define K_BF16_8(N) norm_router_kernel<bf16, 8, N>
+#define K_F32_8(N) norm_router_kernel<float, 8, N>
+  PULSAR_NR_CASE(16)
+  PULSAR_NR_CASE(8)
+#undef K_BF16_16
+#undef K_F32_16
+#undef K_BF16_8
+#undef K_F32_8
+#undef PULSAR_NR_CASE
+  return fail(PULSAR_ERR_UNSUPPORTED, "norm_router: n_experts must be 8 or 16");
+}
 int launch_router_prefill(const RouterArgs& a, int dtype, hipStream_t s) {
   PULSAR_DISPATCH(dtype, router_prefill_kernel, dim3(a.m_fixed), 256, a);
 }
@@ -663,7 +860,14 @@ int launch_prefill_capacity(const int32_t* idx, const float* w, int32_t* cnt, in
   return PULSAR_OK;
 }
 int launch_moe_combine(const CombineArgs& a, int dtype, int max_rows, hipStream_t s) {
-  PULSAR_DISPATCH(dtype, moe_combine_rows_kernel, dim3(max_rows), 256, a);
+  if (dtype == PULSAR_BF16) {
+#define K_(N) moe_combine_rows_kernel<bf16, N>
+    PULSAR_NPER_DISPATCH(a.D, K_, dim3(max_rows), a);
+#undef K_
+  }
+#define K_(N) moe_combine_rows_kernel<float, N>
+  PULSAR_NPER_DISPATCH(a.D, K_, dim3(max_rows), a);
+#undef K_
 }
 int launch_pulse_output(const PulseOutputArgs& a, int dtype, int max_rows, hipStream_t s) {
   PULSAR_DISPATCH(dtype, pulse_output_kernel, dim3(max_rows), 256, a);

@@ -35,6 +35,8 @@ struct SampleArgs {
 
 struct ControllerArgs {
   StepCtl* ctl;
+  StepCtl* last_ctl;    // snapshot of the control block of the step that ran
+  RowDesc* last_rows;   // snapshot of its rows
   SeqState* state;
   RowDesc* rows;
   int32_t* lrow_seq;

@@ -250,18 +250,110 @@ __device__ void fresh(SeqState& s, int tok) {
 
 }  // namespace
 
-__global__ void controller_kernel(ControllerArgs a) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// Advance one sequence's state after the step whose rows it ran.
+__device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
+  const int P = a.n_pulses;
+  s.ctr += 1;
+  const int pulse_ran = s.c_pulse;
+  if (pulse_ran < P - 1) {
+    if (pulse_ran == 0 && a.speculative) {
+      const int lr = s.lrow_c;
+      if (s.c_kind == KIND_TESTED) {
+        s.d_tok = a.draw[lr * 2];
+        s.s_valid = !is_stop(a, s.d_tok);
+        s.s_tok = s.d_tok;
+      } else {
+        const int g = a.argmax[lr];
+        s.s_valid = !is_stop(a, g);
+        s.s_tok = g;
+      }
+    }
+    s.c_pulse = pulse_ran + 1;
+    return;
+  }
+  const int lr = s.lrow_c;
+  const bool s_ran = s.row_s >= 0;
+  if (a.speculative && s.c_kind == KIND_TESTED) {
+    const int v = a.draw[lr * 2];
+    s.tests += 1;
+    if (s.d_tok == v && !is_stop(a, s.d_tok)) {
+      s.accepted += 1;
+      emit(a, s, b, s.d_tok);
+      if (!s.done) promote(a, s, KIND_PLAIN);
+    } else {
+      const int t = a.draw[lr * 2 + 1];
+      if (is_stop(a, t)) {
+        s.done = 1;
+      } else {
+        emit(a, s, b, t);
+        if (!s.done) {
+          if (s_ran && s.s_tok == t)
+            promote(a, s, KIND_TESTED);
+          else
+            fresh(s, t);
+        }
+      }
+    }
+  } else {
+    const int t = a.draw[lr * 2];
+    if (is_stop(a, t)) {
+      s.done = 1;
+    } else {
+      emit(a, s, b, t);
+      if (!s.done) {
+        if (a.speculative && s_ran && s.s_tok == t)
+          promote(a, s, KIND_TESTED);
+        else
+          fresh(s, t);
+      }
+    }
+  }
+}
+
+// Exclusive scan of 4 counters over the block (blockDim 256) in LDS.
+__device__ void scan4(int* v, int* sh, int* total) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) sh[k * 256 + t] = v[k];
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    int add[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) add[k] = t >= off ? sh[k * 256 + t - off] : 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sh[k * 256 + t] += add[k];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    total[k] = sh[k * 256 + 255];
+    v[k] = sh[k * 256 + t] - v[k];
+  }
+  __syncthreads();
+}
+
+// One thread per sequence: advance the state, then lay out the next step's rows grouped by
+// pulse (sequence order within a pulse) and its logits rows. Also snapshots the rows and
+// control block of the step that just ran (readable for testing).
+__global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
+  __shared__ int sh[4 * 256];
+  const int b = threadIdx.x;
   StepCtl* ctl = a.ctl;
   const int P = a.n_pulses;
-  for (int b = 0; b < a.B; ++b) {
-    SeqState s = a.state[b];
+  const int n_prev = ctl->n_rows;
+  for (int i = b; i < n_prev; i += blockDim.x) a.last_rows[i] = a.rows[i];
+  if (b == 0) *a.last_ctl = *ctl;
+  __syncthreads();
+  const bool act = b < a.B;
+  SeqState s{};
+  if (act) {
+    s = a.state[b];
     if (a.init) {
       s = SeqState{};
       s.max_new = a.max_new;
       s.c_pos = a.prompt_len - 1;
       s.c_slot = 1;
-      s.row_c = s.row_s = s.lrow_c = s.lrow_s = -1;
       const int t = a.draw[b * 2];
       if (is_stop(a, t) || s.max_new <= 0) {
         s.done = 1;
@@ -269,104 +361,59 @@ __global__ void controller_kernel(ControllerArgs a) {
         emit(a, s, b, t);
         fresh(s, t);
       }
-      a.state[b] = s;
-      continue;
+    } else if (!s.done) {
+      update_seq(a, s, b);
     }
-    if (s.done) continue;
-    s.ctr += 1;
-    const int pulse_ran = s.c_pulse;
-    if (pulse_ran < P - 1) {
-      if (pulse_ran == 0 && a.speculative) {
-        const int lr = s.lrow_c;
-        if (s.c_kind == KIND_TESTED) {
-          s.d_tok = a.draw[lr * 2];
-          s.s_valid = !is_stop(a, s.d_tok);
-          s.s_tok = s.d_tok;
-        } else {
-          const int g = a.argmax[lr];
-          s.s_valid = !is_stop(a, g);
-          s.s_tok = g;
-        }
-      }
-      s.c_pulse = pulse_ran + 1;
-    } else {
-      const int lr = s.lrow_c;
-      const bool s_ran = s.row_s >= 0;
-      if (a.speculative && s.c_kind == KIND_TESTED) {
-        const int v = a.draw[lr * 2];
-        s.tests += 1;
-        if (s.d_tok == v && !is_stop(a, s.d_tok)) {
-          s.accepted += 1;
-          emit(a, s, b, s.d_tok);
-          if (!s.done) promote(a, s, KIND_PLAIN);
-        } else {
-          const int t = a.draw[lr * 2 + 1];
-          if (is_stop(a, t)) {
-            s.done = 1;
-          } else {
-            emit(a, s, b, t);
-            if (!s.done) {
-              if (s_ran && s.s_tok == t)
-                promote(a, s, KIND_TESTED);
-              else
-                fresh(s, t);
-            }
-          }
-        }
-      } else {
-        const int t = a.draw[lr * 2];
-        if (is_stop(a, t)) {
-          s.done = 1;
-        } else {
-          emit(a, s, b, t);
-          if (!s.done) {
-            if (a.speculative && s_ran && s.s_tok == t)
-              promote(a, s, KIND_TESTED);
-            else
-              fresh(s, t);
-          }
-        }
-      }
-    }
-    a.state[b] = s;
   }
-  // Next step's rows, grouped by pulse.
-  int n = 0, nl = 0, active = 0;
-  for (int p = 0; p < P; ++p) {
-    ctl->pulse_start[p] = n;
-    for (int b = 0; b < a.B; ++b) {
-      SeqState& s = a.state[b];
-      if (p == 0) {
-        s.row_c = s.row_s = s.lrow_c = s.lrow_s = -1;
-        if (!s.done) ++active;
-      }
-      if (s.done) continue;
-      if (s.c_pulse == p) {
-        const bool want = a.all_logits || s.c_pulse == P - 1 || (a.speculative && s.c_pulse == 0);
-        RowDesc r{b, s.c_slot, p, s.c_pos, s.c_tok, want ? nl : -1, -1, 0};
-        if (want) {
-          a.lrow_seq[nl] = b;
-          a.lrow_extra[nl] = -1;
-          s.lrow_c = nl++;
-        }
-        s.row_c = n;
-        a.rows[n++] = r;
-      }
-      if (p == 0 && a.speculative && s.c_pulse == P - 1 && s.s_valid) {
-        RowDesc r{b, 1 - s.c_slot, 0, s.c_pos + 1, s.s_tok, nl, s.s_tok, 0};
-        a.lrow_seq[nl] = b;
-        a.lrow_extra[nl] = s.s_tok;
-        s.lrow_s = nl++;
-        s.row_s = n;
-        a.rows[n++] = r;
-      }
-    }
-    ctl->pulse_count[p] = n - ctl->pulse_start[p];
+  // rows of the next step
+  const bool live = act && !s.done;
+  const bool crow = live;
+  const bool srow = live && a.speculative && s.c_pulse == P - 1 && s.s_valid;
+  const bool cwant = crow && (a.all_logits || s.c_pulse == P - 1 || (a.speculative && s.c_pulse == 0));
+  int v[4] = {0, 0, 0, 0};  // rows of pulse 0, 1, 2; logits rows
+  if (crow) v[s.c_pulse] += 1;
+  if (srow) v[0] += 1;
+  v[3] = (cwant ? 1 : 0) + (srow ? 1 : 0);
+  int total[4];
+  scan4(v, sh, total);
+  int base[4] = {0, total[0], total[0] + total[1], 0};
+  int lr = v[3];
+  s.row_c = s.row_s = s.lrow_c = s.lrow_s = -1;
+  if (srow) {
+    const int idx = base[0] + v[0];
+    s.lrow_s = lr++;
+    a.lrow_seq[s.lrow_s] = b;
+    a.lrow_extra[s.lrow_s] = s.s_tok;
+    a.rows[idx] = RowDesc{b, 1 - s.c_slot, 0, s.c_pos + 1, s.s_tok, s.lrow_s, s.s_tok, 0};
+    s.row_s = idx;
   }
-  ctl->n_rows = n;
-  ctl->n_lrows = nl;
-  ctl->active = active;
-  ctl->step += 1;
+  if (crow) {
+    const int p = s.c_pulse;
+    const int idx = base[p] + v[p] + ((p == 0 && srow) ? 1 : 0);
+    if (cwant) {
+      s.lrow_c = lr++;
+      a.lrow_seq[s.lrow_c] = b;
+      a.lrow_extra[s.lrow_c] = -1;
+    }
+    a.rows[idx] = RowDesc{b, s.c_slot, p, s.c_pos, s.c_tok, s.lrow_c, -1, 0};
+    s.row_c = idx;
+  }
+  if (act) a.state[b] = s;
+  int nact = live ? 1 : 0;
+  sh[b] = nact;  // scan4 left sh free after its final barrier
+  __syncthreads();
+  if (b == 0) {
+    int tot = 0;
+    for (int i = 0; i < blockDim.x; ++i) tot += sh[i];
+    for (int p = 0; p < 4; ++p) {
+      ctl->pulse_start[p] = p < 3 ? base[p] : total[0] + total[1] + total[2];
+      ctl->pulse_count[p] = p < 3 ? total[p] : 0;
+    }
+    ctl->n_rows = total[0] + total[1] + total[2];
+    ctl->n_lrows = total[3];
+    ctl->active = tot;
+    ctl->step += 1;
+  }
 }
 
 int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s) {
@@ -395,7 +442,8 @@ int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s) 
 }
 
 int launch_controller(const ControllerArgs& a, hipStream_t s) {
-  controller_kernel<<<1, 64, 0, s>>>(a);
+  if (a.B > 256) return fail(PULSAR_ERR_UNSUPPORTED, "controller: at most 256 sequences");
+  controller_kernel<<<1, 256, 0, s>>>(a);
   PULSAR_LAUNCH_CHECK();
   return PULSAR_OK;
 }
