@@ -54,16 +54,98 @@ __device__ __forceinline__ float rnd(float v) { return to_f<T>(from_f<T>(v)); }
 
 constexpr int kWave = 64;
 
+// Lane exchange through DPP (quad permutes and row rotations stay in the VALU).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float swz_xor16(float v) {  // lane ^ 16 within each 32-lane half
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+}
+__device__ __forceinline__ float lane_bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Wave64 all-reduce. The partial sums of the 16-lane rows differ in association from lane
+// to lane, so the result is taken from lanes 0 and 32 and broadcast: every lane returns
+// the identical value.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x124>(v);  // row_ror:4
+  v += dpp_mov<0x128>(v);  // row_ror:8
+  v += swz_xor16(v);
+  return lane_bcast(v, 0) + lane_bcast(v, 32);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x124>(v));
+  v = fmaxf(v, dpp_mov<0x128>(v));
+  v = fmaxf(v, swz_xor16(v));
+  return fmaxf(lane_bcast(v, 0), lane_bcast(v, 32));
+}
+
+// Sum over the 16 lanes of each DPP row (lanes 16q..16q+15), broadcast from the row's
+// first lane.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x124>(v);
+  v += dpp_mov<0x128>(v);
+  return __shfl(v, threadIdx.x & 0x30, kWave);
+}
+
+// N contiguous elements (N a multiple of 4) to float, with the widest loads that fit.
+template <int N>
+__device__ __forceinline__ void ldv(const float* p, float* o) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+  for (int i = 0; i < N; i += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p + i);
+    o[i] = v.x; o[i + 1] = v.y; o[i + 2] = v.z; o[i + 3] = v.w;
+  }
+}
+template <int N>
+__device__ __forceinline__ void ldv(const bf16* p, float* o) {
+  if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 8) {
+      const uint4 u = *reinterpret_cast<const uint4*>(p + i);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[i + 2 * j] = __uint_as_float(w[j] << 16);
+        o[i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const uint2 u = *reinterpret_cast<const uint2*>(p + i);
+      o[i] = __uint_as_float(u.x << 16);
+      o[i + 1] = __uint_as_float(u.x & 0xffff0000u);
+      o[i + 2] = __uint_as_float(u.y << 16);
+      o[i + 3] = __uint_as_float(u.y & 0xffff0000u);
+    }
+  }
+}
+// Store N contiguous values (already representable in the storage type).
+template <int N>
+__device__ __forceinline__ void stv(float* p, const float* v) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4)
+    *reinterpret_cast<float4*>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+}
+template <int N>
+__device__ __forceinline__ void stv(bf16* p, const float* v) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    uint2 u;
+    u.x = (uint32_t)f2bf(v[i]).u | ((uint32_t)f2bf(v[i + 1]).u << 16);
+    u.y = (uint32_t)f2bf(v[i + 2]).u | ((uint32_t)f2bf(v[i + 3]).u << 16);
+    *reinterpret_cast<uint2*>(p + i) = u;
+  }
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` needs 16 floats.

@@ -30,7 +30,17 @@ struct StepCtl {
   int32_t pulse_count[4];
   int32_t active;      // sequences not finished
   int32_t step;        // step counter
-  int32_t pad[4];
+  int32_t n_units;     // decode attention units (sequences with rows in the step)
+  int32_t pad[3];
+};
+
+// Decode attention work unit: the rows of one sequence in a step that read the same cache
+// (the current token and, when present, the speculative token one position later).
+struct AttnUnit {
+  int32_t seq;
+  int32_t row_a, row_b;  // row_b = -1 when the unit has one row
+  int32_t pos_a, pos_b;
+  int32_t pad[3];
 };
 
 // GEMM epilogues.

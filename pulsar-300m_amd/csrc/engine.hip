@@ -25,6 +25,7 @@ struct Engine {
   StepCtl* last_ctl = nullptr;
   RowDesc* rows = nullptr;
   RowDesc* last_rows = nullptr;
+  AttnUnit* units = nullptr;
   SeqState* state = nullptr;
   int32_t *lrow_seq = nullptr, *lrow_extra = nullptr, *argmax = nullptr, *draw = nullptr;
   int32_t *tokens = nullptr, *stop_ids = nullptr;
@@ -194,14 +195,16 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   e->max_pages = (c.max_ctx + kPage - 1) / kPage;
   // ring capacity: the prompt's last `window` positions stay intact while max_new tokens
   // (+1 speculative) are appended, so a rewound decode sees the prefill state unchanged
-  e->lcap = m.window + c.max_new + kPage;
-  e->max_splits = (c.max_ctx + kSplitLen - 1) / kSplitLen;
+  e->lcap = (m.window + c.max_new + 2 * kPage - 1) / kPage * kPage;
+  // decode splits start at a 64-aligned position at most 63 keys before the first key
+  e->max_splits = (c.max_ctx + kPage - 1 + kSplitLen - 1) / kSplitLen;
   const size_t es = e->es, D = e->D, R = e->R, MR = e->max_rows;
   Engine& x = *e;
   PULSAR_TRY(x.alloc(&x.ctl, sizeof(StepCtl)));
   PULSAR_TRY(x.alloc(&x.last_ctl, sizeof(StepCtl)));
   PULSAR_TRY(x.alloc(&x.rows, sizeof(RowDesc) * MR));
   PULSAR_TRY(x.alloc(&x.last_rows, sizeof(RowDesc) * MR));
+  PULSAR_TRY(x.alloc(&x.units, sizeof(AttnUnit) * x.B));
   PULSAR_TRY(x.alloc(&x.state, sizeof(SeqState) * x.B));
   PULSAR_TRY(x.alloc(&x.lrow_seq, 4 * MR));
   PULSAR_TRY(x.alloc(&x.lrow_extra, 4 * MR));
@@ -248,6 +251,10 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
     const size_t n = loc ? local_elems : global_elems;
     PULSAR_TRY(x.alloc(&x.kv.k[l], es * n));
     PULSAR_TRY(x.alloc(&x.kv.v[l], es * n));
+    // never-written positions are read (masked) by the block-wise decode attention: keep
+    // them finite
+    PULSAR_CHECK_HIP(hipMemset(x.kv.k[l], 0, es * n));
+    PULSAR_CHECK_HIP(hipMemset(x.kv.v[l], 0, es * n));
   }
   std::vector<int32_t> pt((size_t)x.B * x.max_pages);
   for (size_t i = 0; i < pt.size(); ++i) pt[i] = (int32_t)i;  // sequence b owns pages [b*mp, (b+1)*mp)
@@ -351,6 +358,8 @@ int enqueue_step(Engine& e, hipStream_t s) {
     aa.ldq = e.qkv;
     aa.gate = e.gate;
     aa.out = e.attn_out;
+    aa.units = e.units;
+    aa.max_units = e.B;
     aa.part = e.part;
     aa.max_splits = e.max_splits;
     aa.H = e.H;
@@ -524,6 +533,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   co.ctl = e.ctl;
   co.state = e.state;
   co.rows = e.rows;
+  co.units = e.units;
   co.lrow_seq = e.lrow_seq;
   co.lrow_extra = e.lrow_extra;
   co.seen = e.seen;
@@ -580,6 +590,7 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   co.ctl = e.ctl;
   co.state = e.state;
   co.rows = e.rows;
+  co.units = e.units;
   co.lrow_seq = e.lrow_seq;
   co.lrow_extra = e.lrow_extra;
   co.seen = e.seen;

@@ -6,12 +6,15 @@
 namespace pulsar {
 
 constexpr int kSplitLen = 256;  // keys per decode-attention block
-constexpr int kMaxPer = 8;      // row elements per thread of a 256-thread block (D <= 2048)
 constexpr int kMaxRank = 16;    // re-injection gate rank bound
 
 // KV cache addressing. Local (sliding-window) layers: a per-sequence ring of `lcap`
-// positions, [B][Hkv][lcap][64]. Global layers: pages of 64 positions from a shared pool,
-// [n_pages][Hkv][64][64], located through page_table[b][pos / 64].
+// positions (a multiple of 64). Global layers: pages of 64 positions from a shared pool,
+// located through page_table[b][pos / 64]. K is stored position-major ([..][pos][64]);
+// V is stored transposed, dimension-major ([..][64][pos]), so that the keys of one
+// dimension are contiguous: the layout the P.V matrix-core operand reads.
+//   local  K: [B][Hkv][lcap][64]        V: [B][Hkv][64][lcap]
+//   global K: [pages][Hkv][64 pos][64]  V: [pages][Hkv][64][64 pos]
 struct KVDesc {
   void* k[kMaxLayers];
   void* v[kMaxLayers];
@@ -22,12 +25,50 @@ struct KVDesc {
   int max_pages;
 };
 
+__device__ __forceinline__ bool kv_is_local(const KVDesc& c, int layer) {
+  return (c.local_mask >> layer) & 1u;
+}
+
+// K element (pos, 0).
 __device__ __forceinline__ int64_t kv_offset(const KVDesc& c, int layer, int b, int g, int pos) {
-  if ((c.local_mask >> layer) & 1u) {
+  if (kv_is_local(c, layer)) {
     return (((int64_t)b * c.Hkv + g) * c.lcap + (pos % c.lcap)) * kHeadDim;
   }
   const int page = c.page_table[(int64_t)b * c.max_pages + pos / kPage];
   return (((int64_t)page * c.Hkv + g) * kPage + (pos % kPage)) * kHeadDim;
+}
+
+// V element (pos, dim).
+__device__ __forceinline__ int64_t kv_offset_v(const KVDesc& c, int layer, int b, int g, int pos,
+                                               int dim) {
+  if (kv_is_local(c, layer)) {
+    return (((int64_t)b * c.Hkv + g) * kHeadDim + dim) * c.lcap + (pos % c.lcap);
+  }
+  const int page = c.page_table[(int64_t)b * c.max_pages + pos / kPage];
+  return (((int64_t)page * c.Hkv + g) * kHeadDim + dim) * kPage + (pos % kPage);
+}
+
+// A 64-aligned block of 64 positions starting at kb is contiguous in both caches:
+// K(kb + i, d) = k0 + i*64 + d and V(kb + i, d) = v0 + d*vstride + i.
+struct KVBlock {
+  int64_t k0, v0;
+  int vstride;
+};
+__device__ __forceinline__ KVBlock kv_block(const KVDesc& c, int layer, int b, int g, int kb) {
+  KVBlock r;
+  if (kv_is_local(c, layer)) {
+    const int64_t bg = (int64_t)b * c.Hkv + g;
+    const int ring = kb % c.lcap;
+    r.k0 = (bg * c.lcap + ring) * kHeadDim;
+    r.v0 = bg * kHeadDim * c.lcap + ring;
+    r.vstride = c.lcap;
+  } else {
+    const int64_t pg = (int64_t)c.page_table[(int64_t)b * c.max_pages + kb / kPage] * c.Hkv + g;
+    r.k0 = pg * kPage * kHeadDim;
+    r.v0 = pg * kHeadDim * kPage;
+    r.vstride = kPage;
+  }
+  return r;
 }
 
 struct PulseInputArgs {
@@ -86,12 +127,14 @@ struct QKPostArgs {
 struct AttnArgs {
   const StepCtl* ctl;
   const RowDesc* rows;
+  const AttnUnit* units;  // decode, matrix-core path: units of the step (ctl->n_units)
   const void* qkv;
   int64_t ldq;
   const void* gate;  // [rows][H] T
   void* out;         // [rows][H*64] T
   float* part;       // decode split partials
   int max_splits;
+  int max_units;
   int H, Hkv, layer, is_local, window, prefill_T;
   float scale;
   KVDesc kv;

@@ -44,29 +44,6 @@ __device__ float row_inv_rms(const T* x, int D, float eps, float* red) {
   return 1.0f / sqrtf(ss / (float)D + eps);
 }
 
-// Store a row held as hv[c] (element threadIdx.x + 256c) into h_in and h, and, when w is
-// given, its RMSNorm T(w * (h * inv)) into xn.
-template <typename T, int NPER>
-__device__ void store_and_norm(const float* hv, T* h_in, T* h, const float* w, T* xn, int D,
-                               float eps, float* red) {
-  float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < NPER; ++c) {
-    const int i = threadIdx.x + c * 256;
-    if (h_in) h_in[i] = from_f<T>(hv[c]);
-    h[i] = from_f<T>(hv[c]);
-    ss += hv[c] * hv[c];
-  }
-  if (!w) return;
-  ss = block_sum(ss, red);
-  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-#pragma unroll
-  for (int c = 0; c < NPER; ++c) {
-    const int i = threadIdx.x + c * 256;
-    xn[i] = from_f<T>(w[i] * (hv[c] * inv));
-  }
-}
-
 __device__ __forceinline__ float lerp_ref(float s, float e, float w) {
   // torch.lerp: start + w*(end-start) for |w| < 0.5, else end - (end-start)*(1-w)
   return fabsf(w) < 0.5f ? s + w * (e - s) : e - (e - s) * (1.0f - w);
@@ -78,102 +55,113 @@ __device__ __forceinline__ float lerp_ref(float s, float e, float w) {
 // Pulse input. pulse 0: stem (decode: embed, anchor norm, conv over one token) + step
 // embedding. pulse >= 1: rank-r re-injection gate on (anchor, state-normed previous pulse).
 // ---------------------------------------------------------------------------
-template <typename T, int NPER>
-__global__ void __launch_bounds__(256) pulse_input_kernel(PulseInputArgs a) {
-  __shared__ float red[16];
-  __shared__ float gh[16];
+template <typename T, int EPL, int RT>
+__global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
+  // one wave per row; lane owns elements [lane*EPL, lane*EPL + EPL)
+  const int lane = threadIdx.x;
   if (blockIdx.x == 0 && a.zero_counts) {
-    for (int i = threadIdx.x; i < a.n_zero; i += blockDim.x) a.zero_counts[i] = 0;
+    for (int i = lane; i < a.n_zero; i += 64) a.zero_counts[i] = 0;
   }
   const int r = blockIdx.x;
   if (r >= a.ctl->n_rows) return;
   const RowDesc rd = a.rows[r];
-  const int D = a.D;
+  const int D = a.D, i0 = lane * EPL;
   const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * 2 + rd.slot;
   T* e = reinterpret_cast<T*>(a.e_state) + (int64_t)st * D;
-  T* h_in = reinterpret_cast<T*>(a.h_in) + (int64_t)r * D;
-  T* h = reinterpret_cast<T*>(a.h) + (int64_t)r * D;
   const T* step = reinterpret_cast<const T*>(a.step_emb) + (int64_t)rd.pulse * D;
-  float hv[NPER];
+  float hv[EPL], stp[EPL];
+  ldv<EPL>(step + i0, stp);
   if (rd.pulse == 0) {
     if (!a.prefill) {
       const T* x0 = reinterpret_cast<const T*>(a.tok_emb) + (int64_t)rd.token * D;
-      const float inv = row_inv_rms(x0, D, a.eps, red);
+      float x[EPL], an[EPL];
+      ldv<EPL>(x0 + i0, x);
+      ldv<EPL>(a.anchor_norm + i0, an);
+      float ss = 0.f;
 #pragma unroll
-      for (int c = 0; c < NPER; ++c) {
-        const int i = threadIdx.x + c * 256;
-        float v = rnd<T>(ld(x0, i) * inv * a.anchor_norm[i]);
-        if (a.conv_w) v = rnd<T>(v + a.conv_w[i * 4] * v);
-        e[i] = from_f<T>(v);
-        hv[c] = rnd<T>(v + ld(step, i));
+      for (int c = 0; c < EPL; ++c) ss += x[c] * x[c];
+      const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
+      float ev[EPL];
+#pragma unroll
+      for (int c = 0; c < EPL; ++c) {
+        float v = rnd<T>(x[c] * inv * an[c]);
+        if (a.conv_w) v = rnd<T>(v + a.conv_w[(i0 + c) * 4] * v);
+        ev[c] = v;
+        hv[c] = rnd<T>(v + stp[c]);
       }
+      stv<EPL>(e + i0, ev);
     } else {
+      float ev[EPL];
+      ldv<EPL>(e + i0, ev);
 #pragma unroll
-      for (int c = 0; c < NPER; ++c) {
-        const int i = threadIdx.x + c * 256;
-        hv[c] = rnd<T>(ld(e, i) + ld(step, i));
-      }
+      for (int c = 0; c < EPL; ++c) hv[c] = rnd<T>(ev[c] + stp[c]);
     }
-    store_and_norm<T, NPER>(hv, h_in, h, a.norm_w ? a.norm_w + (int64_t)rd.pulse * D : nullptr,
-                      reinterpret_cast<T*>(a.xn) + (int64_t)r * D, D, a.eps, red);
-    return;
-  }
-  // pulse >= 1
-  const T* hp = reinterpret_cast<const T*>(a.hout_state) + (int64_t)st * D;
-  const float inv = row_inv_rms(hp, D, a.eps, red);
-  const int R = a.rank;
-  const T* wd = reinterpret_cast<const T*>(a.reinject_down) + (int64_t)rd.pulse * R * 2 * D;
-  // g_hidden[j] = T(T(e . wd[j][:D]) + T(r . wd[j][D:])), all 2R partial sums in one pass
-  float pe[kMaxRank], pr[kMaxRank];
+  } else {
+    // rank-R re-injection: g = T(T(e . wd[j][:D]) + T(r . wd[j][D:])), mix = sigmoid(up g + b)
+    const T* hp = reinterpret_cast<const T*>(a.hout_state) + (int64_t)st * D;
+    const int R = a.rank;
+    const T* wd = reinterpret_cast<const T*>(a.reinject_down) + (int64_t)rd.pulse * R * 2 * D;
+    const T* wu = reinterpret_cast<const T*>(a.reinject_up) + (int64_t)rd.pulse * D * R;
+    const T* bu = reinterpret_cast<const T*>(a.reinject_bias) + (int64_t)rd.pulse * D;
+    float ev[EPL], hpv[EPL], sn[EPL], bv[EPL];
+    ldv<EPL>(e + i0, ev);
+    ldv<EPL>(hp + i0, hpv);
+    ldv<EPL>(a.state_norm + i0, sn);
+    ldv<EPL>(bu + i0, bv);
+    float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxRank; ++j) pe[j] = pr[j] = 0.f;
+    for (int c = 0; c < EPL; ++c) ss += hpv[c] * hpv[c];
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
+    float rv[EPL];
 #pragma unroll
-  for (int c = 0; c < NPER; ++c) {
-    const int i = threadIdx.x + c * 256;
-    const float ev = ld(e, i);
-    const float rv = rnd<T>(ld(hp, i) * inv * a.state_norm[i]);
+    for (int c = 0; c < EPL; ++c) rv[c] = rnd<T>(hpv[c] * inv * sn[c]);
+    float gh[RT];
 #pragma unroll
-    for (int j = 0; j < kMaxRank; ++j) {
-      if (j < R) {
-        pe[j] += ev * ld(wd, (int64_t)j * 2 * D + i);
-        pr[j] += rv * ld(wd, (int64_t)j * 2 * D + D + i);
+    for (int j = 0; j < RT; ++j) {
+      const int jj = j < R ? j : 0;  // ranks past R load rank 0 and are dropped
+      float we[EPL], wr[EPL];
+      ldv<EPL>(wd + (int64_t)jj * 2 * D + i0, we);
+      ldv<EPL>(wd + (int64_t)jj * 2 * D + D + i0, wr);
+      float pe = 0.f, pr = 0.f;
+#pragma unroll
+      for (int c = 0; c < EPL; ++c) {
+        pe += ev[c] * we[c];
+        pr += rv[c] * wr[c];
       }
+      gh[j] = 0.f;
+      if (j < R) gh[j] = rnd<T>(rnd<T>(wave_sum(pe)) + rnd<T>(wave_sum(pr)));
+    }
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) {
+      float wv[RT];
+      if (R == RT) {
+        ldv<RT>(wu + (int64_t)(i0 + c) * RT, wv);
+      } else {
+#pragma unroll
+        for (int j = 0; j < RT; ++j) wv[j] = j < R ? ld(wu, (int64_t)(i0 + c) * R + j) : 0.f;
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < RT; ++j)
+        if (j < R) acc += gh[j] * wv[j];
+      const float mix = rnd<T>(sigmoidf_(rnd<T>(acc + bv[c])));
+      hv[c] = rnd<T>(rnd<T>(lerp_ref(rv[c], ev[c], mix)) + stp[c]);
     }
   }
-  __shared__ float gred[4][2 * kMaxRank];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  T* h_in = reinterpret_cast<T*>(a.h_in) + (int64_t)r * D;
+  T* h = reinterpret_cast<T*>(a.h) + (int64_t)r * D;
+  stv<EPL>(h_in + i0, hv);
+  stv<EPL>(h + i0, hv);
+  if (a.norm_w) {
+    float ss = 0.f, w[EPL], y[EPL];
 #pragma unroll
-  for (int j = 0; j < kMaxRank; ++j) {
-    if (j < R) {
-      const float x = wave_sum(pe[j]), y = wave_sum(pr[j]);
-      if (lane == 0) {
-        gred[wv][j] = x;
-        gred[wv][kMaxRank + j] = y;
-      }
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < R) {
-    const int j = threadIdx.x;
-    const float se = gred[0][j] + gred[1][j] + gred[2][j] + gred[3][j];
-    const float sr = gred[0][kMaxRank + j] + gred[1][kMaxRank + j] + gred[2][kMaxRank + j] +
-                     gred[3][kMaxRank + j];
-    gh[j] = rnd<T>(rnd<T>(se) + rnd<T>(sr));
-  }
-  __syncthreads();
-  const T* wu = reinterpret_cast<const T*>(a.reinject_up) + (int64_t)rd.pulse * D * R;
-  const T* bu = reinterpret_cast<const T*>(a.reinject_bias) + (int64_t)rd.pulse * D;
+    for (int c = 0; c < EPL; ++c) ss += hv[c] * hv[c];
+    ldv<EPL>(a.norm_w + (int64_t)rd.pulse * D + i0, w);
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
 #pragma unroll
-  for (int c = 0; c < NPER; ++c) {
-    const int i = threadIdx.x + c * 256;
-    float acc = 0.f;
-    for (int j = 0; j < R; ++j) acc += gh[j] * ld(wu, (int64_t)i * R + j);
-    const float mix = rnd<T>(sigmoidf_(rnd<T>(acc + ld(bu, i))));
-    const float rv = rnd<T>(ld(hp, i) * inv * a.state_norm[i]);
-    hv[c] = rnd<T>(rnd<T>(lerp_ref(rv, ld(e, i), mix)) + ld(step, i));
+    for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(w[c] * (hv[c] * inv));
+    stv<EPL>(reinterpret_cast<T*>(a.xn) + (int64_t)r * D + i0, y);
   }
-  store_and_norm<T, NPER>(hv, h_in, h, a.norm_w ? a.norm_w + (int64_t)rd.pulse * D : nullptr,
-                    reinterpret_cast<T*>(a.xn) + (int64_t)r * D, D, a.eps, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -284,17 +272,20 @@ __global__ void __launch_bounds__(256) qk_post_kernel(QKPostArgs a) {
   }
   const float k = norm_rope(ld(q, H * 64 + g * 64 + lane), a.k_norm + ((int64_t)pulse * Hk + g) * 64);
   if (a.prefill && a.is_local && pos < a.prefill_T - a.window) return;
-  const int64_t off = kv_offset(a.kv, a.layer, rd.seq, g, pos) + lane;
-  reinterpret_cast<T*>(a.kv.k[a.layer])[off] = from_f<T>(k);
-  reinterpret_cast<T*>(a.kv.v[a.layer])[off] = from_f<T>(v);
+  reinterpret_cast<T*>(a.kv.k[a.layer])[kv_offset(a.kv, a.layer, rd.seq, g, pos) + lane] =
+      from_f<T>(k);
+  reinterpret_cast<T*>(a.kv.v[a.layer])[kv_offset_v(a.kv, a.layer, rd.seq, g, pos, lane)] =
+      from_f<T>(v);
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention, split over keys: block (row, kv head, split) serves the 4 query heads
-// of the group over up to 256 keys, 64 per wave. Lane l owns key group (l >> 3), i.e. keys
+// Decode attention for fp32 caches (the bf16 path runs on the matrix cores below), split
+// over keys: block (row, kv head, split) serves the 4 query heads of the group over up to
+// 256 keys, 64 per wave. Lane l owns key group (l >> 3), i.e. keys
 // kbeg + (l >> 3) + 8i for i < 8, and dims 8*(l & 7) .. +8, so each K and V load is 128
 // contiguous bits and every 8 lanes read one 128-byte key row: the wave reads 1 KB of
-// contiguous cache per load instruction. Scores are reduced over the 8 lanes of a key
+// contiguous cache per load instruction (V, stored dimension-major, is gathered per
+// element: this path is for exactness, not speed). Scores are reduced over the 8 lanes of a key
 // group, softmax statistics over the wave; partials (max, sum, acc[64]) per query head go
 // to `part` and the combine kernel merges the splits.
 // ---------------------------------------------------------------------------
@@ -339,7 +330,9 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
     valid[i] = key <= pos;
     const int64_t off = valid[i] ? kv_offset(a.kv, a.layer, rd.seq, g, key) + dc * 8 : 0;
     load8v(Kc + off, kf[i], valid[i]);
-    load8v(Vc + off, vf[i], valid[i]);
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      vf[i][d] = valid[i] ? ld(Vc, kv_offset_v(a.kv, a.layer, rd.seq, g, key, dc * 8 + d)) : 0.f;
   }
   float sc[4][8];
 #pragma unroll
@@ -453,6 +446,208 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention on the matrix cores (bf16 caches). Block (unit, kv head, split): the
+// unit's rows (the current token, and the speculative token one position later when
+// present) read each key block of the cache once. Each wave takes one 64-aligned block of
+// 64 keys (one page of a global layer, a contiguous run of a local ring):
+//   S[16 x 64] = Q . K^T with v_mfma_f32_16x16x32_bf16; A rows 0-3 = the 4 query heads of
+//     row a, 4-7 = row b, 8-15 = zero; A lane l holds row l%16, dims 8*(l/16) + 32*ks;
+//     B lane l holds key l%16 of a 16-key block, same dims: one 16-byte load each.
+//   P = exp(S - rowmax) (fp32), split into bf16 hi + lo with hi + lo = P to 2^-16
+//     relative, transposed through LDS into the A layout (row = head, 8 keys per lane).
+//   O[16 x 64] = P . V; B = the dimension-major V block: lane l holds dim 16n + l%16,
+//     keys 8*(l/16) + 32*ks, 16 contiguous bytes.
+// Row maxima and sums reduce over the 16 lanes of a DPP row. The 4 waves' (max, sum, O)
+// merge in LDS and the split partial goes to `part` [unit][kv head][split][8][66].
+// ---------------------------------------------------------------------------
+typedef __bf16 attn_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float attn_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x124>(v));
+  v = fmaxf(v, dpp_mov<0x128>(v));
+  return __shfl(v, threadIdx.x & 0x30, 64);
+}
+
+__device__ __forceinline__ void unit_range(const AttnArgs& a, const AttnUnit& un, int& lo_a,
+                                           int& lo_b, int& base, int& uhi) {
+  const bool two = un.row_b >= 0;
+  lo_a = a.is_local ? max(0, un.pos_a - a.window + 1) : 0;
+  lo_b = two ? (a.is_local ? max(0, un.pos_b - a.window + 1) : 0) : lo_a;
+  uhi = two ? max(un.pos_a, un.pos_b) : un.pos_a;
+  base = min(lo_a, lo_b) & ~63;
+}
+
+__global__ void __launch_bounds__(256) attn_decode_mfma_kernel(AttnArgs a) {
+  __shared__ float wm[4][8], wl[4][8];
+  __shared__ float wacc[4][8][64];
+  __shared__ __attribute__((aligned(16))) uint16_t pt[4][2][16][72];
+  const int u = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+  const int nu = a.ctl->n_units;
+  const AttnUnit un = a.units[u];
+  if (u >= nu) return;
+  int lo_a, lo_b, base, uhi;
+  unit_range(a, un, lo_a, lo_b, base, uhi);
+  const int nsplit = (uhi + 1 - base + kSplitLen - 1) / kSplitLen;
+  if (s >= nsplit) return;
+  const bool two = un.row_b >= 0;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int m16 = lane & 15, kq = lane >> 4;
+  const int kb = base + s * kSplitLen + wv * 64;  // this wave's key block
+  const bool wact = kb <= uhi;                    // uniform per wave
+  const attn_bf16x8 zero = {};
+
+  // Q operand: row m16 of the 16-row tile
+  const int qrow = m16 < 4 ? un.row_a : ((m16 < 8 && two) ? un.row_b : -1);
+  const bf16* qp = reinterpret_cast<const bf16*>(a.qkv) + (int64_t)(qrow < 0 ? 0 : qrow) * a.ldq +
+                   (g * 4 + (m16 & 3)) * 64 + kq * 8;
+  attn_bf16x8 qa[2], kk[4][2], vv[4][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    qa[ks] = qrow >= 0 ? *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32) : zero;
+  if (wact) {
+    const KVBlock blk = kv_block(a.kv, a.layer, un.seq, g, kb);
+    const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]) + blk.k0 + kq * 8;
+    const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]) + blk.v0 + kq * 8;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        kk[j][ks] = *reinterpret_cast<const attn_bf16x8*>(Kc + (j * 16 + m16) * 64 + ks * 32);
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        vv[n][ks] = *reinterpret_cast<const attn_bf16x8*>(
+            Vc + (int64_t)(n * 16 + m16) * blk.vstride + ks * 32);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kk[j][0] = kk[j][1] = zero;
+      vv[j][0] = vv[j][1] = zero;
+    }
+  }
+  // scores; lane holds head rows kq*4 + i of key kb + 16j + m16
+  const bool rowok = kq == 0 || (kq == 1 && two);
+  const int klo = kq == 0 ? lo_a : lo_b, khi = kq == 0 ? un.pos_a : un.pos_b;
+  float sc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[0], kk[j][0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[1], kk[j][1], acc, 0, 0, 0);
+    const int key = kb + j * 16 + m16;
+    const bool ok = wact && rowok && key >= klo && key <= khi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[j][i] = ok ? acc[i] * a.scale : -INFINITY;
+  }
+  float mx[4], ls[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float m = fmaxf(fmaxf(sc[0][i], sc[1][i]), fmaxf(sc[2][i], sc[3][i]));
+    mx[i] = row16_max(m);
+    float l = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = sc[j][i] == -INFINITY ? 0.f : expf(sc[j][i] - mx[i]);
+      sc[j][i] = p;
+      l += p;
+    }
+    ls[i] = row16_sum(l);
+  }
+  // stage P (hi, lo) as [head row][key] for the A operand of P.V
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bf16 hi = f2bf(sc[j][i]);
+      const bf16 lo = f2bf(sc[j][i] - bf2f(hi));
+      pt[wv][0][kq * 4 + i][j * 16 + m16] = hi.u;
+      pt[wv][1][kq * 4 + i][j * 16 + m16] = lo.u;
+    }
+  __syncthreads();
+  attn_f32x4 o[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) o[n] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const attn_bf16x8 ph = *reinterpret_cast<const attn_bf16x8*>(&pt[wv][0][m16][ks * 32 + kq * 8]);
+    const attn_bf16x8 pl = *reinterpret_cast<const attn_bf16x8*>(&pt[wv][1][m16][ks * 32 + kq * 8]);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vv[n][ks], o[n], 0, 0, 0);
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vv[n][ks], o[n], 0, 0, 0);
+    }
+  }
+  if (kq < 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (m16 == 0) {
+        wm[wv][kq * 4 + i] = mx[i];
+        wl[wv][kq * 4 + i] = ls[i];
+      }
+#pragma unroll
+      for (int n = 0; n < 4; ++n) wacc[wv][kq * 4 + i][n * 16 + m16] = o[n][i];
+    }
+  }
+  __syncthreads();
+  // merge the 4 waves: thread -> head row hr, dims d0, d0 + 1
+  const int hr = threadIdx.x >> 5, d0 = (threadIdx.x & 31) * 2;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][hr]);
+  float L = 0.f, O0 = 0.f, O1 = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (wm[w][hr] == -INFINITY) continue;
+      const float f = expf(wm[w][hr] - M);
+      L += wl[w][hr] * f;
+      O0 += wacc[w][hr][d0] * f;
+      O1 += wacc[w][hr][d0 + 1] * f;
+    }
+  }
+  float* out = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits + s) * 8 + hr) * 66;
+  out[2 + d0] = O0;
+  out[3 + d0] = O1;
+  if (d0 == 0) {
+    out[0] = M;
+    out[1] = L;
+  }
+}
+
+// Merge the split partials of a unit: block (unit, kv head, row of the unit); wave = query
+// head of the group, lane = dim. Normalise, round as the SDPA output, apply the head gate.
+__global__ void __launch_bounds__(256) attn_unit_combine_kernel(AttnArgs a) {
+  const int u = blockIdx.x, g = blockIdx.y, z = blockIdx.z;
+  if (u >= a.ctl->n_units) return;
+  const AttnUnit un = a.units[u];
+  const int row = z == 0 ? un.row_a : un.row_b;
+  if (row < 0) return;
+  int lo_a, lo_b, base, uhi;
+  unit_range(a, un, lo_a, lo_b, base, uhi);
+  const int nsplit = (uhi + 1 - base + kSplitLen - 1) / kSplitLen;
+  const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int head = g * 4 + h;
+  const float* p0 = a.part + (((int64_t)u * a.Hkv + g) * a.max_splits * 8 + z * 4 + h) * 66;
+  float M = -INFINITY;
+  for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, p0[(int64_t)sp * 8 * 66]);
+  float L = 0.f, O = 0.f;
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float* p = p0 + (int64_t)sp * 8 * 66;
+    if (p[0] == -INFINITY) continue;
+    const float f = expf(p[0] - M);
+    L += p[1] * f;
+    O += p[2 + lane] * f;
+  }
+  const float o = rnd<bf16>(O / L);
+  const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
+  reinterpret_cast<bf16*>(a.out)[(int64_t)row * a.H * 64 + head * 64 + lane] = f2bf(o * gate);
+}
+
+// ---------------------------------------------------------------------------
 // Prefill attention: block (sequence, 64-query tile, kv head); wave = query head of the
 // group, lane = query. K/V tiles of 64 keys are staged in LDS (fp32). Key range per query:
 // global or short prompt: [0, t]; local with T > window (reference SDPA is_causal with
@@ -502,14 +697,12 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
     for (int i = threadIdx.x; i < 64 * 64; i += 256) {
       const int kk = i >> 6, d = i & 63;
       const int key = k0 + kk;
-      float kv = 0.f, vv = 0.f;
-      if (key <= thi) {
-        const int64_t off = kv_offset(a.kv, a.layer, b, g, key) + d;
-        kv = ld(Kc, off);
-        vv = ld(Vc, off);
-      }
-      Ks[kk][d] = kv;
-      Vs[kk][d] = vv;
+      Ks[kk][d] = key <= thi ? ld(Kc, kv_offset(a.kv, a.layer, b, g, key) + d) : 0.f;
+    }
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+      const int kk = i & 63, d = i >> 6;  // V is dimension-major: consecutive keys per thread
+      const int key = k0 + kk;
+      Vs[kk][d] = key <= thi ? ld(Vc, kv_offset_v(a.kv, a.layer, b, g, key, d)) : 0.f;
     }
     __syncthreads();
     float sc[64];
@@ -577,50 +770,74 @@ __global__ void __launch_bounds__(256) router_decode_kernel(RouterArgs a) {
 }
 
 // mlp_norm + decode router in one pass over the residual row.
-template <typename T, int E, int NPER>
+// Decode: mlp_norm of the residual stream fused with the router. Block = 4 waves per row;
+// every wave normalises the row (wave 0 stores it), wave w computes the logits of experts
+// [w*E/4, (w+1)*E/4); wave 0 then ranks the experts in parallel (lane = expert).
+template <typename T, int E, int EPL>
 __global__ void __launch_bounds__(256) norm_router_kernel(RouterArgs a) {
-  __shared__ float red[16];
-  __shared__ float part[4][E];
-  __shared__ float lg[32];
+  constexpr int EW = E / 4;
+  __shared__ float lg[E];
   const int r = blockIdx.x;
   if (r >= a.ctl->n_rows) return;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int pulse = a.rows[r].pulse;
-  const int D = a.D;
+  const int D = a.D, i0 = lane * EPL;
   const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)r * D;
-  const float* nw = a.norm_w + (int64_t)pulse * D;
-  const float* W = a.w + (int64_t)pulse * E * D;
-  float xv[NPER];
+  const float* W = a.w + ((int64_t)pulse * E + wv * EW) * D;
+  float xv[EPL], nw[EPL], wt[EW][EPL];
+  ldv<EPL>(x + i0, xv);
+  ldv<EPL>(a.norm_w + (int64_t)pulse * D + i0, nw);
+#pragma unroll
+  for (int q = 0; q < EW; ++q) ldv<EPL>(W + (int64_t)q * D + i0, wt[q]);
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < NPER; ++c) {
-    const int i = threadIdx.x + c * 256;
-    xv[c] = ld(x, i);
-    ss += xv[c] * xv[c];
-  }
-  ss = block_sum(ss, red);
-  const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
-  float acc[E];
+  for (int c = 0; c < EPL; ++c) ss += xv[c] * xv[c];
+  const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
+  float y[EPL];
 #pragma unroll
-  for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  T* xn = reinterpret_cast<T*>(a.xn) + (int64_t)r * D;
+  for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(nw[c] * (xv[c] * inv));
+  if (wv == 0) stv<EPL>(reinterpret_cast<T*>(a.xn) + (int64_t)r * D + i0, y);
 #pragma unroll
-  for (int c = 0; c < NPER; ++c) {
-    const int i = threadIdx.x + c * 256;
-    const float y = rnd<T>(nw[i] * (xv[c] * inv));
-    xn[i] = from_f<T>(y);
+  for (int q = 0; q < EW; ++q) {
+    float acc = 0.f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] += y * W[(int64_t)e * D + i];
-  }
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const float v = wave_sum(acc[e]);
-    if (lane == 0) part[wv][e] = v;
+    for (int c = 0; c < EPL; ++c) acc += y[c] * wt[q][c];
+    acc = wave_sum(acc);
+    if (lane == 0) lg[wv * EW + q] = acc;
   }
   __syncthreads();
-  if (threadIdx.x != 0) return;
-  for (int e = 0; e < E; ++e) lg[e] = part[0][e] + part[1][e] + part[2][e] + part[3][e];
-  route_topk<T>(lg, E, a.K, a.bias + (int64_t)pulse * E, r, a);
+  if (wv != 0) return;
+  // sigmoid of mean-centred logits, + bias; rank = #experts ahead (value desc, index asc)
+  const bool act = lane < E;
+  const float l = act ? lg[lane] : 0.f;
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < E; ++j) sum += lane_bcast(l, j);
+  const float cen = l - sum / (float)E;
+  const float sc = 1.0f / (1.0f + expf(-cen));
+  const float bsc = sc + (act ? a.bias[(int64_t)pulse * E + lane] : 0.f);
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const float bj = lane_bcast(bsc, j);
+    rank += (bj > bsc || (bj == bsc && j < lane)) ? 1 : 0;
+  }
+  const int K = a.K;
+  float tot = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const uint64_t m = __ballot(act && rank == k);
+    tot += lane_bcast(sc, __ffsll((unsigned long long)m) - 1);
+  }
+  tot += 1e-6f;
+  if (act && rank < K) {
+    const int64_t o = (int64_t)r * K + rank;
+    a.topk_idx[o] = lane;
+    a.topk_w[o] = rnd<T>(sc / tot);
+    if (a.lists) {
+      const int p = atomicAdd(&a.list_count[lane], 1);
+      a.lists[(int64_t)lane * a.list_stride + p] = (int)o;
+    }
+  }
 }
 
 // Prefill router: logits in the activation dtype with T-rounded weights.
@@ -696,43 +913,59 @@ __global__ void prefill_slots_kernel(const int32_t* __restrict__ idx, const floa
 // decode: routed = sum_k T(out_k * w_k) in T, mlp = T(shared + T(routed * rs)), h += mlp.
 // prefill: routed = index_add of T(w_k * out_k) in T (dropped = 0), mlp = T(shared + routed).
 // ---------------------------------------------------------------------------
-template <typename T, int NPER>
-__global__ void __launch_bounds__(256) moe_combine_rows_kernel(CombineArgs a) {
+template <typename T, int EPL, int KT>
+__global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
+  // one wave per row; lane owns elements [lane*EPL, lane*EPL + EPL)
   const int r = blockIdx.x;
   const int n = a.ctl ? a.ctl->n_rows : a.m_fixed;
   if (r >= n) return;
-  const int K = a.K, D = a.D;
-  const T* sh = reinterpret_cast<const T*>(a.shared) + (int64_t)r * D;
-  const T* ro = reinterpret_cast<const T*>(a.routed) + (int64_t)r * K * D;
-  T* h = reinterpret_cast<T*>(a.h) + (int64_t)r * D;
-  float w[8];
-  bool kept[8];
-  for (int k = 0; k < K; ++k) {
-    w[k] = a.topk_w[(int64_t)r * K + k];
-    kept[k] = a.keep ? a.keep[(int64_t)r * K + k] != 0 : true;
-  }
+  const int K = a.K, D = a.D, lane = threadIdx.x, i0 = lane * EPL;
   const int pulse = a.ctl ? a.rows[r].pulse : a.pulse;
-  const T* rs = reinterpret_cast<const T*>(a.routed_scale) + (int64_t)pulse * D;
-  float hv[NPER];
+  const T* shp = reinterpret_cast<const T*>(a.shared) + (int64_t)r * D + i0;
+  const T* rop = reinterpret_cast<const T*>(a.routed) + (int64_t)r * K * D + i0;
+  const T* rsp = reinterpret_cast<const T*>(a.routed_scale) + (int64_t)pulse * D + i0;
+  T* h = reinterpret_cast<T*>(a.h) + (int64_t)r * D + i0;
+  float hv[EPL], sh[EPL], rs[EPL], ro[KT][EPL];
+  ldv<EPL>(h, hv);
+  ldv<EPL>(shp, sh);
+  ldv<EPL>(rsp, rs);
 #pragma unroll
-  for (int c = 0; c < NPER; ++c) {
-    const int i = threadIdx.x + c * 256;
+  for (int k = 0; k < KT; ++k) ldv<EPL>(rop + (int64_t)(k < K ? k : 0) * D, ro[k]);
+  float w[KT];
+  bool kept[KT];
+#pragma unroll
+  for (int k = 0; k < KT; ++k) {
+    const int kk = k < K ? k : 0;
+    w[k] = a.topk_w[(int64_t)r * K + kk];
+    kept[k] = a.keep ? a.keep[(int64_t)r * K + kk] != 0 : true;
+  }
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
     float routed = 0.f, mlp;
     if (!a.prefill) {
-      for (int k = 0; k < K; ++k) routed = rnd<T>(routed + rnd<T>(ld(ro, (int64_t)k * D + i) * w[k]));
-      mlp = rnd<T>(ld(sh, i) + rnd<T>(routed * ld(rs, i)));
+#pragma unroll
+      for (int k = 0; k < KT; ++k)
+        if (k < K) routed = rnd<T>(routed + rnd<T>(ro[k][c] * w[k]));
+      mlp = rnd<T>(sh[c] + rnd<T>(routed * rs[c]));
     } else {
-      for (int k = 0; k < K; ++k) {
-        const float cv = kept[k] ? rnd<T>(w[k] * ld(ro, (int64_t)k * D + i)) : 0.f;
-        routed = rnd<T>(routed + cv);
-      }
-      mlp = rnd<T>(ld(sh, i) + routed);
+#pragma unroll
+      for (int k = 0; k < KT; ++k)
+        if (k < K) routed = rnd<T>(routed + (kept[k] ? rnd<T>(w[k] * ro[k][c]) : 0.f));
+      mlp = rnd<T>(sh[c] + routed);
     }
-    hv[c] = rnd<T>(ld(h, i) + mlp);
+    hv[c] = rnd<T>(hv[c] + mlp);
   }
-  __shared__ float red[16];
-  store_and_norm<T, NPER>(hv, (T*)nullptr, h, a.next_norm ? a.next_norm + (int64_t)pulse * D : nullptr,
-                    reinterpret_cast<T*>(a.xn) + (int64_t)r * D, D, a.eps, red);
+  stv<EPL>(h, hv);
+  if (a.next_norm) {
+    float ss = 0.f, nw[EPL], y[EPL];
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) ss += hv[c] * hv[c];
+    ldv<EPL>(a.next_norm + (int64_t)pulse * D + i0, nw);
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(nw[c] * (hv[c] * inv));
+    stv<EPL>(reinterpret_cast<T*>(a.xn) + (int64_t)r * D + i0, y);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -775,30 +1008,41 @@ __global__ void __launch_bounds__(256) pulse_output_kernel(PulseOutputArgs a) {
   } while (0)
 
 // Row kernels hold D/256 elements per thread in registers (D a multiple of 256, <= 2048).
-#define PULSAR_NPER_DISPATCH(D, KERNEL_T, grid, arg)                                         \
+// Wave-per-row kernels: EPL = D / 64 elements per lane.
+#define PULSAR_EPL_DISPATCH(D, KERNEL_T, grid, block, arg)                                   \
   do {                                                                                       \
-    const int _nper = (D) / 256;                                                             \
-    if ((D) % 256 != 0 || _nper < 1 || _nper > kMaxPer)                                      \
-      return fail(PULSAR_ERR_UNSUPPORTED, "d_model must be a multiple of 256 up to 2048");   \
-    switch (_nper) {                                                                         \
-      case 1: KERNEL_T(1)<<<(grid), 256, 0, s>>>(arg); break;                                \
-      case 2: KERNEL_T(2)<<<(grid), 256, 0, s>>>(arg); break;                                \
-      case 4: KERNEL_T(4)<<<(grid), 256, 0, s>>>(arg); break;                                \
-      case 8: KERNEL_T(8)<<<(grid), 256, 0, s>>>(arg); break;                                \
-      default: return fail(PULSAR_ERR_UNSUPPORTED, "d_model/256 must be 1, 2, 4 or 8");      \
+    switch ((D) % 256 == 0 ? (D) / 64 : 0) {                                                 \
+      case 4: KERNEL_T(4)<<<(grid), (block), 0, s>>>(arg); break;                            \
+      case 8: KERNEL_T(8)<<<(grid), (block), 0, s>>>(arg); break;                            \
+      case 16: KERNEL_T(16)<<<(grid), (block), 0, s>>>(arg); break;                          \
+      case 32: KERNEL_T(32)<<<(grid), (block), 0, s>>>(arg); break;                          \
+      default: return fail(PULSAR_ERR_UNSUPPORTED, "d_model must be 256, 512, 1024 or 2048"); \
     }                                                                                        \
     PULSAR_LAUNCH_CHECK();                                                                   \
     return PULSAR_OK;                                                                        \
   } while (0)
 
 int launch_pulse_input(const PulseInputArgs& a, int dtype, int max_rows, hipStream_t s) {
+  if (a.rank < 1 || a.rank > kMaxRank)
+    return fail(PULSAR_ERR_UNSUPPORTED, "pulse_input: reinject rank must be 1..16");
+  const bool r8 = a.rank <= 8;
   if (dtype == PULSAR_BF16) {
-#define K_(N) pulse_input_kernel<bf16, N>
-    PULSAR_NPER_DISPATCH(a.D, K_, dim3(max_rows), a);
+    if (r8) {
+#define K_(N) pulse_input_kernel<bf16, N, 8>
+      PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 64, a);
+#undef K_
+    }
+#define K_(N) pulse_input_kernel<bf16, N, 16>
+    PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 64, a);
 #undef K_
   }
-#define K_(N) pulse_input_kernel<float, N>
-  PULSAR_NPER_DISPATCH(a.D, K_, dim3(max_rows), a);
+  if (r8) {
+#define K_(N) pulse_input_kernel<float, N, 8>
+    PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 64, a);
+#undef K_
+  }
+#define K_(N) pulse_input_kernel<float, N, 16>
+  PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 64, a);
 #undef K_
 }
 int launch_norm_rows(const NormArgs& a, int dtype, int max_rows, hipStream_t s) {
@@ -808,12 +1052,18 @@ int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s) 
   PULSAR_DISPATCH(dtype, qk_post_kernel, dim3(max_rows, (a.H + a.Hkv + 3) / 4), 256, a);
 }
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s) {
-  if (dtype == PULSAR_BF16)
-    attn_decode_kernel<bf16><<<dim3(max_rows, a.Hkv, a.max_splits), 256, 0, s>>>(a);
-  else
-    attn_decode_kernel<float><<<dim3(max_rows, a.Hkv, a.max_splits), 256, 0, s>>>(a);
+  if (dtype == PULSAR_BF16) {
+    attn_decode_mfma_kernel<<<dim3(a.max_units, a.Hkv, a.max_splits), 256, 0, s>>>(a);
+    PULSAR_LAUNCH_CHECK();
+    attn_unit_combine_kernel<<<dim3(a.max_units, a.Hkv, 2), 256, 0, s>>>(a);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  }
+  attn_decode_kernel<float><<<dim3(max_rows, a.Hkv, a.max_splits), 256, 0, s>>>(a);
   PULSAR_LAUNCH_CHECK();
-  PULSAR_DISPATCH(dtype, attn_combine_kernel, dim3(max_rows, a.H / 4), 256, a);
+  attn_combine_kernel<float><<<dim3(max_rows, a.H / 4), 256, 0, s>>>(a);
+  PULSAR_LAUNCH_CHECK();
+  return PULSAR_OK;
 }
 int launch_attn_prefill(const AttnArgs& a, int dtype, int B, hipStream_t s) {
   const int ntile = (a.prefill_T + 63) / 64;
@@ -823,25 +1073,28 @@ int launch_router_decode(const RouterArgs& a, int dtype, int max_rows, hipStream
   PULSAR_DISPATCH(dtype, router_decode_kernel, dim3(max_rows), 256, a);
 }
 int launch_norm_router(const RouterArgs& a, int dtype, int max_rows, hipStream_t s) {
-  if (a.D > 256 * kMaxPer) return fail(PULSAR_ERR_UNSUPPORTED, "norm_router: d_model > 2048");
-#define PULSAR_NR_CASE(EV)                                                  \
-  if (a.E == EV) {                                                          \
-    if (dtype == PULSAR_BF16) {                                             \
-      PULSAR_NPER_DISPATCH(a.D, K_BF16_##EV, dim3(max_rows), a);            \
-    }                                                                       \
-    PULSAR_NPER_DISPATCH(a.D, K_F32_##EV, dim3(max_rows), a);               \
+  if (a.K < 1 || a.K > 8 || a.K > a.E)
+    return fail(PULSAR_ERR_UNSUPPORTED, "norm_router: top_k must be 1..8 and <= n_experts");
+  if (a.E == 16) {
+    if (dtype == PULSAR_BF16) {
+#define K_(N) norm_router_kernel<bf16, 16, N>
+      PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 256, a);
+#undef K_
+    }
+#define K_(N) norm_router_kernel<float, 16, N>
+    PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 256, a);
+#undef K_
   }
-#define K_BF16_16(N) norm_router_kernel<bf16, 16, N>
-#define K_F32_16(N) norm_router_kernel<float, 16, N>
-#define K_BF16_8(N) norm_router_kernel<bf16, 8, N>
-#define K_F32_8(N) norm_router_kernel<float, 8, N>
-  PULSAR_NR_CASE(16)
-  PULSAR_NR_CASE(8)
-#undef K_BF16_16
-#undef K_F32_16
-#undef K_BF16_8
-#undef K_F32_8
-#undef PULSAR_NR_CASE
+  if (a.E == 8) {
+    if (dtype == PULSAR_BF16) {
+#define K_(N) norm_router_kernel<bf16, 8, N>
+      PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 256, a);
+#undef K_
+    }
+#define K_(N) norm_router_kernel<float, 8, N>
+    PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 256, a);
+#undef K_
+  }
   return fail(PULSAR_ERR_UNSUPPORTED, "norm_router: n_experts must be 8 or 16");
 }
 int launch_router_prefill(const RouterArgs& a, int dtype, hipStream_t s) {
@@ -860,14 +1113,32 @@ int launch_prefill_capacity(const int32_t* idx, const float* w, int32_t* cnt, in
   return PULSAR_OK;
 }
 int launch_moe_combine(const CombineArgs& a, int dtype, int max_rows, hipStream_t s) {
-  if (dtype == PULSAR_BF16) {
-#define K_(N) moe_combine_rows_kernel<bf16, N>
-    PULSAR_NPER_DISPATCH(a.D, K_, dim3(max_rows), a);
-#undef K_
+  if (a.K < 1 || a.K > 8) return fail(PULSAR_ERR_UNSUPPORTED, "moe_combine: top_k must be 1..8");
+  const int kt = a.K <= 2 ? 2 : (a.K <= 4 ? 4 : 8);
+#define PULSAR_COMBINE_CASE(KT)                                     \
+  if (kt == KT) {                                                   \
+    if (dtype == PULSAR_BF16) {                                     \
+      PULSAR_EPL_DISPATCH(a.D, K_BF, dim3(max_rows), 64, a);        \
+    }                                                               \
+    PULSAR_EPL_DISPATCH(a.D, K_F32, dim3(max_rows), 64, a);         \
   }
-#define K_(N) moe_combine_rows_kernel<float, N>
-  PULSAR_NPER_DISPATCH(a.D, K_, dim3(max_rows), a);
-#undef K_
+#define K_BF(N) moe_combine_rows_kernel<bf16, N, 2>
+#define K_F32(N) moe_combine_rows_kernel<float, N, 2>
+  PULSAR_COMBINE_CASE(2)
+#undef K_BF
+#undef K_F32
+#define K_BF(N) moe_combine_rows_kernel<bf16, N, 4>
+#define K_F32(N) moe_combine_rows_kernel<float, N, 4>
+  PULSAR_COMBINE_CASE(4)
+#undef K_BF
+#undef K_F32
+#define K_BF(N) moe_combine_rows_kernel<bf16, N, 8>
+#define K_F32(N) moe_combine_rows_kernel<float, N, 8>
+  PULSAR_COMBINE_CASE(8)
+#undef K_BF
+#undef K_F32
+#undef PULSAR_COMBINE_CASE
+  return fail(PULSAR_ERR_UNSUPPORTED, "moe_combine: top_k");
 }
 int launch_pulse_output(const PulseOutputArgs& a, int dtype, int max_rows, hipStream_t s) {
   PULSAR_DISPATCH(dtype, pulse_output_kernel, dim3(max_rows), 256, a);

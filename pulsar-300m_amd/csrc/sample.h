@@ -39,6 +39,7 @@ struct ControllerArgs {
   RowDesc* last_rows;   // snapshot of its rows
   SeqState* state;
   RowDesc* rows;
+  AttnUnit* units;      // decode attention units of the next step
   int32_t* lrow_seq;
   int32_t* lrow_extra;
   uint32_t* seen;

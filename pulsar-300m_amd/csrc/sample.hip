@@ -137,22 +137,42 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
     mx = fmaxf(mx, l[i]);
   }
   mx = block_max(mx, red);
+  // Unnormalised probabilities and order keys, computed once. bf16-rounded scores carry
+  // no information in the low 16 key bits (all zero for positive, all one for negative
+  // values, so equal high halves mean equal keys): the threshold search runs on the high
+  // half there, 16 steps instead of 32, with the same kept set.
+  constexpr int kLow = sizeof(T) == 2 ? 16 : 0;
+  float pr[PER];
+  uint32_t key[PER];
   float zl = 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) zl += expf(l[i] - mx);
+  for (int i = 0; i < PER; ++i) {
+    pr[i] = expf(l[i] - mx);
+    key[i] = order_key(l[i]) >> kLow;
+    zl += pr[i];
+  }
   const float Z = block_sum(zl, red);
   uint32_t kstar = 0;
   if (a.top_p < 1.0f) {
+    // smallest m with mass(key > m) <= top_p * Z; the maximum's key always qualifies.
+    // One barrier per step: partials alternate between two LDS buffers.
+    __shared__ float part[2][16];
     const float lim = a.top_p * Z;
-    uint32_t lo = 0, hi = 0xffffffffu;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    uint32_t lo = 0, hi = order_key(mx) >> kLow;
+    int buf = 0;
     while (lo < hi) {
       const uint32_t mid = lo + ((hi - lo) >> 1);
       float f = 0.f;
 #pragma unroll
-      for (int i = 0; i < PER; ++i)
-        if (order_key(l[i]) > mid) f += expf(l[i] - mx);
-      f = block_sum(f, red);
-      if (f <= lim)
+      for (int i = 0; i < PER; ++i) f += key[i] > mid ? pr[i] : 0.f;
+      f = wave_sum(f);
+      if (lane == 0) part[buf][w] = f;
+      __syncthreads();
+      float t = 0.f;
+      for (int i = 0; i < nw; ++i) t += part[buf][i];
+      buf ^= 1;
+      if (t <= lim)
         hi = mid;
       else
         lo = mid + 1;
@@ -163,8 +183,8 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
   int last_kept = -1;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    if (order_key(l[i]) >= kstar) {
-      own += expf(l[i] - mx);
+    if (key[i] >= kstar) {
+      own += pr[i];
       last_kept = base + i;
     }
   }
@@ -183,8 +203,8 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
       int choice = -1;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        if (order_key(l[i]) >= kstar) {
-          run += expf(l[i] - mx);
+        if (key[i] >= kstar) {
+          run += pr[i];
           if (choice < 0 && target < run) choice = base + i;
         }
       }
@@ -201,7 +221,7 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Controller (single thread; B <= a few hundred).
+// Controller: one thread per sequence (B <= 256); block scans lay out the next step.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -310,23 +330,24 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
   }
 }
 
-// Exclusive scan of 4 counters over the block (blockDim 256) in LDS.
-__device__ void scan4(int* v, int* sh, int* total) {
+// Exclusive scan of N counters over the block (blockDim 256) in LDS.
+template <int N>
+__device__ void scan_counts(int* v, int* sh, int* total) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) sh[k * 256 + t] = v[k];
+  for (int k = 0; k < N; ++k) sh[k * 256 + t] = v[k];
   __syncthreads();
   for (int off = 1; off < 256; off <<= 1) {
-    int add[4];
+    int add[N];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) add[k] = t >= off ? sh[k * 256 + t - off] : 0;
+    for (int k = 0; k < N; ++k) add[k] = t >= off ? sh[k * 256 + t - off] : 0;
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 4; ++k) sh[k * 256 + t] += add[k];
+    for (int k = 0; k < N; ++k) sh[k * 256 + t] += add[k];
     __syncthreads();
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < N; ++k) {
     total[k] = sh[k * 256 + 255];
     v[k] = sh[k * 256 + t] - v[k];
   }
@@ -337,7 +358,7 @@ __device__ void scan4(int* v, int* sh, int* total) {
 // pulse (sequence order within a pulse) and its logits rows. Also snapshots the rows and
 // control block of the step that just ran (readable for testing).
 __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
-  __shared__ int sh[4 * 256];
+  __shared__ int sh[5 * 256];
   const int b = threadIdx.x;
   StepCtl* ctl = a.ctl;
   const int P = a.n_pulses;
@@ -370,12 +391,13 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
   const bool crow = live;
   const bool srow = live && a.speculative && s.c_pulse == P - 1 && s.s_valid;
   const bool cwant = crow && (a.all_logits || s.c_pulse == P - 1 || (a.speculative && s.c_pulse == 0));
-  int v[4] = {0, 0, 0, 0};  // rows of pulse 0, 1, 2; logits rows
+  int v[5] = {0, 0, 0, 0, 0};  // rows of pulse 0, 1, 2; logits rows; attention units
   if (crow) v[s.c_pulse] += 1;
   if (srow) v[0] += 1;
   v[3] = (cwant ? 1 : 0) + (srow ? 1 : 0);
-  int total[4];
-  scan4(v, sh, total);
+  v[4] = live ? 1 : 0;
+  int total[5];
+  scan_counts<5>(v, sh, total);
   int base[4] = {0, total[0], total[0] + total[1], 0};
   int lr = v[3];
   s.row_c = s.row_s = s.lrow_c = s.lrow_s = -1;
@@ -397,21 +419,18 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
     }
     a.rows[idx] = RowDesc{b, s.c_slot, p, s.c_pos, s.c_tok, s.lrow_c, -1, 0};
     s.row_c = idx;
+    a.units[v[4]] = AttnUnit{b, idx, s.row_s, s.c_pos, srow ? s.c_pos + 1 : -1, {0, 0, 0}};
   }
   if (act) a.state[b] = s;
-  int nact = live ? 1 : 0;
-  sh[b] = nact;  // scan4 left sh free after its final barrier
-  __syncthreads();
   if (b == 0) {
-    int tot = 0;
-    for (int i = 0; i < blockDim.x; ++i) tot += sh[i];
     for (int p = 0; p < 4; ++p) {
       ctl->pulse_start[p] = p < 3 ? base[p] : total[0] + total[1] + total[2];
       ctl->pulse_count[p] = p < 3 ? total[p] : 0;
     }
     ctl->n_rows = total[0] + total[1] + total[2];
     ctl->n_lrows = total[3];
-    ctl->active = tot;
+    ctl->n_units = total[4];
+    ctl->active = total[4];
     ctl->step += 1;
   }
 }
