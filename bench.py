@@ -32,6 +32,105 @@ for _p in (ROOT, PKG):
 
 METRIC = "accepted tokens/s at 1 GPU (batch 16, ctx 2k); % HBM roofline; acceptance rate"
 HBM_PEAK = 8.0e12
+# kernels behind each timed class (names as rocprofv3 lists them), bf16 decode
+CLASS_KERNELS = {
+    "attention": ["attn_decode_mfma_kernel", "attn_unit_combine_kernel"],
+    "routed_gate_up": ["gemm_bf16_kernel<3, 8, 1>"],
+    "routed_down": ["gemm_bf16_kernel<0, 4, 1>"],
+    "shared_down": ["gemm_bf16_kernel<0, 8, 2>"],
+    "qkv_gate_gemm": ["gemm_bf16_kernel<1, 8, 0>"],
+    "wo_gemm": ["gemm_bf16_kernel<2, 8, 0>"],
+    "lm_head": ["gemm_bf16_kernel<4, 8, 3>"],
+    "router": ["norm_router_kernel<bf16, 16, 16>"],
+    "moe_combine": ["moe_combine_rows_kernel<bf16, 16, 4>"],
+    "qk_post": ["qk_post_kernel<bf16>"],
+    "sample": ["sample_kernel<bf16, 32>"],
+    "pulse_input": ["pulse_input_kernel<bf16, 16, 8>"],
+    "pulse_output": ["pulse_output_kernel<bf16>"],
+    "controller": ["controller_kernel"],
+}
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_c2_b16_t2048.md")
+
+
+def _short_kernel(name: str) -> str:
+    import re
+    name = name.replace("(anonymous namespace)::", "").replace("pulsar::", "")
+    return re.sub(r"\(.*", "", name).replace("void ", "").strip()
+
+
+def _decode_rows(rows: list) -> list:
+    """Dispatches of the decode phase: after the controller's first launch (which follows
+    the prefill and draws the first tokens)."""
+    first = next((i for i, r in enumerate(rows) if "controller_kernel" in r["Kernel_Name"]), -1)
+    return rows[first + 1:]
+
+
+def _csv(directory: str, suffix: str) -> list:
+    import csv
+    import glob
+    paths = sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True))
+    if not paths:
+        raise SystemExit(f"no *{suffix} under {directory}")
+    with open(paths[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def rocprof_summary(directory: str) -> str:
+    """Markdown table of decode-phase kernel durations from a rocprofv3 kernel trace (csv)."""
+    from collections import defaultdict
+    rows = _decode_rows(_csv(directory, "kernel_trace.csv"))
+    agg = defaultdict(list)
+    for r in rows:
+        agg[_short_kernel(r["Kernel_Name"])].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    total = sum(sum(v) for v in agg.values())
+    out = ["| kernel | dispatches | avg us | total ms | share |", "|---|---|---|---|---|"]
+    for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        out.append(f"| `{k}` | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | {sum(v) / 1e6:.2f} | "
+                   f"{100 * sum(v) / total:.1f}% |")
+    out.append(f"\nDecode kernel time {total / 1e6:.2f} ms over {len(rows)} dispatches.")
+    return "\n".join(out)
+
+
+def pmc_summary(fetch_dir: str, write_dir: str, fetch_copy: str, write_copy: str,
+                copy_mib: int) -> str:
+    """Calibrated HBM bytes per decode dispatch from FETCH_SIZE / WRITE_SIZE runs."""
+    from collections import defaultdict
+    res = {}
+    lines = []
+    for ctr, d, dc in (("FETCH_SIZE", fetch_dir, fetch_copy), ("WRITE_SIZE", write_dir, write_copy)):
+        cal = [float(r["Counter_Value"]) for r in _csv(dc, "counter_collection.csv")
+               if "copyBuffer" in r["Kernel_Name"] and float(r["Counter_Value"]) > copy_mib * 256]
+        factor = copy_mib * 1024 / (sum(cal) / len(cal))
+        lines.append(f"- {ctr}: a {copy_mib} MiB device-to-device copy counts "
+                     f"{sum(cal) / len(cal):.1f} KiB per dispatch -> scale factor {factor:.4f}")
+        agg = defaultdict(list)
+        for r in _decode_rows(_csv(d, "counter_collection.csv")):
+            agg[_short_kernel(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+        for k, v in agg.items():
+            res.setdefault(k, {})[ctr] = round(sum(v) / len(v) * factor * 1024)
+    out = lines + ["", "| kernel | fetch MB / dispatch | write MB / dispatch |", "|---|---|---|"]
+    for k, v in sorted(res.items(), key=lambda kv: -kv[1].get("FETCH_SIZE", 0)):
+        out.append(f"| `{k}` | {v.get('FETCH_SIZE', 0) / 1e6:.3f} | {v.get('WRITE_SIZE', 0) / 1e6:.3f} |")
+    out += ["", "```json", json.dumps(res, sort_keys=True), "```"]
+    return "\n".join(out)
+
+
+def recorded_traffic(kernels: list):
+    """HBM bytes per launch of a kernel class from the committed PMC summary, or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            text = f.read()
+        blob = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    except (OSError, IndexError, ValueError):
+        return None
+    total = 0
+    for k in kernels:
+        if k not in blob:
+            return None
+        total += blob[k].get("FETCH_SIZE", 0) + blob[k].get("WRITE_SIZE", 0)
+    return total
 
 
 def log(msg: str) -> None:
@@ -39,7 +138,9 @@ def log(msg: str) -> None:
 
 
 def profile_generation(eng, cfg, es, seed):
-    """One eager generation with per-class HIP-event timing and algorithmic bytes."""
+    """One eagerly profiled generation (HIP events around every kernel class on the engine's
+    stream, the device kept busy ahead of each group) with the algorithmic bytes of each
+    step's row set."""
     from pulsar_engine import traffic
 
     eng.rewind(seed)
@@ -108,7 +209,20 @@ def main() -> int:
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-new-tokens", type=int, default=12)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run device-to-device copies of MIB MiB (HBM counter calibration)")
+    ap.add_argument("--rocprof-summary", metavar="DIR",
+                    help="print the decode kernel table of a rocprofv3 csv kernel trace and exit")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "FETCH_COPY", "WRITE_COPY"),
+                    help="print calibrated HBM bytes per decode dispatch from rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE csv directories (bench, then copy runs) and exit")
     args = ap.parse_args()
+    if args.rocprof_summary:
+        print(rocprof_summary(args.rocprof_summary))
+        return 0
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary, copy_mib=256))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
               "(the decode path shards by sequence; see DESIGN.md)", file=sys.stderr)
@@ -124,6 +238,16 @@ def main() -> int:
     from pulsar_engine.model import DeviceModel
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.calibrate_copy:
+        # a plain copy of known size: reads and writes exactly n bytes per launch
+        n = args.calibrate_copy << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {n} bytes 5 times")
+        return 0
     cfg = PulsarConfig()
     B, T, N = args.batch, args.prompt_len, args.new_tokens
     t0 = time.perf_counter()
@@ -171,24 +295,36 @@ def main() -> int:
     prof_detail = None
     if not args.no_profile:
         prof, bytes_by_class, psteps = profile_generation(eng, cfg, es, 3000)
-        tot_ms = sum(v[0] for v in prof.values())
-        dom = max(prof, key=lambda k: prof[k][0])
-        ms, n = prof[dom]
+        # Spans are kernel time plus what an event pair adds around a launch (under 1 us
+        # with fence-free timing events, against the kernel trace). An empty pair, which
+        # costs more than the overhead it adds around a kernel, is reported, not subtracted.
+        pair_ms, pair_n = prof.pop("event_pair")
+        pair = pair_ms / max(pair_n, 1)
+        net = {k: v for k, v in prof.items() if v[1]}
+        tot_ms = sum(v[0] for v in net.values())
+        dom = max(net, key=lambda k: net[k][0])
+        ms, n = net[dom]
         per_launch = bytes_by_class[dom] / max(n, 1)
         avg_s = ms / max(n, 1) / 1e3
         achieved = per_launch / avg_s
+        traffic_b = recorded_traffic(CLASS_KERNELS.get(dom, [dom]))
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
-                    "kernel": dom, "bytes_per_launch": int(per_launch),
-                    "avg_launch_us": round(avg_s * 1e6, 2)}
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                    "traffic": round(traffic_b / 1e6, 3) if traffic_b else None,
+                    "traffic_unit": "MB per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                    "copy-calibrated)",
+                    "kernel": dom, "kernels": CLASS_KERNELS.get(dom, [dom]),
+                    "bytes_per_launch": int(per_launch), "avg_launch_us": round(avg_s * 1e6, 2),
+                    "empty_event_pair_us": round(pair * 1e3, 2)}
         all_bytes = sum(bytes_by_class.values())
         # whole-generation algorithmic bytes against the graph-replayed generation time
         step_frac = (all_bytes / (elapsed / args.steps)) / HBM_PEAK
         prof_detail = {k: {"ms": round(v[0], 3), "launches": v[1],
+                           "us_per_launch": round(v[0] / v[1] * 1e3, 2),
                            "GB_per_s": round(bytes_by_class[k] / max(v[0], 1e-9) / 1e6, 1)}
-                       for k, v in prof.items() if v[1]}
-        log(f"profiled eager generation: {psteps} steps, {tot_ms:.1f} ms kernel time, "
-            f"dominant {dom} {ms:.1f} ms")
+                       for k, v in net.items()}
+        log(f"profiled generation: {psteps} steps, {tot_ms:.1f} ms in timed spans (empty event "
+            f"pair {pair * 1e3:.2f} us), dominant {dom} {ms:.1f} ms")
         log("per-class: " + json.dumps(prof_detail))
 
     cpu = None

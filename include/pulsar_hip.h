@@ -202,16 +202,17 @@ typedef struct PulsarEngineConfig {
 #define PULSAR_BUF_ROWS 3      /* int32 [n_rows][8] rows of the next step
                                   (seq, slot, pulse, pos, token, lrow, extra, 0) */
 #define PULSAR_BUF_CTL 4       /* int32 [16] n_rows, n_lrows, pulse_start[4],
-                                  pulse_count[4], active, step */
+                                  pulse_count[4], active, step, n_units */
 #define PULSAR_BUF_LAST_ROWS 5 /* int32 [n_rows][8] rows of the last executed step */
 #define PULSAR_BUF_LAST_CTL 6  /* int32 [16] control block of the last executed step */
 #define PULSAR_BUF_EXPERT_COUNTS 7 /* int32 [n_layers][E] rows routed to each expert, last step */
 
 /* Kernel classes of the per-class timing (pulsar_engine_profile_read). */
-#define PULSAR_PROF_CLASSES 16
+#define PULSAR_PROF_CLASSES 17
 /* 0 pulse input, 1 rmsnorm, 2 qkv+gate GEMM, 3 qk-norm/rope/KV write, 4 attention,
  * 5 wo GEMM, 6 router, 7 shared gate/up, 8 routed gate/up, 9 shared down, 10 routed down,
- * 11 MoE combine, 12 pulse output, 13 lm_head, 14 sampling, 15 controller */
+ * 11 MoE combine, 12 pulse output, 13 lm_head, 14 sampling, 15 controller,
+ * 16 an empty event pair (the timing overhead included in every other class's span) */
 
 int pulsar_engine_create(const PulsarModelDesc* model, const PulsarEngineConfig* cfg,
                          void** handle);
@@ -229,7 +230,9 @@ int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
  * drawn again from the saved prefill logits. Synchronises the stream. */
 int pulsar_engine_rewind(void* handle, uint64_t seed, hipStream_t stream);
 /* Enable (1) or disable (0) per-class event timing; steps then run eagerly (no graph) with
- * a HIP event pair around every kernel launch. Enabling resets the counters. */
+ * a HIP event pair around every kernel group, preceded by a short fixed-length sleep
+ * kernel so that the pair brackets the kernels rather than host launch latency.
+ * Enabling resets the counters. */
 int pulsar_engine_profile(void* handle, int32_t enable);
 /* Accumulated milliseconds and launch counts per class, [PULSAR_PROF_CLASSES] each. */
 int pulsar_engine_profile_read(void* handle, double* host_ms, int64_t* host_launches);

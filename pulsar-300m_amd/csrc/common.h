@@ -22,15 +22,21 @@ __host__ __device__ __forceinline__ float bf2f(bf16 v) {
   return __uint_as_float(static_cast<uint32_t>(v.u) << 16);
 }
 
+// Round to nearest even. On the device this is gfx950's v_cvt_pk_bf16_f32 (no branches);
+// the host form is the same rounding in integer arithmetic.
 __host__ __device__ __forceinline__ bf16 f2bf(float f) {
-  uint32_t x = __float_as_uint(f);
   bf16 r;
+#if defined(__HIP_DEVICE_COMPILE__)
+  r.u = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+#else
+  uint32_t x = __float_as_uint(f);
   if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x007fffffu)) {
     r.u = 0x7fc0;  // quiet NaN
     return r;
   }
   x += 0x7fffu + ((x >> 16) & 1u);
   r.u = static_cast<uint16_t>(x >> 16);
+#endif
   return r;
 }
 

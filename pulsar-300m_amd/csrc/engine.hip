@@ -129,8 +129,9 @@ void kv_desc(Engine& e) {
 int prof_mark(Engine& e, hipStream_t s) {
   if (!e.prof_on) return -1;
   if (e.ev_used == (int)e.ev_pool.size()) {
+    // timing-only events: no system-scope cache writeback/invalidate around the kernels
     hipEvent_t ev;
-    if (hipEventCreate(&ev) != hipSuccess) return -1;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess) return -1;
     e.ev_pool.push_back(ev);
   }
   const int i = e.ev_used++;
@@ -156,8 +157,23 @@ int prof_collect(Engine& e, hipStream_t s) {
   return PULSAR_OK;
 }
 
+// Profiling runs eagerly; a fixed-length sleep kernel ahead of each timed group keeps the
+// device busy while the host enqueues the group's start event, kernels and end event, so
+// the span measures the kernels, not host launch latency.
+__global__ void prof_delay_kernel(int n) {
+  for (int i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(127);
+}
+
+int prof_delay(Engine& e, hipStream_t s) {
+  if (!e.prof_on) return PULSAR_OK;
+  prof_delay_kernel<<<1, 64, 0, s>>>(12);
+  PULSAR_LAUNCH_CHECK();
+  return PULSAR_OK;
+}
+
 #define PULSAR_TIMED(cls, expr)          \
   do {                                   \
+    PULSAR_TRY(prof_delay(e, s));        \
     const int _a = prof_mark(e, s);      \
     PULSAR_TRY(expr);                    \
     prof_span(e, (cls), _a, prof_mark(e, s)); \
@@ -166,7 +182,7 @@ int prof_collect(Engine& e, hipStream_t s) {
 enum ProfClass {
   PC_INPUT = 0, PC_NORM, PC_QKVG, PC_QKPOST, PC_ATTN, PC_WO, PC_ROUTER, PC_SHARED_GU,
   PC_ROUTED_GU, PC_SHARED_DOWN, PC_ROUTED_DOWN, PC_COMBINE, PC_OUTPUT, PC_LMHEAD, PC_SAMPLE,
-  PC_CONTROL
+  PC_CONTROL, PC_EVENT_PAIR
 };
 
 int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) {
@@ -287,6 +303,12 @@ GemmArgs gemm_base(const Engine& e) {
 int enqueue_step(Engine& e, hipStream_t s) {
   const PulsarModelDesc& m = e.m;
   const int D = e.D, MR = e.max_rows, dt = e.dtype;
+  if (e.prof_on) {
+    // an empty timed group: the fixed cost of an event pair around a kernel launch
+    PULSAR_TRY(prof_delay(e, s));
+    const int _a = prof_mark(e, s);
+    prof_span(e, PC_EVENT_PAIR, _a, prof_mark(e, s));
+  }
   PulseInputArgs pi{};
   pi.ctl = e.ctl;
   pi.rows = e.rows;
@@ -526,6 +548,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   sa.out_argmax = e.argmax;
   sa.out_draw = e.draw;
   PULSAR_TIMED(PC_SAMPLE, launch_sample(sa, dt, MR, s));
+  PULSAR_TRY(prof_delay(e, s));
   const int _pc = prof_mark(e, s);
   ControllerArgs co{};
   co.last_ctl = e.last_ctl;
@@ -886,6 +909,24 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   return PULSAR_OK;
 }
 
+// Capture one step into a graph (on the engine's own stream; launched on the caller's).
+int capture_step(Engine& e, hipGraph_t* graph, hipGraphExec_t* exec) {
+  hipStream_t cs = e.capture_stream;
+  PULSAR_CHECK_HIP(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
+  const int rc = enqueue_step(e, cs);
+  hipGraph_t gr = nullptr;
+  const hipError_t ce = hipStreamEndCapture(cs, &gr);
+  if (rc != PULSAR_OK) {
+    if (gr) hipGraphDestroy(gr);
+    return rc;
+  }
+  if (ce != hipSuccess)
+    return fail(PULSAR_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce));
+  *graph = gr;
+  PULSAR_CHECK_HIP(hipGraphInstantiate(exec, gr, nullptr, nullptr, 0));
+  return PULSAR_OK;
+}
+
 int step(Engine& e, int n, int use_graph, hipStream_t s) {
   PULSAR_REQUIRE(e.prefilled, "engine: prefill before stepping");
   if (!use_graph || e.prof_on) {
@@ -895,21 +936,7 @@ int step(Engine& e, int n, int use_graph, hipStream_t s) {
     }
     return PULSAR_OK;
   }
-  if (!e.exec) {
-    // Capture records work without running it; the graph is then launched on `s`.
-    hipStream_t cs = e.capture_stream;
-    PULSAR_CHECK_HIP(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
-    const int rc = enqueue_step(e, cs);
-    hipGraph_t gr = nullptr;
-    const hipError_t ce = hipStreamEndCapture(cs, &gr);
-    if (rc != PULSAR_OK) {
-      if (gr) hipGraphDestroy(gr);
-      return rc;
-    }
-    if (ce != hipSuccess) return fail(PULSAR_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce));
-    e.graph = gr;
-    PULSAR_CHECK_HIP(hipGraphInstantiate(&e.exec, gr, nullptr, nullptr, 0));
-  }
+  if (!e.exec) PULSAR_TRY(capture_step(e, &e.graph, &e.exec));
   for (int i = 0; i < n; ++i) PULSAR_CHECK_HIP(hipGraphLaunch(e.exec, s));
   return PULSAR_OK;
 }

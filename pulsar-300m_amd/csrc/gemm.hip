@@ -132,48 +132,49 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, int epi, int group, 
   }
 }
 
-// Rows of group `group` in the row set: count and the (A row, C row) of entry i.
-__device__ __forceinline__ int group_count(const GemmArgs& g, int mode, int group) {
-  switch (mode) {
-    case ROWS_PULSE: return g.ctl->pulse_count[group];
-    case ROWS_LIST: return g.list_count[group];
-    case ROWS_ALL: return g.ctl ? g.ctl->n_rows : g.m_fixed;
-    default: return g.ctl->n_lrows;
+// Entry i of the group: the row index (pulse / all / logits modes) or the assignment id
+// (list mode; the all-rows group -1 of a fused launch takes row i). Branch-free in the row
+// mode, which is a template parameter: a load pending on one path of a runtime switch
+// would make the join wait for every load in flight, weights included.
+template <int MODE>
+__device__ __forceinline__ int entry_load(const GemmArgs& g, int group, int i) {
+  if constexpr (MODE == ROWS_PULSE) return g.ctl->pulse_start[group] + i;
+  if constexpr (MODE == ROWS_LIST) return g.list[(int64_t)max(group, 0) * g.list_stride + i];
+  return i;
+}
+// Applied after the weight loads are issued (the only use of the loaded value).
+template <int MODE>
+__device__ __forceinline__ int entry_fix(int group, int i, int v) {
+  if constexpr (MODE == ROWS_LIST) return group < 0 ? i : v;
+  return v;
+}
+template <int MODE>
+__device__ __forceinline__ int a_row_of(const GemmArgs& g, int group, int raw) {
+  if constexpr (MODE == ROWS_LIST) return group < 0 ? raw : raw / g.a_div;
+  return raw;
+}
+template <int MODE>
+__device__ __forceinline__ int group_rows(const GemmArgs& g, int group) {
+  if constexpr (MODE == ROWS_PULSE) return g.ctl->pulse_count[group];
+  if constexpr (MODE == ROWS_LOGITS) return g.ctl->n_lrows;
+  if constexpr (MODE == ROWS_LIST) {
+    if (group >= 0) return g.list_count[group];
   }
+  return g.ctl ? g.ctl->n_rows : g.m_fixed;
 }
 
-__device__ __forceinline__ void entry_rows(const GemmArgs& g, int mode, int group, int i, int& ar,
-                                           int& cr) {
-  switch (mode) {
-    case ROWS_PULSE:
-      ar = cr = g.ctl->pulse_start[group] + i;
-      break;
-    case ROWS_LIST: {
-      const int e = g.list[(int64_t)group * g.list_stride + i];
-      ar = e / g.a_div;
-      cr = e;
-      break;
-    }
-    default:
-      ar = cr = i;
-      break;
-  }
-  cr += g.c_row_offset;
-}
-
-template <int EPI, int KITER>
+template <int EPI, int KITER, int MODE>
 __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
   __shared__ float red[3][64][kPair ? 16 : 8];
   // grid.y == 0 is the optional all-rows group (group -1) when has_g0 is set
   const int group = (int)blockIdx.y + g.group_offset - (g.has_g0 ? 1 : 0);
   const bool g0 = group < 0;
-  const int mode = g0 ? ROWS_ALL : g.row_mode;
   const int N = g0 ? g.N0 : g.N;
   const int col0 = blockIdx.x * 16;
   if (col0 >= N) return;
   const int tile0 = blockIdx.z * 32;
-  const int n = min(32, group_count(g, mode, group) - tile0);  // uniform per workgroup
+  const int n = min(32, group_rows<MODE>(g, group) - tile0);  // uniform per workgroup
   if (n <= 0) return;
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -185,8 +186,14 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
   const bf16* w0 = W + (int64_t)(vc ? col0 + m : 0) * ldw;
   const bf16* w1 = W + (int64_t)(vc ? N + col0 + m : 0) * ldw;
 
-  // Weight loads first: they depend only on the group, so their latency overlaps the row
-  // lookup below. Every load of this wave's K quarter is in flight before the first MFMA.
+  // Row entries first, then the weights, then (after a scheduling barrier) the A rows:
+  // vector loads retire in issue order, so waiting for the few entry loads leaves every
+  // weight load of this wave's K quarter in flight. Lanes past the last row re-read the
+  // last entry (always in bounds) and use a zero A operand.
+  const bool two = n > 16;  // second 16-row block present (uniform per workgroup)
+  const int i0 = tile0 + min(m, n - 1), i1 = tile0 + min(m + 16, n - 1);
+  const int l0 = entry_load<MODE>(g, group, i0);
+  const int l1 = entry_load<MODE>(g, group, i1);
   const int kb = wv * (KITER * 32) + kq * 8;
   bf16x8_t bw[KITER], bu[KITER], xa[KITER], xb[KITER];
 #pragma unroll
@@ -194,10 +201,10 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
     bw[i] = load_bf16x8(w0 + kb + 32 * i);
     if constexpr (kPair) bu[i] = load_bf16x8(w1 + kb + 32 * i);
   }
-  const bool two = n > 16;  // second 16-row block present (uniform per workgroup)
-  int ar0 = -1, ar1 = -1, cdummy;
-  if (m < n) entry_rows(g, mode, group, tile0 + m, ar0, cdummy);
-  if (m + 16 < n) entry_rows(g, mode, group, tile0 + m + 16, ar1, cdummy);
+  __builtin_amdgcn_sched_barrier(0);
+  const int e0 = entry_fix<MODE>(group, i0, l0), e1 = entry_fix<MODE>(group, i1, l1);
+  const int ar0 = m < n ? a_row_of<MODE>(g, group, e0) : -1;
+  const int ar1 = m + 16 < n ? a_row_of<MODE>(g, group, e1) : -1;
   const bf16* A = reinterpret_cast<const bf16*>(g0 ? g.A0 : g.A);
   const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * lda;
   const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * lda;
@@ -247,23 +254,23 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
       }
     }
   }
-  // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16.
+  // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16; the C row of
+  // tile row r is the entry held by lane r (rows 0-15: e0, 16-31: e1).
   const int col = col0 + m;
+  int ce0[4], ce1[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ce0[j] = __shfl(e0, kq * 4 + j, 64);
+    ce1[j] = __shfl(e1, kq * 4 + j, 64);
+  }
   if (!vc) return;
   void* Cout = g0 ? g.C0 : g.C;
   const int64_t ldc = g0 ? g.ldc0 : g.ldc;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r0 = kq * 4 + j, r1 = 16 + kq * 4 + j;
-    int ar, cr;
-    if (r0 < n) {
-      entry_rows(g, mode, group, tile0 + r0, ar, cr);
-      epilogue<bf16>(g, EPI, group, Cout, ldc, cr, col, c00[j], c01[j]);
-    }
-    if (r1 < n) {
-      entry_rows(g, mode, group, tile0 + r1, ar, cr);
-      epilogue<bf16>(g, EPI, group, Cout, ldc, cr, col, c10[j], c11[j]);
-    }
+    if (r0 < n) epilogue<bf16>(g, EPI, group, Cout, ldc, ce0[j] + g.c_row_offset, col, c00[j], c01[j]);
+    if (r1 < n) epilogue<bf16>(g, EPI, group, Cout, ldc, ce1[j] + g.c_row_offset, col, c10[j], c11[j]);
   }
 }
 
@@ -306,6 +313,16 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
   }
 }
 
+template <int EPI, int MODE>
+void launch_bf16(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  switch (a.K) {
+    case 256: gemm_bf16_kernel<EPI, 2, MODE><<<grid, 256, 0, s>>>(a); break;
+    case 512: gemm_bf16_kernel<EPI, 4, MODE><<<grid, 256, 0, s>>>(a); break;
+    case 1024: gemm_bf16_kernel<EPI, 8, MODE><<<grid, 256, 0, s>>>(a); break;
+    default: gemm_bf16_kernel<EPI, 16, MODE><<<grid, 256, 0, s>>>(a); break;
+  }
+}
+
 template <int EPI>
 int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream_t s) {
   const int tiles = (max_rows + 31) / 32;
@@ -313,13 +330,17 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
   const int gy = groups + (a.has_g0 ? 1 : 0);
   const int nmax = a.has_g0 ? std::max(a.N, a.N0) : a.N;
   if (dtype == PULSAR_BF16) {
+    if (a.K != 256 && a.K != 512 && a.K != 1024 && a.K != 2048)
+      return fail(PULSAR_ERR_UNSUPPORTED, "gemm: K must be 256, 512, 1024 or 2048");
+    if (a.has_g0 && a.row_mode != ROWS_LIST)
+      return fail(PULSAR_ERR_INVALID, "gemm: the all-rows group fuses into list launches only");
     dim3 grid((unsigned)((nmax + 15) / 16), (unsigned)gy, (unsigned)tiles);
-    switch (a.K) {
-      case 256: gemm_bf16_kernel<EPI, 2><<<grid, 256, 0, s>>>(a); break;
-      case 512: gemm_bf16_kernel<EPI, 4><<<grid, 256, 0, s>>>(a); break;
-      case 1024: gemm_bf16_kernel<EPI, 8><<<grid, 256, 0, s>>>(a); break;
-      case 2048: gemm_bf16_kernel<EPI, 16><<<grid, 256, 0, s>>>(a); break;
-      default: return fail(PULSAR_ERR_UNSUPPORTED, "gemm: K must be 256, 512, 1024 or 2048");
+    switch (a.row_mode) {
+      case ROWS_PULSE: launch_bf16<EPI, ROWS_PULSE>(a, grid, s); break;
+      case ROWS_LIST: launch_bf16<EPI, ROWS_LIST>(a, grid, s); break;
+      case ROWS_ALL: launch_bf16<EPI, ROWS_ALL>(a, grid, s); break;
+      case ROWS_LOGITS: launch_bf16<EPI, ROWS_LOGITS>(a, grid, s); break;
+      default: return fail(PULSAR_ERR_INVALID, "gemm: row mode");
     }
   } else {
     dim3 grid((unsigned)((nmax + 3) / 4), (unsigned)gy, (unsigned)tiles);

@@ -632,15 +632,34 @@ __global__ void __launch_bounds__(256) attn_unit_combine_kernel(AttnArgs a) {
   const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int head = g * 4 + h;
   const float* p0 = a.part + (((int64_t)u * a.Hkv + g) * a.max_splits * 8 + z * 4 + h) * 66;
-  float M = -INFINITY;
-  for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, p0[(int64_t)sp * 8 * 66]);
-  float L = 0.f, O = 0.f;
-  for (int sp = 0; sp < nsplit; ++sp) {
-    const float* p = p0 + (int64_t)sp * 8 * 66;
-    if (p[0] == -INFINITY) continue;
-    const float f = expf(p[0] - M);
-    L += p[1] * f;
-    O += p[2 + lane] * f;
+  // splits in chunks of 8 whose loads are all in flight together (indices past the last
+  // split re-read it and are dropped)
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int c0 = 0; c0 < nsplit; c0 += 8) {
+    float pm[8], pl[8], po[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float* p = p0 + (int64_t)min(c0 + k, nsplit - 1) * 8 * 66;
+      pm[k] = p[0];
+      pl[k] = p[1];
+      po[k] = p[2 + lane];
+    }
+    float cm = M;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (c0 + k < nsplit) cm = fmaxf(cm, pm[k]);
+    const float f0 = M == -INFINITY ? 0.f : expf(M - cm);
+    L *= f0;
+    O *= f0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (c0 + k < nsplit && pm[k] != -INFINITY) {
+        const float f = expf(pm[k] - cm);
+        L += pl[k] * f;
+        O += po[k] * f;
+      }
+    }
+    M = cm;
   }
   const float o = rnd<bf16>(O / L);
   const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
@@ -939,21 +958,32 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
     w[k] = a.topk_w[(int64_t)r * K + kk];
     kept[k] = a.keep ? a.keep[(int64_t)r * K + kk] != 0 : true;
   }
+  // K is uniform: one branch per top-k slot, the element loops inside
+  float routed[EPL];
 #pragma unroll
-  for (int c = 0; c < EPL; ++c) {
-    float routed = 0.f, mlp;
-    if (!a.prefill) {
+  for (int c = 0; c < EPL; ++c) routed[c] = 0.f;
+  if (!a.prefill) {
 #pragma unroll
-      for (int k = 0; k < KT; ++k)
-        if (k < K) routed = rnd<T>(routed + rnd<T>(ro[k][c] * w[k]));
-      mlp = rnd<T>(sh[c] + rnd<T>(routed * rs[c]));
-    } else {
+    for (int k = 0; k < KT; ++k) {
+      if (k < K) {
 #pragma unroll
-      for (int k = 0; k < KT; ++k)
-        if (k < K) routed = rnd<T>(routed + (kept[k] ? rnd<T>(w[k] * ro[k][c]) : 0.f));
-      mlp = rnd<T>(sh[c] + routed);
+        for (int c = 0; c < EPL; ++c) routed[c] = rnd<T>(routed[c] + rnd<T>(ro[k][c] * w[k]));
+      }
     }
-    hv[c] = rnd<T>(hv[c] + mlp);
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) hv[c] = rnd<T>(hv[c] + rnd<T>(sh[c] + rnd<T>(routed[c] * rs[c])));
+  } else {
+#pragma unroll
+    for (int k = 0; k < KT; ++k) {
+      if (k < K) {
+        const float wk = kept[k] ? w[k] : 0.f;
+#pragma unroll
+        for (int c = 0; c < EPL; ++c)
+          routed[c] = rnd<T>(routed[c] + (kept[k] ? rnd<T>(wk * ro[k][c]) : 0.f));
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) hv[c] = rnd<T>(hv[c] + rnd<T>(sh[c] + routed[c]));
   }
   stv<EPL>(h, hv);
   if (a.next_norm) {

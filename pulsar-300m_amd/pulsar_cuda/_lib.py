@@ -23,11 +23,11 @@ BUF_EXPERT_COUNTS = 7
 SEQSTATE_INTS = 20
 ROW_INTS = 8
 CTL_INTS = 16
-PROF_CLASSES = 16
+PROF_CLASSES = 17
 PROF_NAMES = (
     "pulse_input", "rmsnorm", "qkv_gate_gemm", "qk_post", "attention", "wo_gemm", "router",
     "shared_gate_up", "routed_gate_up", "shared_down", "routed_down", "moe_combine",
-    "pulse_output", "lm_head", "sample", "controller",
+    "pulse_output", "lm_head", "sample", "controller", "event_pair",
 )
 
 _c_i32 = ctypes.c_int32

@@ -92,7 +92,9 @@ class HipEngine:
         self.steps = 0
 
     def profile(self, enable: bool) -> None:
-        """Per-kernel-class HIP-event timing; steps run eagerly while enabled."""
+        """Per-kernel-class HIP-event timing; steps run eagerly while enabled, with a short
+        fixed sleep kernel ahead of each timed kernel group so that its events bracket the
+        kernels rather than host launch latency."""
         _lib.check(self.lib.pulsar_engine_profile(self.handle, int(bool(enable))))
 
     def profile_read(self) -> dict:

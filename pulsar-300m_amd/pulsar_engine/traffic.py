@@ -3,8 +3,8 @@
 The figure the roofline fraction is quoted against: every weight byte a step must read once
 (per-pulse projection variants once per pulse present in the step, routed experts once per
 expert that received at least one row, the tied output head once when any row needs
-logits), the KV entries each row attends to, and the activations each kernel reads and
-writes. Caches and re-reads are not counted; measured HBM traffic is reported beside it.
+logits), the KV entries each sequence's rows attend to (the union of their key ranges,
+read once), and the activations each kernel reads and writes. Caches and re-reads are not counted; measured HBM traffic is reported beside it.
 """
 
 from __future__ import annotations
@@ -34,9 +34,16 @@ def step_bytes(cfg: PulsarConfig, es: int, rows, expert_counts, n_lrows: int) ->
     npul = len(pulses)
     r = cfg.reinject_gate_rank
     out["pulse_input"] = n * D * es * 4 + npul * (3 * r * D + 2 * D) * es
+    # decode attention reads each sequence's cache once for all of its rows in the step
+    # (the current token and the speculative token one position later share key blocks)
+    by_seq: dict[int, list[int]] = defaultdict(list)
+    for seq, _, pos in rows:
+        by_seq[seq].append(pos)
     for L in range(cfg.n_core):
         local = cfg.is_local(L)
-        ctx = sum(min(pos + 1, cfg.sliding_window) if local else pos + 1 for _, _, pos in rows)
+        W = cfg.sliding_window
+        ctx = sum(max(ps) - (max(0, min(ps) - W + 1) if local else 0) + 1
+                  for ps in by_seq.values())
         touched = int(sum(1 for c in expert_counts[L] if c > 0))
         assigned = int(sum(expert_counts[L]))
         out["rmsnorm"] += 2 * (n * D * es * 2 + npul * D * 4)

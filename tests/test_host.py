@@ -1,0 +1,115 @@
+"""Host-side logic on the CPU: the algorithmic traffic model and the profile summaries of
+bench.py (the measurement path), and the configuration mirror."""
+
+from __future__ import annotations
+
+import csv
+import importlib.util
+import os
+
+import pytest
+
+from pulsar_engine import traffic
+from pulsar_engine.config import PulsarConfig
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _bench():
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(ROOT, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_attention_bytes_count_a_sequences_key_blocks_once():
+    cfg = PulsarConfig()
+    es, hk, hd = 2, cfg.n_kv_heads, cfg.head_dim
+    counts = [[0] * cfg.n_routed_experts for _ in range(cfg.n_core)]
+    pos = 3000
+    one = traffic.step_bytes(cfg, es, [(0, 2, pos)], counts, 1)["attention"]
+    two = traffic.step_bytes(cfg, es, [(0, 2, pos), (0, 0, pos + 1)], counts, 2)["attention"]
+    W = cfg.sliding_window
+    n_local = sum(cfg.is_local(L) for L in range(cfg.n_core))
+    n_global = cfg.n_core - n_local
+    kv = lambda keys: keys * hk * hd * 2 * es  # noqa: E731
+    act = cfg.q_dim + cfg.n_heads + cfg.q_dim
+    assert one == n_local * kv(W) + n_global * kv(pos + 1) + cfg.n_core * act * es
+    # the speculative row adds one key per layer and its own activations, not a second cache read
+    assert two - one == n_local * kv(1) + n_global * kv(1) + cfg.n_core * act * es
+    # two different sequences read two caches
+    other = traffic.step_bytes(cfg, es, [(0, 2, pos), (1, 0, pos + 1)], counts, 2)["attention"]
+    assert other - one == n_local * kv(W) + n_global * kv(pos + 2) + cfg.n_core * act * es
+
+
+def test_weight_bytes_follow_pulses_and_touched_experts():
+    cfg = PulsarConfig()
+    es = 2
+    counts = [[0] * cfg.n_routed_experts for _ in range(cfg.n_core)]
+    for L in range(cfg.n_core):
+        counts[L][3] = 2
+    b1 = traffic.step_bytes(cfg, es, [(0, 1, 10), (1, 1, 10)], counts, 0)
+    b2 = traffic.step_bytes(cfg, es, [(0, 1, 10), (1, 0, 10)], counts, 0)
+    per_pulse_qkv = cfg.n_core * (cfg.qkv_dim + cfg.n_heads) * cfg.d_model * es
+    assert b2["qkv_gate_gemm"] - b1["qkv_gate_gemm"] == per_pulse_qkv
+    assert b1["routed_gate_up"] == cfg.n_core * (2 * cfg.d_expert * cfg.d_model * es
+                                                 + 2 * (cfg.d_model + cfg.d_expert) * es)
+    assert "lm_head" not in b1
+    assert traffic.step_bytes(cfg, es, [(0, 2, 10)], counts, 1)["lm_head"] > cfg.vocab_size * cfg.d_model * es
+
+
+def _write_csv(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
+        w.writeheader()
+        w.writerows(rows)
+
+
+def test_rocprof_summary_keeps_decode_dispatches(tmp_path):
+    b = _bench()
+    rows = []
+    t = 0
+    for name, dur in [("void pulsar::attn_prefill_kernel<bf16>(pulsar::AttnArgs)", 900),
+                      ("pulsar::controller_kernel(pulsar::ControllerArgs)", 5),
+                      ("pulsar::attn_decode_mfma_kernel(pulsar::AttnArgs)", 10),
+                      ("pulsar::attn_decode_mfma_kernel(pulsar::AttnArgs)", 12),
+                      ("pulsar::controller_kernel(pulsar::ControllerArgs)", 6)]:
+        rows.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + dur * 1000})
+        t += dur * 1000 + 100
+    (tmp_path / "x").mkdir()
+    _write_csv(tmp_path / "x" / "run_kernel_trace.csv", rows)
+    out = b.rocprof_summary(str(tmp_path))
+    assert "attn_prefill" not in out
+    assert "| `attn_decode_mfma_kernel` | 2 | 11.00 |" in out
+    assert "| `controller_kernel` | 1 | 6.00 |" in out
+
+
+def test_pmc_summary_calibrates_and_feeds_traffic(tmp_path, monkeypatch):
+    b = _bench()
+    for ctr, per_copy, per_kernel in (("FETCH_SIZE", 131072.0, 1000.0), ("WRITE_SIZE", 262144.0, 50.0)):
+        d = tmp_path / ctr
+        d.mkdir()
+        _write_csv(d / "bench_counter_collection.csv", [
+            {"Kernel_Name": "pulsar::controller_kernel(x)", "Counter_Value": 1.0},
+            {"Kernel_Name": "pulsar::attn_decode_mfma_kernel(x)", "Counter_Value": per_kernel},
+            {"Kernel_Name": "pulsar::attn_decode_mfma_kernel(x)", "Counter_Value": per_kernel * 3}])
+        c = tmp_path / (ctr + "_copy")
+        c.mkdir()
+        _write_csv(c / "copy_counter_collection.csv", [
+            {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Value": per_copy}])
+    out = b.pmc_summary(str(tmp_path / "FETCH_SIZE"), str(tmp_path / "WRITE_SIZE"),
+                        str(tmp_path / "FETCH_SIZE_copy"), str(tmp_path / "WRITE_SIZE_copy"), 256)
+    assert "scale factor 2.0000" in out and "scale factor 1.0000" in out
+    prof = tmp_path / "traffic.md"
+    prof.write_text(out)
+    monkeypatch.setattr(b, "TRAFFIC_PROFILE", str(prof))
+    # fetch: mean 2000 KiB x 2 (calibration) ; write: mean 100 KiB x 1
+    assert b.recorded_traffic(["attn_decode_mfma_kernel"]) == 4000 * 1024 + 100 * 1024
+    assert b.recorded_traffic(["not_profiled"]) is None
+
+
+def test_config_from_dict_keeps_reference_names():
+    cfg = PulsarConfig.from_dict({"d_model": 512, "n_heads": 8, "n_kv_heads": 2})
+    assert (cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim) == (512, 8, 2, 64)
+    with pytest.warns(RuntimeWarning):
+        PulsarConfig.from_dict({"not_a_field": 1})
