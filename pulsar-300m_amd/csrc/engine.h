@@ -91,6 +91,7 @@ struct GemmArgs {
   // Optional extra group 0 computed over all rows with its own operands (the shared expert
   // fused into the routed-expert launch); list groups then start at grid.y == 1.
   int has_g0;
+  int K0;                  // K of group 0 (K or 2K)
   const void* A0;
   int64_t lda0;
   const void* W0;

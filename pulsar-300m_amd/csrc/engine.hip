@@ -441,6 +441,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.a_div = e.K;
     g.ctl = e.ctl;
     g.has_g0 = 1;
+    g.K0 = D;
     g.A0 = e.xn;
     g.lda0 = D;
     g.W0 = m.shared_gu[l];
@@ -466,8 +467,9 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.list_stride = lstride;
     g.a_div = 1;
     g.ctl = e.ctl;
-    if (e.ds == e.de) {
+    if (e.ds == e.de || e.ds == 2 * e.de) {
       g.has_g0 = 1;
+      g.K0 = e.ds;
       g.A0 = e.act_s;
       g.lda0 = e.ds;
       g.W0 = m.shared_down[l];
@@ -477,7 +479,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
       g.N0 = D;
       PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
     } else {
-      // the fused launch shares K between groups; different widths take two launches
+      // the fused launch takes K0 = K or 2K for the shared group; other widths: two launches
       PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
       GemmArgs gs = gemm_base(e);
       gs.A = e.act_s;

@@ -158,14 +158,22 @@ __device__ __forceinline__ int group_rows(const GemmArgs& g, int group) {
   if constexpr (MODE == ROWS_PULSE) return g.ctl->pulse_count[group];
   if constexpr (MODE == ROWS_LOGITS) return g.ctl->n_lrows;
   if constexpr (MODE == ROWS_LIST) {
-    if (group >= 0) return g.list_count[group];
+    // the fused all-rows group (-1) exists only in launches with a step control block
+    return group >= 0 ? g.list_count[group] : g.ctl->n_rows;
   }
   return g.ctl ? g.ctl->n_rows : g.m_fixed;
 }
 
-template <int EPI, int KITER, int MODE>
+// Workgroup: 16 output columns of one group; 4 waves split K. The workgroup walks the
+// group's 32-row tiles z, z + gridDim.z, ... keeping its weight slice in registers, so a
+// launch needs only as many workgroups along z as the largest row set needs for
+// parallelism (one for decode batches of up to 32 rows per group). KMUL0 > 1: the
+// all-rows group has K0 = KMUL0 * K and runs KMUL0 passes over K-slices (the shared expert
+// down projection fused into the routed one).
+template <int EPI, int KITER, int MODE, int KMUL0>
 __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
+  constexpr int kKPass = KITER * 128;  // K covered by one pass of the 4 waves
   __shared__ float red[3][64][kPair ? 16 : 8];
   // grid.y == 0 is the optional all-rows group (group -1) when has_g0 is set
   const int group = (int)blockIdx.y + g.group_offset - (g.has_g0 ? 1 : 0);
@@ -173,9 +181,8 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
   const int N = g0 ? g.N0 : g.N;
   const int col0 = blockIdx.x * 16;
   if (col0 >= N) return;
-  const int tile0 = blockIdx.z * 32;
-  const int n = min(32, group_rows<MODE>(g, group) - tile0);  // uniform per workgroup
-  if (n <= 0) return;
+  const int cnt = group_rows<MODE>(g, group);  // uniform per workgroup
+  if ((int)blockIdx.z * 32 >= cnt) return;
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = lane & 15, kq = lane >> 4;
@@ -185,93 +192,116 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
   const bool vc = col0 + m < N;  // columns past N (last tile) read row 0 and are dropped
   const bf16* w0 = W + (int64_t)(vc ? col0 + m : 0) * ldw;
   const bf16* w1 = W + (int64_t)(vc ? N + col0 + m : 0) * ldw;
-
-  // Row entries first, then the weights, then (after a scheduling barrier) the A rows:
-  // vector loads retire in issue order, so waiting for the few entry loads leaves every
-  // weight load of this wave's K quarter in flight. Lanes past the last row re-read the
-  // last entry (always in bounds) and use a zero A operand.
-  const bool two = n > 16;  // second 16-row block present (uniform per workgroup)
-  const int i0 = tile0 + min(m, n - 1), i1 = tile0 + min(m + 16, n - 1);
-  const int l0 = entry_load<MODE>(g, group, i0);
-  const int l1 = entry_load<MODE>(g, group, i1);
-  const int kb = wv * (KITER * 32) + kq * 8;
-  bf16x8_t bw[KITER], bu[KITER], xa[KITER], xb[KITER];
-#pragma unroll
-  for (int i = 0; i < KITER; ++i) {
-    bw[i] = load_bf16x8(w0 + kb + 32 * i);
-    if constexpr (kPair) bu[i] = load_bf16x8(w1 + kb + 32 * i);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  const int e0 = entry_fix<MODE>(group, i0, l0), e1 = entry_fix<MODE>(group, i1, l1);
-  const int ar0 = m < n ? a_row_of<MODE>(g, group, e0) : -1;
-  const int ar1 = m + 16 < n ? a_row_of<MODE>(g, group, e1) : -1;
   const bf16* A = reinterpret_cast<const bf16*>(g0 ? g.A0 : g.A);
-  const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * lda;
-  const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * lda;
-  const bf16x8_t zero = {};
-#pragma unroll
-  for (int i = 0; i < KITER; ++i) {
-    xa[i] = ar0 >= 0 ? load_bf16x8(a0 + kb + 32 * i) : zero;
-    if (two) xb[i] = ar1 >= 0 ? load_bf16x8(a1 + kb + 32 * i) : zero;
-  }
-  f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
-#pragma unroll
-  for (int i = 0; i < KITER; ++i) {
-    c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[i], c00, 0, 0, 0);
-    if constexpr (kPair) c01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bu[i], c01, 0, 0, 0);
-  }
-  if (two) {
-#pragma unroll
-    for (int i = 0; i < KITER; ++i) {
-      c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[i], bw[i], c10, 0, 0, 0);
-      if constexpr (kPair) c11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[i], bu[i], c11, 0, 0, 0);
-    }
-  }
-  if (wv > 0) {
-    float* r = red[wv - 1][lane];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      r[j] = c00[j];
-      r[4 + j] = c10[j];
-      if constexpr (kPair) {
-        r[8 + j] = c01[j];
-        r[12 + j] = c11[j];
-      }
-    }
-  }
-  __syncthreads();
-  if (wv != 0) return;
-#pragma unroll
-  for (int w = 0; w < 3; ++w) {
-    const float* r = red[w][lane];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      c00[j] += r[j];
-      c10[j] += r[4 + j];
-      if constexpr (kPair) {
-        c01[j] += r[8 + j];
-        c11[j] += r[12 + j];
-      }
-    }
-  }
-  // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16; the C row of
-  // tile row r is the entry held by lane r (rows 0-15: e0, 16-31: e1).
-  const int col = col0 + m;
-  int ce0[4], ce1[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    ce0[j] = __shfl(e0, kq * 4 + j, 64);
-    ce1[j] = __shfl(e1, kq * 4 + j, 64);
-  }
-  if (!vc) return;
   void* Cout = g0 ? g.C0 : g.C;
   const int64_t ldc = g0 ? g.ldc0 : g.ldc;
+  const int passes = g0 ? KMUL0 : 1;
+  const int kb = wv * (KITER * 32) + kq * 8;
+  const bf16x8_t zero = {};
+  bf16x8_t bw[KITER], bu[KITER], xa[KITER], xb[KITER];
+#define PULSAR_LOAD_W(pass)                                                              \
+  do {                                                                                   \
+    _Pragma("unroll") for (int i = 0; i < KITER; ++i) {                                  \
+      bw[i] = load_bf16x8(w0 + (pass) * kKPass + kb + 32 * i);                           \
+      if constexpr (kPair) bu[i] = load_bf16x8(w1 + (pass) * kKPass + kb + 32 * i);      \
+    }                                                                                    \
+  } while (0)
+
+  // Row entries of the first tile first, then the weights, then (after a scheduling
+  // barrier) the A rows: vector loads retire in issue order, so waiting for the few entry
+  // loads leaves every weight load in flight. Lanes past the last row re-read the last
+  // entry (always in bounds) and use a zero A operand.
+  int tile0 = blockIdx.z * 32;
+  int n = min(32, cnt - tile0);
+  int i0 = tile0 + min(m, n - 1), i1 = tile0 + min(m + 16, n - 1);
+  int l0 = entry_load<MODE>(g, group, i0);
+  int l1 = entry_load<MODE>(g, group, i1);
+  PULSAR_LOAD_W(0);
+  while (true) {
+    __builtin_amdgcn_sched_barrier(0);
+    const bool two = n > 16;  // second 16-row block present (uniform per workgroup)
+    const int e0 = entry_fix<MODE>(group, i0, l0), e1 = entry_fix<MODE>(group, i1, l1);
+    const int ar0 = m < n ? a_row_of<MODE>(g, group, e0) : -1;
+    const int ar1 = m + 16 < n ? a_row_of<MODE>(g, group, e1) : -1;
+    const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * lda;
+    const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * lda;
+    f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
+    for (int pass = 0; pass < passes; ++pass) {
+      if (pass > 0) PULSAR_LOAD_W(pass);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r0 = kq * 4 + j, r1 = 16 + kq * 4 + j;
-    if (r0 < n) epilogue<bf16>(g, EPI, group, Cout, ldc, ce0[j] + g.c_row_offset, col, c00[j], c01[j]);
-    if (r1 < n) epilogue<bf16>(g, EPI, group, Cout, ldc, ce1[j] + g.c_row_offset, col, c10[j], c11[j]);
+      for (int i = 0; i < KITER; ++i) {
+        xa[i] = ar0 >= 0 ? load_bf16x8(a0 + pass * kKPass + kb + 32 * i) : zero;
+        if (two) xb[i] = ar1 >= 0 ? load_bf16x8(a1 + pass * kKPass + kb + 32 * i) : zero;
+      }
+#pragma unroll
+      for (int i = 0; i < KITER; ++i) {
+        c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[i], c00, 0, 0, 0);
+        if constexpr (kPair) c01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bu[i], c01, 0, 0, 0);
+      }
+      if (two) {
+#pragma unroll
+        for (int i = 0; i < KITER; ++i) {
+          c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[i], bw[i], c10, 0, 0, 0);
+          if constexpr (kPair) c11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[i], bu[i], c11, 0, 0, 0);
+        }
+      }
+    }
+    if (wv > 0) {
+      float* r = red[wv - 1][lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        r[j] = c00[j];
+        r[4 + j] = c10[j];
+        if constexpr (kPair) {
+          r[8 + j] = c01[j];
+          r[12 + j] = c11[j];
+        }
+      }
+    }
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+      for (int w = 0; w < 3; ++w) {
+        const float* r = red[w][lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c00[j] += r[j];
+          c10[j] += r[4 + j];
+          if constexpr (kPair) {
+            c01[j] += r[8 + j];
+            c11[j] += r[12 + j];
+          }
+        }
+      }
+      // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16; the C row
+      // of tile row r is the entry held by lane r (rows 0-15: e0, 16-31: e1).
+      const int col = col0 + m;
+      int ce0[4], ce1[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ce0[j] = __shfl(e0, kq * 4 + j, 64);
+        ce1[j] = __shfl(e1, kq * 4 + j, 64);
+      }
+      if (vc) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r0 = kq * 4 + j, r1 = 16 + kq * 4 + j;
+          if (r0 < n) epilogue<bf16>(g, EPI, group, Cout, ldc, ce0[j] + g.c_row_offset, col, c00[j], c01[j]);
+          if (r1 < n) epilogue<bf16>(g, EPI, group, Cout, ldc, ce1[j] + g.c_row_offset, col, c10[j], c11[j]);
+        }
+      }
+    }
+    tile0 += (int)gridDim.z * 32;
+    if (tile0 >= cnt) break;
+    __syncthreads();  // the partial sums in LDS are consumed before the next tile's writes
+    n = min(32, cnt - tile0);
+    i0 = tile0 + min(m, n - 1);
+    i1 = tile0 + min(m + 16, n - 1);
+    l0 = entry_load<MODE>(g, group, i0);
+    l1 = entry_load<MODE>(g, group, i1);
+    if (passes > 1) PULSAR_LOAD_W(0);
   }
+#undef PULSAR_LOAD_W
 }
 
 // fp32: 4 waves per workgroup, one output column per wave, 32-row tile.
@@ -295,10 +325,11 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
   const int64_t ldc = g0 ? g.ldc0 : g.ldc;
   const float* w0 = W + (int64_t)col * ldw;
   const float* w1 = W + (int64_t)(N + col) * ldw;
+  const int Kg = g0 ? g.K0 : g.K;
   for (int r = 0; r < n; ++r) {
     const float* a = A + (int64_t)a_row[r] * lda;
     float s0 = 0.f, s1 = 0.f;
-    for (int k = lane * 4; k < g.K; k += 256) {
+    for (int k = lane * 4; k < Kg; k += 256) {
       const float4 av = *reinterpret_cast<const float4*>(a + k);
       const float4 bv = *reinterpret_cast<const float4*>(w0 + k);
       s0 += av.x * bv.x + av.y * bv.y + av.z * bv.z + av.w * bv.w;
@@ -313,15 +344,18 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
   }
 }
 
-template <int EPI, int MODE>
-void launch_bf16(const GemmArgs& a, dim3 grid, hipStream_t s) {
+template <int EPI, int MODE, int KMUL0>
+void launch_bf16_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
   switch (a.K) {
-    case 256: gemm_bf16_kernel<EPI, 2, MODE><<<grid, 256, 0, s>>>(a); break;
-    case 512: gemm_bf16_kernel<EPI, 4, MODE><<<grid, 256, 0, s>>>(a); break;
-    case 1024: gemm_bf16_kernel<EPI, 8, MODE><<<grid, 256, 0, s>>>(a); break;
-    default: gemm_bf16_kernel<EPI, 16, MODE><<<grid, 256, 0, s>>>(a); break;
+    case 256: gemm_bf16_kernel<EPI, 2, MODE, KMUL0><<<grid, 256, 0, s>>>(a); break;
+    case 512: gemm_bf16_kernel<EPI, 4, MODE, KMUL0><<<grid, 256, 0, s>>>(a); break;
+    case 1024: gemm_bf16_kernel<EPI, 8, MODE, KMUL0><<<grid, 256, 0, s>>>(a); break;
+    default: gemm_bf16_kernel<EPI, 16, MODE, KMUL0><<<grid, 256, 0, s>>>(a); break;
   }
 }
+
+// Row tiles walked by one workgroup (weights stay in registers across them).
+constexpr int kTilesPerWorkgroup = 4;
 
 template <int EPI>
 int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream_t s) {
@@ -329,17 +363,27 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
   if (tiles <= 0 || groups <= 0) return PULSAR_OK;
   const int gy = groups + (a.has_g0 ? 1 : 0);
   const int nmax = a.has_g0 ? std::max(a.N, a.N0) : a.N;
+  const int k0 = a.has_g0 ? a.K0 : a.K;
   if (dtype == PULSAR_BF16) {
     if (a.K != 256 && a.K != 512 && a.K != 1024 && a.K != 2048)
       return fail(PULSAR_ERR_UNSUPPORTED, "gemm: K must be 256, 512, 1024 or 2048");
-    if (a.has_g0 && a.row_mode != ROWS_LIST)
-      return fail(PULSAR_ERR_INVALID, "gemm: the all-rows group fuses into list launches only");
-    dim3 grid((unsigned)((nmax + 15) / 16), (unsigned)gy, (unsigned)tiles);
+    if (a.has_g0 && (a.row_mode != ROWS_LIST || a.ctl == nullptr))
+      return fail(PULSAR_ERR_INVALID,
+                  "gemm: the all-rows group fuses into list launches with a control block only");
+    if (k0 != a.K && k0 != 2 * a.K)
+      return fail(PULSAR_ERR_UNSUPPORTED, "gemm: the all-rows group needs K0 = K or 2K");
+    const int gz = (tiles + kTilesPerWorkgroup - 1) / kTilesPerWorkgroup;
+    dim3 grid((unsigned)((nmax + 15) / 16), (unsigned)gy, (unsigned)gz);
     switch (a.row_mode) {
-      case ROWS_PULSE: launch_bf16<EPI, ROWS_PULSE>(a, grid, s); break;
-      case ROWS_LIST: launch_bf16<EPI, ROWS_LIST>(a, grid, s); break;
-      case ROWS_ALL: launch_bf16<EPI, ROWS_ALL>(a, grid, s); break;
-      case ROWS_LOGITS: launch_bf16<EPI, ROWS_LOGITS>(a, grid, s); break;
+      case ROWS_PULSE: launch_bf16_k<EPI, ROWS_PULSE, 1>(a, grid, s); break;
+      case ROWS_LIST:
+        if (k0 == a.K)
+          launch_bf16_k<EPI, ROWS_LIST, 1>(a, grid, s);
+        else
+          launch_bf16_k<EPI, ROWS_LIST, 2>(a, grid, s);
+        break;
+      case ROWS_ALL: launch_bf16_k<EPI, ROWS_ALL, 1>(a, grid, s); break;
+      case ROWS_LOGITS: launch_bf16_k<EPI, ROWS_LOGITS, 1>(a, grid, s); break;
       default: return fail(PULSAR_ERR_INVALID, "gemm: row mode");
     }
   } else {

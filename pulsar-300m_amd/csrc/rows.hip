@@ -55,7 +55,8 @@ __device__ __forceinline__ float lerp_ref(float s, float e, float w) {
 // Pulse input. pulse 0: stem (decode: embed, anchor norm, conv over one token) + step
 // embedding. pulse >= 1: rank-r re-injection gate on (anchor, state-normed previous pulse).
 // ---------------------------------------------------------------------------
-template <typename T, int EPL, int RT>
+// RT: rank bound of the re-injection gate; EXACT: the rank equals RT (no rank guards).
+template <typename T, int EPL, int RT, bool EXACT>
 __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
   // one wave per row; lane owns elements [lane*EPL, lane*EPL + EPL)
   const int lane = threadIdx.x;
@@ -99,7 +100,7 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
   } else {
     // rank-R re-injection: g = T(T(e . wd[j][:D]) + T(r . wd[j][D:])), mix = sigmoid(up g + b)
     const T* hp = reinterpret_cast<const T*>(a.hout_state) + (int64_t)st * D;
-    const int R = a.rank;
+    const int R = EXACT ? RT : a.rank;
     const T* wd = reinterpret_cast<const T*>(a.reinject_down) + (int64_t)rd.pulse * R * 2 * D;
     const T* wu = reinterpret_cast<const T*>(a.reinject_up) + (int64_t)rd.pulse * D * R;
     const T* bu = reinterpret_cast<const T*>(a.reinject_bias) + (int64_t)rd.pulse * D;
@@ -129,12 +130,12 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
         pr += rv[c] * wr[c];
       }
       gh[j] = 0.f;
-      if (j < R) gh[j] = rnd<T>(rnd<T>(wave_sum(pe)) + rnd<T>(wave_sum(pr)));
+      if (EXACT || j < R) gh[j] = rnd<T>(rnd<T>(wave_sum(pe)) + rnd<T>(wave_sum(pr)));
     }
 #pragma unroll
     for (int c = 0; c < EPL; ++c) {
       float wv[RT];
-      if (R == RT) {
+      if (EXACT) {
         ldv<RT>(wu + (int64_t)(i0 + c) * RT, wv);
       } else {
 #pragma unroll
@@ -143,7 +144,7 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
       float acc = 0.f;
 #pragma unroll
       for (int j = 0; j < RT; ++j)
-        if (j < R) acc += gh[j] * wv[j];
+        if (EXACT || j < R) acc += gh[j] * wv[j];
       const float mix = rnd<T>(sigmoidf_(rnd<T>(acc + bv[c])));
       hv[c] = rnd<T>(rnd<T>(lerp_ref(rv[c], ev[c], mix)) + stp[c]);
     }
@@ -1055,23 +1056,22 @@ __global__ void __launch_bounds__(256) pulse_output_kernel(PulseOutputArgs a) {
 int launch_pulse_input(const PulseInputArgs& a, int dtype, int max_rows, hipStream_t s) {
   if (a.rank < 1 || a.rank > kMaxRank)
     return fail(PULSAR_ERR_UNSUPPORTED, "pulse_input: reinject rank must be 1..16");
-  const bool r8 = a.rank <= 8;
-  if (dtype == PULSAR_BF16) {
-    if (r8) {
-#define K_(N) pulse_input_kernel<bf16, N, 8>
+  if (a.rank == 8) {
+    if (dtype == PULSAR_BF16) {
+#define K_(N) pulse_input_kernel<bf16, N, 8, true>
       PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 64, a);
 #undef K_
     }
-#define K_(N) pulse_input_kernel<bf16, N, 16>
+#define K_(N) pulse_input_kernel<float, N, 8, true>
     PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 64, a);
 #undef K_
   }
-  if (r8) {
-#define K_(N) pulse_input_kernel<float, N, 8>
+  if (dtype == PULSAR_BF16) {
+#define K_(N) pulse_input_kernel<bf16, N, 16, false>
     PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 64, a);
 #undef K_
   }
-#define K_(N) pulse_input_kernel<float, N, 16>
+#define K_(N) pulse_input_kernel<float, N, 16, false>
   PULSAR_EPL_DISPATCH(a.D, K_, dim3(max_rows), 64, a);
 #undef K_
 }

@@ -141,21 +141,28 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
   // no information in the low 16 key bits (all zero for positive, all one for negative
   // values, so equal high halves mean equal keys): the threshold search runs on the high
   // half there, 16 steps instead of 32, with the same kept set.
+  // The 16-bit keys of bf16 scores are stored two per register.
   constexpr int kLow = sizeof(T) == 2 ? 16 : 0;
+  constexpr int kPack = sizeof(T) == 2 ? 2 : 1;
   float pr[PER];
-  uint32_t key[PER];
+  uint32_t kw[PER / kPack];
+#pragma unroll
+  for (int i = 0; i < PER / kPack; ++i) kw[i] = 0u;
   float zl = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     pr[i] = expf(l[i] - mx);
-    key[i] = order_key(l[i]) >> kLow;
+    const uint32_t k = order_key(l[i]) >> kLow;
+    kw[i / kPack] |= kPack == 2 ? k << (16 * (i & 1)) : k;
     zl += pr[i];
   }
+#define KEY(i) (kPack == 2 ? (kw[(i) / kPack] >> (16 * ((i) & 1))) & 0xffffu : kw[(i) / kPack])
   const float Z = block_sum(zl, red);
   uint32_t kstar = 0;
   if (a.top_p < 1.0f) {
     // smallest m with mass(key > m) <= top_p * Z; the maximum's key always qualifies.
-    // One barrier per step: partials alternate between two LDS buffers.
+    // Bisection (per-step cost is the 32-element pass, so wider probes do not pay); one
+    // barrier per step: partials alternate between two LDS buffers.
     __shared__ float part[2][16];
     const float lim = a.top_p * Z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -165,7 +172,7 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
       const uint32_t mid = lo + ((hi - lo) >> 1);
       float f = 0.f;
 #pragma unroll
-      for (int i = 0; i < PER; ++i) f += key[i] > mid ? pr[i] : 0.f;
+      for (int i = 0; i < PER; ++i) f += KEY(i) > mid ? pr[i] : 0.f;
       f = wave_sum(f);
       if (lane == 0) part[buf][w] = f;
       __syncthreads();
@@ -183,7 +190,7 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
   int last_kept = -1;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    if (key[i] >= kstar) {
+    if (KEY(i) >= kstar) {
       own += pr[i];
       last_kept = base + i;
     }
@@ -203,7 +210,7 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
       int choice = -1;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        if (key[i] >= kstar) {
+        if (KEY(i) >= kstar) {
           run += pr[i];
           if (choice < 0 && target < run) choice = base + i;
         }
@@ -218,6 +225,7 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
     a.out_draw[lr * 2] = pick[0];
     a.out_draw[lr * 2 + 1] = pick[1];
   }
+#undef KEY
 }
 
 // ---------------------------------------------------------------------------
