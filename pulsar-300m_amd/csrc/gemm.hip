@@ -164,17 +164,20 @@ __device__ __forceinline__ int group_rows(const GemmArgs& g, int group) {
   return g.ctl ? g.ctl->n_rows : g.m_fixed;
 }
 
-// Workgroup: 16 output columns of one group; 4 waves split K. The workgroup walks the
+// Workgroup: 16 output columns of one group; 8 waves split K (few registers per wave, so
+// a launch's workgroups are resident at once). The workgroup walks the
 // group's 32-row tiles z, z + gridDim.z, ... keeping its weight slice in registers, so a
 // launch needs only as many workgroups along z as the largest row set needs for
 // parallelism (one for decode batches of up to 32 rows per group). KMUL0 > 1: the
 // all-rows group has K0 = KMUL0 * K and runs KMUL0 passes over K-slices (the shared expert
 // down projection fused into the routed one).
+constexpr int kGemmWaves = 8;
+
 template <int EPI, int KITER, int MODE, int KMUL0>
-__global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
-  constexpr int kKPass = KITER * 128;  // K covered by one pass of the 4 waves
-  __shared__ float red[3][64][kPair ? 16 : 8];
+  constexpr int kKPass = KITER * 32 * kGemmWaves;  // K covered by one pass of the waves
+  __shared__ float red[kGemmWaves][64][kPair ? 16 : 8];
   // grid.y == 0 is the optional all-rows group (group -1) when has_g0 is set
   const int group = (int)blockIdx.y + g.group_offset - (g.has_g0 ? 1 : 0);
   const bool g0 = group < 0;
@@ -246,8 +249,10 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
         }
       }
     }
-    if (wv > 0) {
-      float* r = red[wv - 1][lane];
+    // Partial tiles to LDS; then wave w reduces and stores tile value w of every lane:
+    // row block w / 4, accumulator element w % 4 (with its up-projection twin for SwiGLU).
+    {
+      float* r = red[wv][lane];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         r[j] = c00[j];
@@ -259,37 +264,20 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g) {
       }
     }
     __syncthreads();
-    if (wv == 0) {
+    {
+      static_assert(kGemmWaves == 8, "one tile value per wave");
+      const int blk = wv >> 2, j = wv & 3;
+      float acc = 0.f, accu = 0.f;
 #pragma unroll
-      for (int w = 0; w < 3; ++w) {
-        const float* r = red[w][lane];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          c00[j] += r[j];
-          c10[j] += r[4 + j];
-          if constexpr (kPair) {
-            c01[j] += r[8 + j];
-            c11[j] += r[12 + j];
-          }
-        }
+      for (int w = 0; w < kGemmWaves; ++w) {
+        acc += red[w][lane][blk * 4 + j];
+        if constexpr (kPair) accu += red[w][lane][8 + blk * 4 + j];
       }
       // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16; the C row
-      // of tile row r is the entry held by lane r (rows 0-15: e0, 16-31: e1).
-      const int col = col0 + m;
-      int ce0[4], ce1[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        ce0[j] = __shfl(e0, kq * 4 + j, 64);
-        ce1[j] = __shfl(e1, kq * 4 + j, 64);
-      }
-      if (vc) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r0 = kq * 4 + j, r1 = 16 + kq * 4 + j;
-          if (r0 < n) epilogue<bf16>(g, EPI, group, Cout, ldc, ce0[j] + g.c_row_offset, col, c00[j], c01[j]);
-          if (r1 < n) epilogue<bf16>(g, EPI, group, Cout, ldc, ce1[j] + g.c_row_offset, col, c10[j], c11[j]);
-        }
-      }
+      // of tile row r is the entry held by lane r % 16 (rows 0-15: e0, 16-31: e1).
+      const int crow = __shfl(blk ? e1 : e0, kq * 4 + j, 64);
+      const int row = blk * 16 + kq * 4 + j;
+      if (vc && row < n) epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, col0 + m, acc, accu);
     }
     tile0 += (int)gridDim.z * 32;
     if (tile0 >= cnt) break;
@@ -346,11 +334,12 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
 
 template <int EPI, int MODE, int KMUL0>
 void launch_bf16_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  constexpr int T = 64 * kGemmWaves;
   switch (a.K) {
-    case 256: gemm_bf16_kernel<EPI, 2, MODE, KMUL0><<<grid, 256, 0, s>>>(a); break;
-    case 512: gemm_bf16_kernel<EPI, 4, MODE, KMUL0><<<grid, 256, 0, s>>>(a); break;
-    case 1024: gemm_bf16_kernel<EPI, 8, MODE, KMUL0><<<grid, 256, 0, s>>>(a); break;
-    default: gemm_bf16_kernel<EPI, 16, MODE, KMUL0><<<grid, 256, 0, s>>>(a); break;
+    case 256: gemm_bf16_kernel<EPI, 1, MODE, KMUL0><<<grid, T, 0, s>>>(a); break;
+    case 512: gemm_bf16_kernel<EPI, 2, MODE, KMUL0><<<grid, T, 0, s>>>(a); break;
+    case 1024: gemm_bf16_kernel<EPI, 4, MODE, KMUL0><<<grid, T, 0, s>>>(a); break;
+    default: gemm_bf16_kernel<EPI, 8, MODE, KMUL0><<<grid, T, 0, s>>>(a); break;
   }
 }
 
