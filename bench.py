@@ -34,7 +34,7 @@ METRIC = "accepted tokens/s at 1 GPU (batch 16, ctx 2k); % HBM roofline; accepta
 HBM_PEAK = 8.0e12
 # kernels behind each timed class (names as rocprofv3 lists them), bf16 decode
 CLASS_KERNELS = {
-    "attention": ["attn_decode_mfma_kernel", "attn_unit_combine_kernel"],
+    "attention": ["attn_decode_mfma_kernel"],
     "routed_gate_up": ["gemm_bf16_kernel<3, 8, 1>"],
     "routed_down": ["gemm_bf16_kernel<0, 4, 1>"],
     "shared_down": ["gemm_bf16_kernel<0, 8, 2>"],

@@ -26,6 +26,7 @@ struct Engine {
   RowDesc* rows = nullptr;
   RowDesc* last_rows = nullptr;
   AttnUnit* units = nullptr;
+  int32_t* split_done = nullptr;  // [B][Hkv] decode attention split counters
   SeqState* state = nullptr;
   int32_t *lrow_seq = nullptr, *lrow_extra = nullptr, *argmax = nullptr, *draw = nullptr;
   int32_t *tokens = nullptr, *stop_ids = nullptr;
@@ -221,6 +222,8 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.rows, sizeof(RowDesc) * MR));
   PULSAR_TRY(x.alloc(&x.last_rows, sizeof(RowDesc) * MR));
   PULSAR_TRY(x.alloc(&x.units, sizeof(AttnUnit) * x.B));
+  PULSAR_TRY(x.alloc(&x.split_done, 4 * (size_t)x.B * x.Hkv));
+  PULSAR_CHECK_HIP(hipMemset(x.split_done, 0, 4 * (size_t)x.B * x.Hkv));
   PULSAR_TRY(x.alloc(&x.state, sizeof(SeqState) * x.B));
   PULSAR_TRY(x.alloc(&x.lrow_seq, 4 * MR));
   PULSAR_TRY(x.alloc(&x.lrow_extra, 4 * MR));
@@ -381,6 +384,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     aa.gate = e.gate;
     aa.out = e.attn_out;
     aa.units = e.units;
+    aa.split_done = e.split_done;
     aa.max_units = e.B;
     aa.part = e.part;
     aa.max_splits = e.max_splits;

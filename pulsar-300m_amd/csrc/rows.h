@@ -133,6 +133,7 @@ struct AttnArgs {
   const void* gate;  // [rows][H] T
   void* out;         // [rows][H*64] T
   float* part;       // decode split partials
+  int32_t* split_done;  // decode: per (unit, kv head) count of finished splits (self-resetting)
   int max_splits;
   int max_units;
   int H, Hkv, layer, is_local, window, prefill_T;

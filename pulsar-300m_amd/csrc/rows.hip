@@ -459,7 +459,9 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
 //   O[16 x 64] = P . V; B = the dimension-major V block: lane l holds dim 16n + l%16,
 //     keys 8*(l/16) + 32*ks, 16 contiguous bytes.
 // Row maxima and sums reduce over the 16 lanes of a DPP row. The 4 waves' (max, sum, O)
-// merge in LDS and the split partial goes to `part` [unit][kv head][split][8][66].
+// merge in LDS and the split partial goes to `part` [unit][kv head][split][8][66]; the
+// last split block to finish merges the splits, normalises, rounds as the SDPA output and
+// applies the head gate.
 // ---------------------------------------------------------------------------
 typedef __bf16 attn_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float attn_f32x4 __attribute__((ext_vector_type(4)));
@@ -610,61 +612,69 @@ __global__ void __launch_bounds__(256) attn_decode_mfma_kernel(AttnArgs a) {
       O1 += wacc[w][hr][d0 + 1] * f;
     }
   }
+  // Split partials are exchanged between workgroups with device-coherent stores and loads
+  // (they bypass the per-XCD L2), so no cache-wide writeback is needed: each thread waits
+  // for its stores to complete before the workgroup counts itself in, and only the block
+  // that completes the count merges — no block ever waits for another.
   float* out = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits + s) * 8 + hr) * 66;
-  out[2 + d0] = O0;
-  out[3 + d0] = O1;
+  __hip_atomic_store(out + 2 + d0, O0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(out + 3 + d0, O1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (d0 == 0) {
-    out[0] = M;
-    out[1] = L;
+    __hip_atomic_store(out, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(out + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
-
-// Merge the split partials of a unit: block (unit, kv head, row of the unit); wave = query
-// head of the group, lane = dim. Normalise, round as the SDPA output, apply the head gate.
-__global__ void __launch_bounds__(256) attn_unit_combine_kernel(AttnArgs a) {
-  const int u = blockIdx.x, g = blockIdx.y, z = blockIdx.z;
-  if (u >= a.ctl->n_units) return;
-  const AttnUnit un = a.units[u];
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ int s_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t* cnt = a.split_done + (int64_t)u * a.Hkv + g;
+    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == nsplit - 1;
+    // every split has counted in: reset for the next launch
+    if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // merge: thread -> row of the unit (z), head of the group, two dims
+  const int z = threadIdx.x >> 7, h = (threadIdx.x >> 5) & 3, e0 = (threadIdx.x & 31) * 2;
   const int row = z == 0 ? un.row_a : un.row_b;
   if (row < 0) return;
-  int lo_a, lo_b, base, uhi;
-  unit_range(a, un, lo_a, lo_b, base, uhi);
-  const int nsplit = (uhi + 1 - base + kSplitLen - 1) / kSplitLen;
-  const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int head = g * 4 + h;
   const float* p0 = a.part + (((int64_t)u * a.Hkv + g) * a.max_splits * 8 + z * 4 + h) * 66;
-  // splits in chunks of 8 whose loads are all in flight together (indices past the last
-  // split re-read it and are dropped)
-  float M = -INFINITY, L = 0.f, O = 0.f;
+  float Mx = -INFINITY, Ls = 0.f, Oa = 0.f, Ob = 0.f;
   for (int c0 = 0; c0 < nsplit; c0 += 8) {
-    float pm[8], pl[8], po[8];
+    float pm[8], pl[8], pa[8], pb[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const float* p = p0 + (int64_t)min(c0 + k, nsplit - 1) * 8 * 66;
-      pm[k] = p[0];
-      pl[k] = p[1];
-      po[k] = p[2 + lane];
+      pm[k] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pl[k] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pa[k] = __hip_atomic_load(p + 2 + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pb[k] = __hip_atomic_load(p + 3 + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    float cm = M;
+    float cm = Mx;
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       if (c0 + k < nsplit) cm = fmaxf(cm, pm[k]);
-    const float f0 = M == -INFINITY ? 0.f : expf(M - cm);
-    L *= f0;
-    O *= f0;
+    const float f0 = Mx == -INFINITY ? 0.f : expf(Mx - cm);
+    Ls *= f0;
+    Oa *= f0;
+    Ob *= f0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if (c0 + k < nsplit && pm[k] != -INFINITY) {
         const float f = expf(pm[k] - cm);
-        L += pl[k] * f;
-        O += po[k] * f;
+        Ls += pl[k] * f;
+        Oa += pa[k] * f;
+        Ob += pb[k] * f;
       }
     }
-    M = cm;
+    Mx = cm;
   }
-  const float o = rnd<bf16>(O / L);
+  const int head = g * 4 + h;
   const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
-  reinterpret_cast<bf16*>(a.out)[(int64_t)row * a.H * 64 + head * 64 + lane] = f2bf(o * gate);
+  bf16* dst = reinterpret_cast<bf16*>(a.out) + (int64_t)row * a.H * 64 + head * 64 + e0;
+  dst[0] = f2bf(rnd<bf16>(Oa / Ls) * gate);
+  dst[1] = f2bf(rnd<bf16>(Ob / Ls) * gate);
 }
 
 // ---------------------------------------------------------------------------
@@ -1084,8 +1094,6 @@ int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s) 
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s) {
   if (dtype == PULSAR_BF16) {
     attn_decode_mfma_kernel<<<dim3(a.max_units, a.Hkv, a.max_splits), 256, 0, s>>>(a);
-    PULSAR_LAUNCH_CHECK();
-    attn_unit_combine_kernel<<<dim3(a.max_units, a.Hkv, 2), 256, 0, s>>>(a);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   }
