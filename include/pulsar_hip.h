@@ -135,6 +135,13 @@ int pulsar_moe_slots_from_order(const int64_t* flat_e, const int64_t* order, int
 
 #define PULSAR_MAX_LAYERS 16
 
+/* GEMM weight layout. fp32 weights are row-major [N][K]. bf16 weights (wqkvg, wo, shared_gu,
+ * shared_down, routed_gu, routed_down, lm_head) are stored in matrix-core tiles: each
+ * [N][K] matrix becomes [N/16][K/32][64][8], tile (n, k) holding rows 16n..16n+15 and
+ * columns 32k..32k+31 in the order the 16x16x32 bf16 MFMA B operand reads them (lane l:
+ * row 16n + l%16, columns 32k + 8*(l/16) .. +8), so every wave load is 1 KB contiguous.
+ * N must be a multiple of 16 and K of 256. */
+
 /* Architecture constants plus device pointers to the kernel-format weights.
  * T = element type selected by dtype. Per-pulse tensors hold the first n_pulses pulses.
  * Host-side preparation (see pulsar_engine/model.py) merges the per-pulse LoRA into the
@@ -176,6 +183,7 @@ typedef struct PulsarModelDesc {
   const float* router[PULSAR_MAX_LAYERS];      /* [P][E][D] */
   const float* expert_bias[PULSAR_MAX_LAYERS]; /* [P][E] */
   const void* routed_scale[PULSAR_MAX_LAYERS]; /* [P][D] T */
+  const void* lm_head;      /* output head (tied to tok_emb) in the GEMM weight layout */
 } PulsarModelDesc;
 
 /* Generation settings (the reference's generate() arguments, src/infer.py:733-743). */

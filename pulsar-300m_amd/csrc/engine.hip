@@ -528,7 +528,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   GemmArgs g = gemm_base(e);
   g.A = e.xn_final;
   g.lda = D;
-  g.W = m.tok_emb;
+  g.W = m.lm_head ? m.lm_head : m.tok_emb;
   g.ldw = D;
   g.C = e.logits;
   g.ldc = e.V;
@@ -897,7 +897,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   GemmArgs g = gemm_base(e);
   g.A = e.xn_final;
   g.lda = D;
-  g.W = m.tok_emb;
+  g.W = m.lm_head ? m.lm_head : m.tok_emb;
   g.ldw = D;
   g.C = e.plogits;
   g.ldc = e.V;

@@ -189,24 +189,30 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = lane & 15, kq = lane >> 4;
-  const int64_t lda = g0 ? g.lda0 : g.lda, ldw = g0 ? g.ldw0 : g.ldw;
+  const int64_t lda = g0 ? g.lda0 : g.lda;
   const bf16* W = g0 ? reinterpret_cast<const bf16*>(g.W0)
                      : reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
-  const bool vc = col0 + m < N;  // columns past N (last tile) read row 0 and are dropped
-  const bf16* w0 = W + (int64_t)(vc ? col0 + m : 0) * ldw;
-  const bf16* w1 = W + (int64_t)(vc ? N + col0 + m : 0) * ldw;
+  // Weights in matrix-core tiles [N/16][K/32][64 lanes][8]: this lane's 16 bytes of tile
+  // (column tile, k tile) sit at ((ct * KT + kt) * 64 + lane) * 8, and the wave's load of a
+  // tile is 1 KB contiguous. The up-projection rows of SwiGLU are column tiles N/16 on.
+  const int KT = (g0 ? g.K0 : g.K) / 32;
+  const bool vc = col0 + m < N;  // N is a multiple of 16: always true; kept as a guard
+  const bf16* w0 = W + ((int64_t)(col0 / 16) * KT * 64 + lane) * 8;
+  const bf16* w1 = W + ((int64_t)((N + col0) / 16) * KT * 64 + lane) * 8;
   const bf16* A = reinterpret_cast<const bf16*>(g0 ? g.A0 : g.A);
   void* Cout = g0 ? g.C0 : g.C;
   const int64_t ldc = g0 ? g.ldc0 : g.ldc;
   const int passes = g0 ? KMUL0 : 1;
   const int kb = wv * (KITER * 32) + kq * 8;
   const bf16x8_t zero = {};
-  bf16x8_t bw[KITER], bu[KITER], xa[KITER], xb[KITER];
+  bf16x8_t bw[KITER], bu[KITER], xa[KITER];
+  // k tile of step i of this wave in pass p: p * (K / 32 per pass) + wv * KITER + i
 #define PULSAR_LOAD_W(pass)                                                              \
   do {                                                                                   \
     _Pragma("unroll") for (int i = 0; i < KITER; ++i) {                                  \
-      bw[i] = load_bf16x8(w0 + (pass) * kKPass + kb + 32 * i);                           \
-      if constexpr (kPair) bu[i] = load_bf16x8(w1 + (pass) * kKPass + kb + 32 * i);      \
+      const int64_t kt = (int64_t)(pass) * (kKPass / 32) + wv * KITER + i;               \
+      bw[i] = load_bf16x8(w0 + kt * 512);                                                \
+      if constexpr (kPair) bu[i] = load_bf16x8(w1 + kt * 512);                           \
     }                                                                                    \
   } while (0)
 
@@ -232,20 +238,21 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
     for (int pass = 0; pass < passes; ++pass) {
       if (pass > 0) PULSAR_LOAD_W(pass);
 #pragma unroll
-      for (int i = 0; i < KITER; ++i) {
+      for (int i = 0; i < KITER; ++i)
         xa[i] = ar0 >= 0 ? load_bf16x8(a0 + pass * kKPass + kb + 32 * i) : zero;
-        if (two) xb[i] = ar1 >= 0 ? load_bf16x8(a1 + pass * kKPass + kb + 32 * i) : zero;
-      }
 #pragma unroll
       for (int i = 0; i < KITER; ++i) {
         c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[i], c00, 0, 0, 0);
         if constexpr (kPair) c01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bu[i], c01, 0, 0, 0);
       }
-      if (two) {
+      if (two) {  // the second 16-row block reuses the A registers (fewer VGPRs, more waves)
+#pragma unroll
+        for (int i = 0; i < KITER; ++i)
+          xa[i] = ar1 >= 0 ? load_bf16x8(a1 + pass * kKPass + kb + 32 * i) : zero;
 #pragma unroll
         for (int i = 0; i < KITER; ++i) {
-          c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[i], bw[i], c10, 0, 0, 0);
-          if constexpr (kPair) c11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[i], bu[i], c11, 0, 0, 0);
+          c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[i], c10, 0, 0, 0);
+          if constexpr (kPair) c11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bu[i], c11, 0, 0, 0);
         }
       }
     }

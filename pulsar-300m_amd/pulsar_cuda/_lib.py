@@ -56,6 +56,7 @@ class PulsarModelDesc(ctypes.Structure):
         ("shared_down", _vp * MAX_LAYERS), ("routed_gu", _vp * MAX_LAYERS),
         ("routed_down", _vp * MAX_LAYERS), ("router", _vp * MAX_LAYERS),
         ("expert_bias", _vp * MAX_LAYERS), ("routed_scale", _vp * MAX_LAYERS),
+        ("lm_head", _vp),
     ]
 
 

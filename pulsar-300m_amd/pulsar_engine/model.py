@@ -43,6 +43,17 @@ def _policy(name: str, t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return t
 
 
+def pack_mfma(w: torch.Tensor) -> torch.Tensor:
+    """[..., N, K] -> [..., N/16, K/32, 64, 8]: 16x32 tiles in the lane order of the
+    16x16x32 bf16 MFMA B operand (lane l: row l % 16, columns 8 * (l // 16) .. +8)."""
+    *lead, n, k = w.shape
+    if n % 16 or k % 32:
+        raise ValueError(f"GEMM weight {tuple(w.shape)}: N must be a multiple of 16, K of 32")
+    nl = len(lead)
+    t = w.reshape(*lead, n // 16, 16, k // 32, 4, 8)
+    return t.permute(*range(nl), nl, nl + 2, nl + 3, nl + 1, nl + 4).contiguous()
+
+
 def rope_tables(theta: float, dim: int, n: int):
     inv = 1.0 / (theta ** (torch.arange(0, dim, 2).float() / dim))
     t = torch.arange(n, dtype=torch.float32)
@@ -98,8 +109,11 @@ class DeviceModel:
         d.rope_len = self.rope_len
 
         ptr = lambda t: t.data_ptr()  # noqa: E731
+        # GEMM weights: matrix-core tile layout for bf16, row-major for fp32
+        gw = (lambda t: pack_mfma(t)) if dtype == torch.bfloat16 else (lambda t: t)  # noqa: E731
         self.tok_emb = dev(p["tok_emb.weight"], T)
         d.tok_emb = ptr(self.tok_emb)
+        d.lm_head = ptr(dev(gw(self.tok_emb))) if dtype == torch.bfloat16 else d.tok_emb
         d.anchor_norm = ptr(dev(p["anchor_norm.weight"], torch.float32))
         d.state_norm = ptr(dev(p["pulse_state_norm.weight"], torch.float32))
         d.final_norm = ptr(dev(p["final_norm.weight"], torch.float32))
@@ -132,17 +146,17 @@ class DeviceModel:
                     mq, mo = wqkv, wo
                 qkvg.append(torch.cat([mq, p[a + "attn_gate"][k].to(T)], dim=0))
                 wos.append(mo)
-            d.wqkvg[i] = ptr(dev(torch.stack(qkvg)))
-            d.wo[i] = ptr(dev(torch.stack(wos)))
+            d.wqkvg[i] = ptr(dev(gw(torch.stack(qkvg))))
+            d.wo[i] = ptr(dev(gw(torch.stack(wos))))
             d.gate_bias[i] = ptr(dev(p[a + "attn_gate_bias"][:P], T))
             d.q_norm[i] = ptr(dev(p[a + "q_norm_weight"][:P], torch.float32))
             d.k_norm[i] = ptr(dev(p[a + "k_norm_weight"][:P], torch.float32))
             d.v_lambda[i] = ptr(dev(torch.sigmoid(p[a + "v_resid_lambda"][:P]).to(T).float()))
             m = pre + "mlp."
-            d.shared_gu[i] = ptr(dev(p[m + "shared_expert.w_gate_up.weight"], T))
-            d.shared_down[i] = ptr(dev(p[m + "shared_expert.w_down.weight"], T))
-            d.routed_gu[i] = ptr(dev(p[m + "routed_gate_up"].to(T).transpose(1, 2)))
-            d.routed_down[i] = ptr(dev(p[m + "routed_down"].to(T).transpose(1, 2)))
+            d.shared_gu[i] = ptr(dev(gw(p[m + "shared_expert.w_gate_up.weight"].to(T))))
+            d.shared_down[i] = ptr(dev(gw(p[m + "shared_expert.w_down.weight"].to(T))))
+            d.routed_gu[i] = ptr(dev(gw(p[m + "routed_gate_up"].to(T).transpose(1, 2))))
+            d.routed_down[i] = ptr(dev(gw(p[m + "routed_down"].to(T).transpose(1, 2))))
             d.router[i] = ptr(dev(p[m + "router_weight"][:P], torch.float32))
             eb = p[m + "expert_bias"]
             if eb.dim() == 1:
