@@ -119,3 +119,73 @@ def test_greedy_speculative_equals_plain_and_batch_equals_single(models, full_st
     assert spec == plain
     for i, p in enumerate(prompts):
         assert eng.generate_ids([p], speculative=True, **kw)[0] == spec[i]
+
+
+def test_bf16_sampled_acceptance_matches_draft_verify_overlap(models, full_state):
+    """Sampled self-speculation: the number of accepted drafts is a sum of independent
+    Bernoulli(p_i), p_i = sum_x p_draft(x) p_verify(x) from the engine's own pulse-0 and
+    pulse-2 logits of the tested token (src/infer.py:688-725). The observed count must lie
+    within 4 standard deviations of sum p_i (temperature 1.0 gives p_i ~ 0.6 here)."""
+    from oracle import pulsar_ref as R
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+
+    cfg = full_state[0]
+    B, T_, N = 16, 24, 20
+    temp, top_p, rp = 1.0, 0.95, 1.15
+    prompts = np.stack([W.uniform_ids(40 + b, "acc_prompt", T_, cfg.vocab_size) for b in range(B)])
+    eng = HipEngine(models[torch.bfloat16], batch=B, max_prompt=T_, max_new=N, speculative=True,
+                    temperature=temp, top_p=top_p, repetition_penalty=rp, stop_ids=[],
+                    all_logits=True, seed=1234)
+    eng.prefill(prompts)
+    P = cfg.default_pulses
+    pulse0 = {}
+    expected, var, observed, n_tests = 0.0, 0.0, 0, 0
+    for _ in range(4 * (N + 2) * P):
+        before = eng.state().copy()
+        if before[:, 0].all():
+            break
+        eng.step(1)
+        after = eng.state()
+        rows = eng.rows(last=True)
+        lg = eng.logits(len(rows))
+        for r in rows:
+            seq, pulse, pos, tok, lrow = int(r[0]), int(r[2]), int(r[3]), int(r[4]), int(r[5])
+            if lrow < 0:
+                continue
+            if pulse == 0:
+                pulse0[(seq, pos, tok)] = lg[lrow].copy()
+        toks = eng.tokens()
+        for b in range(B):
+            dt = int(after[b, 11] - before[b, 11])
+            if dt == 0:
+                continue
+            assert dt == 1
+            c_tok, c_pos = int(before[b, 3]), int(before[b, 4])
+            v_row = [r for r in rows if int(r[0]) == b and int(r[3]) == c_pos and int(r[2]) == P - 1]
+            assert len(v_row) == 1
+            d_logits = torch.from_numpy(pulse0[(b, c_pos, c_tok)]).view(1, -1)
+            v_logits = torch.from_numpy(lg[int(v_row[0][5])].copy()).view(1, -1)
+            seen = prompts[b].tolist() + toks[b][: c_pos - T_ + 1]
+            p = R.accept_probability(d_logits, v_logits, seen, temp, top_p, rp)
+            expected += p
+            var += p * (1.0 - p)
+            observed += int(after[b, 12] - before[b, 12])
+            n_tests += 1
+    st = eng.state()
+    assert n_tests == int(st[:, 11].sum()) and observed == int(st[:, 12].sum())
+    sigma = max(var, 1e-9) ** 0.5
+    print(f"tests {n_tests}, accepted {observed}, expected {expected:.1f} +- {sigma:.1f}")
+    assert n_tests >= 100 and 0.2 < expected / n_tests < 0.95
+    assert abs(observed - expected) <= 4.0 * sigma + 1.0
+    eng.close()
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_long_prompt_passes_cover_window_and_yarn(models, full_state, dtype, tol):
+    """A 1100-token prompt: local layers keep the newest 1024 positions (prefill top-left
+    SDPA alignment, decode ring), global layers span two pages past 1024 and apply YaRN."""
+    from pulsar_engine import weights as W
+
+    prompt = W.uniform_ids(9, "long_prompt", 1100, full_state[0].vocab_size).tolist()
+    _compare_passes(models, full_state, dtype, prompt, 3, tol=tol, rp=10.0)
