@@ -221,6 +221,10 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.last_ctl, sizeof(StepCtl)));
   PULSAR_TRY(x.alloc(&x.rows, sizeof(RowDesc) * MR));
   PULSAR_TRY(x.alloc(&x.last_rows, sizeof(RowDesc) * MR));
+  // row kernels read the descriptor of every launched row before the row count is known:
+  // keep every slot a valid descriptor
+  PULSAR_CHECK_HIP(hipMemset(x.rows, 0, sizeof(RowDesc) * MR));
+  PULSAR_CHECK_HIP(hipMemset(x.last_rows, 0, sizeof(RowDesc) * MR));
   PULSAR_TRY(x.alloc(&x.units, sizeof(AttnUnit) * x.B));
   PULSAR_TRY(x.alloc(&x.split_done, 4 * (size_t)x.B * x.Hkv));
   PULSAR_CHECK_HIP(hipMemset(x.split_done, 0, 4 * (size_t)x.B * x.Hkv));
