@@ -221,8 +221,7 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.last_ctl, sizeof(StepCtl)));
   PULSAR_TRY(x.alloc(&x.rows, sizeof(RowDesc) * MR));
   PULSAR_TRY(x.alloc(&x.last_rows, sizeof(RowDesc) * MR));
-  // row kernels read the descriptor of every launched row before the row count is known:
-  // keep every slot a valid descriptor
+  // every slot holds a valid descriptor from the start (snapshots copy whole row sets)
   PULSAR_CHECK_HIP(hipMemset(x.rows, 0, sizeof(RowDesc) * MR));
   PULSAR_CHECK_HIP(hipMemset(x.last_rows, 0, sizeof(RowDesc) * MR));
   PULSAR_TRY(x.alloc(&x.units, sizeof(AttnUnit) * x.B));
