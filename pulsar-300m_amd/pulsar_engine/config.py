@@ -123,7 +123,9 @@ def tiny_config(**overrides) -> PulsarConfig:
 def small_config(**overrides) -> PulsarConfig:
     """Reduced configuration that satisfies the HIP engine's shape rules (head_dim 64, four
     query heads per kv head, widths multiples of 256, vocab a multiple of 4096); layer 3 is
-    global and the 16-token window is exceeded by short prompts. For fast GPU checks."""
+    global and the 16-token window is exceeded by short prompts. For fast GPU checks in
+    fp32; bf16 also needs qkv_dim + n_heads to be a multiple of 16 (the matrix-core tile
+    height), e.g. ``n_heads=16, n_kv_heads=4``."""
     base = dict(
         vocab_size=4096,
         d_model=256,

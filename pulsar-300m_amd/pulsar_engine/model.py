@@ -69,31 +69,153 @@ def _merge(base, A, B, M, pulse, K, alpha):
     return torch.addmm(base, (B_perm * coef).reshape(B.shape[1], K * q), A_all)
 
 
+# Names of the kernel-format tensors of one layer (prefixed with "layers.<i>.").
+LAYER_TENSORS = (
+    "attn_norm", "mlp_norm", "wqkvg", "wo", "gate_bias", "q_norm", "k_norm", "v_lambda",
+    "shared_gu", "shared_down", "routed_gu", "routed_down", "router", "expert_bias",
+    "routed_scale",
+)
+GLOBAL_TENSORS = (
+    "tok_emb", "lm_head", "anchor_norm", "state_norm", "final_norm", "conv_w", "step_emb",
+    "reinject_down", "reinject_up", "reinject_bias", "res_scale",
+)
+# Tensors held in the activation dtype; every other one is fp32.
+ACT_DTYPE_TENSORS = frozenset((
+    "tok_emb", "lm_head", "step_emb", "reinject_down", "reinject_up", "reinject_bias",
+    "res_scale", "wqkvg", "wo", "gate_bias", "shared_gu", "shared_down", "routed_gu",
+    "routed_down", "routed_scale",
+))
+
+
+def tensor_dtype(name: str, dtype: torch.dtype) -> torch.dtype:
+    """Storage dtype of kernel tensor ``name`` in a model computing in ``dtype``."""
+    return dtype if name.split(".")[-1] in ACT_DTYPE_TENSORS else torch.float32
+
+
+def expected_kernel_shapes(cfg: PulsarConfig, dtype: torch.dtype) -> dict[str, tuple]:
+    """Name -> shape of every tensor ``kernel_tensors`` produces for ``cfg`` and ``dtype``."""
+    P, D, V = cfg.default_pulses, cfg.d_model, cfg.vocab_size
+    H, Hk, hd, E = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.n_routed_experts
+    de, ds, r = cfg.d_expert, cfg.d_shared, cfg.reinject_gate_rank
+
+    def g(*s):  # GEMM weight [..., N, K]
+        *lead, n, k = s
+        return (*lead, n // 16, k // 32, 4, 16, 8) if dtype == torch.bfloat16 else tuple(s)
+
+    out = {"tok_emb": (V, D), "lm_head": g(V, D), "anchor_norm": (D,), "state_norm": (D,),
+           "final_norm": (D,), "step_emb": (P, D), "reinject_down": (P, r, 2 * D),
+           "reinject_up": (P, D, r), "reinject_bias": (P, D), "res_scale": (P, D)}
+    if cfg.use_canon_conv:
+        out["conv_w"] = (D, cfg.canon_kernel_size)
+    layer = {"attn_norm": (P, D), "mlp_norm": (P, D), "wqkvg": g(P, cfg.qkv_dim + H, D),
+             "wo": g(P, D, cfg.q_dim), "gate_bias": (P, H), "q_norm": (P, H, hd),
+             "k_norm": (P, Hk, hd), "v_lambda": (P,), "shared_gu": g(2 * ds, D),
+             "shared_down": g(D, ds), "routed_gu": g(E, 2 * de, D), "routed_down": g(E, D, de),
+             "router": (P, E, D), "expert_bias": (P, E), "routed_scale": (P, D)}
+    for i in range(cfg.n_core):
+        out.update({f"layers.{i}.{k}": v for k, v in layer.items()})
+    return out
+
+
+def kernel_tensors(cfg: PulsarConfig, state: dict, dtype: torch.dtype = torch.bfloat16) -> dict:
+    """Reference-format state dict -> named CPU tensors in the layout the HIP engine reads.
+
+    Applies, once, what the reference applies at load or on every pulse: the precision
+    policy, the per-pulse LoRA merge, the attention-gate rows appended to the merged qkv
+    weight, the decode-time ``.to(x.dtype)`` casts, expert transposition to [E][out][in],
+    and (bf16) the matrix-core tile layout of every GEMM weight plus a packed copy of the
+    tied output head.
+    """
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("dtype must be torch.float32 or torch.bfloat16")
+    if cfg.head_dim != 64 or cfg.n_heads != 4 * cfg.n_kv_heads:
+        raise ValueError("the HIP engine implements head_dim 64 with 4 query heads per kv head")
+    P = cfg.default_pulses
+    T = dtype
+    f32 = torch.float32
+    p = {k: _policy(k, torch.as_tensor(np.asarray(v)), dtype) for k, v in state.items()}
+    gw = (lambda t: pack_mfma(t)) if dtype == torch.bfloat16 else (lambda t: t)  # noqa: E731
+    out = {}
+    out["tok_emb"] = p["tok_emb.weight"].to(T)
+    out["lm_head"] = gw(out["tok_emb"])
+    out["anchor_norm"] = p["anchor_norm.weight"].to(f32)
+    out["state_norm"] = p["pulse_state_norm.weight"].to(f32)
+    out["final_norm"] = p["final_norm.weight"].to(f32)
+    if cfg.use_canon_conv:
+        out["conv_w"] = p["stem_canon_weight"].to(f32)
+    out["step_emb"] = p["pulse_step_emb.weight"][:P].to(T)
+    out["reinject_down"] = p["reinject_gate_down"][:P].to(T)
+    out["reinject_up"] = p["reinject_gate_up"][:P].to(T)
+    out["reinject_bias"] = p["reinject_gate_bias"][:P].to(T)
+    out["res_scale"] = p["pulse_res_scale"][:P].to(T)
+    alpha = cfg.loop_lora_alpha
+    for i in range(cfg.n_core):
+        pre, L = f"core.{i}.", f"layers.{i}."
+        a, m = pre + "attn.", pre + "mlp."
+        out[L + "attn_norm"] = p[pre + "attn_norm.weight"][:P].to(f32)
+        out[L + "mlp_norm"] = p[pre + "mlp_norm.weight"][:P].to(f32)
+        wqkv = p[a + "wqkv.weight"].to(T)
+        wo = p[a + "wo.weight"].to(T)
+        qkvg, wos = [], []
+        for k in range(P):
+            if cfg.loop_lora_rank > 0:
+                mq = _merge(wqkv, p[a + "wqkv_adapter.lora_A"], p[a + "wqkv_adapter.lora_B"],
+                            p[a + "wqkv_adapter.loop_M"], k, P, alpha)
+                mo = _merge(wo, p[a + "wo_adapter.lora_A"], p[a + "wo_adapter.lora_B"],
+                            p[a + "wo_adapter.loop_M"], k, P, alpha)
+            else:
+                mq, mo = wqkv, wo
+            qkvg.append(torch.cat([mq, p[a + "attn_gate"][k].to(T)], dim=0))
+            wos.append(mo)
+        out[L + "wqkvg"] = gw(torch.stack(qkvg))
+        out[L + "wo"] = gw(torch.stack(wos))
+        out[L + "gate_bias"] = p[a + "attn_gate_bias"][:P].to(T)
+        out[L + "q_norm"] = p[a + "q_norm_weight"][:P].to(f32)
+        out[L + "k_norm"] = p[a + "k_norm_weight"][:P].to(f32)
+        out[L + "v_lambda"] = torch.sigmoid(p[a + "v_resid_lambda"][:P]).to(T).float()
+        out[L + "shared_gu"] = gw(p[m + "shared_expert.w_gate_up.weight"].to(T))
+        out[L + "shared_down"] = gw(p[m + "shared_expert.w_down.weight"].to(T))
+        out[L + "routed_gu"] = gw(p[m + "routed_gate_up"].to(T).transpose(1, 2))
+        out[L + "routed_down"] = gw(p[m + "routed_down"].to(T).transpose(1, 2))
+        out[L + "router"] = p[m + "router_weight"][:P].to(f32)
+        eb = p[m + "expert_bias"]
+        if eb.dim() == 1:
+            eb = eb.unsqueeze(0).expand(cfg.max_pulses, -1)
+        out[L + "expert_bias"] = eb[:P].to(f32)
+        out[L + "routed_scale"] = p[m + "routed_scale"][:P].to(T)
+    return {k: v.contiguous() for k, v in out.items()}
+
+
 class DeviceModel:
-    """Weights of one model in kernel format on a GPU, plus the C descriptor."""
+    """Weights of one model in kernel format on a GPU, plus the C descriptor.
+
+    ``state`` is either a reference-format state dict (converted by ``kernel_tensors``) or,
+    with ``kernel_format=True``, the named kernel-format tensors themselves (as read by
+    ``checkpoint.load_kernel_format``). Names, shapes and dtypes are checked before upload."""
 
     def __init__(self, cfg: PulsarConfig, state: dict, dtype: torch.dtype = torch.bfloat16,
-                 device: str | torch.device = "cuda", rope_len: int | None = None):
+                 device: str | torch.device = "cuda", rope_len: int | None = None,
+                 kernel_format: bool = False):
         from pulsar_cuda import _lib
 
-        if dtype not in (torch.float32, torch.bfloat16):
-            raise ValueError("dtype must be torch.float32 or torch.bfloat16")
-        if cfg.head_dim != 64 or cfg.n_heads != 4 * cfg.n_kv_heads:
-            raise ValueError("the HIP engine implements head_dim 64 with 4 query heads per kv head")
         self.cfg = cfg
         self.dtype = dtype
         self.device = torch.device(device)
         P = cfg.default_pulses
         self.n_pulses = P
-        self._keep: list[torch.Tensor] = []
-        p = {k: _policy(k, torch.as_tensor(np.asarray(v)), dtype) for k, v in state.items()}
+        tensors = state if kernel_format else kernel_tensors(cfg, state, dtype)
+        want = expected_kernel_shapes(cfg, dtype)
+        if set(tensors) != set(want):
+            raise ValueError(f"kernel tensors: missing {sorted(set(want) - set(tensors))}, "
+                             f"unexpected {sorted(set(tensors) - set(want))}")
+        for k, shape in want.items():
+            if tuple(tensors[k].shape) != shape:
+                raise ValueError(f"{k}: shape {tuple(tensors[k].shape)}, expected {shape}")
+            if tensors[k].dtype != tensor_dtype(k, dtype):
+                raise ValueError(f"{k}: dtype {tensors[k].dtype}, expected {tensor_dtype(k, dtype)}")
+        self.tensors = {k: v.to(self.device) for k, v in tensors.items()}
+        t = self.tensors
         T = dtype
-
-        def dev(t: torch.Tensor, dt=None) -> torch.Tensor:
-            t = t.to(dt) if dt is not None else t
-            t = t.contiguous().to(self.device)
-            self._keep.append(t)
-            return t
 
         d = _lib.PulsarModelDesc()
         d.vocab, d.d_model = cfg.vocab_size, cfg.d_model
@@ -107,68 +229,34 @@ class DeviceModel:
         d.rms_eps, d.softcap = cfg.rms_eps, cfg.logit_softcap
         self.rope_len = int(rope_len or cfg.max_seq_len)
         d.rope_len = self.rope_len
-
-        ptr = lambda t: t.data_ptr()  # noqa: E731
-        # GEMM weights: matrix-core tile layout for bf16, row-major for fp32
-        gw = (lambda t: pack_mfma(t)) if dtype == torch.bfloat16 else (lambda t: t)  # noqa: E731
-        self.tok_emb = dev(p["tok_emb.weight"], T)
-        d.tok_emb = ptr(self.tok_emb)
-        d.lm_head = ptr(dev(gw(self.tok_emb))) if dtype == torch.bfloat16 else d.tok_emb
-        d.anchor_norm = ptr(dev(p["anchor_norm.weight"], torch.float32))
-        d.state_norm = ptr(dev(p["pulse_state_norm.weight"], torch.float32))
-        d.final_norm = ptr(dev(p["final_norm.weight"], torch.float32))
-        d.conv_w = ptr(dev(p["stem_canon_weight"], torch.float32)) if cfg.use_canon_conv else None
-        d.step_emb = ptr(dev(p["pulse_step_emb.weight"][:P], T))
-        d.reinject_down = ptr(dev(p["reinject_gate_down"][:P], T))
-        d.reinject_up = ptr(dev(p["reinject_gate_up"][:P], T))
-        d.reinject_bias = ptr(dev(p["reinject_gate_bias"][:P], T))
-        d.res_scale = ptr(dev(p["pulse_res_scale"][:P], T))
+        ptr = lambda x: x.data_ptr()  # noqa: E731
+        self.tok_emb = t["tok_emb"]
+        d.tok_emb = ptr(t["tok_emb"])
+        d.lm_head = ptr(t["lm_head"])
+        d.anchor_norm = ptr(t["anchor_norm"])
+        d.state_norm = ptr(t["state_norm"])
+        d.final_norm = ptr(t["final_norm"])
+        d.conv_w = ptr(t["conv_w"]) if "conv_w" in t else None
+        d.step_emb = ptr(t["step_emb"])
+        d.reinject_down = ptr(t["reinject_down"])
+        d.reinject_up = ptr(t["reinject_up"])
+        d.reinject_bias = ptr(t["reinject_bias"])
+        d.res_scale = ptr(t["res_scale"])
         cl, sl = rope_tables(cfg.rope_theta_local, cfg.head_dim, self.rope_len)
         cg, sg = rope_tables(cfg.rope_theta_global, cfg.head_dim, self.rope_len)
-        d.rope_cos_local, d.rope_sin_local = ptr(dev(cl)), ptr(dev(sl))
-        d.rope_cos_global, d.rope_sin_global = ptr(dev(cg)), ptr(dev(sg))
-        alpha = cfg.loop_lora_alpha
+        self._rope = [x.to(self.device) for x in (cl, sl, cg, sg)]
+        d.rope_cos_local, d.rope_sin_local = ptr(self._rope[0]), ptr(self._rope[1])
+        d.rope_cos_global, d.rope_sin_global = ptr(self._rope[2]), ptr(self._rope[3])
         for i in range(cfg.n_core):
-            pre = f"core.{i}."
-            a = pre + "attn."
-            d.attn_norm[i] = ptr(dev(p[pre + "attn_norm.weight"][:P], torch.float32))
-            d.mlp_norm[i] = ptr(dev(p[pre + "mlp_norm.weight"][:P], torch.float32))
-            wqkv = p[a + "wqkv.weight"].to(T)
-            wo = p[a + "wo.weight"].to(T)
-            qkvg, wos = [], []
-            for k in range(P):
-                if cfg.loop_lora_rank > 0:
-                    mq = _merge(wqkv, p[a + "wqkv_adapter.lora_A"], p[a + "wqkv_adapter.lora_B"],
-                                p[a + "wqkv_adapter.loop_M"], k, P, alpha)
-                    mo = _merge(wo, p[a + "wo_adapter.lora_A"], p[a + "wo_adapter.lora_B"],
-                                p[a + "wo_adapter.loop_M"], k, P, alpha)
-                else:
-                    mq, mo = wqkv, wo
-                qkvg.append(torch.cat([mq, p[a + "attn_gate"][k].to(T)], dim=0))
-                wos.append(mo)
-            d.wqkvg[i] = ptr(dev(gw(torch.stack(qkvg))))
-            d.wo[i] = ptr(dev(gw(torch.stack(wos))))
-            d.gate_bias[i] = ptr(dev(p[a + "attn_gate_bias"][:P], T))
-            d.q_norm[i] = ptr(dev(p[a + "q_norm_weight"][:P], torch.float32))
-            d.k_norm[i] = ptr(dev(p[a + "k_norm_weight"][:P], torch.float32))
-            d.v_lambda[i] = ptr(dev(torch.sigmoid(p[a + "v_resid_lambda"][:P]).to(T).float()))
-            m = pre + "mlp."
-            d.shared_gu[i] = ptr(dev(gw(p[m + "shared_expert.w_gate_up.weight"].to(T))))
-            d.shared_down[i] = ptr(dev(gw(p[m + "shared_expert.w_down.weight"].to(T))))
-            d.routed_gu[i] = ptr(dev(gw(p[m + "routed_gate_up"].to(T).transpose(1, 2))))
-            d.routed_down[i] = ptr(dev(gw(p[m + "routed_down"].to(T).transpose(1, 2))))
-            d.router[i] = ptr(dev(p[m + "router_weight"][:P], torch.float32))
-            eb = p[m + "expert_bias"]
-            if eb.dim() == 1:
-                eb = eb.unsqueeze(0).expand(cfg.max_pulses, -1)
-            d.expert_bias[i] = ptr(dev(eb[:P], torch.float32))
-            d.routed_scale[i] = ptr(dev(p[m + "routed_scale"][:P], T))
+            L = f"layers.{i}."
+            for name in LAYER_TENSORS:
+                getattr(d, name)[i] = ptr(t[L + name])
         self.desc = d
         torch.cuda.synchronize(self.device)
 
     @property
     def nbytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in self._keep)
+        return sum(x.numel() * x.element_size() for x in self.tensors.values())
 
     def desc_ref(self):
         return ctypes.byref(self.desc)
