@@ -103,5 +103,11 @@ struct GemmArgs {
 
 int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
                 hipStream_t s);
+// Same contract, for row sets of hundreds to tens of thousands of rows (prefill): bf16
+// launches without a fused all-rows group use 128 x 128 output tiles; others fall back to
+// launch_gemm. The two kernels sum K in different orders, so a caller that wants results
+// independent of batch composition picks one by a per-sequence property (prompt length).
+int launch_gemm_wide(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
+                     hipStream_t s);
 
 }  // namespace pulsar

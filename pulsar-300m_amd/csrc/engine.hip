@@ -47,7 +47,7 @@ struct Engine {
   int64_t prof_n[PULSAR_PROF_CLASSES] = {};
   int32_t *topk_idx = nullptr, *keep = nullptr;
   int32_t *lists = nullptr, *list_count = nullptr;      // decode: [L][E][max_rows*K], [L][E]
-  int32_t *p_lists = nullptr, *p_lcount = nullptr, *p_cnt = nullptr;  // prefill
+  int32_t *p_lists = nullptr, *p_lcount = nullptr;  // prefill
   int32_t* p_ids = nullptr;
   RowDesc* p_rows = nullptr;  // [P][R]
   StepCtl* p_ctl = nullptr;   // [P]
@@ -260,7 +260,6 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.list_count, 4 * (size_t)x.L * x.E));
   PULSAR_TRY(x.alloc(&x.p_lists, 4 * (size_t)x.E * R * x.K));
   PULSAR_TRY(x.alloc(&x.p_lcount, 4 * (size_t)x.E));
-  PULSAR_TRY(x.alloc(&x.p_cnt, 4 * (size_t)x.B * x.E));
   PULSAR_TRY(x.alloc(&x.p_ids, 4 * (size_t)x.B * c.max_prompt));
   PULSAR_TRY(x.alloc(&x.p_rows, sizeof(RowDesc) * x.P * (size_t)x.B * c.max_prompt));
   PULSAR_TRY(x.alloc(&x.p_ctl, sizeof(StepCtl) * x.P));
@@ -645,6 +644,8 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   return PULSAR_OK;
 }
 
+constexpr int kWidePromptLen = 128;
+
 int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   const PulsarModelDesc& m = e.m;
   PULSAR_REQUIRE(Bq == e.B, "prefill batch must equal max_batch");
@@ -680,6 +681,13 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   PULSAR_TRY(launch_prefill_stem(e.p_ids, m.tok_emb, m.anchor_norm, m.conv_w, e.xn, e.e_state,
                                  Bq, T, D, m.rms_eps, dt, s));
   const int64_t lstride = (int64_t)e.R * e.K;
+  // Wide-tile GEMMs for prompts of kWidePromptLen tokens or more. The choice depends on the
+  // prompt length only, so a sequence gets the same arithmetic alone or in a batch.
+  const bool wide = T >= kWidePromptLen;
+  auto gemm_rows = [&](const GemmArgs& g, int epi, int groups, int rows) {
+    return wide ? launch_gemm_wide(g, dt, epi, groups, rows, s)
+                : launch_gemm(g, dt, epi, groups, rows, s);
+  };
   for (int k = 0; k < P; ++k) {
     const StepCtl* ctl = e.p_ctl + k;
     const RowDesc* prow = e.p_rows + (size_t)k * BT;
@@ -735,7 +743,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
       g.ldc2 = e.H;
       g.bias = m.gate_bias[l];
       g.bias_group_stride = e.H;
-      PULSAR_TRY(launch_gemm(g, dt, EPI_QKVG, 1, BT, s));
+      PULSAR_TRY(gemm_rows(g, EPI_QKVG, 1, BT));
       QKPostArgs qa{};
       qa.ctl = ctl;
       qa.rows = prow;
@@ -787,7 +795,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
       g.row_mode = ROWS_PULSE;
       g.group_offset = k;
       g.ctl = ctl;
-      PULSAR_TRY(launch_gemm(g, dt, EPI_RESID, 1, BT, s));
+      PULSAR_TRY(gemm_rows(g, EPI_RESID, 1, BT));
       na.w = m.mlp_norm[l];
       PULSAR_TRY(launch_norm_rows(na, dt, BT, s));
       RouterArgs ra{};
@@ -806,10 +814,11 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
       const double avg = (double)T * e.K / e.E;
       const long raw = (long)std::ceil(avg * 1.25);
       const int C = (int)std::max<long>(32, ((raw + 31) / 32) * 32);
-      PULSAR_CHECK_HIP(hipMemsetAsync(e.p_cnt, 0, 4 * (size_t)Bq * e.E, s));
+      // an expert keeps at most C tokens of each sequence
+      const int list_max = (int)std::min<long>(BT, (long)Bq * C);
       PULSAR_CHECK_HIP(hipMemsetAsync(e.p_lcount, 0, 4 * (size_t)e.E, s));
-      PULSAR_TRY(launch_prefill_capacity(e.topk_idx, e.topk_w, e.p_cnt, e.keep, e.p_lists,
-                                         e.p_lcount, lstride, Bq, T, e.K, e.E, C, s));
+      PULSAR_TRY(launch_prefill_capacity(e.topk_idx, e.topk_w, e.keep, e.p_lists, e.p_lcount,
+                                         lstride, Bq, T, e.K, e.E, C, s));
       g = gemm_base(e);
       g.A = e.xn;
       g.lda = D;
@@ -821,7 +830,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
       g.N = e.ds;
       g.row_mode = ROWS_ALL;
       g.m_fixed = BT;
-      PULSAR_TRY(launch_gemm(g, dt, EPI_SWIGLU, 1, BT, s));
+      PULSAR_TRY(gemm_rows(g, EPI_SWIGLU, 1, BT));
       g = gemm_base(e);
       g.A = e.xn;
       g.lda = D;
@@ -837,7 +846,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
       g.list_count = e.p_lcount;
       g.list_stride = lstride;
       g.a_div = e.K;
-      PULSAR_TRY(launch_gemm(g, dt, EPI_SWIGLU, e.E, BT, s));
+      PULSAR_TRY(gemm_rows(g, EPI_SWIGLU, e.E, list_max));
       g = gemm_base(e);
       g.A = e.act_s;
       g.lda = e.ds;
@@ -849,7 +858,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
       g.N = D;
       g.row_mode = ROWS_ALL;
       g.m_fixed = BT;
-      PULSAR_TRY(launch_gemm(g, dt, EPI_STORE, 1, BT, s));
+      PULSAR_TRY(gemm_rows(g, EPI_STORE, 1, BT));
       g = gemm_base(e);
       g.A = e.act_r;
       g.lda = e.de;
@@ -866,7 +875,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
       g.list_stride = lstride;
       g.a_div = 1;
       g.bias = reinterpret_cast<const char*>(m.routed_scale[l]) + (size_t)k * D * e.es;
-      PULSAR_TRY(launch_gemm(g, dt, EPI_SCALE, e.E, BT, s));
+      PULSAR_TRY(gemm_rows(g, EPI_SCALE, e.E, list_max));
       CombineArgs ca{};
       ca.m_fixed = BT;
       ca.pulse = k;

@@ -339,6 +339,150 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
   }
 }
 
+// Four consecutive output columns of one row (col0 % 4 == 0, never straddling n_main).
+__device__ __forceinline__ void epilogue4(const GemmArgs& g, int epi, int group, void* Cv,
+                                          int64_t ldc, int crow, int col0, const float* v,
+                                          const float* u) {
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  bf16* C = reinterpret_cast<bf16*>(Cv);
+  bf16x4_t o;
+  switch (epi) {
+    case EPI_STORE:
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = (__bf16)v[j];
+      break;
+    case EPI_RESID: {
+      const bf16x4_t h = *reinterpret_cast<const bf16x4_t*>(C + (int64_t)crow * ldc + col0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = (__bf16)((float)h[j] + rnd<bf16>(v[j]));
+      break;
+    }
+    case EPI_SWIGLU:
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float gt = rnd<bf16>(v[j]), up = rnd<bf16>(u[j]);
+        o[j] = (__bf16)(gt * sigmoidf_(gt) * up);
+      }
+      break;
+    case EPI_SCALE: {
+      const bf16x4_t sc = *reinterpret_cast<const bf16x4_t*>(reinterpret_cast<const bf16*>(g.bias) + col0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = (__bf16)(rnd<bf16>(v[j]) * (float)sc[j]);
+      break;
+    }
+    default:  // EPI_QKVG: q/k/v columns stored, gate columns through the scalar epilogue
+      if (col0 >= g.n_main) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) epilogue<bf16>(g, epi, group, Cv, ldc, crow, col0 + j, v[j], 0.f);
+        return;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = (__bf16)v[j];
+      break;
+  }
+  *reinterpret_cast<bf16x4_t*>(C + (int64_t)crow * ldc + col0) = o;
+}
+
+// Wide row sets (prefill): a workgroup of 4 waves owns a 128-row x 128-column output
+// tile (SwiGLU: 128 rows x 64 gate columns and their 64 up-projection twins); wave
+// (wr, wc) computes the 64 x 64 quarter (wr, wc) as 4 x 4 tiles of
+// v_mfma_f32_16x16x32_bf16. Both operands go from memory straight to registers in MFMA
+// lane order: the weights are stored in that order (one 16x32 tile = 1 KB contiguous per
+// wave) and every lane fetches 16 bytes of its own A row, so gathered expert rows cost
+// nothing extra. The products are formed transposed (weights as the A operand, rows as
+// B), so a lane ends with 4 consecutive output columns of its own row: 8-byte epilogue
+// loads and stores, and the C row is the entry the lane already holds. The k tiles are
+// software-pipelined kWideStages deep in registers.
+constexpr int kWideStages = 2;
+constexpr int kWideRows = 128;
+
+template <int EPI, int MODE>
+__global__ void __launch_bounds__(256) gemm_bf16_wide_kernel(GemmArgs g) {
+  constexpr bool kPair = (EPI == EPI_SWIGLU);
+  constexpr int kCT = kPair ? 2 : 4;  // column tiles per wave (gate tiles for SwiGLU)
+  constexpr int kB = 4;               // weight fragments per k tile (SwiGLU: 2 gate + 2 up)
+  constexpr int S = kWideStages;
+  const int group = (int)blockIdx.y + g.group_offset;
+  const int N = g.N;
+  const int KT = g.K / 32;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wr = wv >> 1, wc = wv & 1;
+  const int m16 = lane & 15, kq = lane >> 4;
+  const int cnt = group_rows<MODE>(g, group);
+  const int r_wg = (int)blockIdx.z * kWideRows;
+  if (r_wg >= cnt) return;
+  const int ct0 = (int)blockIdx.x * (kPair ? 4 : 8) + wc * kCT;  // first gate column tile
+  if (ct0 * 16 >= N) return;  // the wave's column tiles all lie past N (uniform per wave)
+
+  // rows of this lane: row m16 of each 16-row tile rt; rows past the set re-read the last
+  int ent[4];
+  const bf16* ap[4];
+  const bf16* A = reinterpret_cast<const bf16*>(g.A);
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    const int i = min(r_wg + wr * 64 + rt * 16 + m16, cnt - 1);
+    ent[rt] = entry_load<MODE>(g, group, i);
+    ap[rt] = A + (int64_t)a_row_of<MODE>(g, group, ent[rt]) * g.lda + kq * 8;
+  }
+  // weight fragments: tile (ct, kt) of this lane at ((ct * KT + kt) * 64 + lane) * 8
+  const bf16* W = reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
+  const bf16* wp[kB];
+#pragma unroll
+  for (int c = 0; c < kB; ++c) {
+    int ct = kPair ? (c < 2 ? ct0 + c : N / 16 + ct0 + (c - 2)) : ct0 + c;
+    if (!kPair) ct = min(ct, N / 16 - 1);  // tiles past N re-read the last one (never stored)
+    wp[c] = W + ((int64_t)ct * KT * 64 + lane) * 8;
+  }
+  f32x4_t acc[4][kB];  // [row tile][column tile]: lane holds columns 4 kq + j of row m16
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int c = 0; c < kB; ++c) acc[rt][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  bf16x8_t xa[S][4], xb[S][kB];
+#pragma unroll
+  for (int st = 0; st < S; ++st) {
+#pragma unroll
+    for (int c = 0; c < kB; ++c) xb[st][c] = load_bf16x8(wp[c] + (int64_t)st * 512);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) xa[st][rt] = load_bf16x8(ap[rt] + st * 32);
+  }
+  for (int kt0 = 0; kt0 < KT; kt0 += S) {
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int c = 0; c < kB; ++c)
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[st][c], xa[st][rt], acc[rt][c], 0, 0, 0);
+      const int kn = kt0 + st + S;
+      if (kn < KT) {
+#pragma unroll
+        for (int c = 0; c < kB; ++c) xb[st][c] = load_bf16x8(wp[c] + (int64_t)kn * 512);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) xa[st][rt] = load_bf16x8(ap[rt] + kn * 32);
+      }
+    }
+  }
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    const int i = r_wg + wr * 64 + rt * 16 + m16;
+    if (i >= cnt) continue;
+    const int crow = entry_fix<MODE>(group, i, ent[rt]) + g.c_row_offset;
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) {
+      const int col0 = (ct0 + c) * 16 + kq * 4;
+      if (col0 >= N) continue;
+      float v[4], u[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = acc[rt][c][j];
+        u[j] = kPair ? acc[rt][c + 2][j] : 0.f;
+      }
+      epilogue4(g, EPI, group, g.C, g.ldc, crow, col0, v, u);
+    }
+  }
+}
+
 template <int EPI, int MODE, int KMUL0>
 void launch_bf16_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
   constexpr int T = 64 * kGemmWaves;
@@ -390,7 +534,40 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
   return PULSAR_OK;
 }
 
+template <int EPI>
+int launch_wide(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
+  const int colw = EPI == EPI_SWIGLU ? 64 : 128;
+  dim3 grid((unsigned)((a.N + colw - 1) / colw), (unsigned)groups,
+            (unsigned)((max_rows + kWideRows - 1) / kWideRows));
+  switch (a.row_mode) {
+    case ROWS_PULSE: gemm_bf16_wide_kernel<EPI, ROWS_PULSE><<<grid, 256, 0, s>>>(a); break;
+    case ROWS_LIST: gemm_bf16_wide_kernel<EPI, ROWS_LIST><<<grid, 256, 0, s>>>(a); break;
+    case ROWS_ALL: gemm_bf16_wide_kernel<EPI, ROWS_ALL><<<grid, 256, 0, s>>>(a); break;
+    default: return fail(PULSAR_ERR_INVALID, "gemm: row mode of a wide launch");
+  }
+  PULSAR_LAUNCH_CHECK();
+  return PULSAR_OK;
+}
+
 }  // namespace
+
+int launch_gemm_wide(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
+                     hipStream_t s) {
+  if (dtype != PULSAR_BF16 || a.has_g0 || a.row_mode == ROWS_LOGITS)
+    return launch_gemm(a, dtype, epi, groups, max_rows, s);
+  if (groups <= 0) return PULSAR_OK;
+  if (a.K % 256 != 0 || a.N % 16 != 0 || (epi == EPI_SWIGLU && a.N % 64 != 0))
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: wide tiles need K % 256 == 0 and N % 16 == 0 "
+                                        "(SwiGLU: N % 64 == 0)");
+  switch (epi) {
+    case EPI_STORE: return launch_wide<EPI_STORE>(a, groups, max_rows, s);
+    case EPI_QKVG: return launch_wide<EPI_QKVG>(a, groups, max_rows, s);
+    case EPI_RESID: return launch_wide<EPI_RESID>(a, groups, max_rows, s);
+    case EPI_SWIGLU: return launch_wide<EPI_SWIGLU>(a, groups, max_rows, s);
+    case EPI_SCALE: return launch_wide<EPI_SCALE>(a, groups, max_rows, s);
+  }
+  return launch_gemm(a, dtype, epi, groups, max_rows, s);
+}
 
 int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows, hipStream_t s) {
   if (a.K % 256 != 0)

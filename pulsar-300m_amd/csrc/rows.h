@@ -240,9 +240,9 @@ int launch_router_decode(const RouterArgs& a, int dtype, int max_rows, hipStream
 // mlp_norm + router fused: a.x = residual stream h, a.norm_w/a.xn the norm weight/output.
 int launch_norm_router(const RouterArgs& a, int dtype, int max_rows, hipStream_t s);
 int launch_router_prefill(const RouterArgs& a, int dtype, hipStream_t s);
-int launch_prefill_capacity(const int32_t* idx, const float* w, int32_t* cnt, int32_t* keep,
-                            int32_t* lists, int32_t* lcount, int64_t list_stride, int B, int T_,
-                            int K, int E, int C, hipStream_t s);
+int launch_prefill_capacity(const int32_t* idx, const float* w, int32_t* keep, int32_t* lists,
+                            int32_t* lcount, int64_t list_stride, int B, int T_, int K, int E,
+                            int C, hipStream_t s);
 int launch_moe_combine(const CombineArgs& a, int dtype, int max_rows, hipStream_t s);
 int launch_pulse_output(const PulseOutputArgs& a, int dtype, int max_rows, hipStream_t s);
 int launch_prefill_stem(const int32_t* ids, const void* emb, const float* anchor_w,

@@ -773,6 +773,172 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Prefill attention in bf16 on the matrix cores (same key ranges as attn_prefill_kernel).
+// Block = (sequence, 64-query tile, kv head); wave w = query head 4g + w over the tile's 64
+// queries, so each 64-key block staged in LDS serves the 4 heads of the group. Per block:
+// S^T = K Q^T (keys x queries), online softmax per query, O^T += V^T P^T (dims x queries).
+// In this orientation P never leaves the registers: the D tile of S^T gives lane l keys
+// 4*(l/16) + j (j < 4) of query l % 16, and the B operand of the second product takes 8
+// keys of query l % 16 -- here the 4 keys of key tile 2s and the 4 of tile 2s + 1, a
+// permutation of the reduction index that the V^T operand (two 8-byte LDS reads) repeats.
+// Scores use exp2 with log2(e) folded into the scale; P is rounded to bf16 for the second
+// product, the running max, sum and output accumulate in fp32.
+// ---------------------------------------------------------------------------
+typedef __bf16 attn_bf16x4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
+  constexpr int kLd = 72;  // LDS row stride in bf16: 16 bytes of padding against bank conflicts
+  __shared__ __attribute__((aligned(16))) __bf16 Ks[64][kLd];  // [key][dim]
+  __shared__ __attribute__((aligned(16))) __bf16 Vs[64][kLd];  // [dim][key]
+  const int T_ = a.prefill_T;
+  const int ntile = (T_ + 63) / 64;
+  const int b = (int)blockIdx.x / ntile;
+  const int qt = ntile - 1 - (int)blockIdx.x % ntile;  // longest key ranges first
+  const int g = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int m16 = lane & 15, kq = lane >> 4;
+  const int head = g * 4 + wv;
+  const bool quirk = a.is_local && T_ > a.window;
+  const int q0 = qt * 64;
+  const int qlast = min(q0 + 63, T_ - 1);
+  const int tlo = quirk ? T_ - a.window : 0;
+  const int thi = quirk ? T_ - a.window + min(qlast, a.window - 1) : qlast;
+  // keys every query of the tile sees: blocks inside [flo, fhi] need no mask
+  const int flo = tlo;
+  const int fhi = quirk ? T_ - a.window + min(q0, a.window - 1) : q0;
+
+  int qlo[4], qhi[4];
+  attn_bf16x8 qb[4][2];  // Q^T operand: column = query m16 of tile nt, dims kq*8 + 32*ks
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int t = q0 + nt * 16 + m16;
+    const int tc = min(t, T_ - 1);
+    qlo[nt] = tlo;
+    qhi[nt] = t >= T_ ? -1 : (quirk ? T_ - a.window + min(tc, a.window - 1) : tc);
+    const bf16* qp = reinterpret_cast<const bf16*>(a.qkv) + ((int64_t)b * T_ + tc) * a.ldq +
+                     head * 64 + kq * 8;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) qb[nt][ks] = *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32);
+  }
+  attn_f32x4 o[4][4];  // O^T tile (dim tile mt, query tile nt)
+  float mrun[4], lrun[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    mrun[nt] = -INFINITY;
+    lrun[nt] = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[mt][nt] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float sl2 = a.scale * 1.4426950408889634f;
+
+  // staging: thread -> K row tid/4 (dims 16*(tid%4) .. +16) and V row tid/4 (keys likewise)
+  const int sr = tid >> 2, sc16 = (tid & 3) * 16;
+  const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]);
+  const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]);
+  attn_bf16x8 kr[2], vr[2];
+  auto fetch = [&](int kb) {
+    const KVBlock blk = kv_block(a.kv, a.layer, b, g, kb);
+    const bf16* kp = Kc + blk.k0 + sr * 64 + sc16;
+    const bf16* vp = Vc + blk.v0 + (int64_t)sr * blk.vstride + sc16;
+    kr[0] = *reinterpret_cast<const attn_bf16x8*>(kp);
+    kr[1] = *reinterpret_cast<const attn_bf16x8*>(kp + 8);
+    vr[0] = *reinterpret_cast<const attn_bf16x8*>(vp);
+    vr[1] = *reinterpret_cast<const attn_bf16x8*>(vp + 8);
+  };
+  const int kb0 = tlo & ~63;
+  fetch(kb0);
+  for (int kb = kb0; kb <= thi; kb += 64) {
+    __syncthreads();  // the previous block's LDS reads are done
+    *reinterpret_cast<attn_bf16x8*>(&Ks[sr][sc16]) = kr[0];
+    *reinterpret_cast<attn_bf16x8*>(&Ks[sr][sc16 + 8]) = kr[1];
+    *reinterpret_cast<attn_bf16x8*>(&Vs[sr][sc16]) = vr[0];
+    *reinterpret_cast<attn_bf16x8*>(&Vs[sr][sc16 + 8]) = vr[1];
+    __syncthreads();
+    if (kb + 64 <= thi) fetch(kb + 64);  // in flight during this block's products
+
+    attn_f32x4 sv[4][4];  // S^T tile (key tile kt, query tile nt)
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const attn_bf16x8 k0 = *reinterpret_cast<const attn_bf16x8*>(&Ks[kt * 16 + m16][kq * 8]);
+      const attn_bf16x8 k1 = *reinterpret_cast<const attn_bf16x8*>(&Ks[kt * 16 + m16][32 + kq * 8]);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qb[nt][0], acc, 0, 0, 0);
+        sv[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qb[nt][1], acc, 0, 0, 0);
+      }
+    }
+    const bool full = kb >= flo && kb + 63 <= fhi;  // uniform per block
+    attn_bf16x8 pb[4][2];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float v = sv[kt][nt][j] * sl2;
+          if (!full) {
+            const int key = kb + kt * 16 + kq * 4 + j;
+            v = (key >= qlo[nt] && key <= qhi[nt]) ? v : -INFINITY;
+          }
+          sv[kt][nt][j] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, swz_xor16(mx));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(mrun[nt], mx);
+      const float muse = mnew == -INFINITY ? 0.f : mnew;
+      const float f = __builtin_amdgcn_exp2f(mrun[nt] - muse);
+      mrun[nt] = mnew;
+      float ls = lrun[nt] * f;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) o[mt][nt] *= f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p = __builtin_amdgcn_exp2f(sv[kt][nt][j] - muse);
+          ls += p;
+          pb[nt][kt >> 1][(kt & 1) * 4 + j] = (__bf16)p;
+        }
+      lrun[nt] = ls;
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const attn_bf16x4 lo4 = *reinterpret_cast<const attn_bf16x4*>(&Vs[mt * 16 + m16][ks * 32 + kq * 4]);
+        const attn_bf16x4 hi4 = *reinterpret_cast<const attn_bf16x4*>(&Vs[mt * 16 + m16][ks * 32 + 16 + kq * 4]);
+        const attn_bf16x8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[nt][ks], o[mt][nt], 0, 0, 0);
+      }
+  }
+  // lane holds O[query q0 + 16 nt + m16][dims 16 mt + 4 kq + j]
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    float l = lrun[nt];
+    l += swz_xor16(l);
+    l += __shfl_xor(l, 32, 64);
+    const int t = q0 + nt * 16 + m16;
+    if (t >= T_) continue;
+    const int64_t row = (int64_t)b * T_ + t;
+    const float gate = bf2f(reinterpret_cast<const bf16*>(a.gate)[row * a.H + head]);
+    const float inv = 1.0f / l;
+    bf16* op = reinterpret_cast<bf16*>(a.out) + row * a.H * 64 + head * 64 + kq * 4;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      attn_bf16x4 w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = (__bf16)(rnd<bf16>(o[mt][nt][j] * inv) * gate);
+      *reinterpret_cast<attn_bf16x4*>(op + mt * 16) = w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Decode router: fp32 logits of the normed row, centred sigmoid + bias, top-k, and the
 // per-expert assignment lists of this layer.
 // ---------------------------------------------------------------------------
@@ -894,47 +1060,140 @@ __global__ void __launch_bounds__(256) router_prefill_kernel(RouterArgs a) {
   route_topk<T>(lg, E, a.K, a.bias + (int64_t)a.pulse * E, r, a);
 }
 
-// ---------------------------------------------------------------------------
-// Prefill capacity: per (sequence, expert) count, then the rank of each assignment in
-// (weight desc, flat index asc) order via the float key e - 0.5*w/(1+w); assignments
-// ranked >= capacity are dropped. Kept assignments are appended to the expert lists.
-// ---------------------------------------------------------------------------
-__global__ void prefill_count_kernel(const int32_t* __restrict__ idx, int32_t* __restrict__ cnt,
-                                     int T_, int K, int E, int64_t total) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int b = (int)(i / ((int64_t)T_ * K));
-  atomicAdd(&cnt[b * E + idx[i]], 1);
+// Prefill router in bf16 on the matrix cores: logits[rows][E] = X . bf16(W)^T with fp32
+// accumulation, E <= 16 experts as the 16 columns of one v_mfma_f32_16x16x32_bf16 tile;
+// a wave owns 16 rows. The logits, rounded to bf16, go through LDS to the shared top-k
+// routine (one lane per row), so routing is the same as router_prefill_kernel's.
+__global__ void __launch_bounds__(256) router_prefill_mfma_kernel(RouterArgs a) {
+  __shared__ float lg[4][16][17];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int m16 = lane & 15, kq = lane >> 4;
+  const int r0 = ((int)blockIdx.x * 4 + wv) * 16;
+  const int D = a.D, E = a.E;
+  const bf16* xp = reinterpret_cast<const bf16*>(a.x) +
+                   (int64_t)min(r0 + m16, a.m_fixed - 1) * D + kq * 8;
+  const bool ev = m16 < E;
+  const float* wp = a.w + ((int64_t)a.pulse * E + (ev ? m16 : 0)) * D + kq * 8;
+  attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const attn_bf16x8 zero = {};
+  for (int k = 0; k < D; k += 256) {
+    attn_bf16x8 xa[8], wb[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      xa[u] = *reinterpret_cast<const attn_bf16x8*>(xp + k + 32 * u);
+      const float4 w0 = *reinterpret_cast<const float4*>(wp + k + 32 * u);
+      const float4 w1 = *reinterpret_cast<const float4*>(wp + k + 32 * u + 4);
+      attn_bf16x8 t;
+      t[0] = (__bf16)w0.x; t[1] = (__bf16)w0.y; t[2] = (__bf16)w0.z; t[3] = (__bf16)w0.w;
+      t[4] = (__bf16)w1.x; t[5] = (__bf16)w1.y; t[6] = (__bf16)w1.z; t[7] = (__bf16)w1.w;
+      wb[u] = ev ? t : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[u], wb[u], acc, 0, 0, 0);
+  }
+  // lane holds the logits of rows 4 kq + j for expert m16
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lg[wv][kq * 4 + j][m16] = rnd<bf16>(acc[j]);
+  __syncthreads();
+  if (lane < 16 && r0 + lane < a.m_fixed)
+    route_topk<bf16>(lg[wv][lane], E, a.K, a.bias + (int64_t)a.pulse * E, r0 + lane, a);
 }
 
-__global__ void prefill_slots_kernel(const int32_t* __restrict__ idx, const float* __restrict__ w,
-                                     const int32_t* __restrict__ cnt, int32_t* __restrict__ keep,
-                                     int32_t* __restrict__ lists, int32_t* __restrict__ lcount,
-                                     int64_t list_stride, int T_, int K, int E, int C,
-                                     int64_t total) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int64_t per = (int64_t)T_ * K;
-  const int b = (int)(i / per);
-  const int e = idx[i];
-  bool kept = true;
-  if (cnt[b * E + e] > C) {
+// ---------------------------------------------------------------------------
+// Prefill capacity: within each sequence, the assignments of an expert beyond its
+// capacity C are dropped, ranked in (weight desc, flat index asc) order via the float key
+// e - 0.5*w/(1+w). Kept assignments are appended to the expert lists.
+// ---------------------------------------------------------------------------
+// One block per (sequence, expert). A first pass counts the sequence's assignments to the
+// expert and stages up to kCapStage of them in LDS. Under capacity every one is kept; over
+// capacity each is ranked against the others by (key asc, flat index asc), in LDS when
+// staged, else against the sequence's assignments in memory. The block then reserves its
+// kept count in the expert's list with one atomic and writes its entries there.
+constexpr int kCapStage = 4096;
+__global__ void __launch_bounds__(256) prefill_select_kernel(
+    const int32_t* __restrict__ idx, const float* __restrict__ w, int32_t* __restrict__ keep,
+    int32_t* __restrict__ lists, int32_t* __restrict__ lcount, int64_t list_stride, int T_, int K,
+    int E, int C) {
+  __shared__ int s_n, s_base;
+  __shared__ int s_off[256];
+  __shared__ int sidx[kCapStage];
+  __shared__ float skey[kCapStage];
+  const int b = (int)blockIdx.x / E, e = (int)blockIdx.x % E;
+  const int64_t per = (int64_t)T_ * K, s0 = (int64_t)b * per;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  auto key_of = [&](int64_t i) {
     const float wi = fmaxf(w[i], 0.f);
-    const float ki = (float)e - (wi / (1.0f + wi)) * 0.5f;
-    int rank = 0;
-    const int64_t s0 = (int64_t)b * per;
-    for (int64_t j = s0; j < s0 + per; ++j) {
-      if (idx[j] != e || j == i) continue;
-      const float wj = fmaxf(w[j], 0.f);
-      const float kj = (float)e - (wj / (1.0f + wj)) * 0.5f;
-      if (kj < ki || (kj == ki && j < i)) ++rank;
+    return (float)e - (wi / (1.0f + wi)) * 0.5f;
+  };
+  if (tid == 0) s_n = 0;
+  __syncthreads();
+  for (int64_t i = s0 + tid; i < s0 + per; i += nt)
+    if (idx[i] == e) {
+      const int q = atomicAdd(&s_n, 1);
+      if (q < kCapStage) {
+        sidx[q] = (int)(i - s0);
+        skey[q] = key_of(i);
+      }
     }
-    kept = rank < C;
+  __syncthreads();
+  const int n = s_n;
+  const bool staged = n <= kCapStage;
+  int mine = 0;
+  if (staged) {
+    for (int q = tid; q < n; q += nt) {
+      bool kept = true;
+      if (n > C) {
+        const int iq = sidx[q];
+        const float kq = skey[q];
+        int rank = 0;
+        for (int u = 0; u < n; ++u) {
+          const float ku = skey[u];
+          rank += (ku < kq || (ku == kq && sidx[u] < iq)) ? 1 : 0;
+        }
+        kept = rank < C;
+      }
+      keep[s0 + sidx[q]] = kept ? 1 : 0;
+      mine += kept ? 1 : 0;
+    }
+  } else {
+    for (int64_t i = s0 + tid; i < s0 + per; i += nt) {
+      if (idx[i] != e) continue;
+      bool kept = true;
+      if (n > C) {
+        const float ki = key_of(i);
+        int rank = 0;
+        for (int64_t j = s0; j < s0 + per; ++j) {
+          if (idx[j] != e || j == i) continue;
+          const float kj = key_of(j);
+          if (kj < ki || (kj == ki && j < i)) ++rank;
+        }
+        kept = rank < C;
+      }
+      keep[i] = kept ? 1 : 0;
+      mine += kept ? 1 : 0;
+    }
   }
-  keep[i] = kept ? 1 : 0;
-  if (kept) {
-    const int p = atomicAdd(&lcount[e], 1);
-    lists[(int64_t)e * list_stride + p] = (int32_t)i;
+  s_off[tid] = mine;
+  __syncthreads();
+  if (tid == 0) {
+    int tot = 0;
+    for (int t = 0; t < nt; ++t) {
+      const int v = s_off[t];
+      s_off[t] = tot;
+      tot += v;
+    }
+    s_base = tot ? atomicAdd(&lcount[e], tot) : 0;
+  }
+  __syncthreads();
+  int32_t* out = lists + (int64_t)e * list_stride + s_base + s_off[tid];
+  if (staged) {
+    for (int q = tid; q < n; q += nt) {
+      const int64_t i = s0 + sidx[q];
+      if (keep[i]) *out++ = (int32_t)i;
+    }
+  } else {
+    for (int64_t i = s0 + tid; i < s0 + per; i += nt)
+      if (idx[i] == e && keep[i]) *out++ = (int32_t)i;
   }
 }
 
@@ -1105,6 +1364,13 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
 }
 int launch_attn_prefill(const AttnArgs& a, int dtype, int B, hipStream_t s) {
   const int ntile = (a.prefill_T + 63) / 64;
+  if (a.H != 4 * a.Hkv)
+    return fail(PULSAR_ERR_UNSUPPORTED, "prefill attention: four query heads per kv head");
+  if (dtype == PULSAR_BF16) {
+    attn_prefill_mfma_kernel<<<dim3(B * ntile, a.Hkv), 256, 0, s>>>(a);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  }
   PULSAR_DISPATCH(dtype, attn_prefill_kernel, dim3(B * ntile, a.Hkv), 256, a);
 }
 int launch_router_decode(const RouterArgs& a, int dtype, int max_rows, hipStream_t s) {
@@ -1136,17 +1402,20 @@ int launch_norm_router(const RouterArgs& a, int dtype, int max_rows, hipStream_t
   return fail(PULSAR_ERR_UNSUPPORTED, "norm_router: n_experts must be 8 or 16");
 }
 int launch_router_prefill(const RouterArgs& a, int dtype, hipStream_t s) {
+  if (a.E > 32) return fail(PULSAR_ERR_UNSUPPORTED, "router: at most 32 experts");
+  if (dtype == PULSAR_BF16 && a.E <= 16 && a.D % 256 == 0) {
+    router_prefill_mfma_kernel<<<dim3((unsigned)((a.m_fixed + 63) / 64)), 256, 0, s>>>(a);
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  }
   PULSAR_DISPATCH(dtype, router_prefill_kernel, dim3(a.m_fixed), 256, a);
 }
-int launch_prefill_capacity(const int32_t* idx, const float* w, int32_t* cnt, int32_t* keep,
-                            int32_t* lists, int32_t* lcount, int64_t list_stride, int B, int T_,
-                            int K, int E, int C, hipStream_t s) {
-  const int64_t total = (int64_t)B * T_ * K;
-  const unsigned blocks = (unsigned)((total + 255) / 256);
-  prefill_count_kernel<<<blocks, 256, 0, s>>>(idx, cnt, T_, K, E, total);
-  PULSAR_LAUNCH_CHECK();
-  prefill_slots_kernel<<<blocks, 256, 0, s>>>(idx, w, cnt, keep, lists, lcount, list_stride, T_,
-                                              K, E, C, total);
+int launch_prefill_capacity(const int32_t* idx, const float* w, int32_t* keep, int32_t* lists,
+                            int32_t* lcount, int64_t list_stride, int B, int T_, int K, int E,
+                            int C, hipStream_t s) {
+  if (B < 1 || E < 1) return PULSAR_OK;
+  prefill_select_kernel<<<(unsigned)(B * E), 256, 0, s>>>(idx, w, keep, lists, lcount, list_stride,
+                                                           T_, K, E, C);
   PULSAR_LAUNCH_CHECK();
   return PULSAR_OK;
 }

@@ -105,13 +105,16 @@ def test_fp32_greedy_stream_identical_to_reference_golden(models):
     assert ids == g["greedy_rp10_spec_ids"].tolist()
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_greedy_speculative_equals_plain_and_batch_equals_single(models, full_state, dtype):
+@pytest.mark.parametrize("dtype,plen", [(torch.float32, 33), (torch.bfloat16, 33),
+                                         (torch.bfloat16, 160)])
+def test_greedy_speculative_equals_plain_and_batch_equals_single(models, full_state, dtype, plen):
+    """160-token prompts take the wide-tile prefill GEMMs, 33-token ones the row-tile ones;
+    either way a sequence's arithmetic does not depend on the rest of the batch."""
     from pulsar_engine import weights as W
     from pulsar_engine.engine import PulsarInferenceEngine
 
     cfg = full_state[0]
-    prompts = [W.uniform_ids(s, "batch_prompt", 33, cfg.vocab_size).tolist() for s in range(4)]
+    prompts = [W.uniform_ids(s, "batch_prompt", plen, cfg.vocab_size).tolist() for s in range(4)]
     eng = PulsarInferenceEngine(models[dtype])
     kw = dict(max_new_tokens=12, temperature=0.0, repetition_penalty=10.0, stop_ids=[0, 2])
     spec = eng.generate_ids(prompts, speculative=True, **kw)
@@ -189,3 +192,38 @@ def test_long_prompt_passes_cover_window_and_yarn(models, full_state, dtype, tol
 
     prompt = W.uniform_ids(9, "long_prompt", 1100, full_state[0].vocab_size).tolist()
     _compare_passes(models, full_state, dtype, prompt, 3, tol=tol, rp=10.0)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_prefill_capacity_drops_match_oracle(full_state, dtype, tol):
+    """Expert biases that send every token to experts 0-3 put each of them far over the
+    prefill capacity of a 200-token prompt (C = 64 slots for 200 assignments): the kept
+    set, chosen by routing weight, decides every later hidden state. Two sequences in one
+    batch (capacity is per sequence); prefill logits of each against the oracle."""
+    from oracle import pulsar_ref as R
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+    from pulsar_engine.model import DeviceModel
+
+    cfg, st = full_state
+    bias = np.zeros(cfg.n_routed_experts, np.float32)
+    bias[:4] = 1.0
+    st2 = dict(st)
+    for i in range(cfg.n_core):
+        st2[f"core.{i}.mlp.expert_bias"] = np.tile(bias, (cfg.max_pulses, 1))
+    T_ = 200
+    assert R.moe_capacity(T_, cfg) == 64
+    prompts = np.stack([W.uniform_ids(70 + b, "cap_prompt", T_, cfg.vocab_size) for b in range(2)])
+    model = DeviceModel(cfg, st2, dtype)
+    eng = HipEngine(model, batch=2, max_prompt=T_, max_new=4, speculative=False,
+                    temperature=0.0, repetition_penalty=1.0, stop_ids=[])
+    eng.prefill(prompts)
+    got = eng.logits(2)
+    ref_eng = R.load_ref(cfg, st2, dtype, rope_tables_fp32=True, stop_ids=set())
+    for b in range(2):
+        cache = R.RefKVCache(cfg)
+        ref = ref_eng.prefill(torch.as_tensor(prompts[b]).view(1, -1), cache).float().numpy().reshape(-1)
+        err = max_abs_rel(got[b], ref)
+        print(f"{dtype} sequence {b}: {err:.3e}")
+        assert err <= tol, (b, err)
+    eng.close()
