@@ -18,7 +18,7 @@ struct Engine {
   PulsarEngineConfig cfg{};
   int dtype = 0, es = 4;
   int D = 0, H = 0, Hkv = 0, qkv = 0, qkvg = 0, E = 0, K = 0, de = 0, ds = 0, L = 0, P = 0, V = 0;
-  int B = 0, max_rows = 0, R = 0, max_pages = 0, lcap = 0, max_splits = 0;
+  int B = 0, max_rows = 0, R = 0, max_pages = 0, lcap = 0, max_splits = 0, max_splits_unit = 0;
   std::vector<void*> allocs;
 
   StepCtl* ctl = nullptr;
@@ -215,6 +215,7 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   e->lcap = (m.window + c.max_new + 2 * kPage - 1) / kPage * kPage;
   // decode splits start at a 64-aligned position at most 63 keys before the first key
   e->max_splits = (c.max_ctx + kPage - 1 + kSplitLen - 1) / kSplitLen;
+  e->max_splits_unit = (c.max_ctx + kPage - 1 + kUnitSplit - 1) / kUnitSplit;
   const size_t es = e->es, D = e->D, R = e->R, MR = e->max_rows;
   Engine& x = *e;
   PULSAR_TRY(x.alloc(&x.ctl, sizeof(StepCtl)));
@@ -390,6 +391,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     aa.max_units = e.B;
     aa.part = e.part;
     aa.max_splits = e.max_splits;
+    aa.max_splits_unit = e.max_splits_unit;
     aa.H = e.H;
     aa.Hkv = e.Hkv;
     aa.layer = l;

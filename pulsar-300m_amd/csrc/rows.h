@@ -5,7 +5,12 @@
 
 namespace pulsar {
 
-constexpr int kSplitLen = 256;  // keys per decode-attention block
+constexpr int kSplitLen = 256;  // keys per decode-attention block (fp32 path)
+// bf16 decode attention: waves per workgroup and keys per split workgroup (one 64-key
+// block per wave: more, shorter splits measured faster than fewer, longer ones)
+constexpr int kUnitWaves = 4;
+constexpr int kUnitSplit = kUnitWaves * 64;
+static_assert(kUnitSplit >= kSplitLen, "split partial slots are sized for kSplitLen");
 constexpr int kMaxRank = 16;    // re-injection gate rank bound
 
 // KV cache addressing. Local (sliding-window) layers: a per-sequence ring of `lcap`
@@ -134,7 +139,8 @@ struct AttnArgs {
   void* out;         // [rows][H*64] T
   float* part;       // decode split partials
   int32_t* split_done;  // decode: per (unit, kv head) count of finished splits (self-resetting)
-  int max_splits;
+  int max_splits;       // split partial slots per (unit or row, kv head)
+  int max_splits_unit;  // bf16 path: splits of kUnitSplit keys
   int max_units;
   int H, Hkv, layer, is_local, window, prefill_T;
   float scale;

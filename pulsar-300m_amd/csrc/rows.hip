@@ -447,32 +447,12 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention on the matrix cores (bf16 caches). Block (unit, kv head, split): the
-// unit's rows (the current token, and the speculative token one position later when
-// present) read each key block of the cache once. Each wave takes one 64-aligned block of
-// 64 keys (one page of a global layer, a contiguous run of a local ring):
-//   S[16 x 64] = Q . K^T with v_mfma_f32_16x16x32_bf16; A rows 0-3 = the 4 query heads of
-//     row a, 4-7 = row b, 8-15 = zero; A lane l holds row l%16, dims 8*(l/16) + 32*ks;
-//     B lane l holds key l%16 of a 16-key block, same dims: one 16-byte load each.
-//   P = exp(S - rowmax) (fp32), split into bf16 hi + lo with hi + lo = P to 2^-16
-//     relative, transposed through LDS into the A layout (row = head, 8 keys per lane).
-//   O[16 x 64] = P . V; B = the dimension-major V block: lane l holds dim 16n + l%16,
-//     keys 8*(l/16) + 32*ks, 16 contiguous bytes.
-// Row maxima and sums reduce over the 16 lanes of a DPP row. The 4 waves' (max, sum, O)
-// merge in LDS and the split partial goes to `part` [unit][kv head][split][8][66]; the
-// last split block to finish merges the splits, normalises, rounds as the SDPA output and
-// applies the head gate.
+// Decode attention on the matrix cores (bf16 caches): shared types and the unit key range.
+// A unit is the rows of one sequence in a step (the current token, and the speculative
+// token one position later when present); they read each key block of the cache once.
 // ---------------------------------------------------------------------------
 typedef __bf16 attn_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float attn_f32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_mov<0xB1>(v));
-  v = fmaxf(v, dpp_mov<0x4E>(v));
-  v = fmaxf(v, dpp_mov<0x124>(v));
-  v = fmaxf(v, dpp_mov<0x128>(v));
-  return __shfl(v, threadIdx.x & 0x30, 64);
-}
 
 __device__ __forceinline__ void unit_range(const AttnArgs& a, const AttnUnit& un, int& lo_a,
                                            int& lo_b, int& base, int& uhi) {
@@ -483,159 +463,12 @@ __device__ __forceinline__ void unit_range(const AttnArgs& a, const AttnUnit& un
   base = min(lo_a, lo_b) & ~63;
 }
 
-__global__ void __launch_bounds__(256) attn_decode_mfma_kernel(AttnArgs a) {
-  __shared__ float wm[4][8], wl[4][8];
-  __shared__ float wacc[4][8][64];
-  __shared__ __attribute__((aligned(16))) uint16_t pt[4][2][16][72];
-  const int u = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
-  const int nu = a.ctl->n_units;
-  const AttnUnit un = a.units[u];
-  if (u >= nu) return;
-  int lo_a, lo_b, base, uhi;
-  unit_range(a, un, lo_a, lo_b, base, uhi);
-  const int nsplit = (uhi + 1 - base + kSplitLen - 1) / kSplitLen;
-  if (s >= nsplit) return;
-  const bool two = un.row_b >= 0;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int m16 = lane & 15, kq = lane >> 4;
-  const int kb = base + s * kSplitLen + wv * 64;  // this wave's key block
-  const bool wact = kb <= uhi;                    // uniform per wave
-  const attn_bf16x8 zero = {};
-
-  // Q operand: row m16 of the 16-row tile
-  const int qrow = m16 < 4 ? un.row_a : ((m16 < 8 && two) ? un.row_b : -1);
-  const bf16* qp = reinterpret_cast<const bf16*>(a.qkv) + (int64_t)(qrow < 0 ? 0 : qrow) * a.ldq +
-                   (g * 4 + (m16 & 3)) * 64 + kq * 8;
-  attn_bf16x8 qa[2], kk[4][2], vv[4][2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-    qa[ks] = qrow >= 0 ? *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32) : zero;
-  if (wact) {
-    const KVBlock blk = kv_block(a.kv, a.layer, un.seq, g, kb);
-    const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]) + blk.k0 + kq * 8;
-    const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]) + blk.v0 + kq * 8;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        kk[j][ks] = *reinterpret_cast<const attn_bf16x8*>(Kc + (j * 16 + m16) * 64 + ks * 32);
-#pragma unroll
-    for (int n = 0; n < 4; ++n)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        vv[n][ks] = *reinterpret_cast<const attn_bf16x8*>(
-            Vc + (int64_t)(n * 16 + m16) * blk.vstride + ks * 32);
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      kk[j][0] = kk[j][1] = zero;
-      vv[j][0] = vv[j][1] = zero;
-    }
-  }
-  // scores; lane holds head rows kq*4 + i of key kb + 16j + m16
-  const bool rowok = kq == 0 || (kq == 1 && two);
-  const int klo = kq == 0 ? lo_a : lo_b, khi = kq == 0 ? un.pos_a : un.pos_b;
-  float sc[4][4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[0], kk[j][0], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[1], kk[j][1], acc, 0, 0, 0);
-    const int key = kb + j * 16 + m16;
-    const bool ok = wact && rowok && key >= klo && key <= khi;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sc[j][i] = ok ? acc[i] * a.scale : -INFINITY;
-  }
-  float mx[4], ls[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float m = fmaxf(fmaxf(sc[0][i], sc[1][i]), fmaxf(sc[2][i], sc[3][i]));
-    mx[i] = row16_max(m);
-    float l = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float p = sc[j][i] == -INFINITY ? 0.f : expf(sc[j][i] - mx[i]);
-      sc[j][i] = p;
-      l += p;
-    }
-    ls[i] = row16_sum(l);
-  }
-  // stage P (hi, lo) as [head row][key] for the A operand of P.V
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bf16 hi = f2bf(sc[j][i]);
-      const bf16 lo = f2bf(sc[j][i] - bf2f(hi));
-      pt[wv][0][kq * 4 + i][j * 16 + m16] = hi.u;
-      pt[wv][1][kq * 4 + i][j * 16 + m16] = lo.u;
-    }
-  __syncthreads();
-  attn_f32x4 o[4];
-#pragma unroll
-  for (int n = 0; n < 4; ++n) o[n] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const attn_bf16x8 ph = *reinterpret_cast<const attn_bf16x8*>(&pt[wv][0][m16][ks * 32 + kq * 8]);
-    const attn_bf16x8 pl = *reinterpret_cast<const attn_bf16x8*>(&pt[wv][1][m16][ks * 32 + kq * 8]);
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vv[n][ks], o[n], 0, 0, 0);
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vv[n][ks], o[n], 0, 0, 0);
-    }
-  }
-  if (kq < 2) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (m16 == 0) {
-        wm[wv][kq * 4 + i] = mx[i];
-        wl[wv][kq * 4 + i] = ls[i];
-      }
-#pragma unroll
-      for (int n = 0; n < 4; ++n) wacc[wv][kq * 4 + i][n * 16 + m16] = o[n][i];
-    }
-  }
-  __syncthreads();
-  // merge the 4 waves: thread -> head row hr, dims d0, d0 + 1
-  const int hr = threadIdx.x >> 5, d0 = (threadIdx.x & 31) * 2;
-  float M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][hr]);
-  float L = 0.f, O0 = 0.f, O1 = 0.f;
-  if (M != -INFINITY) {
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      if (wm[w][hr] == -INFINITY) continue;
-      const float f = expf(wm[w][hr] - M);
-      L += wl[w][hr] * f;
-      O0 += wacc[w][hr][d0] * f;
-      O1 += wacc[w][hr][d0 + 1] * f;
-    }
-  }
-  // Split partials are exchanged between workgroups with device-coherent stores and loads
-  // (they bypass the per-XCD L2), so no cache-wide writeback is needed: each thread waits
-  // for its stores to complete before the workgroup counts itself in, and only the block
-  // that completes the count merges — no block ever waits for another.
-  float* out = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits + s) * 8 + hr) * 66;
-  __hip_atomic_store(out + 2 + d0, O0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(out + 3 + d0, O1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (d0 == 0) {
-    __hip_atomic_store(out, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(out + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __shared__ int s_last;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int32_t* cnt = a.split_done + (int64_t)u * a.Hkv + g;
-    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == nsplit - 1;
-    // every split has counted in: reset for the next launch
-    if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  // merge: thread -> row of the unit (z), head of the group, two dims
+// Last split block of (unit u, kv head g): merge the split partials (device-coherent loads),
+// normalise, round as the SDPA output and apply the head gate. Threads 0-255:
+// thread -> row of the unit (z), head of the group, two dims.
+__device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int g,
+                                                  const AttnUnit& un, int nsplit) {
+  if (threadIdx.x >= 256) return;
   const int z = threadIdx.x >> 7, h = (threadIdx.x >> 5) & 3, e0 = (threadIdx.x & 31) * 2;
   const int row = z == 0 ? un.row_a : un.row_b;
   if (row < 0) return;
@@ -675,6 +508,181 @@ __global__ void __launch_bounds__(256) attn_decode_mfma_kernel(AttnArgs a) {
   bf16* dst = reinterpret_cast<bf16*>(a.out) + (int64_t)row * a.H * 64 + head * 64 + e0;
   dst[0] = f2bf(rnd<bf16>(Oa / Ls) * gate);
   dst[1] = f2bf(rnd<bf16>(Ob / Ls) * gate);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention, one workgroup per (unit, kv head, split of kUnitSplit keys): kUnitWaves
+// waves stride over the split's 64-key blocks, each keeping an online softmax over its
+// blocks; the waves merge in LDS, and only a unit whose keys span several splits goes
+// through the split partials. Products are formed transposed, as in the prefill kernel:
+// S^T = K Q^T (A = 16 keys x 32 dims of the position-major K block, B = the 8 query rows
+// of the unit: 4 heads x rows a, b), so P^T stays in registers for O^T = V^T P^T, whose
+// A operand takes two 8-byte runs of the dimension-major V block. P = exp(S - max) in fp32
+// is split into bf16 hi + lo (hi + lo = P to 2^-16 relative), two products each. The last
+// split block to count in merges the split partials, normalises, rounds as the SDPA
+// output and applies the head gate.
+// ---------------------------------------------------------------------------
+typedef __bf16 attn_bf16x4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnArgs a) {
+  __shared__ float wm[kUnitWaves][8], wl[kUnitWaves][8];
+  __shared__ float wo[kUnitWaves][8][65];
+  const int u = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+  if (u >= a.ctl->n_units) return;
+  const AttnUnit un = a.units[u];
+  int lo_a, lo_b, base, uhi;
+  unit_range(a, un, lo_a, lo_b, base, uhi);
+  const int nsplit = (uhi + 1 - base + kUnitSplit - 1) / kUnitSplit;
+  if (s >= nsplit) return;
+  const bool two = un.row_b >= 0;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int m16 = lane & 15, kq = lane >> 4;
+  // query column m16: heads 0-3 of row a, heads 0-3 of row b, then unused
+  const int qrow = m16 < 4 ? un.row_a : ((m16 < 8 && two) ? un.row_b : -1);
+  const int qlo = m16 < 4 ? lo_a : lo_b, qhi = qrow < 0 ? -1 : (m16 < 4 ? un.pos_a : un.pos_b);
+  const attn_bf16x8 zero = {};
+  attn_bf16x8 qb[2];
+  {
+    const bf16* qp = reinterpret_cast<const bf16*>(a.qkv) + (int64_t)(qrow < 0 ? 0 : qrow) * a.ldq +
+                     (g * 4 + (m16 & 3)) * 64 + kq * 8;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      qb[ks] = qrow >= 0 ? *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32) : zero;
+  }
+  const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]);
+  const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]);
+  const int s_lo = base + s * kUnitSplit;
+  const int s_hi = min(uhi, s_lo + kUnitSplit - 1);
+  float mrun = -INFINITY, lrun = 0.f;
+  attn_f32x4 o[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) o[mt] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = s_lo + wv * 64; kb <= s_hi; kb += kUnitWaves * 64) {
+    const KVBlock blk = kv_block(a.kv, a.layer, un.seq, g, kb);
+    attn_bf16x8 kk[4][2];
+    attn_bf16x4 vl[4][2], vh[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        kk[kt][ks] = *reinterpret_cast<const attn_bf16x8*>(Kc + blk.k0 + (kt * 16 + m16) * 64 +
+                                                            ks * 32 + kq * 8);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const bf16* vp = Vc + blk.v0 + (int64_t)(mt * 16 + m16) * blk.vstride + s2 * 32 + kq * 4;
+        vl[mt][s2] = *reinterpret_cast<const attn_bf16x4*>(vp);
+        vh[mt][s2] = *reinterpret_cast<const attn_bf16x4*>(vp + 16);
+      }
+    attn_f32x4 sv[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][0], qb[0], acc, 0, 0, 0);
+      sv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][1], qb[1], acc, 0, 0, 0);
+    }
+    // lane holds keys kb + 16 kt + 4 kq + j of query column m16
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = kb + kt * 16 + kq * 4 + j;
+        const float v = (key >= qlo && key <= qhi) ? sv[kt][j] * a.scale : -INFINITY;
+        sv[kt][j] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, swz_xor16(mx));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(mrun, mx);
+    const float muse = mnew == -INFINITY ? 0.f : mnew;
+    const float f = mrun == -INFINITY ? 0.f : expf(mrun - muse);
+    mrun = mnew;
+    lrun *= f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[mt] *= f;
+    attn_bf16x8 ph[2], pl[2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = sv[kt][j] == -INFINITY ? 0.f : expf(sv[kt][j] - muse);
+        lrun += p;
+        const __bf16 hi = (__bf16)p;
+        ph[kt >> 1][(kt & 1) * 4 + j] = hi;
+        pl[kt >> 1][(kt & 1) * 4 + j] = (__bf16)(p - (float)hi);
+      }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const attn_bf16x8 av = __builtin_shufflevector(vl[mt][s2], vh[mt][s2], 0, 1, 2, 3, 4, 5, 6, 7);
+        o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ph[s2], o[mt], 0, 0, 0);
+        o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pl[s2], o[mt], 0, 0, 0);
+      }
+  }
+  lrun += swz_xor16(lrun);
+  lrun += __shfl_xor(lrun, 32, 64);
+  // wave partials: query column m16 < 8; lane holds dims 16 mt + 4 kq + j
+  if (m16 < 8) {
+    if (kq == 0) {
+      wm[wv][m16] = mrun;
+      wl[wv][m16] = lrun;
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wo[wv][m16][mt * 16 + kq * 4 + j] = o[mt][j];
+  }
+  __syncthreads();
+  // merge the waves: element t -> query column hr (0-7), dim d; the block's threads cover
+  // the 8 x 64 elements whatever its size
+  for (int t = threadIdx.x; t < 8 * 64; t += blockDim.x) {
+    const int hr = t >> 6, d = t & 63;
+    float M = -INFINITY, L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kUnitWaves; ++w) M = fmaxf(M, wm[w][hr]);
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kUnitWaves; ++w) {
+        if (wm[w][hr] == -INFINITY) continue;
+        const float f = expf(wm[w][hr] - M);
+        L += wl[w][hr] * f;
+        O += wo[w][hr][d] * f;
+      }
+    }
+    if (nsplit == 1) {
+      const int z = hr >> 2, h = hr & 3;
+      const int row = z == 0 ? un.row_a : un.row_b;
+      if (row < 0) continue;
+      const int head = g * 4 + h;
+      const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
+      reinterpret_cast<bf16*>(a.out)[(int64_t)row * a.H * 64 + head * 64 + d] =
+          f2bf(rnd<bf16>(O / L) * gate);
+    } else {
+      // several splits: device-coherent partials; the last block to count in merges
+      float* out = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits + s) * 8 + hr) * 66;
+      __hip_atomic_store(out + 2 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == 0) {
+        __hip_atomic_store(out, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(out + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (nsplit == 1) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ int s_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t* cnt = a.split_done + (int64_t)u * a.Hkv + g;
+    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == nsplit - 1;
+    if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  attn_merge_splits(a, u, g, un, nsplit);
 }
 
 // ---------------------------------------------------------------------------
@@ -784,7 +792,6 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
 // Scores use exp2 with log2(e) folded into the scale; P is rounded to bf16 for the second
 // product, the running max, sum and output accumulate in fp32.
 // ---------------------------------------------------------------------------
-typedef __bf16 attn_bf16x4 __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
   constexpr int kLd = 72;  // LDS row stride in bf16: 16 bytes of padding against bank conflicts
@@ -1352,7 +1359,7 @@ int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s) 
 }
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s) {
   if (dtype == PULSAR_BF16) {
-    attn_decode_mfma_kernel<<<dim3(a.max_units, a.Hkv, a.max_splits), 256, 0, s>>>(a);
+    attn_decode_unit_kernel<<<dim3(a.max_units, a.Hkv, a.max_splits_unit), 64 * kUnitWaves, 0, s>>>(a);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   }

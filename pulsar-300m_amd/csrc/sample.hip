@@ -122,6 +122,9 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
 #pragma unroll
   for (int i = 0; i < PER; ++i) am = better(am, ArgMax{l[i], base + i});
   am = block_argmax(am, ared);
+  // Non-finite logits compare false everywhere and leave no maximum: a token id outside the
+  // vocabulary is never emitted (it would index the embedding table out of bounds).
+  if (am.i < 0 || am.i >= a.V) am.i = 0;
   if (a.greedy) {
     if (threadIdx.x == 0) {
       a.out_argmax[lr] = am.i;
@@ -222,8 +225,9 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
   __syncthreads();
   if (threadIdx.x == 0) {
     a.out_argmax[lr] = am.i;
-    a.out_draw[lr * 2] = pick[0];
-    a.out_draw[lr * 2 + 1] = pick[1];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+      a.out_draw[lr * 2 + d] = (pick[d] >= 0 && pick[d] < a.V) ? pick[d] : am.i;
   }
 #undef KEY
 }

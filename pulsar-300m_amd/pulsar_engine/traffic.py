@@ -62,3 +62,32 @@ def step_bytes(cfg: PulsarConfig, es: int, rows, expert_counts, n_lrows: int) ->
         out["lm_head"] = V * D * es + n_lrows * (D * es + V * 4)
         out["sample"] = n_lrows * V * 4
     return out
+
+
+def prefill_flops(cfg: PulsarConfig, batch: int, prompt_len: int) -> dict:
+    """Algorithmic multiply-add FLOPs (2 per MAC) of one prefill of ``batch`` prompts of
+    ``prompt_len`` tokens: every pulse of every layer over every token, each token at its
+    top_k experts (capacity drops ignored), attention over the key range each query sees
+    (local layers: the newest ``sliding_window`` positions, top-left aligned when the prompt
+    is longer, as in the reference's prefill), and the output head for the last token."""
+    D, H, hd = cfg.d_model, cfg.n_heads, cfg.head_dim
+    E, K, de, ds = cfg.n_routed_experts, cfg.top_k, cfg.d_expert, cfg.d_shared
+    P, T, W, r = cfg.default_pulses, prompt_len, cfg.sliding_window, cfg.reinject_gate_rank
+    tok = batch * T
+    per_layer = 2 * ((cfg.qkv_dim + H) * D + D * cfg.q_dim + E * D + 3 * ds * D
+                     + K * 3 * de * D)
+    keys_global = T * (T + 1) // 2
+    if T > W:
+        keys_local = W * (W + 1) // 2 + (T - W) * W
+    else:
+        keys_local = keys_global
+    n_local = sum(1 for L in range(cfg.n_core) if cfg.is_local(L))
+    attn_keys = n_local * keys_local + (cfg.n_core - n_local) * keys_global
+    out = {
+        "projections": P * cfg.n_core * tok * per_layer,
+        "attention": P * batch * H * 4 * hd * attn_keys,
+        "reinject": (P - 1) * tok * 2 * 3 * r * D,
+        "lm_head": batch * 2 * cfg.vocab_size * D,
+    }
+    out["total"] = sum(out.values())
+    return out

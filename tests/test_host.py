@@ -71,8 +71,8 @@ def test_rocprof_summary_keeps_decode_dispatches(tmp_path):
     t = 0
     for name, dur in [("void pulsar::attn_prefill_kernel<bf16>(pulsar::AttnArgs)", 900),
                       ("pulsar::controller_kernel(pulsar::ControllerArgs)", 5),
-                      ("pulsar::attn_decode_mfma_kernel(pulsar::AttnArgs)", 10),
-                      ("pulsar::attn_decode_mfma_kernel(pulsar::AttnArgs)", 12),
+                      ("pulsar::attn_decode_unit_kernel(pulsar::AttnArgs)", 10),
+                      ("pulsar::attn_decode_unit_kernel(pulsar::AttnArgs)", 12),
                       ("pulsar::controller_kernel(pulsar::ControllerArgs)", 6)]:
         rows.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + dur * 1000})
         t += dur * 1000 + 100
@@ -80,7 +80,7 @@ def test_rocprof_summary_keeps_decode_dispatches(tmp_path):
     _write_csv(tmp_path / "x" / "run_kernel_trace.csv", rows)
     out = b.rocprof_summary(str(tmp_path))
     assert "attn_prefill" not in out
-    assert "| `attn_decode_mfma_kernel` | 2 | 11.00 |" in out
+    assert "| `attn_decode_unit_kernel` | 2 | 11.00 |" in out
     assert "| `controller_kernel` | 1 | 6.00 |" in out
 
 
@@ -91,8 +91,8 @@ def test_pmc_summary_calibrates_and_feeds_traffic(tmp_path, monkeypatch):
         d.mkdir()
         _write_csv(d / "bench_counter_collection.csv", [
             {"Kernel_Name": "pulsar::controller_kernel(x)", "Counter_Value": 1.0},
-            {"Kernel_Name": "pulsar::attn_decode_mfma_kernel(x)", "Counter_Value": per_kernel},
-            {"Kernel_Name": "pulsar::attn_decode_mfma_kernel(x)", "Counter_Value": per_kernel * 3}])
+            {"Kernel_Name": "pulsar::attn_decode_unit_kernel(x)", "Counter_Value": per_kernel},
+            {"Kernel_Name": "pulsar::attn_decode_unit_kernel(x)", "Counter_Value": per_kernel * 3}])
         c = tmp_path / (ctr + "_copy")
         c.mkdir()
         _write_csv(c / "copy_counter_collection.csv", [
@@ -104,7 +104,7 @@ def test_pmc_summary_calibrates_and_feeds_traffic(tmp_path, monkeypatch):
     prof.write_text(out)
     monkeypatch.setattr(b, "TRAFFIC_PROFILE", str(prof))
     # fetch: mean 2000 KiB x 2 (calibration) ; write: mean 100 KiB x 1
-    assert b.recorded_traffic(["attn_decode_mfma_kernel"]) == 4000 * 1024 + 100 * 1024
+    assert b.recorded_traffic(["attn_decode_unit_kernel"]) == 4000 * 1024 + 100 * 1024
     assert b.recorded_traffic(["not_profiled"]) is None
 
 
@@ -113,3 +113,30 @@ def test_config_from_dict_keeps_reference_names():
     assert (cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim) == (512, 8, 2, 64)
     with pytest.warns(RuntimeWarning):
         PulsarConfig.from_dict({"not_a_field": 1})
+
+
+@pytest.mark.parametrize("T", [5, 16, 23])
+def test_prefill_flops_count_each_query_key_pair(T):
+    """The attention term against a brute-force count of the (query, key) pairs of every
+    layer (local layers: top-left aligned last-window keys when T exceeds the window), and
+    the projection term against a hand count of one token's multiply-adds."""
+    from pulsar_engine.config import tiny_config
+
+    cfg = tiny_config()  # window 16
+    W = cfg.sliding_window
+    pairs = 0
+    for L in range(cfg.n_core):
+        for t in range(T):
+            if cfg.is_local(L) and T > W:
+                lo, hi = T - W, T - W + min(t, W - 1)
+            else:
+                lo, hi = 0, t
+            pairs += hi - lo + 1
+    f = traffic.prefill_flops(cfg, 2, T)
+    assert f["attention"] == cfg.default_pulses * 2 * cfg.n_heads * 4 * cfg.head_dim * pairs
+    D = cfg.d_model
+    macs = ((cfg.qkv_dim + cfg.n_heads) * D + D * cfg.q_dim + cfg.n_routed_experts * D
+            + 2 * cfg.d_shared * D + D * cfg.d_shared
+            + cfg.top_k * (2 * cfg.d_expert * D + D * cfg.d_expert))
+    assert f["projections"] == 2 * macs * cfg.n_core * cfg.default_pulses * 2 * T
+    assert f["total"] == sum(v for k, v in f.items() if k != "total")
