@@ -61,11 +61,20 @@ def _short_kernel(name: str) -> str:
     return re.sub(r"\(.*", "", name).replace("void ", "").strip()
 
 
-def _decode_rows(rows: list) -> list:
-    """Dispatches of the decode phase: after the controller's first launch (which follows
-    the prefill and draws the first tokens)."""
-    first = next((i for i, r in enumerate(rows) if "controller_kernel" in r["Kernel_Name"]), -1)
-    return rows[first + 1:]
+def _phase_rows(rows: list, phase: str) -> list:
+    """Dispatches of one phase of a bench run. The last prefill is the run of dispatches
+    from just after the controller launch that precedes its last prefill kernel up to the
+    controller launch that ends it (drawing the first tokens); decode is everything after."""
+    names = [r["Kernel_Name"] for r in rows]
+    ctl = [i for i, n in enumerate(names) if "controller_kernel" in n]
+    pre = [i for i, n in enumerate(names) if "prefill" in n]
+    if not pre:
+        end = ctl[0] if ctl else -1
+        return rows[end + 1:] if phase == "decode" else []
+    last = pre[-1]
+    end = next((i for i in ctl if i > last), len(rows))
+    start = max((i for i in ctl if i < last), default=-1) + 1
+    return rows[end + 1:] if phase == "decode" else rows[start:end]
 
 
 def _csv(directory: str, suffix: str) -> list:
@@ -78,10 +87,10 @@ def _csv(directory: str, suffix: str) -> list:
         return list(csv.DictReader(f))
 
 
-def rocprof_summary(directory: str) -> str:
-    """Markdown table of decode-phase kernel durations from a rocprofv3 kernel trace (csv)."""
+def rocprof_summary(directory: str, phase: str = "decode") -> str:
+    """Markdown table of one phase's kernel durations from a rocprofv3 kernel trace (csv)."""
     from collections import defaultdict
-    rows = _decode_rows(_csv(directory, "kernel_trace.csv"))
+    rows = _phase_rows(_csv(directory, "kernel_trace.csv"), phase)
     agg = defaultdict(list)
     for r in rows:
         agg[_short_kernel(r["Kernel_Name"])].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
@@ -90,7 +99,7 @@ def rocprof_summary(directory: str) -> str:
     for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
         out.append(f"| `{k}` | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | {sum(v) / 1e6:.2f} | "
                    f"{100 * sum(v) / total:.1f}% |")
-    out.append(f"\nDecode kernel time {total / 1e6:.2f} ms over {len(rows)} dispatches.")
+    out.append(f"\n{phase.capitalize()} kernel time {total / 1e6:.2f} ms over {len(rows)} dispatches.")
     return "\n".join(out)
 
 
@@ -107,7 +116,7 @@ def pmc_summary(fetch_dir: str, write_dir: str, fetch_copy: str, write_copy: str
         lines.append(f"- {ctr}: a {copy_mib} MiB device-to-device copy counts "
                      f"{sum(cal) / len(cal):.1f} KiB per dispatch -> scale factor {factor:.4f}")
         agg = defaultdict(list)
-        for r in _decode_rows(_csv(d, "counter_collection.csv")):
+        for r in _phase_rows(_csv(d, "counter_collection.csv"), "decode"):
             agg[_short_kernel(r["Kernel_Name"])].append(float(r["Counter_Value"]))
         for k, v in agg.items():
             res.setdefault(k, {})[ctr] = round(sum(v) / len(v) * factor * 1024)
@@ -212,6 +221,8 @@ def main() -> int:
     ap.add_argument("--cpu-new-tokens", type=int, default=12)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (HBM counter calibration)")
+    ap.add_argument("--phase", choices=("decode", "prefill"), default="decode",
+                    help="phase of the trace --rocprof-summary tabulates")
     ap.add_argument("--rocprof-summary", metavar="DIR",
                     help="print the decode kernel table of a rocprofv3 csv kernel trace and exit")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "FETCH_COPY", "WRITE_COPY"),
@@ -219,7 +230,7 @@ def main() -> int:
                          "FETCH_SIZE / WRITE_SIZE csv directories (bench, then copy runs) and exit")
     args = ap.parse_args()
     if args.rocprof_summary:
-        print(rocprof_summary(args.rocprof_summary))
+        print(rocprof_summary(args.rocprof_summary, args.phase))
         return 0
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary, copy_mib=256))

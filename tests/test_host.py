@@ -65,23 +65,32 @@ def _write_csv(path, rows):
         w.writerows(rows)
 
 
-def test_rocprof_summary_keeps_decode_dispatches(tmp_path):
+def test_rocprof_summary_splits_warm_prefill_and_decode(tmp_path):
     b = _bench()
     rows = []
     t = 0
-    for name, dur in [("void pulsar::attn_prefill_kernel<bf16>(pulsar::AttnArgs)", 900),
-                      ("pulsar::controller_kernel(pulsar::ControllerArgs)", 5),
-                      ("pulsar::attn_decode_unit_kernel(pulsar::AttnArgs)", 10),
-                      ("pulsar::attn_decode_unit_kernel(pulsar::AttnArgs)", 12),
-                      ("pulsar::controller_kernel(pulsar::ControllerArgs)", 6)]:
+    trace = [("void pulsar::attn_prefill_mfma_kernel(pulsar::AttnArgs)", 900),   # cold prefill
+             ("pulsar::controller_kernel(pulsar::ControllerArgs)", 5),
+             ("pulsar::prefill_embed_kernel(x)", 70),                             # warm prefill
+             ("pulsar::attn_prefill_mfma_kernel(pulsar::AttnArgs)", 480),
+             ("void gemm_bf16_wide_kernel<1, 0>(GemmArgs)", 250),
+             ("pulsar::controller_kernel(pulsar::ControllerArgs)", 5),
+             ("pulsar::attn_decode_unit_kernel(pulsar::AttnArgs)", 10),         # decode
+             ("pulsar::attn_decode_unit_kernel(pulsar::AttnArgs)", 12),
+             ("pulsar::controller_kernel(pulsar::ControllerArgs)", 6)]
+    for name, dur in trace:
         rows.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + dur * 1000})
         t += dur * 1000 + 100
     (tmp_path / "x").mkdir()
     _write_csv(tmp_path / "x" / "run_kernel_trace.csv", rows)
     out = b.rocprof_summary(str(tmp_path))
-    assert "attn_prefill" not in out
+    assert "prefill" not in out and "gemm_bf16_wide" not in out
     assert "| `attn_decode_unit_kernel` | 2 | 11.00 |" in out
     assert "| `controller_kernel` | 1 | 6.00 |" in out
+    pre = b.rocprof_summary(str(tmp_path), "prefill")
+    assert "| `attn_prefill_mfma_kernel` | 1 | 480.00 |" in pre
+    assert "| `gemm_bf16_wide_kernel<1, 0>` | 1 | 250.00 |" in pre
+    assert "controller_kernel" not in pre and "decode" not in pre
 
 
 def test_pmc_summary_calibrates_and_feeds_traffic(tmp_path, monkeypatch):
