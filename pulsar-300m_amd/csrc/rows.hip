@@ -1116,6 +1116,32 @@ __global__ void __launch_bounds__(256) router_prefill_mfma_kernel(RouterArgs a) 
 // capacity each is ranked against the others by (key asc, flat index asc), in LDS when
 // staged, else against the sequence's assignments in memory. The block then reserves its
 // kept count in the expert's list with one atomic and writes its entries there.
+__device__ int block_excl_scan_int(int v, int* scratch, int* total) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  __syncthreads();  // previous users of the scratch are done
+  scratch[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < nt; off <<= 1) {
+    const int add = tid >= off ? scratch[tid - off] : 0;
+    __syncthreads();
+    scratch[tid] += add;
+    __syncthreads();
+  }
+  *total = scratch[nt - 1];
+  return scratch[tid] - v;
+}
+// Order-preserving map of a float onto unsigned integers.
+__device__ __forceinline__ uint32_t ordered_bits(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+// Block-wide sum and exclusive prefix sum of one int per thread (blockDim.x <= 1024,
+// scratch of blockDim.x ints); every thread returns the same total.
+__device__ int block_sum_int(int v, int* scratch) {
+  int tot;
+  block_excl_scan_int(v, scratch, &tot);
+  return tot;
+}
 constexpr int kCapStage = 4096;
 __global__ void __launch_bounds__(256) prefill_select_kernel(
     const int32_t* __restrict__ idx, const float* __restrict__ w, int32_t* __restrict__ keep,
@@ -1162,24 +1188,48 @@ __global__ void __launch_bounds__(256) prefill_select_kernel(
       keep[s0 + sidx[q]] = kept ? 1 : 0;
       mine += kept ? 1 : 0;
     }
-  } else {
-    for (int64_t i = s0 + tid; i < s0 + per; i += nt) {
-      if (idx[i] != e) continue;
-      bool kept = true;
-      if (n > C) {
-        const float ki = key_of(i);
-        int rank = 0;
-        for (int64_t j = s0; j < s0 + per; ++j) {
-          if (idx[j] != e || j == i) continue;
-          const float kj = key_of(j);
-          if (kj < ki || (kj == ki && j < i)) ++rank;
-        }
-        kept = rank < C;
+  } else if (n <= C) {
+    for (int64_t i = s0 + tid; i < s0 + per; i += nt)
+      if (idx[i] == e) {
+        keep[i] = 1;
+        ++mine;
       }
-      keep[i] = kept ? 1 : 0;
-      mine += kept ? 1 : 0;
+  } else {
+    // Too many to stage: the C-th smallest key by bisection over its ordered bits (one
+    // counting pass per step), then the assignments on that key ranked by flat index with
+    // an ordered scan over chunks of nt consecutive assignments.
+    uint32_t lo = 0u, hi = 0xffffffffu;
+    while (lo < hi) {
+      const uint32_t mid = lo + ((hi - lo) >> 1);
+      int c = 0;
+      for (int64_t i = s0 + tid; i < s0 + per; i += nt)
+        c += (idx[i] == e && ordered_bits(key_of(i)) <= mid) ? 1 : 0;
+      if (block_sum_int(c, s_off) >= C)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    const uint32_t uc = lo;
+    int c = 0;
+    for (int64_t i = s0 + tid; i < s0 + per; i += nt)
+      c += (idx[i] == e && ordered_bits(key_of(i)) < uc) ? 1 : 0;
+    const int below = block_sum_int(c, s_off);
+    int run = 0;  // assignments on the threshold key in earlier chunks
+    for (int64_t c0 = s0; c0 < s0 + per; c0 += nt) {
+      const int64_t i = c0 + tid;
+      const bool my = i < s0 + per && idx[i] == e;
+      const uint32_t uk = my ? ordered_bits(key_of(i)) : 0u;
+      int tot;
+      const int before = block_excl_scan_int(my && uk == uc ? 1 : 0, s_off, &tot);
+      if (my) {
+        const bool kept = uk < uc || (uk == uc && below + run + before < C);
+        keep[i] = kept ? 1 : 0;
+        mine += kept ? 1 : 0;
+      }
+      run += tot;
     }
   }
+  __syncthreads();  // s_off doubles as scan scratch above
   s_off[tid] = mine;
   __syncthreads();
   if (tid == 0) {

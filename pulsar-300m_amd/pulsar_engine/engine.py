@@ -52,8 +52,7 @@ class HipEngine:
         for i, s in enumerate(stops):
             c.stop_ids[i] = s
         c.seed = seed & 0xFFFFFFFFFFFFFFFF
-        if c.max_ctx > model.rope_len:
-            raise ValueError(f"max_ctx {c.max_ctx} exceeds the model's RoPE tables ({model.rope_len})")
+        model.ensure_rope(c.max_ctx)
         self.cfg = c
         h = ctypes.c_void_p()
         _lib.check(self.lib.pulsar_engine_create(model.desc_ref(), ctypes.byref(c), ctypes.byref(h)))

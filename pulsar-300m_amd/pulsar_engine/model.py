@@ -228,7 +228,6 @@ class DeviceModel:
         d.local_mask = sum(1 << i for i in range(cfg.n_core) if cfg.is_local(i))
         d.rms_eps, d.softcap = cfg.rms_eps, cfg.logit_softcap
         self.rope_len = int(rope_len or cfg.max_seq_len)
-        d.rope_len = self.rope_len
         ptr = lambda x: x.data_ptr()  # noqa: E731
         self.tok_emb = t["tok_emb"]
         d.tok_emb = ptr(t["tok_emb"])
@@ -242,16 +241,34 @@ class DeviceModel:
         d.reinject_up = ptr(t["reinject_up"])
         d.reinject_bias = ptr(t["reinject_bias"])
         d.res_scale = ptr(t["res_scale"])
-        cl, sl = rope_tables(cfg.rope_theta_local, cfg.head_dim, self.rope_len)
-        cg, sg = rope_tables(cfg.rope_theta_global, cfg.head_dim, self.rope_len)
-        self._rope = [x.to(self.device) for x in (cl, sl, cg, sg)]
-        d.rope_cos_local, d.rope_sin_local = ptr(self._rope[0]), ptr(self._rope[1])
-        d.rope_cos_global, d.rope_sin_global = ptr(self._rope[2]), ptr(self._rope[3])
+        self.desc = d
+        self._rope_retired: list = []
+        self._set_rope(self.rope_len)
         for i in range(cfg.n_core):
             L = f"layers.{i}."
             for name in LAYER_TENSORS:
                 getattr(d, name)[i] = ptr(t[L + name])
-        self.desc = d
+        torch.cuda.synchronize(self.device)
+
+    def _set_rope(self, n: int) -> None:
+        cfg, d = self.cfg, self.desc
+        cl, sl = rope_tables(cfg.rope_theta_local, cfg.head_dim, n)
+        cg, sg = rope_tables(cfg.rope_theta_global, cfg.head_dim, n)
+        self._rope = [x.to(self.device) for x in (cl, sl, cg, sg)]
+        d.rope_cos_local, d.rope_sin_local = self._rope[0].data_ptr(), self._rope[1].data_ptr()
+        d.rope_cos_global, d.rope_sin_global = self._rope[2].data_ptr(), self._rope[3].data_ptr()
+        d.rope_len = n
+        self.rope_len = n
+
+    def ensure_rope(self, n: int) -> None:
+        """Grow the RoPE tables to ``n`` positions, as the reference's rotary cache grows
+        when a sequence outruns it (src/model.py:553-556; entries of a position do not
+        depend on the table length). Engines created earlier keep the tables they were
+        given: the old tensors stay alive with the model."""
+        if n <= self.rope_len:
+            return
+        self._rope_retired.append(self._rope)
+        self._set_rope(int(n))
         torch.cuda.synchronize(self.device)
 
     @property

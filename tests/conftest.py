@@ -34,6 +34,20 @@ def full_state():
 
 
 @pytest.fixture(scope="session")
+def models(full_state):
+    """The full-size synthetic model on the GPU in fp32 and bf16, shared by the GPU suites."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from pulsar_engine.model import DeviceModel
+
+    cfg, st = full_state
+    return {
+        torch.float32: DeviceModel(cfg, st, torch.float32),
+        torch.bfloat16: DeviceModel(cfg, st, torch.bfloat16),
+    }
+
+
+@pytest.fixture(scope="session")
 def tiny_state():
     from pulsar_engine import weights as W
     from pulsar_engine.config import tiny_config

@@ -1,0 +1,107 @@
+"""GPU cases at the sizes of the reference's benchmark configurations.
+
+* c4-like: 4 sequences of 32768-token prompts (global layers past 32 pages, YaRN in decode,
+  the RoPE tables grown past max_seq_len as the reference grows its cache): greedy
+  self-speculative == plain, and a sequence decodes the same alone as in the batch.
+* c5-like: 256 sequences of 512-token Zipf(1.1) prompts with router weights x4 (skewed
+  routing, capacity drops in prefill): every pass of one sequence against the oracle in
+  bf16, greedy self-speculative == plain over the whole batch, batch == single.
+* Capacity with more assignments per (sequence, expert) than the kernel stages in LDS
+  (4200 tokens all routed to experts 0-3): prefill logits against the oracle in fp32.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import max_abs_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _spec_plain_single(model, prompts, n_new, singles):
+    from pulsar_engine.engine import PulsarInferenceEngine
+
+    eng = PulsarInferenceEngine(model)
+    kw = dict(max_new_tokens=n_new, temperature=0.0, repetition_penalty=10.0, stop_ids=[0, 2])
+    spec = eng.generate_ids(prompts, speculative=True, **kw)
+    plain = eng.generate_ids(prompts, speculative=False, **kw)
+    assert spec == plain
+    for i in singles:
+        assert eng.generate_ids([prompts[i]], speculative=True, **kw)[0] == spec[i], i
+    assert all(len(s) == n_new for s in spec)
+    return spec
+
+
+def test_c4_long_context_spec_equals_plain_and_batch_equals_single(models, full_state):
+    from pulsar_engine import weights as W
+
+    cfg = full_state[0]
+    T_ = 32768
+    prompts = [W.uniform_ids(90 + b, "c4_prompt", T_, cfg.vocab_size).tolist() for b in range(4)]
+    spec = _spec_plain_single(models[torch.bfloat16], prompts, 24, singles=[0])
+    assert models[torch.bfloat16].rope_len >= T_ + 24
+    print("c4 first tokens", [s[:6] for s in spec])
+
+
+@pytest.fixture(scope="module")
+def c5_model(full_state):
+    from pulsar_engine import weights as W
+    from pulsar_engine.model import DeviceModel
+
+    cfg = full_state[0]
+    st = W.synthetic_state(cfg, seed=0, router_scale=4.0)
+    return st, DeviceModel(cfg, st, torch.bfloat16)
+
+
+def test_c5_skewed_routing_passes_match_oracle(full_state, c5_model):
+    from test_gpu_engine import _compare_passes
+
+    from pulsar_engine import weights as W
+
+    cfg = full_state[0]
+    st, model = c5_model
+    prompt = W.zipf_ids(5, "c5_prompt_0", 512, cfg.vocab_size).tolist()
+    _compare_passes({torch.bfloat16: model}, (cfg, st), torch.bfloat16, prompt, 3, tol=2e-2,
+                    rp=10.0)
+
+
+def test_c5_batch_256_spec_equals_plain_and_batch_equals_single(full_state, c5_model):
+    from pulsar_engine import weights as W
+
+    cfg = full_state[0]
+    prompts = [W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size).tolist() for b in range(256)]
+    spec = _spec_plain_single(c5_model[1], prompts, 8, singles=[0, 255])
+    print("c5 first tokens", [s[:4] for s in spec[:4]])
+
+
+def test_prefill_capacity_beyond_lds_staging_matches_oracle(full_state):
+    """4200 assignments per (sequence, expert) against capacity 1344: the threshold is found
+    by bisection over the key bits and ties on it are ranked by flat index."""
+    from oracle import pulsar_ref as R
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+    from pulsar_engine.model import DeviceModel
+
+    cfg, st = full_state
+    bias = np.zeros(cfg.n_routed_experts, np.float32)
+    bias[:4] = 1.0
+    st2 = dict(st)
+    for i in range(cfg.n_core):
+        st2[f"core.{i}.mlp.expert_bias"] = np.tile(bias, (cfg.max_pulses, 1))
+    T_ = 4200
+    assert R.moe_capacity(T_, cfg) == 1344
+    prompt = W.uniform_ids(80, "cap_big", T_, cfg.vocab_size)
+    model = DeviceModel(cfg, st2, torch.float32)
+    eng = HipEngine(model, batch=1, max_prompt=T_, max_new=4, speculative=False,
+                    temperature=0.0, repetition_penalty=1.0, stop_ids=[])
+    eng.prefill(prompt[None])
+    got = eng.logits(1)[0]
+    ref_eng = R.load_ref(cfg, st2, torch.float32, rope_tables_fp32=True, stop_ids=set())
+    ref = ref_eng.prefill(torch.as_tensor(prompt).view(1, -1), R.RefKVCache(cfg))
+    err = max_abs_rel(got, ref.float().numpy().reshape(-1))
+    print(f"capacity beyond staging: {err:.3e}")
+    assert err <= 1e-4
+    eng.close()

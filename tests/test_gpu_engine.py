@@ -18,19 +18,6 @@ from conftest import golden, max_abs_rel
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def models(full_state):
-    if not torch.cuda.is_available():
-        pytest.skip("no GPU")
-    from pulsar_engine.model import DeviceModel
-
-    cfg, st = full_state
-    return {
-        torch.float32: DeviceModel(cfg, st, torch.float32),
-        torch.bfloat16: DeviceModel(cfg, st, torch.bfloat16),
-    }
-
-
 def _oracle(full_state, dtype):
     from oracle import pulsar_ref as R
 
