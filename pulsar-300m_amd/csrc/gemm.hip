@@ -1,12 +1,16 @@
-// Row-tiled GEMMs for decode and prefill: C[rows, N] = epi(A[rows, K] . W[N, K]^T).
+// Row-set GEMMs for decode and prefill: C[rows, N] = epi(A[rows, K] . W[N, K]^T), bf16
+// weights stored in matrix-core tile order [N/16][K/32][64 lanes][8].
 //
-// bf16: a workgroup of 4 waves owns a 32-row x 16-column output tile and splits K four
-// ways; each wave runs v_mfma_f32_16x16x32_bf16 on two 16-row blocks that share the
-// weight operand, with every weight element loaded exactly once (128-bit loads, k
-// contiguous per lane). Partial tiles are summed through LDS and wave 0 applies the
+// Decode (gemm_bf16_kernel): a workgroup of 8 waves owns 16 output columns and walks the
+// group's 32-row tiles; the waves split K, each runs v_mfma_f32_16x16x32_bf16 on two
+// 16-row blocks that share the weight operand, so every weight byte is read once per
+// launch. Partial tiles are summed through LDS (one tile value per wave) before the fused
 // epilogue. Row sets come from the step control block (rows of one pulse, rows of one
 // expert, all rows, or logits rows), so one launch serves every pulse / expert group and
 // groups without rows exit before touching their weights.
+//
+// Prefill (gemm_bf16_lds_kernel): 128 x 256 output tiles staged through LDS for row sets
+// of thousands of rows, where the work is matrix-core bound rather than weight-bound.
 //
 // fp32: one wave per output column, lanes split K with 128-bit loads, wave64 reduction.
 #include <algorithm>
@@ -383,100 +387,117 @@ __device__ __forceinline__ void epilogue4(const GemmArgs& g, int epi, int group,
   *reinterpret_cast<bf16x4_t*>(C + (int64_t)crow * ldc + col0) = o;
 }
 
-// Wide row sets (prefill): a workgroup of 4 waves owns a 128-row x 128-column output
-// tile (SwiGLU: 128 rows x 64 gate columns and their 64 up-projection twins); wave
-// (wr, wc) computes the 64 x 64 quarter (wr, wc) as 4 x 4 tiles of
-// v_mfma_f32_16x16x32_bf16. Both operands go from memory straight to registers in MFMA
-// lane order: the weights are stored in that order (one 16x32 tile = 1 KB contiguous per
-// wave) and every lane fetches 16 bytes of its own A row, so gathered expert rows cost
-// nothing extra. The products are formed transposed (weights as the A operand, rows as
-// B), so a lane ends with 4 consecutive output columns of its own row: 8-byte epilogue
-// loads and stores, and the C row is the entry the lane already holds. The k tiles are
-// software-pipelined kWideStages deep in registers.
-constexpr int kWideStages = 2;
-constexpr int kWideRows = 128;
+// LDS-staged tiles for wide row sets: a workgroup of 4 waves owns 128 rows x 256 output
+// columns (SwiGLU: 128 gate columns and their 128 up-projection twins); wave (wr, wc)
+// computes 64 rows x 128 columns as 4 x 8 MFMA tiles (128 accumulators). Per 32-wide k
+// step the workgroup stages the A tile (gathered rows, written in MFMA lane order) and
+// 16 weight tiles (1 KB each, stored in lane order) in LDS, double-buffered: the next
+// step's global loads are in flight while this step's 32 MFMAs per wave run, and one
+// barrier per step separates the buffers. Each staged byte feeds 2 waves from LDS, and
+// each wave's 12 fragment reads feed 32 products. The weights go in as the A operand and
+// the rows as B, so a lane ends with 4 consecutive output columns of its own row: 8-byte
+// epilogue loads and stores, and the C row is an entry the lane loads itself. Gathered
+// expert rows cost nothing extra: each staging thread fetches 16 bytes of its own row.
+constexpr int kTileRows = 128;
 
 template <int EPI, int MODE>
-__global__ void __launch_bounds__(256) gemm_bf16_wide_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
-  constexpr int kCT = kPair ? 2 : 4;  // column tiles per wave (gate tiles for SwiGLU)
-  constexpr int kB = 4;               // weight fragments per k tile (SwiGLU: 2 gate + 2 up)
-  constexpr int S = kWideStages;
+  __shared__ bf16x8_t sA[2][8][64];   // [buffer][row tile][lane]
+  __shared__ bf16x8_t sW[2][16][64];  // [buffer][column tile][lane]
   const int group = (int)blockIdx.y + g.group_offset;
   const int N = g.N;
   const int KT = g.K / 32;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wr = wv >> 1, wc = wv & 1;
   const int m16 = lane & 15, kq = lane >> 4;
   const int cnt = group_rows<MODE>(g, group);
-  const int r_wg = (int)blockIdx.z * kWideRows;
+  const int r_wg = (int)blockIdx.z * kTileRows;
   if (r_wg >= cnt) return;
-  const int ct0 = (int)blockIdx.x * (kPair ? 4 : 8) + wc * kCT;  // first gate column tile
-  if (ct0 * 16 >= N) return;  // the wave's column tiles all lie past N (uniform per wave)
-
-  // rows of this lane: row m16 of each 16-row tile rt; rows past the set re-read the last
-  int ent[4];
-  const bf16* ap[4];
+  const int ct_wg = (int)blockIdx.x * (kPair ? 8 : 16);  // first (gate) column tile
+  if (ct_wg * 16 >= N) return;
   const bf16* A = reinterpret_cast<const bf16*>(g.A);
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    const int i = min(r_wg + wr * 64 + rt * 16 + m16, cnt - 1);
-    ent[rt] = entry_load<MODE>(g, group, i);
-    ap[rt] = A + (int64_t)a_row_of<MODE>(g, group, ent[rt]) * g.lda + kq * 8;
-  }
-  // weight fragments: tile (ct, kt) of this lane at ((ct * KT + kt) * 64 + lane) * 8
   const bf16* W = reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
-  const bf16* wp[kB];
+
+  // staging: A chunks q = tid + 256 h (h < 2): row q / 4, k chunk q % 4; weight chunks
+  // q = tid + 256 h (h < 4): tile q / 64, lane q % 64
+  const bf16* ga[2];
 #pragma unroll
-  for (int c = 0; c < kB; ++c) {
-    int ct = kPair ? (c < 2 ? ct0 + c : N / 16 + ct0 + (c - 2)) : ct0 + c;
-    if (!kPair) ct = min(ct, N / 16 - 1);  // tiles past N re-read the last one (never stored)
-    wp[c] = W + ((int64_t)ct * KT * 64 + lane) * 8;
+  for (int h = 0; h < 2; ++h) {
+    const int r = (tid >> 2) + 64 * h;
+    const int i = min(r_wg + r, cnt - 1);
+    const int e = entry_load<MODE>(g, group, i);
+    ga[h] = A + (int64_t)a_row_of<MODE>(g, group, e) * g.lda + (tid & 3) * 8;
   }
-  f32x4_t acc[4][kB];  // [row tile][column tile]: lane holds columns 4 kq + j of row m16
+  const int sa_tile = (tid >> 2) >> 4, sa_lane = (tid & 3) * 16 + ((tid >> 2) & 15);
+  const bf16* gw[4];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int c = 0; c < kB; ++c) acc[rt][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  bf16x8_t xa[S][4], xb[S][kB];
-#pragma unroll
-  for (int st = 0; st < S; ++st) {
-#pragma unroll
-    for (int c = 0; c < kB; ++c) xb[st][c] = load_bf16x8(wp[c] + (int64_t)st * 512);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) xa[st][rt] = load_bf16x8(ap[rt] + st * 32);
+  for (int h = 0; h < 4; ++h) {
+    const int c = (tid >> 6) + 4 * h;
+    int ct;
+    if constexpr (kPair)
+      ct = c < 8 ? ct_wg + c : N / 16 + ct_wg + (c - 8);
+    else
+      ct = min(ct_wg + c, N / 16 - 1);  // tiles past N re-read the last one (never stored)
+    gw[h] = W + ((int64_t)ct * KT * 64 + lane) * 8;
   }
-  for (int kt0 = 0; kt0 < KT; kt0 += S) {
+  bf16x8_t ra[2], rw[4];
+  auto fetch = [&](int kt) {
 #pragma unroll
-    for (int st = 0; st < S; ++st) {
+    for (int h = 0; h < 4; ++h) rw[h] = load_bf16x8(gw[h] + (int64_t)kt * 512);
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
+    for (int h = 0; h < 2; ++h) ra[h] = load_bf16x8(ga[h] + kt * 32);
+  };
+  auto stage = [&](int buf) {
 #pragma unroll
-        for (int c = 0; c < kB; ++c)
-          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[st][c], xa[st][rt], acc[rt][c], 0, 0, 0);
-      const int kn = kt0 + st + S;
-      if (kn < KT) {
+    for (int h = 0; h < 4; ++h) sW[buf][(tid >> 6) + 4 * h][lane] = rw[h];
 #pragma unroll
-        for (int c = 0; c < kB; ++c) xb[st][c] = load_bf16x8(wp[c] + (int64_t)kn * 512);
+    for (int h = 0; h < 2; ++h) sA[buf][sa_tile + 4 * h][sa_lane] = ra[h];
+  };
+  // this wave's column tiles in the staged set: 8 of 16 (SwiGLU: 4 gate + their 4 up)
+  int wcol[8];
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) xa[st][rt] = load_bf16x8(ap[rt] + kn * 32);
-      }
-    }
+  for (int j = 0; j < 8; ++j) wcol[j] = kPair ? (j < 4 ? wc * 4 + j : 8 + wc * 4 + (j - 4)) : wc * 8 + j;
+
+  f32x4_t acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) fetch(kt + 1);
+    bf16x8_t fa[4], fw[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i] = sA[buf][wr * 4 + i][lane];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) fw[j] = sW[buf][wcol[j]][lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[j], fa[i], acc[i][j], 0, 0, 0);
+    if (kt + 1 < KT) stage(buf ^ 1);
+    __syncthreads();
   }
+  // lane holds columns 4 kq + e of column tile wcol[j] for row m16 of row tile wr * 4 + i
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    const int i = r_wg + wr * 64 + rt * 16 + m16;
-    if (i >= cnt) continue;
-    const int crow = entry_fix<MODE>(group, i, ent[rt]) + g.c_row_offset;
+  for (int i = 0; i < 4; ++i) {
+    const int r = r_wg + wr * 64 + i * 16 + m16;
+    if (r >= cnt) continue;
+    const int crow = entry_fix<MODE>(group, r, entry_load<MODE>(g, group, r)) + g.c_row_offset;
 #pragma unroll
-    for (int c = 0; c < kCT; ++c) {
-      const int col0 = (ct0 + c) * 16 + kq * 4;
+    for (int j = 0; j < (kPair ? 4 : 8); ++j) {
+      const int col0 = (ct_wg + wcol[j]) * 16 + kq * 4;
       if (col0 >= N) continue;
       float v[4], u[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[j] = acc[rt][c][j];
-        u[j] = kPair ? acc[rt][c + 2][j] : 0.f;
+      for (int e = 0; e < 4; ++e) {
+        v[e] = acc[i][j][e];
+        u[e] = kPair ? acc[i][j + 4][e] : 0.f;
       }
       epilogue4(g, EPI, group, g.C, g.ldc, crow, col0, v, u);
     }
@@ -536,13 +557,13 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
 
 template <int EPI>
 int launch_wide(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
-  const int colw = EPI == EPI_SWIGLU ? 64 : 128;
+  const int colw = EPI == EPI_SWIGLU ? 128 : 256;
   dim3 grid((unsigned)((a.N + colw - 1) / colw), (unsigned)groups,
-            (unsigned)((max_rows + kWideRows - 1) / kWideRows));
+            (unsigned)((max_rows + kTileRows - 1) / kTileRows));
   switch (a.row_mode) {
-    case ROWS_PULSE: gemm_bf16_wide_kernel<EPI, ROWS_PULSE><<<grid, 256, 0, s>>>(a); break;
-    case ROWS_LIST: gemm_bf16_wide_kernel<EPI, ROWS_LIST><<<grid, 256, 0, s>>>(a); break;
-    case ROWS_ALL: gemm_bf16_wide_kernel<EPI, ROWS_ALL><<<grid, 256, 0, s>>>(a); break;
+    case ROWS_PULSE: gemm_bf16_lds_kernel<EPI, ROWS_PULSE><<<grid, 256, 0, s>>>(a); break;
+    case ROWS_LIST: gemm_bf16_lds_kernel<EPI, ROWS_LIST><<<grid, 256, 0, s>>>(a); break;
+    case ROWS_ALL: gemm_bf16_lds_kernel<EPI, ROWS_ALL><<<grid, 256, 0, s>>>(a); break;
     default: return fail(PULSAR_ERR_INVALID, "gemm: row mode of a wide launch");
   }
   PULSAR_LAUNCH_CHECK();
@@ -556,9 +577,9 @@ int launch_gemm_wide(const GemmArgs& a, int dtype, int epi, int groups, int max_
   if (dtype != PULSAR_BF16 || a.has_g0 || a.row_mode == ROWS_LOGITS)
     return launch_gemm(a, dtype, epi, groups, max_rows, s);
   if (groups <= 0) return PULSAR_OK;
-  if (a.K % 256 != 0 || a.N % 16 != 0 || (epi == EPI_SWIGLU && a.N % 64 != 0))
+  if (a.K % 256 != 0 || a.N % 16 != 0 || (epi == EPI_SWIGLU && a.N % 128 != 0))
     return fail(PULSAR_ERR_UNSUPPORTED, "gemm: wide tiles need K % 256 == 0 and N % 16 == 0 "
-                                        "(SwiGLU: N % 64 == 0)");
+                                        "(SwiGLU: N % 128 == 0)");
   switch (epi) {
     case EPI_STORE: return launch_wide<EPI_STORE>(a, groups, max_rows, s);
     case EPI_QKVG: return launch_wide<EPI_QKVG>(a, groups, max_rows, s);
