@@ -51,7 +51,6 @@ struct Engine {
   int32_t* p_ids = nullptr;
   RowDesc* p_rows = nullptr;  // [P][R]
   StepCtl* p_ctl = nullptr;   // [P]
-  int32_t* page_table = nullptr;
   KVDesc kv{};
   int prompt_len = 0;
   bool prefilled = false;
@@ -120,7 +119,6 @@ __global__ void set_seen_kernel(const int32_t* ids, uint32_t* seen, int T, int V
 }
 
 void kv_desc(Engine& e) {
-  e.kv.page_table = e.page_table;
   e.kv.local_mask = e.m.local_mask;
   e.kv.Hkv = e.Hkv;
   e.kv.lcap = e.lcap;
@@ -264,7 +262,6 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.p_ids, 4 * (size_t)x.B * c.max_prompt));
   PULSAR_TRY(x.alloc(&x.p_rows, sizeof(RowDesc) * x.P * (size_t)x.B * c.max_prompt));
   PULSAR_TRY(x.alloc(&x.p_ctl, sizeof(StepCtl) * x.P));
-  PULSAR_TRY(x.alloc(&x.page_table, 4 * (size_t)x.B * x.max_pages));
   // KV cache
   const size_t local_elems = (size_t)x.B * x.Hkv * x.lcap * kHeadDim;
   const size_t global_elems = (size_t)x.B * x.max_pages * x.Hkv * kPage * kHeadDim;
@@ -278,9 +275,6 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
     PULSAR_CHECK_HIP(hipMemset(x.kv.k[l], 0, es * n));
     PULSAR_CHECK_HIP(hipMemset(x.kv.v[l], 0, es * n));
   }
-  std::vector<int32_t> pt((size_t)x.B * x.max_pages);
-  for (size_t i = 0; i < pt.size(); ++i) pt[i] = (int32_t)i;  // sequence b owns pages [b*mp, (b+1)*mp)
-  PULSAR_CHECK_HIP(hipMemcpy(x.page_table, pt.data(), pt.size() * 4, hipMemcpyHostToDevice));
   std::vector<int32_t> stops(8, -1);
   for (int i = 0; i < c.n_stop; ++i) stops[i] = c.stop_ids[i];
   PULSAR_CHECK_HIP(hipMemcpy(x.stop_ids, stops.data(), 32, hipMemcpyHostToDevice));

@@ -14,8 +14,9 @@ static_assert(kUnitSplit >= kSplitLen, "split partial slots are sized for kSplit
 constexpr int kMaxRank = 16;    // re-injection gate rank bound
 
 // KV cache addressing. Local (sliding-window) layers: a per-sequence ring of `lcap`
-// positions (a multiple of 64). Global layers: pages of 64 positions from a shared pool,
-// located through page_table[b][pos / 64]. K is stored position-major ([..][pos][64]);
+// positions (a multiple of 64). Global layers: pages of 64 positions, sequence b owning
+// the run of pages [b * max_pages, (b + 1) * max_pages), so a page's address is computed,
+// never looked up (no dependent load ahead of the KV loads). K is stored position-major ([..][pos][64]);
 // V is stored transposed, dimension-major ([..][64][pos]), so that the keys of one
 // dimension are contiguous: the layout the P.V matrix-core operand reads.
 //   local  K: [B][Hkv][lcap][64]        V: [B][Hkv][64][lcap]
@@ -23,7 +24,6 @@ constexpr int kMaxRank = 16;    // re-injection gate rank bound
 struct KVDesc {
   void* k[kMaxLayers];
   void* v[kMaxLayers];
-  const int32_t* page_table;
   uint32_t local_mask;
   int Hkv;
   int lcap;
@@ -39,8 +39,8 @@ __device__ __forceinline__ int64_t kv_offset(const KVDesc& c, int layer, int b, 
   if (kv_is_local(c, layer)) {
     return (((int64_t)b * c.Hkv + g) * c.lcap + (pos % c.lcap)) * kHeadDim;
   }
-  const int page = c.page_table[(int64_t)b * c.max_pages + pos / kPage];
-  return (((int64_t)page * c.Hkv + g) * kPage + (pos % kPage)) * kHeadDim;
+  const int64_t page = (int64_t)b * c.max_pages + pos / kPage;
+  return ((page * c.Hkv + g) * kPage + (pos % kPage)) * kHeadDim;
 }
 
 // V element (pos, dim).
@@ -49,8 +49,8 @@ __device__ __forceinline__ int64_t kv_offset_v(const KVDesc& c, int layer, int b
   if (kv_is_local(c, layer)) {
     return (((int64_t)b * c.Hkv + g) * kHeadDim + dim) * c.lcap + (pos % c.lcap);
   }
-  const int page = c.page_table[(int64_t)b * c.max_pages + pos / kPage];
-  return (((int64_t)page * c.Hkv + g) * kHeadDim + dim) * kPage + (pos % kPage);
+  const int64_t page = (int64_t)b * c.max_pages + pos / kPage;
+  return ((page * c.Hkv + g) * kHeadDim + dim) * kPage + (pos % kPage);
 }
 
 // A 64-aligned block of 64 positions starting at kb is contiguous in both caches:
@@ -68,7 +68,7 @@ __device__ __forceinline__ KVBlock kv_block(const KVDesc& c, int layer, int b, i
     r.v0 = bg * kHeadDim * c.lcap + ring;
     r.vstride = c.lcap;
   } else {
-    const int64_t pg = (int64_t)c.page_table[(int64_t)b * c.max_pages + kb / kPage] * c.Hkv + g;
+    const int64_t pg = ((int64_t)b * c.max_pages + kb / kPage) * c.Hkv + g;
     r.k0 = pg * kPage * kHeadDim;
     r.v0 = pg * kHeadDim * kPage;
     r.vstride = kPage;

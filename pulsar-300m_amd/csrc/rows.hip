@@ -466,6 +466,7 @@ __device__ __forceinline__ void unit_range(const AttnArgs& a, const AttnUnit& un
 // Last split block of (unit u, kv head g): merge the split partials (device-coherent loads),
 // normalise, round as the SDPA output and apply the head gate. Threads 0-255:
 // thread -> row of the unit (z), head of the group, two dims.
+constexpr int kMergeChunk = 8;  // split partials loaded per round trip
 __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int g,
                                                   const AttnUnit& un, int nsplit) {
   if (threadIdx.x >= 256) return;
@@ -474,10 +475,10 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
   if (row < 0) return;
   const float* p0 = a.part + (((int64_t)u * a.Hkv + g) * a.max_splits * 8 + z * 4 + h) * 66;
   float Mx = -INFINITY, Ls = 0.f, Oa = 0.f, Ob = 0.f;
-  for (int c0 = 0; c0 < nsplit; c0 += 8) {
-    float pm[8], pl[8], pa[8], pb[8];
+  for (int c0 = 0; c0 < nsplit; c0 += kMergeChunk) {
+    float pm[kMergeChunk], pl[kMergeChunk], pa[kMergeChunk], pb[kMergeChunk];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kMergeChunk; ++k) {
       const float* p = p0 + (int64_t)min(c0 + k, nsplit - 1) * 8 * 66;
       pm[k] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pl[k] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -486,14 +487,14 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
     }
     float cm = Mx;
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < kMergeChunk; ++k)
       if (c0 + k < nsplit) cm = fmaxf(cm, pm[k]);
     const float f0 = Mx == -INFINITY ? 0.f : expf(Mx - cm);
     Ls *= f0;
     Oa *= f0;
     Ob *= f0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kMergeChunk; ++k) {
       if (c0 + k < nsplit && pm[k] != -INFINITY) {
         const float f = expf(pm[k] - cm);
         Ls += pl[k] * f;
