@@ -112,6 +112,15 @@ __device__ __forceinline__ void ldv(const float* p, float* o) {
     o[i] = v.x; o[i + 1] = v.y; o[i + 2] = v.z; o[i + 3] = v.w;
   }
 }
+// 8 bf16 held in 16 bytes to float.
+__device__ __forceinline__ void unpack_bf16x8(const uint4& u, float* o) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    o[2 * j] = __uint_as_float(w[j] << 16);
+    o[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+  }
+}
 template <int N>
 __device__ __forceinline__ void ldv(const bf16* p, float* o) {
   if constexpr (N % 8 == 0) {

@@ -97,6 +97,68 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
 #pragma unroll
       for (int c = 0; c < EPL; ++c) hv[c] = rnd<T>(ev[c] + stp[c]);
     }
+  } else if constexpr (EXACT && sizeof(T) == 2 && EPL % 8 == 0 && EPL <= 16) {
+    // The same re-injection as the general branch below, with every load of the row (state,
+    // norm, bias and all 2R + D/64 weight vectors of this lane) issued before the first
+    // reduction: one memory round trip instead of one per rank.
+    const bf16* hp = reinterpret_cast<const bf16*>(a.hout_state) + (int64_t)st * D;
+    const bf16* wd = reinterpret_cast<const bf16*>(a.reinject_down) + (int64_t)rd.pulse * RT * 2 * D;
+    const bf16* wu = reinterpret_cast<const bf16*>(a.reinject_up) + (int64_t)rd.pulse * D * RT;
+    const bf16* bu = reinterpret_cast<const bf16*>(a.reinject_bias) + (int64_t)rd.pulse * D;
+    constexpr int QV = EPL / 8, QU = RT / 8;
+    uint4 rwe[RT][QV], rwr[RT][QV], rwu[EPL][QU];
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+      for (int q = 0; q < QV; ++q) {
+        rwe[j][q] = *reinterpret_cast<const uint4*>(wd + (int64_t)j * 2 * D + i0 + 8 * q);
+        rwr[j][q] = *reinterpret_cast<const uint4*>(wd + (int64_t)j * 2 * D + D + i0 + 8 * q);
+      }
+#pragma unroll
+    for (int c = 0; c < EPL; ++c)
+#pragma unroll
+      for (int q = 0; q < QU; ++q)
+        rwu[c][q] = *reinterpret_cast<const uint4*>(wu + (int64_t)(i0 + c) * RT + 8 * q);
+    float ev[EPL], hpv[EPL], sn[EPL], bv[EPL];
+    ldv<EPL>(e + i0, ev);
+    ldv<EPL>(hp + i0, hpv);
+    ldv<EPL>(a.state_norm + i0, sn);
+    ldv<EPL>(bu + i0, bv);
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) ss += hpv[c] * hpv[c];
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
+    float rv[EPL];
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) rv[c] = rnd<T>(hpv[c] * inv * sn[c]);
+    float gh[RT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      float we[EPL], wr[EPL];
+#pragma unroll
+      for (int q = 0; q < QV; ++q) {
+        unpack_bf16x8(rwe[j][q], we + 8 * q);
+        unpack_bf16x8(rwr[j][q], wr + 8 * q);
+      }
+      float pe = 0.f, pr = 0.f;
+#pragma unroll
+      for (int c = 0; c < EPL; ++c) {
+        pe += ev[c] * we[c];
+        pr += rv[c] * wr[c];
+      }
+      gh[j] = rnd<T>(rnd<T>(wave_sum(pe)) + rnd<T>(wave_sum(pr)));
+    }
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) {
+      float wv[RT];
+#pragma unroll
+      for (int q = 0; q < QU; ++q) unpack_bf16x8(rwu[c][q], wv + 8 * q);
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < RT; ++j) acc += gh[j] * wv[j];
+      const float mix = rnd<T>(sigmoidf_(rnd<T>(acc + bv[c])));
+      hv[c] = rnd<T>(rnd<T>(lerp_ref(rv[c], ev[c], mix)) + stp[c]);
+    }
   } else {
     // rank-R re-injection: g = T(T(e . wd[j][:D]) + T(r . wd[j][D:])), mix = sigmoid(up g + b)
     const T* hp = reinterpret_cast<const T*>(a.hout_state) + (int64_t)st * D;
