@@ -248,6 +248,24 @@ int pulsar_engine_profile_read(void* handle, double* host_ms, int64_t* host_laun
 int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes,
                        hipStream_t stream);
 
+/* The engine's sampler on caller buffers. No counterpart in the reference's C surface: it
+ * is the device form of the reference's _sample (src/infer.py:658-685) for hosts that hold
+ * their own logits, and lets tests check the sampling rule kernel against the oracle.
+ *   logits [n_rows][V] fp32; seen [n_seq][V/32] bitmaps of the tokens each sequence has
+ *   seen; row_seq [n_rows] its sequence; row_extra [n_rows] one more token counted as seen
+ *   (-1: none); seq_ctr [n_seq] the per-sequence draw counters. dtype (PULSAR_BF16 or
+ *   PULSAR_F32) is the activation dtype whose rounding the penalty and temperature follow.
+ *   Outputs: out_argmax [n_rows] (penalised argmax, lowest index on ties) and out_draw
+ *   [n_rows][2] (two independent draws from the top-p set; equal to the argmax when
+ *   greedy). workspace: pulsar_sample_workspace_bytes(n_seq) bytes of device memory,
+ *   256-byte aligned. V must be a multiple of 4096 with V / 1024 a power of two <= 64. */
+int64_t pulsar_sample_workspace_bytes(int32_t n_seq);
+int pulsar_sample_rows(const float* logits, int32_t n_rows, int32_t V, int32_t dtype,
+                       const uint32_t* seen, const int32_t* row_seq, const int32_t* row_extra,
+                       const uint32_t* seq_ctr, int32_t n_seq, uint64_t seed, float temperature,
+                       float top_p, float repetition_penalty, int32_t greedy, int32_t* out_argmax,
+                       int32_t* out_draw, void* workspace, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

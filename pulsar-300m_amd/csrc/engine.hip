@@ -1086,4 +1086,26 @@ int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes
   return PULSAR_OK;
 }
 
+int64_t pulsar_sample_workspace_bytes(int32_t n_seq) {
+  return n_seq < 0 ? -1 : (int64_t)sample_workspace_bytes(n_seq);
+}
+
+int pulsar_sample_rows(const float* logits, int32_t n_rows, int32_t V, int32_t dtype,
+                       const uint32_t* seen, const int32_t* row_seq, const int32_t* row_extra,
+                       const uint32_t* seq_ctr, int32_t n_seq, uint64_t seed, float temperature,
+                       float top_p, float repetition_penalty, int32_t greedy, int32_t* out_argmax,
+                       int32_t* out_draw, void* workspace, hipStream_t stream) {
+  PULSAR_REQUIRE(logits && seen && row_seq && row_extra && seq_ctr && out_argmax && out_draw &&
+                     workspace,
+                 "sample_rows: null argument");
+  PULSAR_REQUIRE(n_rows >= 0 && n_seq >= 1, "sample_rows: n_rows >= 0 and n_seq >= 1");
+  PULSAR_REQUIRE(dtype == PULSAR_BF16 || dtype == PULSAR_F32, "sample_rows: dtype");
+  PULSAR_REQUIRE(temperature > 0.f && top_p > 0.f && top_p <= 1.f && repetition_penalty > 0.f,
+                 "sample_rows: temperature > 0, 0 < top_p <= 1, repetition_penalty > 0");
+  if (n_rows == 0) return PULSAR_OK;
+  return launch_sample_rows(logits, n_rows, V, dtype, seen, row_seq, row_extra, seq_ctr, n_seq,
+                            seed, temperature, top_p, repetition_penalty, greedy, out_argmax,
+                            out_draw, workspace, stream);
+}
+
 }  // extern "C"

@@ -31,6 +31,7 @@ struct SampleArgs {
   const uint64_t* seed;  // device word, so a captured graph follows re-seeding
   int32_t* out_argmax;  // [lrows]
   int32_t* out_draw;    // [lrows][2]
+  int n_seq;            // > 0: rows naming a sequence outside [0, n_seq) output -1
 };
 
 struct ControllerArgs {
@@ -51,6 +52,13 @@ struct ControllerArgs {
 };
 
 int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s);
+// Standalone sampling of n_rows logits rows (the engine's kernel on caller buffers).
+size_t sample_workspace_bytes(int n_seq);
+int launch_sample_rows(const float* logits, int n_rows, int V, int dtype, const uint32_t* seen,
+                       const int32_t* row_seq, const int32_t* row_extra, const uint32_t* seq_ctr,
+                       int n_seq, uint64_t seed, float temperature, float top_p, float rep_penalty,
+                       int greedy, int32_t* out_argmax, int32_t* out_draw, void* workspace,
+                       hipStream_t s);
 int launch_controller(const ControllerArgs& a, hipStream_t s);
 
 }  // namespace pulsar

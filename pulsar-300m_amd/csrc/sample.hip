@@ -97,6 +97,10 @@ __global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
   const int lr = blockIdx.x;
   if (lr >= a.ctl->n_lrows) return;
   const int seq = a.lrow_seq[lr];
+  if (a.n_seq > 0 && (seq < 0 || seq >= a.n_seq)) {
+    if (threadIdx.x < 3) (threadIdx.x == 0 ? a.out_argmax[lr] : a.out_draw[lr * 2 + threadIdx.x - 1]) = -1;
+    return;
+  }
   const int extra = a.lrow_extra[lr];
   const float* lg = a.logits + (int64_t)lr * a.V;
   const uint32_t* seen = a.seen + (int64_t)seq * (a.V / 32);
@@ -470,6 +474,60 @@ int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s) 
 #undef PULSAR_SAMPLE_CASE
   PULSAR_LAUNCH_CHECK();
   return PULSAR_OK;
+}
+
+namespace {
+// Control block, seed word and per-sequence counters of a standalone sampling call.
+__global__ void sample_setup_kernel(StepCtl* ctl, uint64_t* seed_dev, SeqState* st,
+                                    const uint32_t* ctr, int n_rows, int n_seq, uint64_t seed) {
+  int32_t* c = reinterpret_cast<int32_t*>(ctl);
+  for (int i = threadIdx.x; i < (int)(sizeof(StepCtl) / 4); i += blockDim.x) c[i] = 0;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ctl->n_lrows = n_rows;
+    *seed_dev = seed;
+  }
+  for (int i = threadIdx.x; i < n_seq; i += blockDim.x) {
+    SeqState z{};
+    z.ctr = ctr[i];
+    st[i] = z;
+  }
+}
+}  // namespace
+
+size_t sample_workspace_bytes(int n_seq) {
+  return 256 + 256 + (size_t)n_seq * sizeof(SeqState);
+}
+
+int launch_sample_rows(const float* logits, int n_rows, int V, int dtype, const uint32_t* seen,
+                       const int32_t* row_seq, const int32_t* row_extra, const uint32_t* seq_ctr,
+                       int n_seq, uint64_t seed, float temperature, float top_p, float rep_penalty,
+                       int greedy, int32_t* out_argmax, int32_t* out_draw, void* workspace,
+                       hipStream_t s) {
+  static_assert(sizeof(StepCtl) <= 256, "control block fits its workspace slot");
+  char* ws = static_cast<char*>(workspace);
+  StepCtl* ctl = reinterpret_cast<StepCtl*>(ws);
+  uint64_t* seed_dev = reinterpret_cast<uint64_t*>(ws + 256);
+  SeqState* st = reinterpret_cast<SeqState*>(ws + 512);
+  sample_setup_kernel<<<1, 256, 0, s>>>(ctl, seed_dev, st, seq_ctr, n_rows, n_seq, seed);
+  PULSAR_LAUNCH_CHECK();
+  SampleArgs a{};
+  a.ctl = ctl;
+  a.logits = logits;
+  a.lrow_seq = row_seq;
+  a.lrow_extra = row_extra;
+  a.seen = seen;
+  a.state = st;
+  a.V = V;
+  a.greedy = greedy;
+  a.temperature = temperature;
+  a.top_p = top_p;
+  a.rep_penalty = rep_penalty;
+  a.seed = seed_dev;
+  a.out_argmax = out_argmax;
+  a.out_draw = out_draw;
+  a.n_seq = n_seq;
+  return launch_sample(a, dtype, n_rows, s);
 }
 
 int launch_controller(const ControllerArgs& a, hipStream_t s) {

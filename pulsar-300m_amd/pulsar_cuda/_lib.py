@@ -97,7 +97,12 @@ _PROTOS = {
     "pulsar_engine_rewind": [_vp, ctypes.c_uint64, _vp],
     "pulsar_engine_profile": [_vp, _c_i32],
     "pulsar_engine_profile_read": [_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)],
+    "pulsar_sample_workspace_bytes": [_c_i32],
+    "pulsar_sample_rows": [_vp, _c_i32, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _c_i32,
+                           ctypes.c_uint64, _c_f32, _c_f32, _c_f32, _c_i32, _vp, _vp, _vp, _vp],
 }
+# entries whose result is not an int status
+_RESTYPES = {"pulsar_sample_workspace_bytes": _c_i64}
 
 EXPORTED = tuple(["pulsar_last_error", *_PROTOS])
 
@@ -118,7 +123,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.pulsar_last_error.argtypes = []
     for name, args in _PROTOS.items():
         fn = getattr(lib, name)
-        fn.restype = ctypes.c_int
+        fn.restype = _RESTYPES.get(name, ctypes.c_int)
         fn.argtypes = args
     _lib = lib
     return lib

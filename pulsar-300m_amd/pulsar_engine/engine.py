@@ -161,6 +161,41 @@ class HipEngine:
         return int(st[:, ST_TESTS].sum()), int(st[:, ST_ACCEPTED].sum())
 
 
+def sample_rows(logits: torch.Tensor, seen: Sequence[Iterable[int]], row_seq: Sequence[int],
+                row_extra: Sequence[int], ctr: Sequence[int], seed: int, temperature: float,
+                top_p: float, repetition_penalty: float, greedy: bool = False,
+                dtype: torch.dtype = torch.bfloat16) -> tuple[np.ndarray, np.ndarray]:
+    """The engine's sampling kernel on given fp32 logits rows (device tensor [n, V]).
+
+    ``seen[s]`` are the token ids sequence s has seen, ``row_seq[i]`` the sequence of row i,
+    ``row_extra[i]`` one more token counted as seen for row i (-1: none), ``ctr[s]`` the
+    sequence's draw counter. Returns (penalised argmax [n], two draws per row [n, 2]),
+    following the reference's _sample (src/infer.py:658-685) with the engine's generator."""
+    lib = _lib.load()
+    n, V = logits.shape
+    dev = logits.device
+    bits = np.zeros((len(seen), V // 32), dtype=np.uint32)
+    for s_, ids in enumerate(seen):
+        for t in set(int(x) for x in ids):
+            bits[s_, t >> 5] |= np.uint32(1 << (t & 31))
+    seen_d = torch.from_numpy(bits.view(np.int32)).to(dev)
+    rs = torch.as_tensor(list(row_seq), dtype=torch.int32, device=dev)
+    rx = torch.as_tensor(list(row_extra), dtype=torch.int32, device=dev)
+    cd = torch.as_tensor(np.asarray(ctr, dtype=np.uint32).view(np.int32), device=dev)
+    ws = torch.empty(int(lib.pulsar_sample_workspace_bytes(len(seen))), dtype=torch.uint8,
+                     device=dev)
+    am = torch.empty(n, dtype=torch.int32, device=dev)
+    dr = torch.empty(n, 2, dtype=torch.int32, device=dev)
+    lg = logits.contiguous().float()
+    _lib.check(lib.pulsar_sample_rows(
+        lg.data_ptr(), n, V, _lib.PULSAR_BF16 if dtype == torch.bfloat16 else _lib.PULSAR_F32,
+        seen_d.data_ptr(), rs.data_ptr(), rx.data_ptr(), cd.data_ptr(), len(seen),
+        seed & 0xFFFFFFFFFFFFFFFF, temperature, top_p, repetition_penalty, int(bool(greedy)),
+        am.data_ptr(), dr.data_ptr(), ws.data_ptr(), _stream()))
+    torch.cuda.synchronize(dev)
+    return am.cpu().numpy(), dr.cpu().numpy()
+
+
 def stop_ids_for(cfg, tokenizer=None) -> set[int]:
     """{eos} plus the tokenizer ids of the reference's stop strings (src/infer.py:649-656)."""
     ids = {cfg.eos_token_id}
