@@ -40,7 +40,8 @@ __device__ __forceinline__ float uniform01(uint64_t seed, int seq, uint32_t ctr,
   return (float)(k >> 40) * (1.0f / 16777216.0f);
 }
 
-// Block-wide exclusive scan of one float per thread (blockDim 1024). `red` needs 16 floats.
+// Block-wide exclusive scan of one float per thread (blockDim <= 1024). `red` needs
+// blockDim / 64 floats.
 __device__ float block_excl_scan(float v, float* red, float* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   float incl = v;
@@ -90,8 +91,13 @@ __device__ ArgMax block_argmax(ArgMax x, ArgMax* red) {
 
 }  // namespace
 
-template <typename T, int PER>
-__global__ void __launch_bounds__(1024) sample_kernel(SampleArgs a) {
+#ifndef PULSAR_SAMPLE_THREADS
+#define PULSAR_SAMPLE_THREADS 1024
+#endif
+constexpr int kSampleThreads = PULSAR_SAMPLE_THREADS;
+
+template <typename T, int PER, int NT>
+__global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
   __shared__ float red[16];
   __shared__ ArgMax ared[16];
   const int lr = blockIdx.x;
@@ -452,15 +458,16 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
 }
 
 int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s) {
-  if (a.V % 4096 != 0 || a.V / 1024 > 64)
+  // kSampleThreads threads per logits row, PER = V / kSampleThreads logits per thread
+  if (a.V % 4096 != 0 || a.V > 65536)
     return fail(PULSAR_ERR_UNSUPPORTED, "sample: vocab must be a multiple of 4096 and <= 65536");
-  const int per = a.V / 1024;
-#define PULSAR_SAMPLE_CASE(N)                                                              \
-  case N:                                                                                  \
-    if (dtype == PULSAR_BF16)                                                              \
-      sample_kernel<bf16, N><<<max_lrows, 1024, 0, s>>>(a);                                \
-    else                                                                                   \
-      sample_kernel<float, N><<<max_lrows, 1024, 0, s>>>(a);                               \
+  const int per = a.V / kSampleThreads;
+#define PULSAR_SAMPLE_CASE(N)                                                                   \
+  case N:                                                                                       \
+    if (dtype == PULSAR_BF16)                                                                   \
+      sample_kernel<bf16, N, kSampleThreads><<<max_lrows, kSampleThreads, 0, s>>>(a);          \
+    else                                                                                        \
+      sample_kernel<float, N, kSampleThreads><<<max_lrows, kSampleThreads, 0, s>>>(a);         \
     break;
   switch (per) {
     PULSAR_SAMPLE_CASE(4)
@@ -469,7 +476,7 @@ int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s) 
     PULSAR_SAMPLE_CASE(32)
     PULSAR_SAMPLE_CASE(64)
     default:
-      return fail(PULSAR_ERR_UNSUPPORTED, "sample: vocab/1024 must be a power of two");
+      return fail(PULSAR_ERR_UNSUPPORTED, "sample: vocab / 4096 must be a power of two");
   }
 #undef PULSAR_SAMPLE_CASE
   PULSAR_LAUNCH_CHECK();
