@@ -845,8 +845,9 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
 
 // ---------------------------------------------------------------------------
 // Prefill attention in bf16 on the matrix cores (same key ranges as attn_prefill_kernel).
-// Block = (sequence, 64-query tile, kv head); wave w = query head 4g + w over the tile's 64
-// queries, so each 64-key block staged in LDS serves the 4 heads of the group. Per block:
+// Block = (sequence, 64-query tile, kv head); wave w takes query head 4g + w % 4 over
+// 16·NQ of the tile's 64 queries, so each 64-key block staged in LDS serves every head and
+// query of the block. Per block:
 // S^T = K Q^T (keys x queries), online softmax per query, O^T += V^T P^T (dims x queries).
 // In this orientation P never leaves the registers: the D tile of S^T gives lane l keys
 // 4*(l/16) + j (j < 4) of query l % 16, and the B operand of the second product takes 8
@@ -856,7 +857,14 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
 // product, the running max, sum and output accumulate in fp32.
 // ---------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
+template <int NQ>
+__global__ void __launch_bounds__(256 * (4 / NQ)) attn_prefill_mfma_kernel(AttnArgs a) {
+  // NQ 16-query tiles per wave: the 64 queries of the block are split over 4 / NQ waves
+  // per head, so the block has 4 heads x (4 / NQ) waves
+  constexpr int kThreads = 256 * (4 / NQ);
+  // 16-byte chunks of each staged tile per staging thread (the first 512 threads stage)
+  constexpr int CH = kThreads >= 512 ? 1 : 512 / kThreads;
+  const bool stager = threadIdx.x < 512;
   constexpr int kLd = 72;  // LDS row stride in bf16: 16 bytes of padding against bank conflicts
   __shared__ __attribute__((aligned(16))) __bf16 Ks[64][kLd];  // [key][dim]
   __shared__ __attribute__((aligned(16))) __bf16 Vs[64][kLd];  // [dim][key]
@@ -867,7 +875,8 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
   const int g = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int m16 = lane & 15, kq = lane >> 4;
-  const int head = g * 4 + wv;
+  const int head = g * 4 + (wv & 3);
+  const int qoff = (wv >> 2) * 16 * NQ;  // this wave's first query within the block
   const bool quirk = a.is_local && T_ > a.window;
   const int q0 = qt * 64;
   const int qlast = min(q0 + 63, T_ - 1);
@@ -877,11 +886,11 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
   const int flo = tlo;
   const int fhi = quirk ? T_ - a.window + min(q0, a.window - 1) : q0;
 
-  int qlo[4], qhi[4];
-  attn_bf16x8 qb[4][2];  // Q^T operand: column = query m16 of tile nt, dims kq*8 + 32*ks
+  int qlo[NQ], qhi[NQ];
+  attn_bf16x8 qb[NQ][2];  // Q^T operand: column = query m16 of tile nt, dims kq*8 + 32*ks
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int t = q0 + nt * 16 + m16;
+  for (int nt = 0; nt < NQ; ++nt) {
+    const int t = q0 + qoff + nt * 16 + m16;
     const int tc = min(t, T_ - 1);
     qlo[nt] = tlo;
     qhi[nt] = t >= T_ ? -1 : (quirk ? T_ - a.window + min(tc, a.window - 1) : tc);
@@ -890,10 +899,10 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) qb[nt][ks] = *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32);
   }
-  attn_f32x4 o[4][4];  // O^T tile (dim tile mt, query tile nt)
-  float mrun[4], lrun[4];
+  attn_f32x4 o[4][NQ];  // O^T tile (dim tile mt, query tile nt)
+  float mrun[NQ], lrun[NQ];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
+  for (int nt = 0; nt < NQ; ++nt) {
     mrun[nt] = -INFINITY;
     lrun[nt] = 0.f;
 #pragma unroll
@@ -901,47 +910,51 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
   }
   const float sl2 = a.scale * 1.4426950408889634f;
 
-  // staging: thread -> K row tid/4 (dims 16*(tid%4) .. +16) and V row tid/4 (keys likewise)
-  const int sr = tid >> 2, sc16 = (tid & 3) * 16;
+  // staging: thread -> CH 16-byte chunks of K row sr (dims from sc) and of V row sr (keys)
+  const int sr = ((tid & 511) * CH) >> 3, sc16 = (((tid & 511) * CH) & 7) * 8;
   const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]);
   const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]);
-  attn_bf16x8 kr[2], vr[2];
+  attn_bf16x8 kr[CH], vr[CH];
   auto fetch = [&](int kb) {
     const KVBlock blk = kv_block(a.kv, a.layer, b, g, kb);
     const bf16* kp = Kc + blk.k0 + sr * 64 + sc16;
     const bf16* vp = Vc + blk.v0 + (int64_t)sr * blk.vstride + sc16;
-    kr[0] = *reinterpret_cast<const attn_bf16x8*>(kp);
-    kr[1] = *reinterpret_cast<const attn_bf16x8*>(kp + 8);
-    vr[0] = *reinterpret_cast<const attn_bf16x8*>(vp);
-    vr[1] = *reinterpret_cast<const attn_bf16x8*>(vp + 8);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      kr[c] = *reinterpret_cast<const attn_bf16x8*>(kp + 8 * c);
+      vr[c] = *reinterpret_cast<const attn_bf16x8*>(vp + 8 * c);
+    }
   };
   const int kb0 = tlo & ~63;
   fetch(kb0);
   for (int kb = kb0; kb <= thi; kb += 64) {
     __syncthreads();  // the previous block's LDS reads are done
-    *reinterpret_cast<attn_bf16x8*>(&Ks[sr][sc16]) = kr[0];
-    *reinterpret_cast<attn_bf16x8*>(&Ks[sr][sc16 + 8]) = kr[1];
-    *reinterpret_cast<attn_bf16x8*>(&Vs[sr][sc16]) = vr[0];
-    *reinterpret_cast<attn_bf16x8*>(&Vs[sr][sc16 + 8]) = vr[1];
+    if (stager) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        *reinterpret_cast<attn_bf16x8*>(&Ks[sr][sc16 + 8 * c]) = kr[c];
+        *reinterpret_cast<attn_bf16x8*>(&Vs[sr][sc16 + 8 * c]) = vr[c];
+      }
+    }
     __syncthreads();
     if (kb + 64 <= thi) fetch(kb + 64);  // in flight during this block's products
 
-    attn_f32x4 sv[4][4];  // S^T tile (key tile kt, query tile nt)
+    attn_f32x4 sv[4][NQ];  // S^T tile (key tile kt, query tile nt)
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
       const attn_bf16x8 k0 = *reinterpret_cast<const attn_bf16x8*>(&Ks[kt * 16 + m16][kq * 8]);
       const attn_bf16x8 k1 = *reinterpret_cast<const attn_bf16x8*>(&Ks[kt * 16 + m16][32 + kq * 8]);
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
+      for (int nt = 0; nt < NQ; ++nt) {
         attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qb[nt][0], acc, 0, 0, 0);
         sv[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qb[nt][1], acc, 0, 0, 0);
       }
     }
     const bool full = kb >= flo && kb + 63 <= fhi;  // uniform per block
-    attn_bf16x8 pb[4][2];
+    attn_bf16x8 pb[NQ][2];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int nt = 0; nt < NQ; ++nt) {
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -982,17 +995,17 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
         const attn_bf16x4 hi4 = *reinterpret_cast<const attn_bf16x4*>(&Vs[mt * 16 + m16][ks * 32 + 16 + kq * 4]);
         const attn_bf16x8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
+        for (int nt = 0; nt < NQ; ++nt)
           o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[nt][ks], o[mt][nt], 0, 0, 0);
       }
   }
   // lane holds O[query q0 + 16 nt + m16][dims 16 mt + 4 kq + j]
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
+  for (int nt = 0; nt < NQ; ++nt) {
     float l = lrun[nt];
     l += swz_xor16(l);
     l += __shfl_xor(l, 32, 64);
-    const int t = q0 + nt * 16 + m16;
+    const int t = q0 + qoff + nt * 16 + m16;
     if (t >= T_) continue;
     const int64_t row = (int64_t)b * T_ + t;
     const float gate = bf2f(reinterpret_cast<const bf16*>(a.gate)[row * a.H + head]);
@@ -1487,7 +1500,9 @@ int launch_attn_prefill(const AttnArgs& a, int dtype, int B, hipStream_t s) {
   if (a.H != 4 * a.Hkv)
     return fail(PULSAR_ERR_UNSUPPORTED, "prefill attention: four query heads per kv head");
   if (dtype == PULSAR_BF16) {
-    attn_prefill_mfma_kernel<<<dim3(B * ntile, a.Hkv), 256, 0, s>>>(a);
+    // one 16-query tile per wave: 16 waves of about 95 registers each hide the MFMA, LDS
+    // and exp latencies better than 4 waves of 4 tiles (measured 1.5x on 16 x 2048 tokens)
+    attn_prefill_mfma_kernel<1><<<dim3(B * ntile, a.Hkv), 1024, 0, s>>>(a);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   }
