@@ -82,3 +82,25 @@ def test_missing_library_fails_loudly(tmp_path):
             _lib.load(str(tmp_path / "nope.so"))
     finally:
         _lib._lib = saved
+
+
+def test_sample_rows_validates_before_touching_the_device():
+    """The sampler entry rejects bad arguments with a message, without a GPU."""
+    from pulsar_cuda import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libpulsar_hip.so not built")
+    lib = _lib.load()
+    assert lib.pulsar_sample_workspace_bytes(4) >= 512 + 4 * 64
+    assert lib.pulsar_sample_workspace_bytes(-1) == -1
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    args = [p, 2, 32768, _lib.PULSAR_BF16, p, p, p, p, 1, 0, 0.8, 0.9, 1.1, 0, p, p, p, None]
+    bad = dict(null=(0, None), temperature=(10, 0.0), top_p=(11, 1.5), n_seq=(8, 0),
+               dtype=(3, 7))
+    for name, (i, v) in bad.items():
+        a = list(args)
+        a[i] = v
+        rc = lib.pulsar_sample_rows(*a)
+        assert rc != 0, name
+        assert b"sample_rows" in lib.pulsar_last_error(), name
