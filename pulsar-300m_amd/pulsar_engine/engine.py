@@ -42,7 +42,9 @@ class HipEngine:
         self.batch = batch
         self.max_new = max_new
         self.V = model.cfg.vocab_size
-        stops = [int(s) for s in stop_ids][:8]
+        stops = sorted({int(s) for s in stop_ids})
+        if len(stops) > 8:
+            raise ValueError(f"at most 8 stop ids are supported, got {len(stops)}")
         c = _lib.PulsarEngineConfig()
         c.max_batch, c.max_prompt, c.max_new = batch, max_prompt, max_new
         c.max_ctx = max_ctx or (max_prompt + max_new + 2)
@@ -203,10 +205,10 @@ def stop_ids_for(cfg, tokenizer=None) -> set[int]:
         for s in ("<|im_end|>", "<|endoftext|>", "</s>"):
             try:
                 sid = tokenizer.convert_tokens_to_ids(s)
-                if sid is not None and sid != getattr(tokenizer, "unk_token_id", None):
-                    ids.add(int(sid))
-            except Exception:
-                pass
+            except (KeyError, ValueError, TypeError):  # tokenizer without this token
+                continue
+            if sid is not None and sid != getattr(tokenizer, "unk_token_id", None):
+                ids.add(int(sid))
     return ids
 
 
