@@ -99,6 +99,11 @@ struct GemmArgs {
   void* C0;
   int64_t ldc0;
   int N0;
+  // ROWS_LIST, bf16 SwiGLU with K0 == K: stream every group's weights and first rows
+  // without waiting for its row count (for launches where nearly every group has rows; an
+  // empty group's weights are then read for nothing)
+  int eager_w;
+  int a_rows, a_rows0;  // rows of A and A0 (eager_w clamps speculative row indices into them)
 };
 
 int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,

@@ -303,6 +303,10 @@ GemmArgs gemm_base(const Engine& e) {
 int enqueue_step(Engine& e, hipStream_t s) {
   const PulsarModelDesc& m = e.m;
   const int D = e.D, MR = e.max_rows, dt = e.dtype;
+  // at two or more assignments per expert on average, nearly every expert has rows: the
+  // routed gate/up GEMM then streams weights and rows without first waiting for each
+  // expert's row count (12.2 -> 11.5 us at batch 16; the down GEMM measured no gain)
+  const int eager_experts = (int64_t)MR * e.K >= 2 * (int64_t)e.E ? 1 : 0;
   if (e.prof_on) {
     // an empty timed group: the fixed cost of an event pair around a kernel launch
     PULSAR_TRY(prof_delay(e, s));
@@ -442,6 +446,9 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.list_stride = lstride;
     g.a_div = e.K;
     g.ctl = e.ctl;
+    g.eager_w = eager_experts;
+    g.a_rows = MR;
+    g.a_rows0 = MR;
     g.has_g0 = 1;
     g.K0 = D;
     g.A0 = e.xn;

@@ -177,10 +177,11 @@ __device__ __forceinline__ int group_rows(const GemmArgs& g, int group) {
 // down projection fused into the routed one).
 constexpr int kGemmWaves = 8;
 
-template <int EPI, int KITER, int MODE, int KMUL0>
+template <int EPI, int KITER, int MODE, int KMUL0, bool EAGER>
 __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
   constexpr int kKPass = KITER * 32 * kGemmWaves;  // K covered by one pass of the waves
+  static_assert(!EAGER || MODE == ROWS_LIST, "eager weight loads are for expert lists");
   __shared__ float red[kGemmWaves][64][kPair ? 16 : 8];
   // grid.y == 0 is the optional all-rows group (group -1) when has_g0 is set
   const int group = (int)blockIdx.y + g.group_offset - (g.has_g0 ? 1 : 0);
@@ -188,8 +189,11 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   const int N = g0 ? g.N0 : g.N;
   const int col0 = blockIdx.x * 16;
   if (col0 >= N) return;
-  const int cnt = group_rows<MODE>(g, group);  // uniform per workgroup
-  if ((int)blockIdx.z * 32 >= cnt) return;
+  int cnt = 0;
+  if constexpr (!EAGER) {
+    cnt = group_rows<MODE>(g, group);  // uniform per workgroup
+    if ((int)blockIdx.z * 32 >= cnt) return;
+  }
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = lane & 15, kq = lane >> 4;
@@ -225,17 +229,52 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   // loads leaves every weight load in flight. Lanes past the last row re-read the last
   // entry (always in bounds) and use a zero A operand.
   int tile0 = blockIdx.z * 32;
-  int n = min(32, cnt - tile0);
-  int i0 = tile0 + min(m, n - 1), i1 = tile0 + min(m + 16, n - 1);
-  int l0 = entry_load<MODE>(g, group, i0);
-  int l1 = entry_load<MODE>(g, group, i1);
-  PULSAR_LOAD_W(0);
+  int n, i0, i1, l0, l1;
+  if constexpr (EAGER) {
+    // Most experts have rows (the host decides from the batch size): the first tile's
+    // entries and the weights go out before the row count, whose scalar load retires apart
+    // from them, instead of one round trip later. Entries past the count are read from the
+    // list's spare capacity; the rows they name are clamped, computed and never stored.
+    const int64_t cap = g.list_stride - 1;
+    i0 = tile0 + m;
+    i1 = tile0 + m + 16;
+    const int32_t* lst = g.list + (int64_t)max(group, 0) * g.list_stride;
+    l0 = lst[min((int64_t)i0, cap)];
+    l1 = lst[min((int64_t)i1, cap)];
+    __builtin_amdgcn_sched_barrier(0);
+    PULSAR_LOAD_W(0);
+    // no early exit on the count: a branch on it would let the compiler test it before
+    // issuing the weight loads. A workgroup without rows runs on clamped rows and stores
+    // nothing.
+    cnt = group_rows<MODE>(g, group);
+    // Use the entries here: the wait for them then leaves the weight loads behind them in
+    // flight, and the compiler cannot merge these loads into the next tile's (which would
+    // put them behind the weights and the count).
+    asm volatile("" ::"v"(l0), "v"(l1));
+    n = max(0, min(32, cnt - tile0));
+  } else {
+    n = min(32, cnt - tile0);
+    i0 = tile0 + min(m, n - 1);
+    i1 = tile0 + min(m + 16, n - 1);
+    l0 = entry_load<MODE>(g, group, i0);
+    l1 = entry_load<MODE>(g, group, i1);
+    PULSAR_LOAD_W(0);
+  }
   while (true) {
     __builtin_amdgcn_sched_barrier(0);
     const bool two = n > 16;  // second 16-row block present (uniform per workgroup)
     const int e0 = entry_fix<MODE>(group, i0, l0), e1 = entry_fix<MODE>(group, i1, l1);
-    const int ar0 = m < n ? a_row_of<MODE>(g, group, e0) : -1;
-    const int ar1 = m + 16 < n ? a_row_of<MODE>(g, group, e1) : -1;
+    int ar0, ar1;
+    if constexpr (EAGER) {
+      // every lane of the first row block loads a row (clamped into the A buffer): rows
+      // past the count are computed and never stored, so no A load waits on the count
+      const int lim = (g0 ? g.a_rows0 : g.a_rows) - 1;
+      ar0 = min(max(a_row_of<MODE>(g, group, e0), 0), lim);
+      ar1 = m + 16 < n ? min(max(a_row_of<MODE>(g, group, e1), 0), lim) : -1;
+    } else {
+      ar0 = m < n ? a_row_of<MODE>(g, group, e0) : -1;
+      ar1 = m + 16 < n ? a_row_of<MODE>(g, group, e1) : -1;
+    }
     const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * lda;
     const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * lda;
     f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
@@ -243,7 +282,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
       if (pass > 0) PULSAR_LOAD_W(pass);
 #pragma unroll
       for (int i = 0; i < KITER; ++i)
-        xa[i] = ar0 >= 0 ? load_bf16x8(a0 + pass * kKPass + kb + 32 * i) : zero;
+        xa[i] = (EAGER || ar0 >= 0) ? load_bf16x8(a0 + pass * kKPass + kb + 32 * i) : zero;
 #pragma unroll
       for (int i = 0; i < KITER; ++i) {
         c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[i], c00, 0, 0, 0);
@@ -504,14 +543,14 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   }
 }
 
-template <int EPI, int MODE, int KMUL0>
+template <int EPI, int MODE, int KMUL0, bool EAGER = false>
 void launch_bf16_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
   constexpr int T = 64 * kGemmWaves;
   switch (a.K) {
-    case 256: gemm_bf16_kernel<EPI, 1, MODE, KMUL0><<<grid, T, 0, s>>>(a); break;
-    case 512: gemm_bf16_kernel<EPI, 2, MODE, KMUL0><<<grid, T, 0, s>>>(a); break;
-    case 1024: gemm_bf16_kernel<EPI, 4, MODE, KMUL0><<<grid, T, 0, s>>>(a); break;
-    default: gemm_bf16_kernel<EPI, 8, MODE, KMUL0><<<grid, T, 0, s>>>(a); break;
+    case 256: gemm_bf16_kernel<EPI, 1, MODE, KMUL0, EAGER><<<grid, T, 0, s>>>(a); break;
+    case 512: gemm_bf16_kernel<EPI, 2, MODE, KMUL0, EAGER><<<grid, T, 0, s>>>(a); break;
+    case 1024: gemm_bf16_kernel<EPI, 4, MODE, KMUL0, EAGER><<<grid, T, 0, s>>>(a); break;
+    default: gemm_bf16_kernel<EPI, 8, MODE, KMUL0, EAGER><<<grid, T, 0, s>>>(a); break;
   }
 }
 
@@ -538,10 +577,19 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
     switch (a.row_mode) {
       case ROWS_PULSE: launch_bf16_k<EPI, ROWS_PULSE, 1>(a, grid, s); break;
       case ROWS_LIST:
-        if (k0 == a.K)
-          launch_bf16_k<EPI, ROWS_LIST, 1>(a, grid, s);
-        else
-          launch_bf16_k<EPI, ROWS_LIST, 2>(a, grid, s);
+        if (a.eager_w) {
+          if (EPI != EPI_SWIGLU || k0 != a.K)
+            return fail(PULSAR_ERR_UNSUPPORTED,
+                        "gemm: eager expert launches are SwiGLU with K0 == K");
+          if (a.a_rows < 1 || (a.has_g0 && a.a_rows0 < 1))
+            return fail(PULSAR_ERR_INVALID, "gemm: eager expert launches need A row counts");
+          if constexpr (EPI == EPI_SWIGLU) launch_bf16_k<EPI, ROWS_LIST, 1, true>(a, grid, s);
+        } else {
+          if (k0 == a.K)
+            launch_bf16_k<EPI, ROWS_LIST, 1>(a, grid, s);
+          else
+            launch_bf16_k<EPI, ROWS_LIST, 2>(a, grid, s);
+        }
         break;
       case ROWS_ALL: launch_bf16_k<EPI, ROWS_ALL, 1>(a, grid, s); break;
       case ROWS_LOGITS: launch_bf16_k<EPI, ROWS_LOGITS, 1>(a, grid, s); break;
