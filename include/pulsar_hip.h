@@ -200,11 +200,21 @@ typedef struct PulsarEngineConfig {
   int32_t n_stop;
   int32_t stop_ids[8];
   uint64_t seed;
+  /* 0: the reference's exact self-speculation (one pulse-0 draft per token, pipelined).
+   * 1..7: draft-block mode, a multi-token draft with no reference counterpart: per round,
+   * up to draft_len drafts from pulse 0 alone, then one verify of the block [t, drafts]
+   * with every pulse (row i attends the cache plus the block's same-pulse keys at positions
+   * <= its own, the reference prefill's rule), drafts accepted down the block by the
+   * reference's equal-draw rule (src/infer.py:704-725). Needs max_ctx >= max_prompt +
+   * max_new + 2 + draft_len. */
+  int32_t draft_len;
+  int32_t reserved;
 } PulsarEngineConfig;
 
 /* Buffers readable with pulsar_engine_read. */
 #define PULSAR_BUF_TOKENS 0    /* int32 [B][max_new] emitted ids */
-#define PULSAR_BUF_SEQSTATE 1  /* int32 [B][20] controller state: [0]=done [1]=produced
+#define PULSAR_BUF_SEQSTATE 1  /* int32 [B][32] controller state: [0]=done [1]=produced
+                                  [4]=position of the current token or block
                                   [11]=tests [12]=accepted */
 #define PULSAR_BUF_LOGITS 2    /* fp32 [n_lrows][V] logits of the last step */
 #define PULSAR_BUF_ROWS 3      /* int32 [n_rows][8] rows of the next step
@@ -234,6 +244,22 @@ int pulsar_engine_step(void* handle, int32_t n_steps, int32_t use_graph, hipStre
 /* Steps until every sequence is done (or max_steps), checking every `check_every` steps. */
 int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
                            hipStream_t stream, int32_t* steps_run);
+/* Block verify: n tokens per sequence (host ids [B][n]) at positions P0 .. P0 + n - 1, where
+ * P0 is the prefilled prompt length (or fill_kv's ctx), run through every pulse: pulse k is
+ * one pass over the B*n rows, a row attending the cache and the block's pulse-k keys at
+ * positions <= its own. The last pass's logits (row b*n + i) are readable as
+ * PULSAR_BUF_LOGITS. n <= draft_len + 1 (<= 2 in exact mode). The decode state is not
+ * touched; the block positions' keys/values are overwritten. host_tokens == NULL re-runs
+ * the last uploaded block without a host synchronisation (timing); otherwise the upload
+ * synchronises the stream. use_graph=1 replays a captured HIP graph of the passes.
+ * No reference counterpart: it is the verify step of the draft-block mode, and of the
+ * verify microbenchmark (a 5-token verify over pre-filled caches). */
+int pulsar_engine_verify(void* handle, const int32_t* host_tokens, int32_t n, int32_t use_graph,
+                         hipStream_t stream);
+/* Synthetic cache: every key and value element of every layer ~ N(0,1) (counter-based
+ * generator keyed by seed), positions [0, ctx) then count as cached context for
+ * pulsar_engine_verify. Decoding afterwards needs a prefill. Synchronises the stream. */
+int pulsar_engine_fill_kv(void* handle, int32_t ctx, uint64_t seed, hipStream_t stream);
 /* Restart decoding from the prefilled cache with a new sampling seed: the first token is
  * drawn again from the saved prefill logits. Synchronises the stream. */
 int pulsar_engine_rewind(void* handle, uint64_t seed, hipStream_t stream);

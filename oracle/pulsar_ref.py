@@ -590,6 +590,193 @@ class RefEngine:
             else:
                 logits = v_logits
 
+    # -- draft-block mode (this build's multi-token draft; no reference counterpart) -----
+    #
+    # The reference drafts one token (src/infer.py:688-725). The draft-block mode drafts up
+    # to G tokens with pulse 0 only and verifies the block [t, d1..dG] with all pulses in
+    # one pass per pulse. Its attention rule is the reference prefill's (src/infer.py:
+    # 353-461, src/model.py:880-901): at pulse k a block row sees the committed cache plus
+    # the block's own pulse-k keys at positions <= its own. Everything else in a row is the
+    # decode pass (src/infer.py:463-524): stem of one token, fp32 router, dropless MoE,
+    # YaRN, softcapped logits. Block row 0 is therefore exactly the reference's decode of t,
+    # and the first draft test of every round is the reference's test.
+
+    def block_pass(self, tokens, pos0: int, cache: RefKVCache, pulse: int, h_prev=None,
+                   e_cached=None):
+        """One pulse of the block `tokens` at positions pos0.. over a committed cache.
+
+        The cache is not modified. Returns (logits [n, V], h_out list, e list, kv) where
+        kv[L] = (k, v) [1, Hkv, n, hd] are the block's keys/values of this pulse."""
+        m, cfg = self.m, self.cfg
+        n = len(tokens)
+        W = cfg.sliding_window
+        if pulse == 0:
+            es = [self._stem(torch.tensor([[int(t)]], dtype=torch.long))[1] for t in tokens]
+        else:
+            es = list(e_cached)
+        h_in = [self._pulse_input(pulse, es[i], h_prev[i] if pulse else None) for i in range(n)]
+        h = list(h_in)
+        v_first = [None] * n
+        kv = []
+        gqa = cfg.n_heads > cfg.n_kv_heads
+        for L in range(cfg.n_core):
+            local = cfg.is_local(L)
+            cos, sin = m.rope(local, pos0 + n)
+            qs, ks, vs, xs = [], [], [], []
+            for i in range(n):
+                x = rmsnorm(h[i], m.w(f"core.{L}.attn_norm.weight")[pulse], cfg.rms_eps)
+                q, kk, v, v_first[i] = self._qkv(L, x, pulse, v_first[i])
+                p = pos0 + i
+                c, s = cos[p:p + 1], sin[p:p + 1]
+                q = apply_rope(q, c, s)
+                kk = apply_rope(kk, c, s)
+                if not local and p + 1 > cfg.base_seq_len:
+                    q = q * yarn_scale(p, cfg.base_seq_len)
+                qs.append(q)
+                ks.append(kk)
+                vs.append(v)
+                xs.append(x)
+            kb, vb = torch.cat(ks, dim=2), torch.cat(vs, dim=2)
+            kv.append((kb, vb))
+            ck, cv = cache.k[L], cache.v[L]
+            for i in range(n):
+                kk, vv = kb[:, :, :i + 1], vb[:, :, :i + 1]
+                if ck is not None:
+                    kk, vv = torch.cat([ck, kk], dim=2), torch.cat([cv, vv], dim=2)
+                if local and kk.shape[2] > W:
+                    kk, vv = kk[:, :, -W:], vv[:, :, -W:]
+                a = F.scaled_dot_product_attention(qs[i], kk.contiguous(), vv.contiguous(),
+                                                   is_causal=False, enable_gqa=gqa)
+                h[i] = h[i] + self._gate_and_out(L, xs[i], a, pulse)
+                y = rmsnorm(h[i], m.w(f"core.{L}.mlp_norm.weight")[pulse], cfg.rms_eps)
+                h[i] = h[i] + self.moe_decode(L, y, pulse)
+        h_out = [self._pulse_output(pulse, h_in[i], h[i]) for i in range(n)]
+        rows = []
+        for i in range(n):
+            hf = rmsnorm(h_out[i], m.w("final_norm.weight"), cfg.rms_eps)
+            lg = F.linear(hf, m.w("tok_emb.weight"))[:, -1, :]
+            if cfg.logit_softcap > 0:
+                lg = softcap(lg, cfg.logit_softcap)
+            rows.append(lg)
+        logits = torch.cat(rows, dim=0)
+        if self.trace is not None:
+            self.trace.append(("block", tuple(int(t) for t in tokens), pos0, pulse,
+                               logits.clone()))
+        return logits, h_out, es, kv
+
+    def commit_block(self, cache: RefKVCache, kv, n_keep: int) -> None:
+        """Append the first n_keep block rows' keys/values (the last pulse's) to the cache;
+        local layers keep the newest `sliding_window` entries (src/infer.py:139-150)."""
+        W = self.cfg.sliding_window
+        for L, (kb, vb) in enumerate(kv):
+            k, v = kb[:, :, :n_keep], vb[:, :, :n_keep]
+            if cache.k[L] is not None:
+                k, v = torch.cat([cache.k[L], k], dim=2), torch.cat([cache.v[L], v], dim=2)
+            if self.cfg.is_local(L) and k.shape[2] > W:
+                k, v = k[:, :, -W:], v[:, :, -W:]
+            cache.k[L], cache.v[L] = k.contiguous(), v.contiguous()
+
+    def block_verify(self, tokens, pos0: int, cache: RefKVCache):
+        """All pulses of a block; returns (last-pulse logits [n, V], per-pulse logits, kv)."""
+        h = e = None
+        per_pulse = []
+        kv = None
+        for k in range(self.cfg.default_pulses):
+            lg, h, e, kv = self.block_pass(tokens, pos0, cache, k, h, e)
+            per_pulse.append(lg)
+        return per_pulse[-1], per_pulse, kv
+
+    def block_speculative_ids(self, prompt_ids, max_new_tokens: int, temperature: float,
+                              top_p: float, repetition_penalty: float, draft_len: int,
+                              generator=None, stats: Optional[dict] = None) -> Iterator[int]:
+        """Draft up to `draft_len` tokens with pulse 0, verify the block with all pulses,
+        accept drafts while each equals an independent draw from the verify logits of the
+        row before it (the reference's rule, src/infer.py:704-725, applied down the block).
+
+        A round starts from an emitted token t at position pos. Draft j (j < G, G =
+        min(draft_len, tokens still wanted - 1)) is a draw from the pulse-0 logits of block
+        row j; a stop id ends the block. Verify row i gives draw v_i (and a second draw
+        f_i); the draft of row i+1 is accepted iff it equals v_i and is not a stop id. At
+        the first rejection (row i) the next t is f_i; when no draft is left it is the
+        draw from the last row. Accepted rows' last-pulse keys/values are committed; the
+        rejected rows' are discarded. Row i samples with the seen set plus block tokens
+        1..i. With draft_len = 0 every round is one decode step of t, so the stream is
+        stream_generate_ids's, draw for draw."""
+        cfg = self.cfg
+        ids = torch.as_tensor(prompt_ids, dtype=torch.long).view(1, -1)
+        cache = RefKVCache(cfg)
+        logits = self.prefill(ids, cache)[:, -1, :].clone()
+        seen = ids[0].tolist()
+        pos = len(seen)
+        produced = 0
+        if stats is not None:
+            stats.setdefault("tests", 0)
+            stats.setdefault("accepted", 0)
+            stats.setdefault("rounds", 0)
+            stats.setdefault("p_accept", [])
+        stops = self.stop_ids
+
+        def smp(lg, extra):
+            return self.sample(lg, seen + list(extra), temperature, top_p, repetition_penalty,
+                               generator)
+
+        if max_new_tokens <= 0:
+            return
+        t = smp(logits, [])
+        if t in stops:
+            return
+        seen.append(t)
+        produced += 1
+        yield t
+        while produced < max_new_tokens:
+            g = min(draft_len, max_new_tokens - produced - 1)
+            blk = [t]
+            draft_lg = []
+            for j in range(g):
+                lg0, _, _, _ = self.block_pass(blk, pos, cache, 0)
+                draft_lg.append(lg0[j:j + 1].clone())
+                d = smp(lg0[j:j + 1], blk[1:j + 1])
+                if d in stops:
+                    break
+                blk.append(d)
+            lg, _, kv = self.block_verify(blk, pos, cache)
+            if stats is not None:
+                stats["rounds"] += 1
+            n = len(blk)
+            acc = 0
+            nxt = None
+            done = False
+            for i in range(n):
+                extra = blk[1:i + 1]
+                if i < n - 1:
+                    v = smp(lg[i:i + 1], extra)
+                    if stats is not None:
+                        stats["tests"] += 1
+                        stats["p_accept"].append(accept_probability(
+                            draft_lg[i], lg[i:i + 1], seen + list(extra), temperature, top_p,
+                            repetition_penalty))
+                    if v == blk[i + 1] and blk[i + 1] not in stops:
+                        if stats is not None:
+                            stats["accepted"] += 1
+                        acc = i + 1
+                        seen.append(blk[i + 1])
+                        produced += 1
+                        yield blk[i + 1]
+                        if produced >= max_new_tokens:
+                            done = True
+                            break
+                        continue
+                nxt = smp(lg[i:i + 1], extra)
+                break
+            self.commit_block(cache, kv, acc + 1)
+            pos += acc + 1
+            if done or nxt in stops:
+                return
+            seen.append(nxt)
+            produced += 1
+            yield nxt
+            t = nxt
+
 
 def sampling_distribution(lgt: torch.Tensor, seen: list, temperature: float, top_p: float,
                           repetition_penalty: float) -> torch.Tensor:

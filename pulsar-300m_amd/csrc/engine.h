@@ -34,13 +34,17 @@ struct StepCtl {
   int32_t pad[3];
 };
 
-// Decode attention work unit: the rows of one sequence in a step that read the same cache
-// (the current token and, when present, the speculative token one position later).
+constexpr int kMaxBlock = 8;  // rows of one sequence in a step (draft block + 1)
+
+// Decode attention work unit: the rows of one sequence in a step that read the same cache,
+// at consecutive positions pos0, pos0 + 1, ... (exact mode: the current token and, when
+// present, the speculative token one position later; draft-block mode: the block's rows).
 struct AttnUnit {
   int32_t seq;
-  int32_t row_a, row_b;  // row_b = -1 when the unit has one row
-  int32_t pos_a, pos_b;
-  int32_t pad[3];
+  int32_t n;     // rows (1..kMaxBlock)
+  int32_t pos0;  // position of row[0]; row[i] sits at pos0 + i
+  int32_t pad;
+  int32_t row[kMaxBlock];
 };
 
 // GEMM epilogues.

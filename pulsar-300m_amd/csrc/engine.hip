@@ -19,6 +19,8 @@ struct Engine {
   int dtype = 0, es = 4;
   int D = 0, H = 0, Hkv = 0, qkv = 0, qkvg = 0, E = 0, K = 0, de = 0, ds = 0, L = 0, P = 0, V = 0;
   int B = 0, max_rows = 0, R = 0, max_pages = 0, lcap = 0, max_splits = 0, max_splits_unit = 0;
+  int G = 0;  // drafts per round (draft-block mode), 0 = exact mode
+  int S = 2;  // token-state slots per sequence: rows of one sequence in a step
   std::vector<void*> allocs;
 
   StepCtl* ctl = nullptr;
@@ -29,6 +31,7 @@ struct Engine {
   int32_t* split_done = nullptr;  // [B][Hkv] decode attention split counters
   SeqState* state = nullptr;
   int32_t *lrow_seq = nullptr, *lrow_extra = nullptr, *argmax = nullptr, *draw = nullptr;
+  uint32_t* lrow_ctr = nullptr;  // draft-block mode: per logits row draw counter
   int32_t *tokens = nullptr, *stop_ids = nullptr;
   uint32_t* seen = nullptr;
   void *e_state = nullptr, *hout_state = nullptr;
@@ -54,6 +57,13 @@ struct Engine {
   KVDesc kv{};
   int prompt_len = 0;
   bool prefilled = false;
+  bool kv_ready = false;  // the cache holds positions [0, prompt_len) (prefill or fill_kv)
+  // block verify: host-built rows, control blocks and units of its passes
+  RowDesc* v_rows = nullptr;  // [P][max_rows]
+  StepCtl* v_ctl = nullptr;   // [P]
+  AttnUnit* v_units = nullptr;  // [P][B]
+  hipGraphExec_t vexec = nullptr;
+  hipGraph_t vgraph = nullptr;
 
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
@@ -62,6 +72,8 @@ struct Engine {
   ~Engine() {
     if (exec) hipGraphExecDestroy(exec);
     if (graph) hipGraphDestroy(graph);
+    if (vexec) hipGraphExecDestroy(vexec);
+    if (vgraph) hipGraphDestroy(vgraph);
     if (capture_stream) hipStreamDestroy(capture_stream);
     for (hipEvent_t ev : ev_pool) hipEventDestroy(ev);
     for (void* p : allocs) hipFree(p);
@@ -104,7 +116,10 @@ int validate(const PulsarModelDesc& m, const PulsarEngineConfig& c) {
   PULSAR_REQUIRE(m.vocab % 4096 == 0, "vocab must be a multiple of 4096");
   PULSAR_REQUIRE(c.max_batch >= 1 && c.max_batch <= 256, "max_batch must be 1..256");
   PULSAR_REQUIRE(c.max_prompt >= 1 && c.max_new >= 0, "max_prompt/max_new");
-  PULSAR_REQUIRE(c.max_ctx >= c.max_prompt + c.max_new + 2, "max_ctx < max_prompt + max_new + 2");
+  PULSAR_REQUIRE(c.draft_len >= 0 && c.draft_len < kMaxBlock, "draft_len must be 0..7");
+  PULSAR_REQUIRE(c.draft_len == 0 || m.n_pulses <= 3, "draft-block mode needs n_pulses <= 3");
+  PULSAR_REQUIRE(c.max_ctx >= c.max_prompt + c.max_new + 2 + c.draft_len,
+                 "max_ctx < max_prompt + max_new + 2 + draft_len");
   PULSAR_REQUIRE(m.rope_len >= c.max_ctx, "rope tables shorter than max_ctx");
   PULSAR_REQUIRE(c.n_stop >= 0 && c.n_stop <= 8, "n_stop must be 0..8");
   return PULSAR_OK;
@@ -205,12 +220,16 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   e->P = m.n_pulses;
   e->V = m.vocab;
   e->B = c.max_batch;
-  e->max_rows = 2 * c.max_batch;
+  e->G = c.draft_len;
+  e->S = c.draft_len > 0 ? c.draft_len + 1 : 2;
+  e->max_rows = e->S * c.max_batch;
   e->R = std::max(e->max_rows, c.max_batch * c.max_prompt);
   e->max_pages = (c.max_ctx + kPage - 1) / kPage;
   // ring capacity: the prompt's last `window` positions stay intact while max_new tokens
-  // (+1 speculative) are appended, so a rewound decode sees the prefill state unchanged
+  // (+ speculative or draft rows, at most kMaxBlock) are appended, so a rewound decode sees
+  // the prefill state unchanged
   e->lcap = (m.window + c.max_new + 2 * kPage - 1) / kPage * kPage;
+  static_assert(kMaxBlock <= kPage, "ring slack holds a draft block");
   // decode splits start at a 64-aligned position at most 63 keys before the first key
   e->max_splits = (c.max_ctx + kPage - 1 + kSplitLen - 1) / kSplitLen;
   e->max_splits_unit = (c.max_ctx + kPage - 1 + kUnitSplit - 1) / kUnitSplit;
@@ -224,11 +243,15 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_CHECK_HIP(hipMemset(x.rows, 0, sizeof(RowDesc) * MR));
   PULSAR_CHECK_HIP(hipMemset(x.last_rows, 0, sizeof(RowDesc) * MR));
   PULSAR_TRY(x.alloc(&x.units, sizeof(AttnUnit) * x.B));
+  PULSAR_TRY(x.alloc(&x.v_rows, sizeof(RowDesc) * x.P * MR));
+  PULSAR_TRY(x.alloc(&x.v_ctl, sizeof(StepCtl) * x.P));
+  PULSAR_TRY(x.alloc(&x.v_units, sizeof(AttnUnit) * x.P * x.B));
   PULSAR_TRY(x.alloc(&x.split_done, 4 * (size_t)x.B * x.Hkv));
   PULSAR_CHECK_HIP(hipMemset(x.split_done, 0, 4 * (size_t)x.B * x.Hkv));
   PULSAR_TRY(x.alloc(&x.state, sizeof(SeqState) * x.B));
   PULSAR_TRY(x.alloc(&x.lrow_seq, 4 * MR));
-  PULSAR_TRY(x.alloc(&x.lrow_extra, 4 * MR));
+  PULSAR_TRY(x.alloc(&x.lrow_extra, 4 * MR * kMaxExtra));
+  PULSAR_TRY(x.alloc(&x.lrow_ctr, 4 * MR));
   PULSAR_TRY(x.alloc(&x.argmax, 4 * MR));
   PULSAR_TRY(x.alloc(&x.draw, 8 * MR));
   PULSAR_TRY(x.alloc(&x.tokens, 4 * (size_t)x.B * std::max(1, c.max_new)));
@@ -254,7 +277,10 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.topk_idx, 4 * R * x.K));
   PULSAR_TRY(x.alloc(&x.topk_w, 4 * R * x.K));
   PULSAR_TRY(x.alloc(&x.keep, 4 * R * x.K));
-  PULSAR_TRY(x.alloc(&x.part, 4 * MR * x.Hkv * x.max_splits * 4 * 66));
+  // split partials: fp32 path per (row, kv head, split, head); bf16 path per (unit, kv
+  // head, split, query column), up to 32 columns per unit (8 rows x 4 heads)
+  PULSAR_TRY(x.alloc(&x.part, 4 * std::max<size_t>(MR * 4, (size_t)x.B * 4 * kMaxBlock) * x.Hkv *
+                                  x.max_splits * 66));
   PULSAR_TRY(x.alloc(&x.lists, 4 * (size_t)x.L * x.E * MR * x.K));
   PULSAR_TRY(x.alloc(&x.list_count, 4 * (size_t)x.L * x.E));
   PULSAR_TRY(x.alloc(&x.p_lists, 4 * (size_t)x.E * R * x.K));
@@ -295,12 +321,14 @@ GemmArgs gemm_base(const Engine& e) {
   return g;
 }
 
-// One pulse pass of every active row + logits + sampling + controller.
+// One pass over a row set (the rows of a step, or of one pulse of a block verify): pulse
+// input, every layer, pulse output and the logits of the rows that need them.
 // Per layer: qkv+gate GEMM, qk-norm/RoPE/KV write, attention (+ split combine), wo GEMM with
 // residual, mlp-norm + router, shared+routed gate/up GEMM, shared+routed down GEMM, MoE
 // combine with residual and the next layer's attn-norm (the first layer's attn-norm is
 // fused into the pulse-input kernel).
-int enqueue_step(Engine& e, hipStream_t s) {
+int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnUnit* units,
+                 hipStream_t s) {
   const PulsarModelDesc& m = e.m;
   const int D = e.D, MR = e.max_rows, dt = e.dtype;
   // at two or more assignments per expert on average, nearly every expert has rows: the
@@ -314,9 +342,10 @@ int enqueue_step(Engine& e, hipStream_t s) {
     prof_span(e, PC_EVENT_PAIR, _a, prof_mark(e, s));
   }
   PulseInputArgs pi{};
-  pi.ctl = e.ctl;
-  pi.rows = e.rows;
+  pi.ctl = ctl;
+  pi.rows = rows;
   pi.D = D;
+  pi.slots = e.S;
   pi.rank = m.reinject_rank;
   pi.eps = m.rms_eps;
   pi.tok_emb = m.tok_emb;
@@ -351,15 +380,15 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.N = e.qkvg;
     g.n_main = e.qkv;
     g.row_mode = ROWS_PULSE;
-    g.ctl = e.ctl;
+    g.ctl = ctl;
     g.C2 = e.gate;
     g.ldc2 = e.H;
     g.bias = m.gate_bias[l];
     g.bias_group_stride = e.H;
     PULSAR_TIMED(PC_QKVG, launch_gemm(g, dt, EPI_QKVG, e.P, MR, s));
     QKPostArgs qa{};
-    qa.ctl = e.ctl;
-    qa.rows = e.rows;
+    qa.ctl = ctl;
+    qa.rows = rows;
     qa.qkv = e.qkvbuf;
     qa.ldq = e.qkv;
     qa.H = e.H;
@@ -378,15 +407,16 @@ int enqueue_step(Engine& e, hipStream_t s) {
     qa.kv = e.kv;
     PULSAR_TIMED(PC_QKPOST, launch_qk_post(qa, dt, MR, s));
     AttnArgs aa{};
-    aa.ctl = e.ctl;
-    aa.rows = e.rows;
+    aa.ctl = ctl;
+    aa.rows = rows;
     aa.qkv = e.qkvbuf;
     aa.ldq = e.qkv;
     aa.gate = e.gate;
     aa.out = e.attn_out;
-    aa.units = e.units;
+    aa.units = units;
     aa.split_done = e.split_done;
     aa.max_units = e.B;
+    aa.unit_rows = e.S;
     aa.part = e.part;
     aa.max_splits = e.max_splits;
     aa.max_splits_unit = e.max_splits_unit;
@@ -409,11 +439,11 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.K = e.H * kHeadDim;
     g.N = D;
     g.row_mode = ROWS_PULSE;
-    g.ctl = e.ctl;
+    g.ctl = ctl;
     PULSAR_TIMED(PC_WO, launch_gemm(g, dt, EPI_RESID, e.P, MR, s));
     RouterArgs ra{};
-    ra.ctl = e.ctl;
-    ra.rows = e.rows;
+    ra.ctl = ctl;
+    ra.rows = rows;
     ra.x = e.h;
     ra.w = m.router[l];
     ra.bias = m.expert_bias[l];
@@ -445,7 +475,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.list_count = ra.list_count;
     g.list_stride = lstride;
     g.a_div = e.K;
-    g.ctl = e.ctl;
+    g.ctl = ctl;
     g.eager_w = eager_experts;
     g.a_rows = MR;
     g.a_rows0 = MR;
@@ -475,7 +505,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
     g.list_count = ra.list_count;
     g.list_stride = lstride;
     g.a_div = 1;
-    g.ctl = e.ctl;
+    g.ctl = ctl;
     if (e.ds == e.de || e.ds == 2 * e.de) {
       g.has_g0 = 1;
       g.K0 = e.ds;
@@ -500,12 +530,12 @@ int enqueue_step(Engine& e, hipStream_t s) {
       gs.K = e.ds;
       gs.N = D;
       gs.row_mode = ROWS_ALL;
-      gs.ctl = e.ctl;
+      gs.ctl = ctl;
       PULSAR_TIMED(PC_SHARED_DOWN, launch_gemm(gs, dt, EPI_STORE, 1, MR, s));
     }
     CombineArgs ca{};
-    ca.ctl = e.ctl;
-    ca.rows = e.rows;
+    ca.ctl = ctl;
+    ca.rows = rows;
     ca.K = e.K;
     ca.D = D;
     ca.shared = e.out_s;
@@ -519,9 +549,10 @@ int enqueue_step(Engine& e, hipStream_t s) {
     PULSAR_TIMED(PC_COMBINE, launch_moe_combine(ca, dt, MR, s));
   }
   PulseOutputArgs po{};
-  po.ctl = e.ctl;
-  po.rows = e.rows;
+  po.ctl = ctl;
+  po.rows = rows;
   po.D = D;
+  po.slots = e.S;
   po.eps = m.rms_eps;
   po.h_in = e.h_in;
   po.h = e.h;
@@ -540,14 +571,24 @@ int enqueue_step(Engine& e, hipStream_t s) {
   g.K = D;
   g.N = e.V;
   g.row_mode = ROWS_LOGITS;
-  g.ctl = e.ctl;
+  g.ctl = ctl;
   g.softcap = m.softcap;
   PULSAR_TIMED(PC_LMHEAD, launch_gemm(g, dt, EPI_LOGITS, 1, MR, s));
+  return PULSAR_OK;
+}
+
+// One step: a pass over the step's rows, sampling of its logits rows and the controller,
+// which lays out the next step.
+int enqueue_step(Engine& e, hipStream_t s) {
+  PULSAR_TRY(enqueue_pass(e, e.ctl, e.rows, e.units, s));
   SampleArgs sa{};
   sa.ctl = e.ctl;
   sa.logits = e.logits;
   sa.lrow_seq = e.lrow_seq;
   sa.lrow_extra = e.lrow_extra;
+  sa.extra_stride = e.G > 0 ? kMaxExtra : 1;
+  sa.n_extra = sa.extra_stride;
+  sa.lrow_ctr = e.G > 0 ? e.lrow_ctr : nullptr;
   sa.seen = e.seen;
   sa.state = e.state;
   sa.V = e.V;
@@ -558,7 +599,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   sa.seed = e.d_seed;
   sa.out_argmax = e.argmax;
   sa.out_draw = e.draw;
-  PULSAR_TIMED(PC_SAMPLE, launch_sample(sa, dt, MR, s));
+  PULSAR_TIMED(PC_SAMPLE, launch_sample(sa, e.dtype, e.max_rows, s));
   PULSAR_TRY(prof_delay(e, s));
   const int _pc = prof_mark(e, s);
   ControllerArgs co{};
@@ -570,6 +611,8 @@ int enqueue_step(Engine& e, hipStream_t s) {
   co.units = e.units;
   co.lrow_seq = e.lrow_seq;
   co.lrow_extra = e.lrow_extra;
+  co.lrow_ctr = e.lrow_ctr;
+  co.draft_len = e.G;
   co.seen = e.seen;
   co.out_tokens = e.tokens;
   co.argmax = e.argmax;
@@ -603,6 +646,8 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   sa.logits = e.plogits;
   sa.lrow_seq = e.lrow_seq;
   sa.lrow_extra = e.lrow_extra;
+  sa.extra_stride = 1;
+  sa.n_extra = 0;
   sa.seen = e.seen;
   sa.state = e.state;
   sa.V = e.V;
@@ -627,6 +672,8 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   co.units = e.units;
   co.lrow_seq = e.lrow_seq;
   co.lrow_extra = e.lrow_extra;
+  co.lrow_ctr = e.lrow_ctr;
+  co.draft_len = e.G;
   co.seen = e.seen;
   co.out_tokens = e.tokens;
   co.argmax = e.argmax;
@@ -927,6 +974,133 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   PULSAR_TRY(first_token(e, e.cfg.seed, s));
   PULSAR_CHECK_HIP(hipStreamSynchronize(s));
   e.prefilled = true;
+  e.kv_ready = true;
+  return PULSAR_OK;
+}
+
+// Synthetic cache contents: every key and value element of every layer ~ N(0, 1), from a
+// counter-based generator (SplitMix64 finaliser of (seed, layer, K/V, element), Box-Muller).
+__host__ __device__ __forceinline__ uint64_t fill_mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) fill_normal_kernel(T* p, int64_t n, uint64_t seed) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint64_t h = fill_mix64(seed + 0x9E3779B97F4A7C15ull * (uint64_t)(i + 1));
+    const float u1 = (float)((h >> 40) + 1) * (1.0f / 16777216.0f);  // (0, 1]
+    const float u2 = (float)((h >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    p[i] = from_f<T>(sqrtf(-2.0f * logf(u1)) * cosf(6.28318530718f * u2));
+  }
+}
+
+int fill_kv(Engine& e, int ctx, uint64_t seed, hipStream_t s) {
+  PULSAR_REQUIRE(ctx >= 1 && ctx + 1 <= e.cfg.max_ctx, "engine_fill_kv: 1 <= ctx < max_ctx");
+  const size_t local_elems = (size_t)e.B * e.Hkv * e.lcap * kHeadDim;
+  const size_t global_elems = (size_t)e.B * e.max_pages * e.Hkv * kPage * kHeadDim;
+  for (int l = 0; l < e.L; ++l) {
+    const bool loc = (e.m.local_mask >> l) & 1u;
+    const int64_t n = (int64_t)(loc ? local_elems : global_elems);
+    for (int kvi = 0; kvi < 2; ++kvi) {
+      void* p = kvi == 0 ? e.kv.k[l] : e.kv.v[l];
+      const uint64_t sd = fill_mix64(seed ^ (uint64_t)(2 * l + kvi + 1));
+      const unsigned grid = (unsigned)std::min<int64_t>(8192, (n + 255) / 256);
+      if (e.dtype == PULSAR_BF16)
+        fill_normal_kernel<bf16><<<grid, 256, 0, s>>>(reinterpret_cast<bf16*>(p), n, sd);
+      else
+        fill_normal_kernel<float><<<grid, 256, 0, s>>>(reinterpret_cast<float*>(p), n, sd);
+      PULSAR_LAUNCH_CHECK();
+    }
+  }
+  PULSAR_CHECK_HIP(hipStreamSynchronize(s));
+  e.prompt_len = ctx;
+  e.kv_ready = true;
+  e.prefilled = false;  // no prefill logits: decoding needs a prefill
+  return PULSAR_OK;
+}
+
+// Block verify (draft-block mode's verify, and the verify microbenchmark): n tokens per
+// sequence at positions prompt_len .. prompt_len + n - 1 run every pulse, pulse k as one
+// pass over the B*n rows (row b*n + i = token i of sequence b, state slot i); a row
+// attends the cache and the block's pulse-k keys at positions <= its own. The last pass
+// computes logits for every row (readable as the step logits, row b*n + i). The
+// controller state is not touched; the keys/values of the block positions are
+// overwritten. host_tokens == nullptr re-runs the last uploaded block.
+int verify(Engine& e, const int32_t* host_tokens, int n, int use_graph, hipStream_t s) {
+  PULSAR_REQUIRE(e.kv_ready, "engine_verify: prefill or fill_kv first");
+  const int P = e.P, B = e.B, MR = e.max_rows;
+  if (host_tokens) {
+    PULSAR_REQUIRE(n >= 1 && n <= e.S,
+                   "engine_verify: 1 <= n <= rows per sequence (draft_len + 1, or 2)");
+    PULSAR_REQUIRE(e.prompt_len + n <= e.cfg.max_ctx, "engine_verify: block past max_ctx");
+    for (int i = 0; i < B * n; ++i)
+      PULSAR_REQUIRE(host_tokens[i] >= 0 && host_tokens[i] < e.V,
+                     "engine_verify: token id out of vocabulary");
+    const int pos = e.prompt_len, BN = B * n;
+    std::vector<RowDesc> rows((size_t)P * MR, RowDesc{0, 0, 0, 0, 0, -1, -1, 0});
+    std::vector<StepCtl> ctls(P);
+    std::vector<AttnUnit> units((size_t)P * B);
+    for (int k = 0; k < P; ++k) {
+      for (int b = 0; b < B; ++b) {
+        AttnUnit un{};
+        un.seq = b;
+        un.n = n;
+        un.pos0 = pos;
+        for (int i = 0; i < kMaxBlock; ++i) un.row[i] = i < n ? b * n + i : -1;
+        for (int i = 0; i < n; ++i) {
+          const int r = b * n + i;
+          rows[(size_t)k * MR + r] =
+              RowDesc{b, i, k, pos + i, host_tokens[r], k == P - 1 ? r : -1, -1, 0};
+        }
+        units[(size_t)k * B + b] = un;
+      }
+      StepCtl c{};
+      c.n_rows = BN;
+      c.n_lrows = k == P - 1 ? BN : 0;
+      c.pulse_start[k] = 0;
+      c.pulse_count[k] = BN;
+      c.n_units = B;
+      c.active = B;
+      ctls[k] = c;
+    }
+    PULSAR_CHECK_HIP(hipMemcpyAsync(e.v_rows, rows.data(), sizeof(RowDesc) * rows.size(),
+                                    hipMemcpyHostToDevice, s));
+    PULSAR_CHECK_HIP(hipMemcpyAsync(e.v_ctl, ctls.data(), sizeof(StepCtl) * P,
+                                    hipMemcpyHostToDevice, s));
+    PULSAR_CHECK_HIP(hipMemcpyAsync(e.v_units, units.data(), sizeof(AttnUnit) * units.size(),
+                                    hipMemcpyHostToDevice, s));
+    // the host vectors must outlive the copies
+    PULSAR_CHECK_HIP(hipStreamSynchronize(s));
+  }
+  auto passes = [&](hipStream_t st) -> int {
+    for (int k = 0; k < P; ++k)
+      PULSAR_TRY(enqueue_pass(e, e.v_ctl + k, e.v_rows + (size_t)k * MR, e.v_units + (size_t)k * B,
+                              st));
+    return PULSAR_OK;
+  };
+  if (!use_graph || e.prof_on) {
+    PULSAR_TRY(passes(s));
+    return prof_collect(e, s);
+  }
+  if (!e.vexec) {
+    hipStream_t cs = e.capture_stream;
+    PULSAR_CHECK_HIP(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
+    const int rc = passes(cs);
+    hipGraph_t gr = nullptr;
+    const hipError_t ce = hipStreamEndCapture(cs, &gr);
+    if (rc != PULSAR_OK) {
+      if (gr) hipGraphDestroy(gr);
+      return rc;
+    }
+    if (ce != hipSuccess)
+      return fail(PULSAR_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce));
+    e.vgraph = gr;
+    PULSAR_CHECK_HIP(hipGraphInstantiate(&e.vexec, gr, nullptr, nullptr, 0));
+  }
+  PULSAR_CHECK_HIP(hipGraphLaunch(e.vexec, s));
   return PULSAR_OK;
 }
 
@@ -1011,6 +1185,17 @@ int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
   }
   if (steps_run) *steps_run = done;
   return PULSAR_OK;
+}
+
+int pulsar_engine_verify(void* handle, const int32_t* host_tokens, int32_t n, int32_t use_graph,
+                         hipStream_t stream) {
+  PULSAR_REQUIRE(handle, "engine_verify: null handle");
+  return verify(*reinterpret_cast<Engine*>(handle), host_tokens, n, use_graph, stream);
+}
+
+int pulsar_engine_fill_kv(void* handle, int32_t ctx, uint64_t seed, hipStream_t stream) {
+  PULSAR_REQUIRE(handle, "engine_fill_kv: null handle");
+  return fill_kv(*reinterpret_cast<Engine*>(handle), ctx, seed, stream);
 }
 
 int pulsar_engine_rewind(void* handle, uint64_t seed, hipStream_t stream) {

@@ -80,6 +80,7 @@ struct PulseInputArgs {
   const StepCtl* ctl;
   const RowDesc* rows;
   int D, rank, prefill, prefill_T;
+  int slots;                // token-state slots per sequence (decode state = seq*slots+slot)
   float eps;
   const void* tok_emb;
   const float* anchor_norm;
@@ -142,6 +143,7 @@ struct AttnArgs {
   int max_splits;       // split partial slots per (unit or row, kv head)
   int max_splits_unit;  // bf16 path: splits of kUnitSplit keys
   int max_units;
+  int unit_rows;        // bf16 path: most rows a unit of this launch holds (1..kMaxBlock)
   int H, Hkv, layer, is_local, window, prefill_T;
   float scale;
   KVDesc kv;
@@ -183,6 +185,7 @@ struct PulseOutputArgs {
   const StepCtl* ctl;
   const RowDesc* rows;
   int D, prefill, prefill_T;
+  int slots;                // token-state slots per sequence
   float eps;
   const void* h_in;
   const void* h;

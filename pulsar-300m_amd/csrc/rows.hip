@@ -67,7 +67,7 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
   if (r >= a.ctl->n_rows) return;
   const RowDesc rd = a.rows[r];
   const int D = a.D, i0 = lane * EPL;
-  const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * 2 + rd.slot;
+  const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * a.slots + rd.slot;
   T* e = reinterpret_cast<T*>(a.e_state) + (int64_t)st * D;
   const T* step = reinterpret_cast<const T*>(a.step_emb) + (int64_t)rd.pulse * D;
   float hv[EPL], stp[EPL];
@@ -510,67 +510,80 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
 
 // ---------------------------------------------------------------------------
 // Decode attention on the matrix cores (bf16 caches): shared types and the unit key range.
-// A unit is the rows of one sequence in a step (the current token, and the speculative
-// token one position later when present); they read each key block of the cache once.
+// A unit is the rows of one sequence in a step, at consecutive positions pos0 + i (the
+// current token and the speculative token one position later, or the rows of a draft
+// block); they read each key block of the cache once. Row i sees keys
+// [lo(pos0 + i), pos0 + i]: row 0 has the lowest bound, the last row the highest key.
 // ---------------------------------------------------------------------------
 typedef __bf16 attn_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float attn_f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void unit_range(const AttnArgs& a, const AttnUnit& un, int& lo_a,
-                                           int& lo_b, int& base, int& uhi) {
-  const bool two = un.row_b >= 0;
-  lo_a = a.is_local ? max(0, un.pos_a - a.window + 1) : 0;
-  lo_b = two ? (a.is_local ? max(0, un.pos_b - a.window + 1) : 0) : lo_a;
-  uhi = two ? max(un.pos_a, un.pos_b) : un.pos_a;
-  base = min(lo_a, lo_b) & ~63;
+__device__ __forceinline__ void unit_range(const AttnArgs& a, const AttnUnit& un, int& base,
+                                           int& uhi) {
+  const int lo0 = a.is_local ? max(0, un.pos0 - a.window + 1) : 0;
+  uhi = un.pos0 + un.n - 1;
+  base = lo0 & ~63;
+}
+
+// Row of unit row z (z < NZ), -1 past the unit's rows: a select chain, so the unit stays
+// in registers (no indexed register access).
+template <int NZ>
+__device__ __forceinline__ int unit_row(const AttnUnit& un, int z) {
+  int row = -1;
+#pragma unroll
+  for (int i = 0; i < NZ; ++i)
+    if (z == i) row = un.row[i];
+  return z < un.n ? row : -1;
 }
 
 // Last split block of (unit u, kv head g): merge the split partials (device-coherent loads),
-// normalise, round as the SDPA output and apply the head gate. Threads 0-255:
-// thread -> row of the unit (z), head of the group, two dims.
+// normalise, round as the SDPA output and apply the head gate. Query column c = 4 z + h
+// (unit row z, head h of the group); a thread takes two dims of one column at a time.
 constexpr int kMergeChunk = 8;  // split partials loaded per round trip
+template <int COLS>
 __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int g,
                                                   const AttnUnit& un, int nsplit) {
-  if (threadIdx.x >= 256) return;
-  const int z = threadIdx.x >> 7, h = (threadIdx.x >> 5) & 3, e0 = (threadIdx.x & 31) * 2;
-  const int row = z == 0 ? un.row_a : un.row_b;
-  if (row < 0) return;
-  const float* p0 = a.part + (((int64_t)u * a.Hkv + g) * a.max_splits * 8 + z * 4 + h) * 66;
-  float Mx = -INFINITY, Ls = 0.f, Oa = 0.f, Ob = 0.f;
-  for (int c0 = 0; c0 < nsplit; c0 += kMergeChunk) {
-    float pm[kMergeChunk], pl[kMergeChunk], pa[kMergeChunk], pb[kMergeChunk];
+  for (int t = threadIdx.x; t < COLS * 32; t += blockDim.x) {
+    const int c = t >> 5, e0 = (t & 31) * 2;
+    const int row = unit_row<COLS / 4>(un, c >> 2);
+    if (row < 0) continue;
+    const float* p0 = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits) * COLS + c) * 66;
+    float Mx = -INFINITY, Ls = 0.f, Oa = 0.f, Ob = 0.f;
+    for (int c0 = 0; c0 < nsplit; c0 += kMergeChunk) {
+      float pm[kMergeChunk], pl[kMergeChunk], pa[kMergeChunk], pb[kMergeChunk];
 #pragma unroll
-    for (int k = 0; k < kMergeChunk; ++k) {
-      const float* p = p0 + (int64_t)min(c0 + k, nsplit - 1) * 8 * 66;
-      pm[k] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      pl[k] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      pa[k] = __hip_atomic_load(p + 2 + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      pb[k] = __hip_atomic_load(p + 3 + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    float cm = Mx;
-#pragma unroll
-    for (int k = 0; k < kMergeChunk; ++k)
-      if (c0 + k < nsplit) cm = fmaxf(cm, pm[k]);
-    const float f0 = Mx == -INFINITY ? 0.f : expf(Mx - cm);
-    Ls *= f0;
-    Oa *= f0;
-    Ob *= f0;
-#pragma unroll
-    for (int k = 0; k < kMergeChunk; ++k) {
-      if (c0 + k < nsplit && pm[k] != -INFINITY) {
-        const float f = expf(pm[k] - cm);
-        Ls += pl[k] * f;
-        Oa += pa[k] * f;
-        Ob += pb[k] * f;
+      for (int k = 0; k < kMergeChunk; ++k) {
+        const float* p = p0 + (int64_t)min(c0 + k, nsplit - 1) * COLS * 66;
+        pm[k] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pl[k] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pa[k] = __hip_atomic_load(p + 2 + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pb[k] = __hip_atomic_load(p + 3 + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+      float cm = Mx;
+#pragma unroll
+      for (int k = 0; k < kMergeChunk; ++k)
+        if (c0 + k < nsplit) cm = fmaxf(cm, pm[k]);
+      const float f0 = Mx == -INFINITY ? 0.f : expf(Mx - cm);
+      Ls *= f0;
+      Oa *= f0;
+      Ob *= f0;
+#pragma unroll
+      for (int k = 0; k < kMergeChunk; ++k) {
+        if (c0 + k < nsplit && pm[k] != -INFINITY) {
+          const float f = expf(pm[k] - cm);
+          Ls += pl[k] * f;
+          Oa += pa[k] * f;
+          Ob += pb[k] * f;
+        }
+      }
+      Mx = cm;
     }
-    Mx = cm;
+    const int head = g * 4 + (c & 3);
+    const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
+    bf16* dst = reinterpret_cast<bf16*>(a.out) + (int64_t)row * a.H * 64 + head * 64 + e0;
+    dst[0] = f2bf(rnd<bf16>(Oa / Ls) * gate);
+    dst[1] = f2bf(rnd<bf16>(Ob / Ls) * gate);
   }
-  const int head = g * 4 + h;
-  const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
-  bf16* dst = reinterpret_cast<bf16*>(a.out) + (int64_t)row * a.H * 64 + head * 64 + e0;
-  dst[0] = f2bf(rnd<bf16>(Oa / Ls) * gate);
-  dst[1] = f2bf(rnd<bf16>(Ob / Ls) * gate);
 }
 
 // ---------------------------------------------------------------------------
@@ -578,48 +591,60 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
 // waves stride over the split's 64-key blocks, each keeping an online softmax over its
 // blocks; the waves merge in LDS, and only a unit whose keys span several splits goes
 // through the split partials. Products are formed transposed, as in the prefill kernel:
-// S^T = K Q^T (A = 16 keys x 32 dims of the position-major K block, B = the 8 query rows
-// of the unit: 4 heads x rows a, b), so P^T stays in registers for O^T = V^T P^T, whose
-// A operand takes two 8-byte runs of the dimension-major V block. P = exp(S - max) in fp32
-// is split into bf16 hi + lo (hi + lo = P to 2^-16 relative), two products each. The last
-// split block to count in merges the split partials, normalises, rounds as the SDPA
-// output and applies the head gate.
+// S^T = K Q^T (A = 16 keys x 32 dims of the position-major K block, B = 16 query columns:
+// column c = 4 z + h is head h of unit row z; COLS columns in COLS/16 tiles), so P^T stays
+// in registers for O^T = V^T P^T, whose A operand takes two 8-byte runs of the
+// dimension-major V block. P = exp(S - max) in fp32 is split into bf16 hi + lo (hi + lo =
+// P to 2^-16 relative), two products each. The last split block to count in merges the
+// split partials, normalises, rounds as the SDPA output and applies the head gate.
+// COLS = 8 serves units of up to 2 rows (exact mode), 16 up to 4, 32 up to 8.
 // ---------------------------------------------------------------------------
 typedef __bf16 attn_bf16x4 __attribute__((ext_vector_type(4)));
 
+template <int COLS>
 __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnArgs a) {
-  __shared__ float wm[kUnitWaves][8], wl[kUnitWaves][8];
-  __shared__ float wo[kUnitWaves][8][65];
+  constexpr int NQT = (COLS + 15) / 16;
+  constexpr int NZ = COLS / 4;
+  __shared__ float wm[kUnitWaves][COLS], wl[kUnitWaves][COLS];
+  __shared__ float wo[kUnitWaves][COLS][65];
   const int u = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
   if (u >= a.ctl->n_units) return;
   const AttnUnit un = a.units[u];
-  int lo_a, lo_b, base, uhi;
-  unit_range(a, un, lo_a, lo_b, base, uhi);
+  int base, uhi;
+  unit_range(a, un, base, uhi);
   const int nsplit = (uhi + 1 - base + kUnitSplit - 1) / kUnitSplit;
   if (s >= nsplit) return;
-  const bool two = un.row_b >= 0;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m16 = lane & 15, kq = lane >> 4;
-  // query column m16: heads 0-3 of row a, heads 0-3 of row b, then unused
-  const int qrow = m16 < 4 ? un.row_a : ((m16 < 8 && two) ? un.row_b : -1);
-  const int qlo = m16 < 4 ? lo_a : lo_b, qhi = qrow < 0 ? -1 : (m16 < 4 ? un.pos_a : un.pos_b);
   const attn_bf16x8 zero = {};
-  attn_bf16x8 qb[2];
-  {
+  int qlo[NQT], qhi[NQT];
+  attn_bf16x8 qb[NQT][2];
+#pragma unroll
+  for (int t = 0; t < NQT; ++t) {
+    const int c = t * 16 + m16, z = c >> 2;
+    const int qrow = c < COLS ? unit_row<NZ>(un, z) : -1;
+    const int qpos = un.pos0 + z;
+    qlo[t] = a.is_local ? max(0, qpos - a.window + 1) : 0;
+    qhi[t] = qrow < 0 ? -1 : qpos;
     const bf16* qp = reinterpret_cast<const bf16*>(a.qkv) + (int64_t)(qrow < 0 ? 0 : qrow) * a.ldq +
-                     (g * 4 + (m16 & 3)) * 64 + kq * 8;
+                     (g * 4 + (c & 3)) * 64 + kq * 8;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      qb[ks] = qrow >= 0 ? *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32) : zero;
+      qb[t][ks] = qrow >= 0 ? *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32) : zero;
   }
   const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]);
   const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]);
   const int s_lo = base + s * kUnitSplit;
   const int s_hi = min(uhi, s_lo + kUnitSplit - 1);
-  float mrun = -INFINITY, lrun = 0.f;
-  attn_f32x4 o[4];
+  float mrun[NQT], lrun[NQT];
+  attn_f32x4 o[NQT][4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) o[mt] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NQT; ++t) {
+    mrun[t] = -INFINITY;
+    lrun[t] = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[t][mt] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   for (int kb = s_lo + wv * 64; kb <= s_hi; kb += kUnitWaves * 64) {
     const KVBlock blk = kv_block(a.kv, a.layer, un.seq, g, kb);
     attn_bf16x8 kk[4][2];
@@ -638,71 +663,81 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
         vl[mt][s2] = *reinterpret_cast<const attn_bf16x4*>(vp);
         vh[mt][s2] = *reinterpret_cast<const attn_bf16x4*>(vp + 16);
       }
-    attn_f32x4 sv[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][0], qb[0], acc, 0, 0, 0);
-      sv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][1], qb[1], acc, 0, 0, 0);
+    for (int t = 0; t < NQT; ++t) {
+      attn_f32x4 sv[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][0], qb[t][0], acc, 0, 0, 0);
+        sv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][1], qb[t][1], acc, 0, 0, 0);
+      }
+      // lane holds keys kb + 16 kt + 4 kq + j of query column 16 t + m16
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = kb + kt * 16 + kq * 4 + j;
+          const float v = (key >= qlo[t] && key <= qhi[t]) ? sv[kt][j] * a.scale : -INFINITY;
+          sv[kt][j] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, swz_xor16(mx));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(mrun[t], mx);
+      const float muse = mnew == -INFINITY ? 0.f : mnew;
+      const float f = mrun[t] == -INFINITY ? 0.f : expf(mrun[t] - muse);
+      mrun[t] = mnew;
+      lrun[t] *= f;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) o[t][mt] *= f;
+      attn_bf16x8 ph[2], pl[2];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p = sv[kt][j] == -INFINITY ? 0.f : expf(sv[kt][j] - muse);
+          lrun[t] += p;
+          const __bf16 hi = (__bf16)p;
+          ph[kt >> 1][(kt & 1) * 4 + j] = hi;
+          pl[kt >> 1][(kt & 1) * 4 + j] = (__bf16)(p - (float)hi);
+        }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const attn_bf16x8 av = __builtin_shufflevector(vl[mt][s2], vh[mt][s2], 0, 1, 2, 3, 4, 5, 6, 7);
+          o[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ph[s2], o[t][mt], 0, 0, 0);
+          o[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pl[s2], o[t][mt], 0, 0, 0);
+        }
     }
-    // lane holds keys kb + 16 kt + 4 kq + j of query column m16
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = kb + kt * 16 + kq * 4 + j;
-        const float v = (key >= qlo && key <= qhi) ? sv[kt][j] * a.scale : -INFINITY;
-        sv[kt][j] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, swz_xor16(mx));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(mrun, mx);
-    const float muse = mnew == -INFINITY ? 0.f : mnew;
-    const float f = mrun == -INFINITY ? 0.f : expf(mrun - muse);
-    mrun = mnew;
-    lrun *= f;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) o[mt] *= f;
-    attn_bf16x8 ph[2], pl[2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p = sv[kt][j] == -INFINITY ? 0.f : expf(sv[kt][j] - muse);
-        lrun += p;
-        const __bf16 hi = (__bf16)p;
-        ph[kt >> 1][(kt & 1) * 4 + j] = hi;
-        pl[kt >> 1][(kt & 1) * 4 + j] = (__bf16)(p - (float)hi);
-      }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const attn_bf16x8 av = __builtin_shufflevector(vl[mt][s2], vh[mt][s2], 0, 1, 2, 3, 4, 5, 6, 7);
-        o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ph[s2], o[mt], 0, 0, 0);
-        o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pl[s2], o[mt], 0, 0, 0);
-      }
   }
-  lrun += swz_xor16(lrun);
-  lrun += __shfl_xor(lrun, 32, 64);
-  // wave partials: query column m16 < 8; lane holds dims 16 mt + 4 kq + j
-  if (m16 < 8) {
-    if (kq == 0) {
-      wm[wv][m16] = mrun;
-      wl[wv][m16] = lrun;
+  // wave partials: query column 16 t + m16 < COLS; lane holds dims 16 mt + 4 kq + j
+#pragma unroll
+  for (int t = 0; t < NQT; ++t) {
+    float lr = lrun[t];
+    lr += swz_xor16(lr);
+    lr += __shfl_xor(lr, 32, 64);
+    const int c = t * 16 + m16;
+    if (c < COLS) {
+      if (kq == 0) {
+        wm[wv][c] = mrun[t];
+        wl[wv][c] = lr;
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wo[wv][c][mt * 16 + kq * 4 + j] = o[t][mt][j];
     }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) wo[wv][m16][mt * 16 + kq * 4 + j] = o[mt][j];
   }
   __syncthreads();
-  // merge the waves: element t -> query column hr (0-7), dim d; the block's threads cover
-  // the 8 x 64 elements whatever its size
-  for (int t = threadIdx.x; t < 8 * 64; t += blockDim.x) {
+  // merge the waves: element t -> query column hr, dim d; the block's threads cover the
+  // COLS x 64 elements whatever its size
+  for (int t = threadIdx.x; t < COLS * 64; t += blockDim.x) {
     const int hr = t >> 6, d = t & 63;
+    const int row = unit_row<NZ>(un, hr >> 2);
+    if (row < 0) continue;
     float M = -INFINITY, L = 0.f, O = 0.f;
 #pragma unroll
     for (int w = 0; w < kUnitWaves; ++w) M = fmaxf(M, wm[w][hr]);
@@ -716,16 +751,13 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
       }
     }
     if (nsplit == 1) {
-      const int z = hr >> 2, h = hr & 3;
-      const int row = z == 0 ? un.row_a : un.row_b;
-      if (row < 0) continue;
-      const int head = g * 4 + h;
+      const int head = g * 4 + (hr & 3);
       const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
       reinterpret_cast<bf16*>(a.out)[(int64_t)row * a.H * 64 + head * 64 + d] =
           f2bf(rnd<bf16>(O / L) * gate);
     } else {
       // several splits: device-coherent partials; the last block to count in merges
-      float* out = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits + s) * 8 + hr) * 66;
+      float* out = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits + s) * COLS + hr) * 66;
       __hip_atomic_store(out + 2 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (d == 0) {
         __hip_atomic_store(out, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -745,7 +777,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   }
   __syncthreads();
   if (!s_last) return;
-  attn_merge_splits(a, u, g, un, nsplit);
+  attn_merge_splits<COLS>(a, u, g, un, nsplit);
 }
 
 // ---------------------------------------------------------------------------
@@ -1411,7 +1443,7 @@ __global__ void __launch_bounds__(256) pulse_output_kernel(PulseOutputArgs a) {
   if (r >= a.ctl->n_rows) return;
   const RowDesc rd = a.rows[r];
   const int D = a.D;
-  const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * 2 + rd.slot;
+  const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * a.slots + rd.slot;
   const T* hi = reinterpret_cast<const T*>(a.h_in) + (int64_t)r * D;
   const T* h = reinterpret_cast<const T*>(a.h) + (int64_t)r * D;
   const T* rs = reinterpret_cast<const T*>(a.res_scale) + (int64_t)rd.pulse * D;
@@ -1485,7 +1517,15 @@ int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s) 
 }
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s) {
   if (dtype == PULSAR_BF16) {
-    attn_decode_unit_kernel<<<dim3(a.max_units, a.Hkv, a.max_splits_unit), 64 * kUnitWaves, 0, s>>>(a);
+    const dim3 grid(a.max_units, a.Hkv, a.max_splits_unit);
+    if (a.unit_rows <= 2)
+      attn_decode_unit_kernel<8><<<grid, 64 * kUnitWaves, 0, s>>>(a);
+    else if (a.unit_rows <= 4)
+      attn_decode_unit_kernel<16><<<grid, 64 * kUnitWaves, 0, s>>>(a);
+    else if (a.unit_rows <= kMaxBlock)
+      attn_decode_unit_kernel<32><<<grid, 64 * kUnitWaves, 0, s>>>(a);
+    else
+      return fail(PULSAR_ERR_UNSUPPORTED, "decode attention: at most 8 rows per unit");
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   }

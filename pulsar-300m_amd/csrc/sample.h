@@ -8,6 +8,8 @@ namespace pulsar {
 constexpr int KIND_TESTED = 0;  // token drawn at the top of the reference loop (gets a draft test)
 constexpr int KIND_PLAIN = 1;   // accepted draft (its successor is a plain draw)
 
+constexpr int kMaxExtra = kMaxBlock;  // extra seen tokens per logits row (draft-block mode)
+
 // Per-sequence decode state, owned by the controller.
 struct SeqState {
   int32_t done, produced, max_new;
@@ -17,13 +19,20 @@ struct SeqState {
   int32_t row_c, row_s, lrow_c, lrow_s;
   uint32_t ctr;
   int32_t pad[2];
+  // draft-block mode: block tokens (blk[0] = the round's emitted token at position c_pos),
+  // tokens known, phase (0 draft, 1 verify), step within the phase (draft index or verify
+  // pulse), drafts wanted this round
+  int32_t blk_n, blk_phase, blk_step, blk_g;
+  int32_t blk[kMaxBlock];
 };
 
 struct SampleArgs {
   const StepCtl* ctl;
   const float* logits;  // [lrows][V]
   const int32_t* lrow_seq;
-  const int32_t* lrow_extra;
+  const int32_t* lrow_extra;  // [lrows][extra_stride], first n_extra entries read (-1: none)
+  int extra_stride, n_extra;
+  const uint32_t* lrow_ctr;   // per logits row draw counter (nullable: state ctr scheme)
   const uint32_t* seen;  // [B][V/32]
   const SeqState* state;
   int V, greedy;
@@ -42,13 +51,15 @@ struct ControllerArgs {
   RowDesc* rows;
   AttnUnit* units;      // decode attention units of the next step
   int32_t* lrow_seq;
-  int32_t* lrow_extra;
+  int32_t* lrow_extra;  // [lrows][kMaxExtra] in draft-block mode, [lrows] otherwise
+  uint32_t* lrow_ctr;   // draft-block mode: per logits row draw counter
   uint32_t* seen;
   int32_t* out_tokens;  // [B][max_new]
   const int32_t* argmax;
   const int32_t* draw;
   const int32_t* stop_ids;
   int n_stop, B, V, n_pulses, max_new, speculative, all_logits, init, prompt_len;
+  int draft_len;        // > 0: draft-block mode with up to draft_len drafts per round
 };
 
 int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s);

@@ -107,10 +107,20 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
     if (threadIdx.x < 3) (threadIdx.x == 0 ? a.out_argmax[lr] : a.out_draw[lr * 2 + threadIdx.x - 1]) = -1;
     return;
   }
-  const int extra = a.lrow_extra[lr];
   const float* lg = a.logits + (int64_t)lr * a.V;
   const uint32_t* seen = a.seen + (int64_t)seq * (a.V / 32);
   const int base = threadIdx.x * PER;
+  // tokens counted as seen for this row beyond the sequence's bitmap, as a mask over this
+  // thread's PER logits
+  uint64_t xmask = 0;
+  bool has_extra = false;
+  for (int x = 0; x < a.n_extra; ++x) {
+    const int t = a.lrow_extra[(int64_t)lr * a.extra_stride + x];
+    if (t < 0) continue;
+    has_extra = true;
+    const int off = t - base;
+    if (off >= 0 && off < PER) xmask |= 1ull << off;
+  }
   float l[PER];
 #pragma unroll
   for (int i = 0; i < PER; i += 4) {
@@ -124,7 +134,7 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int idx = base + i;
-      const bool s = ((seen[idx >> 5] >> (idx & 31)) & 1u) || idx == extra;
+      const bool s = ((seen[idx >> 5] >> (idx & 31)) & 1u) || ((xmask >> i) & 1u);
       if (s) l[i] = l[i] > 0.f ? rnd<T>(l[i] / a.rep_penalty) : rnd<T>(l[i] * a.rep_penalty);
     }
   }
@@ -214,8 +224,9 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
   __shared__ int pick[2];
   if (threadIdx.x < 2) pick[threadIdx.x] = (int)lk.v;
   __syncthreads();
-  // stream: step counter of the sequence, and whether this is the speculative row
-  const uint32_t ctr = a.state[seq].ctr * 2u + (extra >= 0 ? 1u : 0u);
+  // stream: the row's own counter (draft-block mode), else the step counter of the
+  // sequence and whether this is the speculative row
+  const uint32_t ctr = a.lrow_ctr ? a.lrow_ctr[lr] : a.state[seq].ctr * 2u + (has_extra ? 1u : 0u);
   for (int d = 0; d < 2; ++d) {
     const float target = uniform01(*a.seed, seq, ctr, d) * total;
     if (own > 0.f && target >= pre && target < pre + own) {
@@ -441,7 +452,181 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
     }
     a.rows[idx] = RowDesc{b, s.c_slot, p, s.c_pos, s.c_tok, s.lrow_c, -1, 0};
     s.row_c = idx;
-    a.units[v[4]] = AttnUnit{b, idx, s.row_s, s.c_pos, srow ? s.c_pos + 1 : -1, {0, 0, 0}};
+    AttnUnit un{};
+    un.seq = b;
+    un.n = srow ? 2 : 1;
+    un.pos0 = s.c_pos;
+    un.row[0] = idx;
+    un.row[1] = s.row_s;
+    for (int i = 2; i < kMaxBlock; ++i) un.row[i] = -1;
+    a.units[v[4]] = un;
+  }
+  if (act) a.state[b] = s;
+  if (b == 0) {
+    for (int p = 0; p < 4; ++p) {
+      ctl->pulse_start[p] = p < 3 ? base[p] : total[0] + total[1] + total[2];
+      ctl->pulse_count[p] = p < 3 ? total[p] : 0;
+    }
+    ctl->n_rows = total[0] + total[1] + total[2];
+    ctl->n_lrows = total[3];
+    ctl->n_units = total[4];
+    ctl->active = total[4];
+    ctl->step += 1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Draft-block controller (draft_len > 0). A round starts from an emitted token t = blk[0]
+// at position c_pos. Draft steps run pulse 0 of block row j alone (slot j, position
+// c_pos + j) and draw blk[j + 1] from its logits (a stop id ends the block); verify steps
+// run pulse k of every block row; after the last pulse, the draft of row i + 1 is accepted
+// iff it equals draw 0 of row i and is not a stop id. The first rejection (row i) emits
+// draw 1 of row i (an independent draw from the same logits); a block without rejection
+// emits draw 0 of its last row. Accepted rows keep the last pulse's keys/values at their
+// positions; the next round starts one position after the last accepted row. A logits row
+// counts block tokens 1..i of its row i as seen. Matches the oracle's
+// block_speculative_ids.
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ void new_round(const ControllerArgs& a, SeqState& s, int tok) {
+  s.blk[0] = tok;
+  for (int i = 1; i < kMaxBlock; ++i) s.blk[i] = -1;
+  s.blk_n = 1;
+  s.ctr += 1;
+  // drafts beyond the tokens still wanted are never emitted
+  s.blk_g = min(a.draft_len, s.max_new - s.produced - 1);
+  s.blk_phase = s.blk_g > 0 ? 0 : 1;
+  s.blk_step = 0;
+}
+
+__device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
+  const int P = a.n_pulses;
+  if (s.blk_phase == 0) {
+    const int j = s.blk_step;
+    const int d = a.draw[s.lrow_c * 2];
+    if (is_stop(a, d)) {
+      s.blk_phase = 1;
+      s.blk_step = 0;
+      return;
+    }
+    s.blk[j + 1] = d;
+    s.blk_n = j + 2;
+    if (j + 1 >= s.blk_g) {
+      s.blk_phase = 1;
+      s.blk_step = 0;
+    } else {
+      s.blk_step = j + 1;
+    }
+    return;
+  }
+  if (s.blk_step < P - 1) {
+    s.blk_step += 1;
+    return;
+  }
+  const int n = s.blk_n, lr0 = s.lrow_c;
+  int acc = 0, nxt = -1;
+  for (int i = 0; i < n; ++i) {
+    if (i < n - 1) {
+      const int v = a.draw[(lr0 + i) * 2];
+      s.tests += 1;
+      if (v == s.blk[i + 1] && !is_stop(a, v)) {
+        s.accepted += 1;
+        emit(a, s, b, v);
+        acc = i + 1;
+        if (s.done) return;
+        continue;
+      }
+      nxt = a.draw[(lr0 + i) * 2 + 1];
+    } else {
+      nxt = a.draw[(lr0 + i) * 2];
+    }
+    break;
+  }
+  s.c_pos += acc + 1;
+  if (is_stop(a, nxt)) {
+    s.done = 1;
+    return;
+  }
+  emit(a, s, b, nxt);
+  if (!s.done) new_round(a, s, nxt);
+}
+
+}  // namespace
+
+__global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a) {
+  __shared__ int sh[5 * 256];
+  const int b = threadIdx.x;
+  StepCtl* ctl = a.ctl;
+  const int P = a.n_pulses;
+  const int n_prev = ctl->n_rows;
+  for (int i = b; i < n_prev; i += blockDim.x) a.last_rows[i] = a.rows[i];
+  if (b == 0) *a.last_ctl = *ctl;
+  __syncthreads();
+  const bool act = b < a.B;
+  SeqState s{};
+  if (act) {
+    s = a.state[b];
+    if (a.init) {
+      s = SeqState{};
+      s.max_new = a.max_new;
+      s.c_pos = a.prompt_len;
+      const int t = a.draw[b * 2];
+      if (is_stop(a, t) || s.max_new <= 0) {
+        s.done = 1;
+      } else {
+        emit(a, s, b, t);
+        if (!s.done) new_round(a, s, t);
+      }
+    } else if (!s.done) {
+      update_block(a, s, b);
+    }
+  }
+  const bool live = act && !s.done;
+  int nrow = 0, pulse = 0, lrows = 0, pos0 = 0, slot0 = 0;
+  if (live) {
+    if (s.blk_phase == 0) {
+      nrow = 1;
+      lrows = 1;
+      slot0 = s.blk_step;
+    } else {
+      nrow = s.blk_n;
+      pulse = s.blk_step;
+      lrows = (pulse == P - 1 || a.all_logits) ? nrow : 0;
+    }
+    pos0 = s.c_pos + slot0;
+  }
+  int v[5] = {0, 0, 0, 0, 0};  // rows of pulse 0, 1, 2; logits rows; attention units
+  v[pulse] = nrow;
+  v[3] = lrows;
+  v[4] = live ? 1 : 0;
+  int total[5];
+  scan_counts<5>(v, sh, total);
+  const int base[3] = {0, total[0], total[0] + total[1]};
+  s.row_c = s.row_s = s.lrow_c = s.lrow_s = -1;
+  if (live) {
+    const int r0 = base[pulse] + v[pulse];
+    const int lr0 = v[3];
+    s.row_c = r0;
+    s.lrow_c = lrows ? lr0 : -1;
+    AttnUnit un{};
+    un.seq = b;
+    un.n = nrow;
+    un.pos0 = pos0;
+    for (int i = 0; i < kMaxBlock; ++i) un.row[i] = i < nrow ? r0 + i : -1;
+    for (int i = 0; i < nrow; ++i) {
+      const int slot = slot0 + i;
+      const int lr = lrows ? lr0 + i : -1;
+      a.rows[r0 + i] = RowDesc{b, slot, pulse, pos0 + i, s.blk[slot], lr, -1, 0};
+      if (lr >= 0) {
+        a.lrow_seq[lr] = b;
+        for (int x = 0; x < kMaxExtra; ++x)
+          a.lrow_extra[(int64_t)lr * kMaxExtra + x] = x < slot ? s.blk[1 + x] : -1;
+        // distinct stream per (round, draft or verify, block row)
+        a.lrow_ctr[lr] = (s.ctr * 2u + (s.blk_phase == 0 ? 0u : 1u)) * (uint32_t)kMaxBlock + slot;
+      }
+    }
+    a.units[v[4]] = un;
   }
   if (act) a.state[b] = s;
   if (b == 0) {
@@ -523,6 +708,8 @@ int launch_sample_rows(const float* logits, int n_rows, int V, int dtype, const 
   a.logits = logits;
   a.lrow_seq = row_seq;
   a.lrow_extra = row_extra;
+  a.extra_stride = 1;
+  a.n_extra = 1;
   a.seen = seen;
   a.state = st;
   a.V = V;
@@ -539,7 +726,13 @@ int launch_sample_rows(const float* logits, int n_rows, int V, int dtype, const 
 
 int launch_controller(const ControllerArgs& a, hipStream_t s) {
   if (a.B > 256) return fail(PULSAR_ERR_UNSUPPORTED, "controller: at most 256 sequences");
-  controller_kernel<<<1, 256, 0, s>>>(a);
+  if (a.draft_len > 0) {
+    if (a.draft_len >= kMaxBlock || a.n_pulses > 3 || !a.lrow_ctr)
+      return fail(PULSAR_ERR_INVALID, "controller: draft-block mode arguments");
+    controller_block_kernel<<<1, 256, 0, s>>>(a);
+  } else {
+    controller_kernel<<<1, 256, 0, s>>>(a);
+  }
   PULSAR_LAUNCH_CHECK();
   return PULSAR_OK;
 }

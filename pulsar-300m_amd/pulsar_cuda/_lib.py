@@ -20,7 +20,7 @@ BUF_CTL = 4
 BUF_LAST_ROWS = 5
 BUF_LAST_CTL = 6
 BUF_EXPERT_COUNTS = 7
-SEQSTATE_INTS = 20
+SEQSTATE_INTS = 32
 ROW_INTS = 8
 CTL_INTS = 16
 PROF_CLASSES = 17
@@ -66,6 +66,7 @@ class PulsarEngineConfig(ctypes.Structure):
         ("speculative", _c_i32), ("all_logits", _c_i32),
         ("temperature", _c_f32), ("top_p", _c_f32), ("repetition_penalty", _c_f32),
         ("n_stop", _c_i32), ("stop_ids", _c_i32 * 8), ("seed", ctypes.c_uint64),
+        ("draft_len", _c_i32), ("reserved", _c_i32),
     ]
 
 
@@ -95,6 +96,8 @@ _PROTOS = {
     "pulsar_engine_generate": [_vp, _c_i32, _c_i32, _vp, ctypes.POINTER(_c_i32)],
     "pulsar_engine_read": [_vp, _c_i32, _vp, _c_i64, _vp],
     "pulsar_engine_rewind": [_vp, ctypes.c_uint64, _vp],
+    "pulsar_engine_verify": [_vp, _vp, _c_i32, _c_i32, _vp],
+    "pulsar_engine_fill_kv": [_vp, _c_i32, ctypes.c_uint64, _vp],
     "pulsar_engine_profile": [_vp, _c_i32],
     "pulsar_engine_profile_read": [_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)],
     "pulsar_sample_workspace_bytes": [_c_i32],

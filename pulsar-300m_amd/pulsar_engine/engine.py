@@ -36,18 +36,25 @@ class HipEngine:
     def __init__(self, model: DeviceModel, *, batch: int, max_prompt: int, max_new: int,
                  speculative: bool = True, temperature: float = 0.7, top_p: float = 0.9,
                  repetition_penalty: float = 1.15, stop_ids: Iterable[int] = (0,),
-                 seed: int = 0, all_logits: bool = False, max_ctx: Optional[int] = None):
+                 seed: int = 0, all_logits: bool = False, max_ctx: Optional[int] = None,
+                 draft_len: int = 0):
+        """draft_len = 0 runs the reference's exact self-speculation; 1..7 the draft-block
+        mode (up to draft_len pulse-0 drafts per round, one all-pulse verify of the block)."""
         self.lib = _lib.load()
         self.model = model
         self.batch = batch
         self.max_new = max_new
+        self.draft_len = int(draft_len)
+        # rows of one sequence in a step
+        self.slots = self.draft_len + 1 if self.draft_len > 0 else 2
         self.V = model.cfg.vocab_size
         stops = sorted({int(s) for s in stop_ids})
         if len(stops) > 8:
             raise ValueError(f"at most 8 stop ids are supported, got {len(stops)}")
         c = _lib.PulsarEngineConfig()
         c.max_batch, c.max_prompt, c.max_new = batch, max_prompt, max_new
-        c.max_ctx = max_ctx or (max_prompt + max_new + 2)
+        c.max_ctx = max_ctx or (max_prompt + max_new + 2 + self.draft_len)
+        c.draft_len = self.draft_len
         c.speculative, c.all_logits = int(bool(speculative)), int(bool(all_logits))
         c.temperature, c.top_p, c.repetition_penalty = temperature, top_p, repetition_penalty
         c.n_stop = len(stops)
@@ -87,6 +94,25 @@ class HipEngine:
                                                   a.shape[1], _stream()))
         self.steps = 0
 
+    def fill_kv(self, ctx: int, seed: int = 0) -> None:
+        """Synthetic cache: every cached key/value element ~ N(0, 1); positions [0, ctx)
+        then count as context for verify()."""
+        _lib.check(self.lib.pulsar_engine_fill_kv(self.handle, int(ctx), seed & 0xFFFFFFFFFFFFFFFF,
+                                                  _stream()))
+
+    def verify(self, tokens=None, graph: bool = False) -> None:
+        """Block verify of tokens [batch, n] at the positions after the cached context,
+        through every pulse; the last pulse's logits are then readable with logits(batch*n)
+        (row b*n + i). tokens=None re-runs the last block (no host synchronisation)."""
+        if tokens is None:
+            _lib.check(self.lib.pulsar_engine_verify(self.handle, None, 0, int(graph), _stream()))
+            return
+        a = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+        if a.ndim != 2 or a.shape[0] != self.batch:
+            raise ValueError(f"verify tokens must be [batch={self.batch}, n]")
+        _lib.check(self.lib.pulsar_engine_verify(self.handle, a.ctypes.data, a.shape[1],
+                                                 int(graph), _stream()))
+
     def rewind(self, seed: int) -> None:
         """Restart decoding from the prefilled cache with a new sampling seed."""
         _lib.check(self.lib.pulsar_engine_rewind(self.handle, seed & 0xFFFFFFFFFFFFFFFF, _stream()))
@@ -111,7 +137,7 @@ class HipEngine:
     def run(self, max_steps: Optional[int] = None, check_every: int = 16) -> int:
         """Step until every sequence finished; returns the number of steps run."""
         if max_steps is None:
-            max_steps = 4 * (self.max_new + 2) * self.model.n_pulses
+            max_steps = 4 * (self.max_new + 2) * (self.model.n_pulses + self.draft_len)
         ran = ctypes.c_int32(0)
         _lib.check(self.lib.pulsar_engine_generate(self.handle, max_steps, check_every, _stream(),
                                                    ctypes.byref(ran)))
@@ -149,7 +175,7 @@ class HipEngine:
         the next step when last=False."""
         ctl = self._read(_lib.BUF_LAST_CTL if last else _lib.BUF_CTL,
                          np.zeros(_lib.CTL_INTS, np.int32))
-        buf = np.zeros((2 * self.batch, _lib.ROW_INTS), np.int32)
+        buf = np.zeros((self.slots * self.batch, _lib.ROW_INTS), np.int32)
         self._read(_lib.BUF_LAST_ROWS if last else _lib.BUF_ROWS, buf)
         return buf[: int(ctl[0])]
 
@@ -226,8 +252,10 @@ class PulsarInferenceEngine:
     def generate_ids(self, prompt_ids: Sequence[Sequence[int]], max_new_tokens: int = 512,
                      temperature: float = 0.7, top_p: float = 0.9,
                      repetition_penalty: float = 1.15, speculative: bool = True,
-                     stop_ids: Optional[Iterable[int]] = None, seed: int = 0) -> list[list[int]]:
-        """Batched id-level generation; prompts must share one length."""
+                     stop_ids: Optional[Iterable[int]] = None, seed: int = 0,
+                     draft_len: int = 0) -> list[list[int]]:
+        """Batched id-level generation; prompts must share one length. draft_len > 0 selects
+        the draft-block mode (no reference counterpart; see HipEngine)."""
         ids = np.asarray(prompt_ids, dtype=np.int32)
         if ids.ndim == 1:
             ids = ids[None, :]
@@ -235,7 +263,8 @@ class PulsarInferenceEngine:
         eng = HipEngine(self.model, batch=ids.shape[0], max_prompt=ids.shape[1],
                         max_new=max_new_tokens, speculative=speculative,
                         temperature=temperature, top_p=top_p,
-                        repetition_penalty=repetition_penalty, stop_ids=stops, seed=seed)
+                        repetition_penalty=repetition_penalty, stop_ids=stops, seed=seed,
+                        draft_len=draft_len)
         try:
             eng.prefill(ids)
             eng.run()

@@ -1,0 +1,156 @@
+"""Pins for the oracle's draft-block mode (block_pass / block_verify / block_speculative_ids).
+
+The mode has no reference counterpart, so each part is pinned by what fixes it:
+
+* a one-token block is the reference's decode pass: every pass of the reference's own greedy
+  stream (tests/golden, written by the reference) is reproduced bit for bit;
+* with draft length 0 the generator is the reference's plain generator, draw for draw
+  (goldens for greedy; the oracle's reference restatement for seeded sampling);
+* the block attention rule (row i sees the committed keys and the block's same-pulse keys
+  at positions <= its own) is the reference prefill's rule: a block over a whole prompt
+  from an empty cache reproduces the prefill's cached keys/values of every row and its
+  last-row logits (conv taps beyond the current token zeroed, since a block stem sees one
+  token, and a prompt short enough that the capacity MoE drops nothing);
+* causality: a row's results do not depend on later block tokens;
+* the acceptance bookkeeping on a rigged model with hand-worked expected streams.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from oracle import pulsar_ref as R
+
+
+@pytest.mark.parametrize("tag,dtype", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_one_token_block_reproduces_reference_passes(tiny_state, tag, dtype):
+    cfg, st = tiny_state
+    g = golden(f"tiny_{tag}.npz")
+    eng = R.load_ref(cfg, st, dtype, stop_ids={0, 2})
+    cache = R.RefKVCache(cfg)
+    eng.prefill(torch.as_tensor(g["prompt"]).view(1, -1), cache)
+    toks, poss, puls = g["pass_token"], g["pass_pos"], g["pass_pulse"]
+    got = []
+    for i in range(0, len(toks), cfg.default_pulses):
+        assert list(puls[i:i + cfg.default_pulses]) == list(range(cfg.default_pulses))
+        _, per_pulse, kv = eng.block_verify([int(toks[i])], int(poss[i]), cache)
+        got += [p.float().numpy().reshape(-1) for p in per_pulse]
+        eng.commit_block(cache, kv, 1)
+    np.testing.assert_array_equal(np.stack(got), g["pass_logits"])
+
+
+@pytest.mark.parametrize("tag,dtype", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_draft_length_zero_is_the_plain_generator(tiny_state, tag, dtype):
+    cfg, st = tiny_state
+    g = golden(f"tiny_{tag}.npz")
+    eng = R.load_ref(cfg, st, dtype, stop_ids={0, 2})
+    ids = list(eng.block_speculative_ids(g["prompt"], 6, 0.0, 1.0, 1.15, 0))
+    assert ids == g["greedy_plain_ids"].tolist()
+    ids = list(eng.block_speculative_ids(g["prompt"], 20, 0.0, 1.0, 10.0, 0))
+    assert ids == g["greedy_rp10_plain_ids"].tolist()
+    a = list(eng.stream_generate_ids(g["prompt"], 20, 0.9, 0.9, 1.15,
+                                     torch.Generator().manual_seed(5)))
+    b = list(eng.block_speculative_ids(g["prompt"], 20, 0.9, 0.9, 1.15, 0,
+                                       torch.Generator().manual_seed(5)))
+    assert a == b
+
+
+def test_block_over_prompt_equals_prefill(tiny_state):
+    """Same-pulse causal attention over the block = the reference prefill's attention."""
+    cfg, st = tiny_state
+    st = dict(st)
+    conv = st["stem_canon_weight"].copy()
+    conv[:, 1:] = 0.0
+    st["stem_canon_weight"] = conv
+    eng = R.load_ref(cfg, st, torch.float32, stop_ids=set())
+    from pulsar_engine import weights as W
+
+    T = 12
+    assert T <= cfg.sliding_window and T <= cfg.base_seq_len
+    prompt = W.uniform_ids(3, "block_prefill", T, cfg.vocab_size).tolist()
+    cache = R.RefKVCache(cfg)
+    pre = eng.prefill(torch.as_tensor(prompt).view(1, -1), cache)
+    last, _, kv = eng.block_verify(prompt, 0, R.RefKVCache(cfg))
+    for L in range(cfg.n_core):
+        torch.testing.assert_close(kv[L][0], cache.k[L], atol=2e-5, rtol=1e-4)
+        torch.testing.assert_close(kv[L][1], cache.v[L], atol=2e-5, rtol=1e-4)
+    torch.testing.assert_close(last[-1], R.softcap(pre[0, -1], cfg.logit_softcap),
+                               atol=1e-4, rtol=1e-4)
+    # a dropped row would show: rows differ from each other
+    assert (kv[0][0][:, :, 0] - kv[0][0][:, :, 1]).abs().max() > 1e-3
+
+
+def test_block_rows_are_causal(tiny_state):
+    cfg, st = tiny_state
+    eng = R.load_ref(cfg, st, torch.float32, stop_ids=set())
+    cache = R.RefKVCache(cfg)
+    prompt = list(range(5, 25))
+    eng.prefill(torch.as_tensor(prompt).view(1, -1), cache)
+    a, _, _ = eng.block_verify([7, 9, 11, 13], len(prompt), cache)
+    b, _, _ = eng.block_verify([7, 9, 11, 200], len(prompt), cache)
+    c, _, _ = eng.block_verify([7, 9, 50, 13], len(prompt), cache)
+    assert torch.equal(a[:3], b[:3]) and not torch.equal(a[3], b[3])
+    assert torch.equal(a[:2], c[:2]) and not torch.equal(a[2], c[2])
+
+
+class _Rigged(R.RefEngine):
+    """A stand-in model over 8 tokens: the prefill favours 3, a pulse-0 row favours its
+    token + 1, and the verify rows favour scripted tokens, one script per round."""
+
+    V = 8
+
+    def __init__(self, scripts, stop_ids):
+        from pulsar_engine.config import tiny_config
+
+        self.cfg = tiny_config(vocab_size=self.V)
+        self.stop_ids = set(stop_ids)
+        self.trace = None
+        self.scripts = list(scripts)
+        self.rounds = []
+        self.commits = []
+
+    @classmethod
+    def _peak(cls, tok):
+        lg = torch.full((1, cls.V), -5.0)
+        lg[0, tok] = 5.0
+        return lg
+
+    def prefill(self, ids, cache):
+        return self._peak(3).view(1, 1, self.V)
+
+    def block_pass(self, tokens, pos0, cache, pulse, h_prev=None, e_cached=None):
+        lg = torch.cat([self._peak((t + 1) % self.V) for t in tokens])
+        return lg, None, None, None
+
+    def block_verify(self, tokens, pos0, cache):
+        self.rounds.append((list(tokens), pos0))
+        script = self.scripts.pop(0)
+        lg = torch.cat([self._peak(script[i]) for i in range(len(tokens))])
+        return lg, [lg], ("kv", pos0)
+
+    def commit_block(self, cache, kv, n_keep):
+        self.commits.append((kv[1], n_keep))
+
+
+def test_block_acceptance_bookkeeping_hand_worked():
+    # round 1: t=3, drafts 4 5 6; verify favours 4 5 7 ...: accept 4, 5; reject 6 -> 7
+    # round 2: t=7, draft (7+1)%8 = 0 is a stop id: block [7]; verify favours 2 -> 2
+    # round 3: t=2, drafts 3 4 5; verify favours 3 4 5 6: all accepted, last row -> 6
+    # round 4: t=6, one token wanted: no draft; verify favours 1 -> 1 (10 tokens)
+    eng = _Rigged([[4, 5, 7, 1], [2], [3, 4, 5, 6], [1]], stop_ids={0})
+    stats = {}
+    out = list(eng.block_speculative_ids([1, 2], 10, 0.0, 1.0, 1.0, 3, stats=stats))
+    assert out == [3, 4, 5, 7, 2, 3, 4, 5, 6, 1]
+    assert eng.rounds == [([3, 4, 5, 6], 2), ([7], 5), ([2, 3, 4, 5], 6), ([6], 10)]
+    assert eng.commits == [(2, 3), (5, 1), (6, 4), (10, 1)]
+    assert stats["tests"] == 3 + 0 + 3 and stats["accepted"] == 2 + 0 + 3
+    # max_new stops mid-block: round 1 accepts 4 and 5 and the stream ends at 3 tokens
+    eng = _Rigged([[4, 5, 7, 1]], stop_ids={0})
+    assert list(eng.block_speculative_ids([1, 2], 3, 0.0, 1.0, 1.0, 3)) == [3, 4, 5]
+    assert eng.rounds == [([3, 4], 2)]
+    # a rejection whose fresh draw is a stop id ends the stream
+    eng = _Rigged([[0, 1]], stop_ids={0})
+    assert list(eng.block_speculative_ids([1, 2], 10, 0.0, 1.0, 1.0, 1)) == [3]
