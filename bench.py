@@ -35,7 +35,7 @@ HBM_PEAK = 8.0e12
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 matrix-core peak (no sparsity)
 # kernels behind each timed class (names as rocprofv3 lists them), bf16 decode
 CLASS_KERNELS = {
-    "attention": ["attn_decode_unit_kernel"],
+    "attention": ["attn_decode_unit_kernel<8>"],
     "routed_gate_up": ["gemm_bf16_kernel<3, 8, 1>"],
     "routed_down": ["gemm_bf16_kernel<0, 4, 1>"],
     "shared_down": ["gemm_bf16_kernel<0, 8, 2>"],
@@ -53,6 +53,7 @@ CLASS_KERNELS = {
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_c2_b16_t2048.md")
+VERIFY_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_verify_b64_ctx8192.md")
 
 
 def _short_kernel(name: str) -> str:
@@ -127,10 +128,10 @@ def pmc_summary(fetch_dir: str, write_dir: str, fetch_copy: str, write_copy: str
     return "\n".join(out)
 
 
-def recorded_traffic(kernels: list):
-    """HBM bytes per launch of a kernel class from the committed PMC summary, or None."""
+def recorded_traffic(kernels: list, path: str = TRAFFIC_PROFILE):
+    """HBM bytes per launch of a kernel class from a committed PMC summary, or None."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             text = f.read()
         blob = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
     except (OSError, IndexError, ValueError):
@@ -168,6 +169,125 @@ def profile_generation(eng, cfg, es, seed):
     prof = eng.profile_read()
     eng.profile(False)
     return prof, totals, steps
+
+
+def verify_microbench(model, cfg, es, args):
+    """Verify-step microbenchmark: batch 64 sequences with a synthetic bf16 cache of 8192
+    positions (every K/V element ~ N(0, 1)), one verify of a 5-token block (4 drafts + 1) per
+    sequence through every pulse of every layer, graph-replayed. Reports ms per verify, the
+    whole verify's algorithmic bytes against the HBM peak, and the attention kernel's
+    per-launch bytes against its event-timed launch duration (eager profiled verify)."""
+    import numpy as np
+    import torch
+
+    from pulsar_engine import traffic
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+
+    B, ctx, n = args.verify_batch, args.verify_ctx, args.verify_tokens
+    blocks = np.stack([W.uniform_ids(7, f"verify_block_{b}", n, cfg.vocab_size) for b in range(B)])
+    eng = HipEngine(model, batch=B, max_prompt=1, max_new=8, temperature=0.0, stop_ids=[],
+                    draft_len=n - 1, max_ctx=ctx + 16)
+    eng.fill_kv(ctx, seed=5)
+    eng.verify(blocks, graph=True)
+    for _ in range(3):
+        eng.verify(None, graph=True)
+    torch.cuda.synchronize()
+    reps = args.verify_reps
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        eng.verify(None, graph=True)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    counts = eng.expert_counts()  # the last pass's; every expert has rows at 320 rows a pass
+    P = cfg.default_pulses
+    by_class: dict = {}
+    for k in range(P):
+        rows = [(b, k, ctx + i) for b in range(B) for i in range(n)]
+        step = traffic.step_bytes(cfg, es, rows, counts, B * n if k == P - 1 else 0)
+        for c, v in step.items():
+            by_class[c] = by_class.get(c, 0.0) + v
+    total = sum(by_class.values())
+    eng.profile(True)
+    eng.verify(None)
+    prof = eng.profile_read()
+    eng.profile(False)
+    att_ms, att_n = prof["attention"]
+    att_bytes = by_class["attention"] / max(att_n, 1)
+    att_s = att_ms / max(att_n, 1) / 1e3
+    att_kernel = f"attn_decode_unit_kernel<{8 if n <= 2 else 16 if n <= 4 else 32}>"
+    att_traffic = recorded_traffic([att_kernel], VERIFY_TRAFFIC_PROFILE)
+    per_class = {c: {"ms": round(v[0], 3), "launches": v[1],
+                     "us_per_launch": round(v[0] / v[1] * 1e3, 2),
+                     "GB_per_s": round(by_class.get(c, 0.0) / max(v[0], 1e-9) / 1e6, 1)}
+                 for c, v in prof.items() if v[1] and c != "event_pair"}
+    eng.close()
+    return {
+        "workload": f"verify of {n} tokens (4 drafts + 1) for each of {B} sequences over a "
+                    f"synthetic bf16 cache of {ctx} positions (K/V ~ N(0,1)), every pulse of "
+                    f"every layer, graph-replayed",
+        "ms_per_verify": round(ms, 4),
+        "algorithmic_bytes": int(total),
+        "weight_bytes": int(sum(v for c, v in by_class.items() if c != "attention")),
+        "kv_bytes": int(by_class["attention"]),
+        "hbm_frac": round(total / (ms / 1e3) / HBM_PEAK, 4),
+        "roofline": {"bound": "hbm", "kernel": "attention",
+                     "kernels": [att_kernel],
+                     "achieved": round(att_bytes / att_s / 1e9, 1), "peak": 8000.0,
+                     "unit": "GB/s", "frac": round(att_bytes / att_s / HBM_PEAK, 4),
+                     "bytes_per_launch": int(att_bytes), "avg_launch_us": round(att_s * 1e6, 2),
+                     "traffic": round(att_traffic / 1e6, 3) if att_traffic else None,
+                     "traffic_unit": "MB per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                     "copy-calibrated)"},
+        "kernel_profile": per_class,
+    }
+
+
+def draft_block_run(model, cfg, prompts, args):
+    """The bench workload in draft-block mode (draft length args.draft_len): accepted
+    tokens/s over timed generations from the prefilled cache, acceptance rate."""
+    import torch
+
+    from pulsar_engine.engine import HipEngine
+
+    B, T = prompts.shape
+    N = args.new_tokens
+    eng = HipEngine(model, batch=B, max_prompt=T, max_new=N, temperature=args.temperature,
+                    top_p=args.top_p, repetition_penalty=args.repetition_penalty, stop_ids=[],
+                    seed=1, draft_len=args.draft_len)
+    eng.prefill(prompts)
+
+    def generation(seed):
+        eng.rewind(seed)
+        steps = eng.run(check_every=16)
+        st = eng.state()
+        return steps, int(st[:, 1].sum()), int(st[:, 11].sum()), int(st[:, 12].sum())
+
+    for w in range(args.warmup):
+        generation(4000 + w)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    produced = tests = accepted = steps = 0
+    for k in range(args.steps):
+        s_, p, t, a = generation(5000 + k)
+        steps += s_
+        produced += p
+        tests += t
+        accepted += a
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    eng.close()
+    return {
+        "schedule": f"draft-block (no reference counterpart): up to {args.draft_len} pulse-0 "
+                    "drafts per round, one all-pulse verify of the block, drafts accepted down "
+                    "the block by the reference's equal-draw rule",
+        "draft_len": args.draft_len,
+        "value": round(produced / el, 1), "unit": "tokens/s",
+        "ms_per_step": round(el / args.steps * 1e3, 2),
+        "acceptance_rate": round(accepted / tests, 4) if tests else None,
+        "tokens_per_round": round(produced / max(1, produced - accepted), 3),
+        "pulse_steps_per_generation": round(steps / args.steps, 1),
+    }
 
 
 def cpu_baseline(cfg, state, prompt, n_new, temperature, top_p, rp):
@@ -219,6 +339,15 @@ def main() -> int:
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-new-tokens", type=int, default=12)
+    ap.add_argument("--draft-len", type=int, default=4,
+                    help="draft length of the draft-block run (0 skips it)")
+    ap.add_argument("--no-verify", action="store_true", help="skip the verify microbenchmark")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="run only the verify microbenchmark (profiling)")
+    ap.add_argument("--verify-batch", type=int, default=64)
+    ap.add_argument("--verify-ctx", type=int, default=8192)
+    ap.add_argument("--verify-tokens", type=int, default=5)
+    ap.add_argument("--verify-reps", type=int, default=20)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (HBM counter calibration)")
     ap.add_argument("--phase", choices=("decode", "prefill"), default="decode",
@@ -265,8 +394,13 @@ def main() -> int:
     t0 = time.perf_counter()
     state = W.synthetic_state(cfg, seed=0)
     log(f"weights generated in {time.perf_counter() - t0:.1f}s")
-    model = DeviceModel(cfg, state, torch.bfloat16, rope_len=max(cfg.max_seq_len, T + N + 8))
+    model = DeviceModel(cfg, state, torch.bfloat16,
+                        rope_len=max(cfg.max_seq_len, T + N + 16, args.verify_ctx + 32))
     es = 2
+    if args.verify_only:
+        vr = verify_microbench(model, cfg, es, args)
+        print(json.dumps({"verify": vr}), flush=True)
+        return 0
     prompts = np.stack([W.uniform_ids(0, f"bench_prompt_{b}", T, cfg.vocab_size) for b in range(B)])
     eng = HipEngine(model, batch=B, max_prompt=T, max_new=N, speculative=not args.plain,
                     temperature=args.temperature, top_p=args.top_p,
@@ -354,6 +488,14 @@ def main() -> int:
             f"pair {pair * 1e3:.2f} us), dominant {dom} {ms:.1f} ms")
         log("per-class: " + json.dumps(prof_detail))
 
+    block = None
+    if args.draft_len > 0:
+        block = draft_block_run(model, cfg, prompts, args)
+        log(f"draft-block run: {json.dumps(block)}")
+    verify = None
+    if not args.no_verify:
+        verify = verify_microbench(model, cfg, es, args)
+        log(f"verify microbenchmark: {json.dumps(verify)}")
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, state, prompts[0], args.cpu_new_tokens, args.temperature,
@@ -386,6 +528,8 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernel_profile": prof_detail,
+        "draft_block": block,
+        "verify": verify,
     }
     print(json.dumps(line), flush=True)
     return 0
