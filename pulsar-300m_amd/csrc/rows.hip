@@ -597,14 +597,43 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
 // dimension-major V block. P = exp(S - max) in fp32 is split into bf16 hi + lo (hi + lo =
 // P to 2^-16 relative), two products each. The last split block to count in merges the
 // split partials, normalises, rounds as the SDPA output and applies the head gate.
-// COLS = 8 serves units of up to 2 rows (exact mode), 16 up to 4, 32 up to 8.
+// COLS = 8 serves units of up to 2 rows (exact mode), 16 up to 4, 32 up to 8. BPW = 64-key
+// blocks per wave and split: long caches take BPW = 4 (1024-key splits, a quarter of the
+// split partials). PF: a wave loads its next block's K/V while it computes the current one
+// (64 more registers).
 // ---------------------------------------------------------------------------
 typedef __bf16 attn_bf16x4 __attribute__((ext_vector_type(4)));
 
-template <int COLS>
+struct AttnKV {
+  attn_bf16x8 k[4][2];
+  attn_bf16x4 vl[4][2], vh[4][2];
+};
+
+// Lane (m16, kq): K rows 16 kt + m16, dims 32 ks + 8 kq (16 bytes); V^T rows (dims)
+// 16 mt + m16, keys 32 s2 + 4 kq and 32 s2 + 16 + 4 kq (8 bytes each).
+__device__ __forceinline__ void attn_load_block(const bf16* Kc, const bf16* Vc, const KVBlock& blk,
+                                                int m16, int kq, AttnKV& r) {
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      r.k[kt][ks] = *reinterpret_cast<const attn_bf16x8*>(Kc + blk.k0 + (kt * 16 + m16) * 64 +
+                                                          ks * 32 + kq * 8);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const bf16* vp = Vc + blk.v0 + (int64_t)(mt * 16 + m16) * blk.vstride + s2 * 32 + kq * 4;
+      r.vl[mt][s2] = *reinterpret_cast<const attn_bf16x4*>(vp);
+      r.vh[mt][s2] = *reinterpret_cast<const attn_bf16x4*>(vp + 16);
+    }
+}
+
+template <int COLS, int BPW, bool PF>
 __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnArgs a) {
   constexpr int NQT = (COLS + 15) / 16;
   constexpr int NZ = COLS / 4;
+  constexpr int SPLIT = kUnitSplit * BPW;
   __shared__ float wm[kUnitWaves][COLS], wl[kUnitWaves][COLS];
   __shared__ float wo[kUnitWaves][COLS][65];
   const int u = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
@@ -612,11 +641,22 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   const AttnUnit un = a.units[u];
   int base, uhi;
   unit_range(a, un, base, uhi);
-  const int nsplit = (uhi + 1 - base + kUnitSplit - 1) / kUnitSplit;
+  const int nsplit = (uhi + 1 - base + SPLIT - 1) / SPLIT;
   if (s >= nsplit) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m16 = lane & 15, kq = lane >> 4;
   const attn_bf16x8 zero = {};
+  const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]);
+  const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]);
+  const int s_lo = base + s * SPLIT;
+  const int s_hi = min(uhi, s_lo + SPLIT - 1);
+  constexpr int kStride = kUnitWaves * 64;
+  AttnKV cur;
+  if constexpr (PF) {
+    // the wave's first block goes out before the query loads
+    if (s_lo + wv * 64 <= s_hi)
+      attn_load_block(Kc, Vc, kv_block(a.kv, a.layer, un.seq, g, s_lo + wv * 64), m16, kq, cur);
+  }
   int qlo[NQT], qhi[NQT];
   attn_bf16x8 qb[NQT][2];
 #pragma unroll
@@ -632,10 +672,6 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
     for (int ks = 0; ks < 2; ++ks)
       qb[t][ks] = qrow >= 0 ? *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32) : zero;
   }
-  const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]);
-  const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]);
-  const int s_lo = base + s * kUnitSplit;
-  const int s_hi = min(uhi, s_lo + kUnitSplit - 1);
   float mrun[NQT], lrun[NQT];
   attn_f32x4 o[NQT][4];
 #pragma unroll
@@ -645,24 +681,17 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) o[t][mt] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  for (int kb = s_lo + wv * 64; kb <= s_hi; kb += kUnitWaves * 64) {
-    const KVBlock blk = kv_block(a.kv, a.layer, un.seq, g, kb);
-    attn_bf16x8 kk[4][2];
-    attn_bf16x4 vl[4][2], vh[4][2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        kk[kt][ks] = *reinterpret_cast<const attn_bf16x8*>(Kc + blk.k0 + (kt * 16 + m16) * 64 +
-                                                            ks * 32 + kq * 8);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16* vp = Vc + blk.v0 + (int64_t)(mt * 16 + m16) * blk.vstride + s2 * 32 + kq * 4;
-        vl[mt][s2] = *reinterpret_cast<const attn_bf16x4*>(vp);
-        vh[mt][s2] = *reinterpret_cast<const attn_bf16x4*>(vp + 16);
-      }
+  for (int kb = s_lo + wv * 64; kb <= s_hi; kb += kStride) {
+    AttnKV nxt;
+    if constexpr (PF) {
+      if (kb + kStride <= s_hi)
+        attn_load_block(Kc, Vc, kv_block(a.kv, a.layer, un.seq, g, kb + kStride), m16, kq, nxt);
+    } else {
+      attn_load_block(Kc, Vc, kv_block(a.kv, a.layer, un.seq, g, kb), m16, kq, cur);
+    }
+    const auto& kk = cur.k;
+    const auto& vl = cur.vl;
+    const auto& vh = cur.vh;
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
       attn_f32x4 sv[4];
@@ -712,6 +741,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
           o[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pl[s2], o[t][mt], 0, 0, 0);
         }
     }
+    if constexpr (PF) cur = nxt;
   }
   // wave partials: query column 16 t + m16 < COLS; lane holds dims 16 mt + 4 kq + j
 #pragma unroll
@@ -1517,15 +1547,29 @@ int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s) 
 }
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s) {
   if (dtype == PULSAR_BF16) {
-    const dim3 grid(a.max_units, a.Hkv, a.max_splits_unit);
+    // caches longer than kLongCacheSplits 256-key splits take 1024-key splits; the choice
+    // depends on the engine's context length only, never on the batch
+    const bool lng = a.max_splits_unit > kLongCacheSplits;
+    const dim3 grid(a.max_units, a.Hkv, lng ? (a.max_splits_unit + 3) / 4 : a.max_splits_unit);
+#ifndef PULSAR_ATTN_PF32
+#define PULSAR_ATTN_PF32 false
+#endif
+#define PULSAR_ATTN_UNIT(C, PF)                                                 \
+  do {                                                                          \
+    if (lng)                                                                    \
+      attn_decode_unit_kernel<C, 4, PF><<<grid, 64 * kUnitWaves, 0, s>>>(a);    \
+    else                                                                        \
+      attn_decode_unit_kernel<C, 1, false><<<grid, 64 * kUnitWaves, 0, s>>>(a); \
+  } while (0)
     if (a.unit_rows <= 2)
-      attn_decode_unit_kernel<8><<<grid, 64 * kUnitWaves, 0, s>>>(a);
+      PULSAR_ATTN_UNIT(8, true);
     else if (a.unit_rows <= 4)
-      attn_decode_unit_kernel<16><<<grid, 64 * kUnitWaves, 0, s>>>(a);
+      PULSAR_ATTN_UNIT(16, true);
     else if (a.unit_rows <= kMaxBlock)
-      attn_decode_unit_kernel<32><<<grid, 64 * kUnitWaves, 0, s>>>(a);
+      PULSAR_ATTN_UNIT(32, PULSAR_ATTN_PF32);
     else
       return fail(PULSAR_ERR_UNSUPPORTED, "decode attention: at most 8 rows per unit");
+#undef PULSAR_ATTN_UNIT
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   }
