@@ -563,14 +563,14 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
 #pragma unroll
       for (int k = 0; k < kMergeChunk; ++k)
         if (c0 + k < nsplit) cm = fmaxf(cm, pm[k]);
-      const float f0 = Mx == -INFINITY ? 0.f : expf(Mx - cm);
+      const float f0 = Mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(Mx - cm);
       Ls *= f0;
       Oa *= f0;
       Ob *= f0;
 #pragma unroll
       for (int k = 0; k < kMergeChunk; ++k) {
         if (c0 + k < nsplit && pm[k] != -INFINITY) {
-          const float f = expf(pm[k] - cm);
+          const float f = __builtin_amdgcn_exp2f(pm[k] - cm);
           Ls += pl[k] * f;
           Oa += pa[k] * f;
           Ob += pb[k] * f;
@@ -599,8 +599,9 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
 // split partials, normalises, rounds as the SDPA output and applies the head gate.
 // COLS = 8 serves units of up to 2 rows (exact mode), 16 up to 4, 32 up to 8. BPW = 64-key
 // blocks per wave and split: long caches take BPW = 4 (1024-key splits, a quarter of the
-// split partials). PF: a wave loads its next block's K/V while it computes the current one
-// (64 more registers).
+// split partials). Holding the next block in registers while computing the current one
+// (64 more registers: one wave per SIMD) and touching the next blocks' lines ahead of their
+// loads were both measured slower at 64 x 8192 positions.
 // ---------------------------------------------------------------------------
 typedef __bf16 attn_bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -629,7 +630,7 @@ __device__ __forceinline__ void attn_load_block(const bf16* Kc, const bf16* Vc, 
     }
 }
 
-template <int COLS, int BPW, bool PF>
+template <int COLS, int BPW>
 __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnArgs a) {
   constexpr int NQT = (COLS + 15) / 16;
   constexpr int NZ = COLS / 4;
@@ -652,11 +653,6 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   const int s_hi = min(uhi, s_lo + SPLIT - 1);
   constexpr int kStride = kUnitWaves * 64;
   AttnKV cur;
-  if constexpr (PF) {
-    // the wave's first block goes out before the query loads
-    if (s_lo + wv * 64 <= s_hi)
-      attn_load_block(Kc, Vc, kv_block(a.kv, a.layer, un.seq, g, s_lo + wv * 64), m16, kq, cur);
-  }
   int qlo[NQT], qhi[NQT];
   attn_bf16x8 qb[NQT][2];
 #pragma unroll
@@ -681,14 +677,14 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) o[t][mt] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  for (int kb = s_lo + wv * 64; kb <= s_hi; kb += kStride) {
-    AttnKV nxt;
-    if constexpr (PF) {
-      if (kb + kStride <= s_hi)
-        attn_load_block(Kc, Vc, kv_block(a.kv, a.layer, un.seq, g, kb + kStride), m16, kq, nxt);
-    } else {
-      attn_load_block(Kc, Vc, kv_block(a.kv, a.layer, un.seq, g, kb), m16, kq, cur);
-    }
+  // scores in the base-2 domain: exp(x - m) = exp2(x log2e - m log2e)
+  const float scale2 = a.scale * 1.4426950408889634f;
+  // keys every row of the unit sees: [lo of the last row, position of the first row]
+  const int full_lo = a.is_local ? max(0, uhi - a.window + 1) : 0;
+  const int full_hi = un.pos0;
+  const int kb0 = s_lo + wv * 64;
+  for (int kb = kb0; kb <= s_hi; kb += kStride) {
+    attn_load_block(Kc, Vc, kv_block(a.kv, a.layer, un.seq, g, kb), m16, kq, cur);
     const auto& kk = cur.k;
     const auto& vl = cur.vl;
     const auto& vh = cur.vh;
@@ -701,22 +697,34 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][0], qb[t][0], acc, 0, 0, 0);
         sv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][1], qb[t][1], acc, 0, 0, 0);
       }
-      // lane holds keys kb + 16 kt + 4 kq + j of query column 16 t + m16
+      // lane holds keys kb + 16 kt + 4 kq + j of query column 16 t + m16; a block inside
+      // every row's key range needs no mask (unused columns hold zero queries: finite)
       float mx = -INFINITY;
+      if (kb >= full_lo && kb + 63 <= full_hi) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = kb + kt * 16 + kq * 4 + j;
-          const float v = (key >= qlo[t] && key <= qhi[t]) ? sv[kt][j] * a.scale : -INFINITY;
-          sv[kt][j] = v;
-          mx = fmaxf(mx, v);
-        }
+          for (int j = 0; j < 4; ++j) {
+            sv[kt][j] *= scale2;
+            mx = fmaxf(mx, sv[kt][j]);
+          }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int key = kb + kt * 16 + kq * 4 + j;
+            const float v = (key >= qlo[t] && key <= qhi[t]) ? sv[kt][j] * scale2 : -INFINITY;
+            sv[kt][j] = v;
+            mx = fmaxf(mx, v);
+          }
+      }
       mx = fmaxf(mx, swz_xor16(mx));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float mnew = fmaxf(mrun[t], mx);
       const float muse = mnew == -INFINITY ? 0.f : mnew;
-      const float f = mrun[t] == -INFINITY ? 0.f : expf(mrun[t] - muse);
+      // exp2(-inf) = 0 covers an empty running state and masked keys
+      const float f = __builtin_amdgcn_exp2f(mrun[t] - muse);
       mrun[t] = mnew;
       lrun[t] *= f;
 #pragma unroll
@@ -726,7 +734,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float p = sv[kt][j] == -INFINITY ? 0.f : expf(sv[kt][j] - muse);
+          const float p = __builtin_amdgcn_exp2f(sv[kt][j] - muse);
           lrun[t] += p;
           const __bf16 hi = (__bf16)p;
           ph[kt >> 1][(kt & 1) * 4 + j] = hi;
@@ -741,7 +749,6 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
           o[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pl[s2], o[t][mt], 0, 0, 0);
         }
     }
-    if constexpr (PF) cur = nxt;
   }
   // wave partials: query column 16 t + m16 < COLS; lane holds dims 16 mt + 4 kq + j
 #pragma unroll
@@ -775,7 +782,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
 #pragma unroll
       for (int w = 0; w < kUnitWaves; ++w) {
         if (wm[w][hr] == -INFINITY) continue;
-        const float f = expf(wm[w][hr] - M);
+        const float f = __builtin_amdgcn_exp2f(wm[w][hr] - M);
         L += wl[w][hr] * f;
         O += wo[w][hr][d] * f;
       }
@@ -1551,22 +1558,19 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     // depends on the engine's context length only, never on the batch
     const bool lng = a.max_splits_unit > kLongCacheSplits;
     const dim3 grid(a.max_units, a.Hkv, lng ? (a.max_splits_unit + 3) / 4 : a.max_splits_unit);
-#ifndef PULSAR_ATTN_PF32
-#define PULSAR_ATTN_PF32 false
-#endif
-#define PULSAR_ATTN_UNIT(C, PF)                                                 \
-  do {                                                                          \
-    if (lng)                                                                    \
-      attn_decode_unit_kernel<C, 4, PF><<<grid, 64 * kUnitWaves, 0, s>>>(a);    \
-    else                                                                        \
-      attn_decode_unit_kernel<C, 1, false><<<grid, 64 * kUnitWaves, 0, s>>>(a); \
+#define PULSAR_ATTN_UNIT(C)                                                 \
+  do {                                                                      \
+    if (lng)                                                                \
+      attn_decode_unit_kernel<C, 4><<<grid, 64 * kUnitWaves, 0, s>>>(a);    \
+    else                                                                    \
+      attn_decode_unit_kernel<C, 1><<<grid, 64 * kUnitWaves, 0, s>>>(a);    \
   } while (0)
     if (a.unit_rows <= 2)
-      PULSAR_ATTN_UNIT(8, true);
+      PULSAR_ATTN_UNIT(8);
     else if (a.unit_rows <= 4)
-      PULSAR_ATTN_UNIT(16, true);
+      PULSAR_ATTN_UNIT(16);
     else if (a.unit_rows <= kMaxBlock)
-      PULSAR_ATTN_UNIT(32, PULSAR_ATTN_PF32);
+      PULSAR_ATTN_UNIT(32);
     else
       return fail(PULSAR_ERR_UNSUPPORTED, "decode attention: at most 8 rows per unit");
 #undef PULSAR_ATTN_UNIT
