@@ -108,6 +108,7 @@ struct GemmArgs {
   // empty group's weights are then read for nothing)
   int eager_w;
   int a_rows, a_rows0;  // rows of A and A0 (eager_w clamps speculative row indices into them)
+  int grid_x, grid_y, grid_z;  // decode bf16 launches: (column block, group, row tile) extents
 };
 
 int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,

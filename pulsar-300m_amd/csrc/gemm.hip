@@ -176,23 +176,50 @@ __device__ __forceinline__ int group_rows(const GemmArgs& g, int group) {
 // all-rows group has K0 = KMUL0 * K and runs KMUL0 passes over K-slices (the shared expert
 // down projection fused into the routed one).
 constexpr int kGemmWaves = 8;
+constexpr int kXcds = 8;  // MI355X: consecutive workgroups go to the 8 XCDs in turn
 
-template <int EPI, int KITER, int MODE, int KMUL0, bool EAGER>
+// A launch with several row tiles per group is a 1-D grid over (column block x, group y,
+// row tile z), ordered so that the z workgroups of one (x, y) run one after another on the
+// same XCD: workgroup L goes to XCD L % 8, and within an XCD the slots enumerate (x, y)
+// pairs with z fastest. They then share that XCD's L2 for the weight slice instead of each
+// fetching it from HBM. Pairs are padded to a multiple of 8; padding workgroups exit.
+// With one row tile (decode batches) the grid is the plain (x, y) grid: no index
+// arithmetic ahead of the weight loads.
+struct GemmBlock {
+  int x, y, z;
+  bool valid;
+};
+template <bool XCD>
+__device__ __forceinline__ GemmBlock gemm_block(const GemmArgs& g) {
+  if constexpr (!XCD) return GemmBlock{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, true};
+  const int L = blockIdx.x, slot = L / kXcds;
+  const int pair = (slot / g.grid_z) * kXcds + L % kXcds;
+  GemmBlock b;
+  b.z = slot % g.grid_z;
+  b.x = pair % g.grid_x;
+  b.y = pair / g.grid_x;
+  b.valid = b.y < g.grid_y;
+  return b;
+}
+
+template <int EPI, int KITER, int MODE, int KMUL0, bool EAGER, bool XCD>
 __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
   constexpr int kKPass = KITER * 32 * kGemmWaves;  // K covered by one pass of the waves
   static_assert(!EAGER || MODE == ROWS_LIST, "eager weight loads are for expert lists");
   __shared__ float red[kGemmWaves][64][kPair ? 16 : 8];
+  const GemmBlock blk = gemm_block<XCD>(g);
+  if (!blk.valid) return;
   // grid.y == 0 is the optional all-rows group (group -1) when has_g0 is set
-  const int group = (int)blockIdx.y + g.group_offset - (g.has_g0 ? 1 : 0);
+  const int group = blk.y + g.group_offset - (g.has_g0 ? 1 : 0);
   const bool g0 = group < 0;
   const int N = g0 ? g.N0 : g.N;
-  const int col0 = blockIdx.x * 16;
+  const int col0 = blk.x * 16;
   if (col0 >= N) return;
   int cnt = 0;
   if constexpr (!EAGER) {
     cnt = group_rows<MODE>(g, group);  // uniform per workgroup
-    if ((int)blockIdx.z * 32 >= cnt) return;
+    if (blk.z * 32 >= cnt) return;
   }
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -228,7 +255,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   // barrier) the A rows: vector loads retire in issue order, so waiting for the few entry
   // loads leaves every weight load in flight. Lanes past the last row re-read the last
   // entry (always in bounds) and use a zero A operand.
-  int tile0 = blockIdx.z * 32;
+  int tile0 = blk.z * 32;
   int n, i0, i1, l0, l1;
   if constexpr (EAGER) {
     // Most experts have rows (the host decides from the batch size): the first tile's
@@ -329,7 +356,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
       const int row = blk * 16 + kq * 4 + j;
       if (vc && row < n) epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, col0 + m, acc, accu);
     }
-    tile0 += (int)gridDim.z * 32;
+    tile0 += (XCD ? g.grid_z : (int)gridDim.z) * 32;
     if (tile0 >= cnt) break;
     __syncthreads();  // the partial sums in LDS are consumed before the next tile's writes
     n = min(32, cnt - tile0);
@@ -543,18 +570,32 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   }
 }
 
-template <int EPI, int MODE, int KMUL0, bool EAGER = false>
-void launch_bf16_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
+template <int EPI, int MODE, int KMUL0, bool EAGER, bool XCD>
+void launch_bf16_kx(const GemmArgs& a, dim3 grid, hipStream_t s) {
   constexpr int T = 64 * kGemmWaves;
   switch (a.K) {
-    case 256: gemm_bf16_kernel<EPI, 1, MODE, KMUL0, EAGER><<<grid, T, 0, s>>>(a); break;
-    case 512: gemm_bf16_kernel<EPI, 2, MODE, KMUL0, EAGER><<<grid, T, 0, s>>>(a); break;
-    case 1024: gemm_bf16_kernel<EPI, 4, MODE, KMUL0, EAGER><<<grid, T, 0, s>>>(a); break;
-    default: gemm_bf16_kernel<EPI, 8, MODE, KMUL0, EAGER><<<grid, T, 0, s>>>(a); break;
+    case 256: gemm_bf16_kernel<EPI, 1, MODE, KMUL0, EAGER, XCD><<<grid, T, 0, s>>>(a); break;
+    case 512: gemm_bf16_kernel<EPI, 2, MODE, KMUL0, EAGER, XCD><<<grid, T, 0, s>>>(a); break;
+    case 1024: gemm_bf16_kernel<EPI, 4, MODE, KMUL0, EAGER, XCD><<<grid, T, 0, s>>>(a); break;
+    default: gemm_bf16_kernel<EPI, 8, MODE, KMUL0, EAGER, XCD><<<grid, T, 0, s>>>(a); break;
   }
 }
 
-// Row tiles walked by one workgroup (weights stay in registers across them).
+template <int EPI, int MODE, int KMUL0, bool EAGER = false>
+void launch_bf16_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  if (a.grid_z > 1) {
+    // 1-D launch in the XCD-aware order of gemm_block
+    const int pairs = (a.grid_x * a.grid_y + kXcds - 1) / kXcds * kXcds;
+    launch_bf16_kx<EPI, MODE, KMUL0, EAGER, true>(a, dim3((unsigned)(pairs * a.grid_z)), s);
+  } else {
+    launch_bf16_kx<EPI, MODE, KMUL0, EAGER, false>(a, grid, s);
+  }
+}
+
+// Row tiles walked by one workgroup of an expert-list or logits launch (weights stay in
+// registers across them). Launches over the rows of a pulse (the attention projections,
+// whose weights are a few MiB) give every 32-row tile its own workgroup: their tiles run
+// in parallel, and the re-read weights come from the XCD's L2.
 constexpr int kTilesPerWorkgroup = 4;
 
 template <int EPI>
@@ -572,10 +613,15 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
                   "gemm: the all-rows group fuses into list launches with a control block only");
     if (k0 != a.K && k0 != 2 * a.K)
       return fail(PULSAR_ERR_UNSUPPORTED, "gemm: the all-rows group needs K0 = K or 2K");
-    const int gz = (tiles + kTilesPerWorkgroup - 1) / kTilesPerWorkgroup;
+    const int per_wg = a.row_mode == ROWS_PULSE ? 1 : kTilesPerWorkgroup;
+    const int gz = (tiles + per_wg - 1) / per_wg;
     dim3 grid((unsigned)((nmax + 15) / 16), (unsigned)gy, (unsigned)gz);
+    GemmArgs ga = a;
+    ga.grid_x = (int)grid.x;
+    ga.grid_y = (int)grid.y;
+    ga.grid_z = (int)grid.z;
     switch (a.row_mode) {
-      case ROWS_PULSE: launch_bf16_k<EPI, ROWS_PULSE, 1>(a, grid, s); break;
+      case ROWS_PULSE: launch_bf16_k<EPI, ROWS_PULSE, 1>(ga, grid, s); break;
       case ROWS_LIST:
         if (a.eager_w) {
           if (EPI != EPI_SWIGLU || k0 != a.K)
@@ -583,16 +629,16 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
                         "gemm: eager expert launches are SwiGLU with K0 == K");
           if (a.a_rows < 1 || (a.has_g0 && a.a_rows0 < 1))
             return fail(PULSAR_ERR_INVALID, "gemm: eager expert launches need A row counts");
-          if constexpr (EPI == EPI_SWIGLU) launch_bf16_k<EPI, ROWS_LIST, 1, true>(a, grid, s);
+          if constexpr (EPI == EPI_SWIGLU) launch_bf16_k<EPI, ROWS_LIST, 1, true>(ga, grid, s);
         } else {
           if (k0 == a.K)
-            launch_bf16_k<EPI, ROWS_LIST, 1>(a, grid, s);
+            launch_bf16_k<EPI, ROWS_LIST, 1>(ga, grid, s);
           else
-            launch_bf16_k<EPI, ROWS_LIST, 2>(a, grid, s);
+            launch_bf16_k<EPI, ROWS_LIST, 2>(ga, grid, s);
         }
         break;
-      case ROWS_ALL: launch_bf16_k<EPI, ROWS_ALL, 1>(a, grid, s); break;
-      case ROWS_LOGITS: launch_bf16_k<EPI, ROWS_LOGITS, 1>(a, grid, s); break;
+      case ROWS_ALL: launch_bf16_k<EPI, ROWS_ALL, 1>(ga, grid, s); break;
+      case ROWS_LOGITS: launch_bf16_k<EPI, ROWS_LOGITS, 1>(ga, grid, s); break;
       default: return fail(PULSAR_ERR_INVALID, "gemm: row mode");
     }
   } else {
