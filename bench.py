@@ -35,18 +35,17 @@ HBM_PEAK = 8.0e12
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 matrix-core peak (no sparsity)
 # kernels behind each timed class (names as rocprofv3 lists them), bf16 decode
 CLASS_KERNELS = {
-    "attention": ["attn_decode_unit_kernel<8>"],
-    "routed_gate_up": ["gemm_bf16_kernel<3, 8, 1>"],
-    "routed_down": ["gemm_bf16_kernel<0, 4, 1>"],
-    "shared_down": ["gemm_bf16_kernel<0, 8, 2>"],
-    "qkv_gate_gemm": ["gemm_bf16_kernel<1, 8, 0>"],
-    "wo_gemm": ["gemm_bf16_kernel<2, 8, 0>"],
-    "lm_head": ["gemm_bf16_kernel<4, 8, 3>"],
+    "attention": ["attn_decode_unit_kernel<8, 1>"],
+    "routed_gate_up": ["gemm_bf16_kernel<3, 4, 1, 1, true, false>"],
+    "routed_down": ["gemm_bf16_kernel<0, 2, 1, 2, false, false>"],
+    "qkv_gate_gemm": ["gemm_bf16_kernel<1, 4, 0, 1, false, false>"],
+    "wo_gemm": ["gemm_bf16_kernel<2, 4, 0, 1, false, false>"],
+    "lm_head": ["gemm_bf16_kernel<4, 4, 3, 1, false, false>"],
     "router": ["norm_router_kernel<bf16, 16, 16>"],
     "moe_combine": ["moe_combine_rows_kernel<bf16, 16, 4>"],
     "qk_post": ["qk_post_kernel<bf16>"],
-    "sample": ["sample_kernel<bf16, 32>"],
-    "pulse_input": ["pulse_input_kernel<bf16, 16, 8>"],
+    "sample": ["sample_kernel<bf16, 32, 1024>"],
+    "pulse_input": ["pulse_input_kernel<bf16, 16, 8, true>"],
     "pulse_output": ["pulse_output_kernel<bf16>"],
     "controller": ["controller_kernel"],
 }
@@ -215,7 +214,11 @@ def verify_microbench(model, cfg, es, args):
     att_ms, att_n = prof["attention"]
     att_bytes = by_class["attention"] / max(att_n, 1)
     att_s = att_ms / max(att_n, 1) / 1e3
-    att_kernel = f"attn_decode_unit_kernel<{8 if n <= 2 else 16 if n <= 4 else 32}>"
+    # query columns of a unit (4 per row) and 64-key blocks per wave (4 for caches past
+    # 16 splits of 256 keys)
+    cols = 8 if n <= 2 else 16 if n <= 4 else 32
+    bpw = 4 if (ctx + 16 + 63 + 255) // 256 > 16 else 1
+    att_kernel = f"attn_decode_unit_kernel<{cols}, {bpw}>"
     att_traffic = recorded_traffic([att_kernel], VERIFY_TRAFFIC_PROFILE)
     per_class = {c: {"ms": round(v[0], 3), "launches": v[1],
                      "us_per_launch": round(v[0] / v[1] * 1e3, 2),
