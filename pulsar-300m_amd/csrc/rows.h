@@ -10,7 +10,8 @@ constexpr int kSplitLen = 256;  // keys per decode-attention block (fp32 path)
 // block per wave: more, shorter splits measured faster than fewer, longer ones)
 constexpr int kUnitWaves = 4;
 constexpr int kUnitSplit = kUnitWaves * 64;
-// engines whose context needs more 256-key splits than this use 1024-key splits
+// engines whose context needs more 256-key splits than this use 2048-key splits in the
+// global layers
 constexpr int kLongCacheSplits = 16;
 static_assert(kUnitSplit >= kSplitLen, "split partial slots are sized for kSplitLen");
 constexpr int kMaxRank = 16;    // re-injection gate rank bound

@@ -598,10 +598,10 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
 // P to 2^-16 relative), two products each. The last split block to count in merges the
 // split partials, normalises, rounds as the SDPA output and applies the head gate.
 // COLS = 8 serves units of up to 2 rows (exact mode), 16 up to 4, 32 up to 8. BPW = 64-key
-// blocks per wave and split: long caches take BPW = 4 (1024-key splits, a quarter of the
-// split partials). Holding the next block in registers while computing the current one
-// (64 more registers: one wave per SIMD) and touching the next blocks' lines ahead of their
-// loads were both measured slower at 64 x 8192 positions.
+// blocks per wave and split: long caches take BPW = 8 (2048-key splits) in the global
+// layers and 4 in the sliding-window layers. Holding the next block in registers while
+// computing the current one (64 more registers: one wave per SIMD) and touching the next
+// blocks' lines ahead of their loads were both measured slower at 64 x 8192 positions.
 // ---------------------------------------------------------------------------
 typedef __bf16 attn_bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -1554,16 +1554,28 @@ int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s) 
 }
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s) {
   if (dtype == PULSAR_BF16) {
-    // caches longer than kLongCacheSplits 256-key splits take 1024-key splits; the choice
-    // depends on the engine's context length only, never on the batch
+    // Key split per launch, from the layer type and the engine's context length only (never
+    // the batch). Engines whose context needs more than kLongCacheSplits 256-key splits
+    // take 2048-key splits (8 blocks per wave) in the global layers, which spread each
+    // workgroup's fixed start and merge costs over 8x the keys, and 1024-key splits in the
+    // sliding-window layers (at most window + unit rows keys: two splits); shorter engines
+    // take 256-key splits (one block per wave, many workgroups in parallel).
     const bool lng = a.max_splits_unit > kLongCacheSplits;
-    const dim3 grid(a.max_units, a.Hkv, lng ? (a.max_splits_unit + 3) / 4 : a.max_splits_unit);
-#define PULSAR_ATTN_UNIT(C)                                                 \
-  do {                                                                      \
-    if (lng)                                                                \
-      attn_decode_unit_kernel<C, 4><<<grid, 64 * kUnitWaves, 0, s>>>(a);    \
-    else                                                                    \
-      attn_decode_unit_kernel<C, 1><<<grid, 64 * kUnitWaves, 0, s>>>(a);    \
+    const int bpw = !lng ? 1 : (a.is_local ? 4 : 8);
+    int splits = a.max_splits_unit;
+    if (a.is_local) {
+      const int local_splits = (a.window + a.unit_rows - 1 + 63 + kUnitSplit - 1) / kUnitSplit;
+      if (local_splits < splits) splits = local_splits;
+    }
+    const dim3 grid(a.max_units, a.Hkv, (splits + bpw - 1) / bpw);
+#define PULSAR_ATTN_UNIT(C)                                                         \
+  do {                                                                              \
+    if (bpw == 8)                                                                   \
+      attn_decode_unit_kernel<C, 8><<<grid, 64 * kUnitWaves, 0, s>>>(a);            \
+    else if (bpw == 4)                                                              \
+      attn_decode_unit_kernel<C, 4><<<grid, 64 * kUnitWaves, 0, s>>>(a);            \
+    else                                                                            \
+      attn_decode_unit_kernel<C, 1><<<grid, 64 * kUnitWaves, 0, s>>>(a);            \
   } while (0)
     if (a.unit_rows <= 2)
       PULSAR_ATTN_UNIT(8);
