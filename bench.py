@@ -127,10 +127,11 @@ def pmc_summary(fetch_dir: str, write_dir: str, fetch_copy: str, write_copy: str
     return "\n".join(out)
 
 
-def recorded_traffic(kernels: list, path: str = TRAFFIC_PROFILE):
-    """HBM bytes per launch of a kernel class from a committed PMC summary, or None."""
+def recorded_traffic(kernels: list, path: str = None):
+    """HBM bytes per launch of a kernel class from a committed PMC summary (default: the c2
+    decode summary), or None."""
     try:
-        with open(path) as f:
+        with open(path or TRAFFIC_PROFILE) as f:
             text = f.read()
         blob = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
     except (OSError, IndexError, ValueError):

@@ -221,7 +221,7 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   e->V = m.vocab;
   e->B = c.max_batch;
   e->G = c.draft_len;
-  e->S = c.draft_len > 0 ? c.draft_len + 1 : 2;
+  e->S = engine_slots(c.draft_len);
   e->max_rows = e->S * c.max_batch;
   e->R = std::max(e->max_rows, c.max_batch * c.max_prompt);
   e->max_pages = (c.max_ctx + kPage - 1) / kPage;

@@ -10,6 +10,16 @@ constexpr int KIND_PLAIN = 1;   // accepted draft (its successor is a plain draw
 
 constexpr int kMaxExtra = kMaxBlock;  // extra seen tokens per logits row (draft-block mode)
 
+// Draft-block rounds are pipelined (the next round's first pulse-0 row rides in the last
+// verify step, one slot past the block) when a block plus that row fits a unit.
+__host__ __device__ constexpr bool block_pipelined(int draft_len) {
+  return draft_len + 2 <= kMaxBlock;
+}
+// Token-state slots (rows of one sequence in a step) of an engine.
+__host__ __device__ constexpr int engine_slots(int draft_len) {
+  return draft_len <= 0 ? 2 : (block_pipelined(draft_len) ? draft_len + 2 : draft_len + 1);
+}
+
 // Per-sequence decode state, owned by the controller.
 struct SeqState {
   int32_t done, produced, max_new;

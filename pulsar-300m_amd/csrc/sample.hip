@@ -112,13 +112,18 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
   const int base = threadIdx.x * PER;
   // tokens counted as seen for this row beyond the sequence's bitmap, as a mask over this
   // thread's PER logits
+  // (all loads issued before the first use)
   uint64_t xmask = 0;
   bool has_extra = false;
-  for (int x = 0; x < a.n_extra; ++x) {
-    const int t = a.lrow_extra[(int64_t)lr * a.extra_stride + x];
-    if (t < 0) continue;
+  int xt[kMaxExtra];
+#pragma unroll
+  for (int x = 0; x < kMaxExtra; ++x)
+    xt[x] = x < a.n_extra ? a.lrow_extra[(int64_t)lr * a.extra_stride + x] : -1;
+#pragma unroll
+  for (int x = 0; x < kMaxExtra; ++x) {
+    if (xt[x] < 0) continue;
     has_extra = true;
-    const int off = t - base;
+    const int off = xt[x] - base;
     if (off >= 0 && off < PER) xmask |= 1ull << off;
   }
   float l[PER];
@@ -486,6 +491,16 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
 // positions; the next round starts one position after the last accepted row. A logits row
 // counts block tokens 1..i of its row i as seen. Matches the oracle's
 // block_speculative_ids.
+//
+// Pipelined rounds (block_pipelined): the verify's pulse-0 pass also yields the penalised
+// argmax of the last block row, a guess of the next round's first token (the token that
+// follows when every draft is accepted). The last verify step then runs one more row for
+// the sequence: the guess at the position after the block, pulse 0, in the slot past the
+// block's, attending the block's last-pulse keys written earlier in the same layer. If
+// every draft is accepted and the emitted token equals the guess, that row was the next
+// round's first draft step (same keys, same logits, same draw counter and seen tokens), so
+// the round goes straight to its second draft; otherwise the row's work is dropped. The
+// emitted streams are those of unpipelined rounds.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -494,6 +509,7 @@ __device__ void new_round(const ControllerArgs& a, SeqState& s, int tok) {
   for (int i = 1; i < kMaxBlock; ++i) s.blk[i] = -1;
   s.blk_n = 1;
   s.ctr += 1;
+  s.s_valid = 0;
   // drafts beyond the tokens still wanted are never emitted
   s.blk_g = min(a.draft_len, s.max_new - s.produced - 1);
   s.blk_phase = s.blk_g > 0 ? 0 : 1;
@@ -521,9 +537,16 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
     return;
   }
   if (s.blk_step < P - 1) {
+    if (s.blk_step == 0 && s.lrow_s >= 0) {
+      // guess of the next round's first token (pipelined rounds)
+      s.s_tok = a.argmax[s.lrow_s];
+      s.s_valid = !is_stop(a, s.s_tok);
+    }
     s.blk_step += 1;
     return;
   }
+  const bool spec_ran = s.row_s >= 0;
+  const int spec_lrow = s.lrow_s, guess = s.s_tok;
   const int n = s.blk_n, lr0 = s.lrow_c;
   int acc = 0, nxt = -1;
   for (int i = 0; i < n; ++i) {
@@ -549,7 +572,20 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
     return;
   }
   emit(a, s, b, nxt);
-  if (!s.done) new_round(a, s, nxt);
+  if (s.done) return;
+  new_round(a, s, nxt);
+  if (spec_ran && acc == n - 1 && nxt == guess && s.blk_phase == 0) {
+    // the speculative row was this round's first draft step
+    const int d = a.draw[spec_lrow * 2];
+    if (is_stop(a, d)) {
+      s.blk_phase = 1;
+    } else {
+      s.blk[1] = d;
+      s.blk_n = 2;
+      if (s.blk_g <= 1) s.blk_phase = 1;
+      else s.blk_step = 1;
+    }
+  }
 }
 
 }  // namespace
@@ -583,7 +619,9 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
     }
   }
   const bool live = act && !s.done;
+  const bool pipe = block_pipelined(a.draft_len);
   int nrow = 0, pulse = 0, lrows = 0, pos0 = 0, slot0 = 0;
+  bool guess_row = false, spec = false;
   if (live) {
     if (s.blk_phase == 0) {
       nrow = 1;
@@ -593,12 +631,18 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
       nrow = s.blk_n;
       pulse = s.blk_step;
       lrows = (pulse == P - 1 || a.all_logits) ? nrow : 0;
+      // pulse 0 of a verify: the last row's logits give the guess
+      guess_row = pipe && pulse == 0 && P > 1;
+      if (guess_row && lrows == 0) lrows = 1;
+      // last pulse: the guessed next token's first row, when a next round can follow
+      spec = pipe && pulse == P - 1 && P > 1 && s.s_valid && s.produced + nrow < s.max_new;
     }
     pos0 = s.c_pos + slot0;
   }
   int v[5] = {0, 0, 0, 0, 0};  // rows of pulse 0, 1, 2; logits rows; attention units
   v[pulse] = nrow;
-  v[3] = lrows;
+  if (spec) v[0] += 1;
+  v[3] = lrows + (spec ? 1 : 0);
   v[4] = live ? 1 : 0;
   int total[5];
   scan_counts<5>(v, sh, total);
@@ -611,12 +655,13 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
     s.lrow_c = lrows ? lr0 : -1;
     AttnUnit un{};
     un.seq = b;
-    un.n = nrow;
+    un.n = nrow + (spec ? 1 : 0);
     un.pos0 = pos0;
     for (int i = 0; i < kMaxBlock; ++i) un.row[i] = i < nrow ? r0 + i : -1;
+    if (guess_row) s.lrow_s = lrows == nrow ? lr0 + nrow - 1 : lr0;
     for (int i = 0; i < nrow; ++i) {
       const int slot = slot0 + i;
-      const int lr = lrows ? lr0 + i : -1;
+      const int lr = lrows == nrow ? lr0 + i : (lrows && i == nrow - 1 ? lr0 : -1);
       a.rows[r0 + i] = RowDesc{b, slot, pulse, pos0 + i, s.blk[slot], lr, -1, 0};
       if (lr >= 0) {
         a.lrow_seq[lr] = b;
@@ -625,6 +670,22 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
         // distinct stream per (round, draft or verify, block row)
         a.lrow_ctr[lr] = (s.ctr * 2u + (s.blk_phase == 0 ? 0u : 1u)) * (uint32_t)kMaxBlock + slot;
       }
+    }
+    if (spec) {
+      // next round's first row: position after the block, the slot past the block's; its
+      // draw is the next round's first draft (that round's counter, seen tokens = this
+      // round's drafts and the guess)
+      const int r = base[0] + v[0] + (pulse == 0 ? nrow : 0);
+      const int lr = lr0 + lrows;
+      a.rows[r] = RowDesc{b, engine_slots(a.draft_len) - 1, 0, s.c_pos + nrow, s.s_tok, lr, -1, 0};
+      un.row[nrow] = r;
+      s.row_s = r;
+      s.lrow_s = lr;
+      a.lrow_seq[lr] = b;
+      for (int x = 0; x < kMaxExtra; ++x)
+        a.lrow_extra[(int64_t)lr * kMaxExtra + x] =
+            x < nrow - 1 ? s.blk[1 + x] : (x == nrow - 1 ? s.s_tok : -1);
+      a.lrow_ctr[lr] = ((s.ctr + 1u) * 2u) * (uint32_t)kMaxBlock;
     }
     a.units[v[4]] = un;
   }

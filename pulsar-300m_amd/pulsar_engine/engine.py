@@ -45,8 +45,11 @@ class HipEngine:
         self.batch = batch
         self.max_new = max_new
         self.draft_len = int(draft_len)
-        # rows of one sequence in a step
-        self.slots = self.draft_len + 1 if self.draft_len > 0 else 2
+        # rows of one sequence in a step: 2 in the exact schedule; the block (+ the next
+        # round's first row when it fits the 8 rows of an attention unit) in the draft-block
+        # mode (engine_slots in csrc/sample.h)
+        g = self.draft_len
+        self.slots = 2 if g <= 0 else (g + 2 if g + 2 <= 8 else g + 1)
         self.V = model.cfg.vocab_size
         stops = sorted({int(s) for s in stop_ids})
         if len(stops) > 8:

@@ -71,25 +71,37 @@ def _compare_block_passes(models, full_state, dtype, G, tol):
     eng.prefill(np.asarray(prompt)[None])
     errs = [("prefill", max_abs_rel(eng.logits(1)[0], ref_prefill))]
     cur = []  # tokens of the current round's block, by slot, as the draft rows reveal them
+    S = eng.slots
     for _ in range(200):
         if eng.state()[0, 0]:
             break
         eng.step(1)
-        rows = sorted(eng.rows(last=True).tolist(), key=lambda r: r[1])
+        rows = eng.rows(last=True).tolist()
         lg = eng.logits(len(rows))
+        groups = {}
         for r in rows:
-            slot, pulse, pos, tok, lrow = r[1], r[2], r[3], r[4], r[5]
-            if len(rows) == 1:
-                cur = cur[:slot] + [tok] if slot > 0 else [tok]
-                prefix = tuple(cur)
-            else:
-                prefix = tuple(x[4] for x in rows[:slot + 1])
-            # row `slot` of any oracle block at this position and pulse with the same
-            # tokens up to it (rows do not depend on later block tokens)
-            hit = [v for (p0, toks, k), v in table.items()
-                   if p0 == pos - slot and k == pulse and toks[:slot + 1] == prefix]
-            if hit:
-                errs.append(((pos, pulse, tok), max_abs_rel(lg[lrow], hit[0][slot])))
+            groups.setdefault(r[2], []).append(r)
+        for pulse, grp in sorted(groups.items()):
+            grp.sort(key=lambda r: r[1])
+            for r in grp:
+                slot, pos, tok, lrow = r[1], r[3], r[4], r[5]
+                if lrow < 0:
+                    continue
+                if len(grp) == 1:
+                    # a draft row, a one-row block, or (slot S - 1 beside a verify pass) the
+                    # next round's first row
+                    if slot == S - 1 and len(groups) > 1:
+                        slot = 0
+                    cur = cur[:slot] + [tok] if slot > 0 else [tok]
+                    prefix = tuple(cur)
+                else:
+                    prefix = tuple(x[4] for x in grp[:slot + 1])
+                # row `slot` of any oracle block at this position and pulse with the same
+                # tokens up to it (rows do not depend on later block tokens)
+                hit = [v for (p0, toks, k), v in table.items()
+                       if p0 == pos - slot and k == pulse and toks[:slot + 1] == prefix]
+                if hit:
+                    errs.append(((pos, pulse, tok), max_abs_rel(lg[lrow], hit[0][slot])))
     print(f"{dtype} G={G} block passes compared: {len(errs)}; worst: {max(e for _, e in errs):.3e}")
     bad = [(k, e) for k, e in errs if e > tol]
     assert not bad, bad[:5]
@@ -177,8 +189,12 @@ def test_bf16_block_sampled_acceptance_matches_draft_verify_overlap(models, full
                 # draft row of slot j: keep its logits for the verify's tests
                 draft_lg[(b, int(rs[0][1]))] = lg[int(rs[0][5])].copy()
                 continue
-            if int(rs[0][2]) != P - 1:
+            blk_rows = sorted((r for r in rs if int(r[2]) == P - 1), key=lambda r: int(r[1]))
+            # the next round's first row riding in the last verify step (pipelined rounds)
+            spec = [r for r in rs if int(r[2]) == 0 and int(r[1]) == eng.slots - 1]
+            if before[b, 21] != 1 or before[b, 22] != P - 1 or not blk_rows:
                 continue
+            rs = blk_rows
             blk = [int(r[4]) for r in rs]
             seen = [int(x) for x in prompts[b]] + toks_before[b]
             # tests 0 .. ran-1 of the block ran (each one only after every earlier draft of
@@ -195,6 +211,10 @@ def test_bf16_block_sampled_acceptance_matches_draft_verify_overlap(models, full
                 var += p * (1 - p)
                 n_tests += 1
             draft_lg = {k: v for k, v in draft_lg.items() if k[0] != b}
+            if spec:
+                # the next round's first draft, when the guess holds (else its own draft
+                # step overwrites this)
+                draft_lg[(b, 0)] = lg[int(spec[0][5])].copy()
     tests, accepted = eng.acceptance()
     sd = max(var, 1e-9) ** 0.5
     print(f"block tests {tests} (tracked {n_tests}), accepted {accepted}, "
