@@ -49,16 +49,17 @@ def test_fp32_block_greedy_streams_equal_oracle(models, full_state, G):
     assert got == want
 
 
-def _compare_block_passes(models, full_state, dtype, G, tol):
+def _compare_block_passes(models, full_state, dtype, G, tol, prompt=None, n_new=12):
     from oracle import pulsar_ref as R
     from pulsar_engine import weights as W
     from pulsar_engine.engine import HipEngine
 
     cfg = full_state[0]
-    prompt = W.uniform_ids(70, "block_pass_prompt", 40, cfg.vocab_size).tolist()
+    if prompt is None:
+        prompt = W.uniform_ids(70, "block_pass_prompt", 40, cfg.vocab_size).tolist()
     ref = _oracle(full_state, dtype)
     ref.trace = []
-    list(ref.block_speculative_ids(prompt, 12, 0.0, 1.0, 10.0, G))
+    list(ref.block_speculative_ids(prompt, n_new, 0.0, 1.0, 10.0, G))
     table = {}
     for t in ref.trace:
         if t[0] == "block":
@@ -66,8 +67,9 @@ def _compare_block_passes(models, full_state, dtype, G, tol):
     cache = R.RefKVCache(cfg)
     ref_prefill = ref.prefill(torch.as_tensor(prompt).view(1, -1), cache).float().numpy().reshape(-1)
 
-    eng = HipEngine(models[dtype], batch=1, max_prompt=len(prompt), max_new=12, temperature=0.0,
-                    repetition_penalty=10.0, stop_ids=[], all_logits=True, draft_len=G)
+    eng = HipEngine(models[dtype], batch=1, max_prompt=len(prompt), max_new=n_new,
+                    temperature=0.0, repetition_penalty=10.0, stop_ids=[], all_logits=True,
+                    draft_len=G)
     eng.prefill(np.asarray(prompt)[None])
     errs = [("prefill", max_abs_rel(eng.logits(1)[0], ref_prefill))]
     cur = []  # tokens of the current round's block, by slot, as the draft rows reveal them

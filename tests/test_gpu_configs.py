@@ -6,6 +6,9 @@
 * c5-like: 256 sequences of 512-token Zipf(1.1) prompts with router weights x4 (skewed
   routing, capacity drops in prefill): every pass of one sequence against the oracle in
   bf16, greedy self-speculative == plain over the whole batch, batch == single.
+* The same two shapes in the draft-block mode at the configs' draft lengths (c4: 4, c5: 6,
+  2048 rows per step at batch 256): a sequence decodes the same alone as in the batch; at
+  c5 every pass of one sequence against the oracle's block restatement in bf16.
 * Capacity with more assignments per (sequence, expert) than the kernel stages in LDS
   (4200 tokens all routed to experts 0-3): prefill logits against the oracle in fp32.
 """
@@ -75,6 +78,49 @@ def test_c5_batch_256_spec_equals_plain_and_batch_equals_single(full_state, c5_m
     prompts = [W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size).tolist() for b in range(256)]
     spec = _spec_plain_single(c5_model[1], prompts, 8, singles=[0, 255])
     print("c5 first tokens", [s[:4] for s in spec[:4]])
+
+
+def _block_batch_single(model, prompts, n_new, G, singles):
+    from pulsar_engine.engine import PulsarInferenceEngine
+
+    eng = PulsarInferenceEngine(model)
+    kw = dict(max_new_tokens=n_new, temperature=0.0, repetition_penalty=10.0, stop_ids=[0, 2],
+              draft_len=G)
+    out = eng.generate_ids(prompts, **kw)
+    for i in singles:
+        assert eng.generate_ids([prompts[i]], **kw)[0] == out[i], i
+    assert all(len(s) == n_new for s in out)
+    return out
+
+
+def test_c4_long_context_draft_block_batch_equals_single(models, full_state):
+    from pulsar_engine import weights as W
+
+    cfg = full_state[0]
+    prompts = [W.uniform_ids(90 + b, "c4_prompt", 32768, cfg.vocab_size).tolist() for b in range(4)]
+    out = _block_batch_single(models[torch.bfloat16], prompts, 24, 4, singles=[0])
+    print("c4 draft-block first tokens", [s[:6] for s in out])
+
+
+def test_c5_draft6_block_passes_match_oracle(full_state, c5_model):
+    from test_gpu_block import _compare_block_passes
+
+    from pulsar_engine import weights as W
+
+    cfg = full_state[0]
+    st, model = c5_model
+    prompt = W.zipf_ids(5, "c5_prompt_0", 512, cfg.vocab_size).tolist()
+    _compare_block_passes({torch.bfloat16: model}, (cfg, st), torch.bfloat16, 6, 2e-2,
+                          prompt=prompt, n_new=8)
+
+
+def test_c5_batch_256_draft6_batch_equals_single(full_state, c5_model):
+    from pulsar_engine import weights as W
+
+    cfg = full_state[0]
+    prompts = [W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size).tolist() for b in range(256)]
+    out = _block_batch_single(c5_model[1], prompts, 8, 6, singles=[0, 255])
+    print("c5 draft-block first tokens", [s[:4] for s in out[:4]])
 
 
 def test_prefill_capacity_beyond_lds_staging_matches_oracle(full_state):
