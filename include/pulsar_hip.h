@@ -125,6 +125,84 @@ int pulsar_moe_slots_from_order(const int64_t* flat_e, const int64_t* order, int
                                 int64_t* counts, int64_t M, int64_t E, int64_t C,
                                 hipStream_t stream);
 
+/* ---------------------------------------------------------------------------------
+ * Backward ops of the same surface (the training path through model.forward).
+ * fp32 arithmetic; activation gradients in the activation dtype, norm / conv weight
+ * gradients fp32 (zeroed by the call, then summed with atomics, so their last bits
+ * depend on scheduling order).
+ * ------------------------------------------------------------------------------- */
+
+/* rmsnorm_backward(dy, x, weight, rsqrt) -> (dx, dweight)
+ * Replaces csrc/pulsar_cuda.cpp:203 / csrc/kernels.cu:268-310.
+ * dy, x, dx: [rows, dim] contiguous; w, dw: fp32 [dim]; rsqrt: the forward's fp32 [rows].
+ * dim <= 8192. */
+int pulsar_rmsnorm_backward(const void* dy, const void* x, const float* w, const float* rsqrt,
+                            void* dx, float* dw, int64_t rows, int64_t dim, int dtype,
+                            hipStream_t stream);
+
+/* qk_rmsnorm_rope_backward(dy, x, weight, rsqrt_in, cos, sin, T) -> (dx, dweight)
+ * Replaces csrc/pulsar_cuda.cpp:227-228 / csrc/kernels.cu:2767-2835.
+ * dy: contiguous [B,H,T,64]; x: strides (sB, sH, sT, 1); dx: strides (dB, dH, dT, 1);
+ * w, dw: fp32 [H,64]; rsqrt: fp32 [B*H*T]; cos, sin: fp32 [T,32]. */
+int pulsar_qk_rmsnorm_rope_backward(const void* dy, const void* x, int64_t sB, int64_t sH,
+                                    int64_t sT, void* dx, int64_t dB, int64_t dH, int64_t dT,
+                                    int64_t B, int64_t H, int64_t T, int64_t head_dim,
+                                    const float* w, const float* rsqrt, const float* cos,
+                                    const float* sin, float* dw, int dtype,
+                                    hipStream_t stream);
+
+/* fused_attn_gate_backward(grad_out, attn_out, gate_logits) -> (d_attn, d_gate)
+ * Replaces csrc/pulsar_cuda.cpp:232-233 / csrc/kernels.cu:2960-2992.
+ * grad_out: [B,T,H*64]; attn, d_attn: [B,H,T,64]; gate_logits, d_gate: fp32 [B,T,H]. */
+int pulsar_fused_attn_gate_backward(const void* grad_out, const void* attn,
+                                    const float* gate_logits, void* d_attn, float* d_gate,
+                                    int64_t B, int64_t H, int64_t T, int64_t head_dim,
+                                    int dtype, hipStream_t stream);
+
+/* fused_swiglu_backward(dout, gu, d_ff) -> dgu = [d_gate | d_up]
+ * Replaces csrc/pulsar_cuda.cpp:210 / csrc/kernels.cu:865-900.
+ * dout: [rows, d_ff]; gu, dgu: [rows, 2*d_ff]. */
+int pulsar_fused_swiglu_backward(const void* dout, const void* gu, void* dgu, int64_t rows,
+                                 int64_t d_ff, int dtype, hipStream_t stream);
+
+/* moe_dispatch_backward(d_expert_inputs, topk_idx, token_to_slot, N, D) -> dx [N,D]
+ * Replaces csrc/pulsar_cuda.cpp:216 / csrc/kernels.cu:1607-1631.
+ * dx[t] = sum of d_expert_inputs[e, slot] over t's kept assignments, in top-k order. */
+int pulsar_moe_dispatch_backward(const void* d_expert_inputs, const int64_t* topk_idx,
+                                 const int32_t* slots, void* dx, int64_t N, int64_t D,
+                                 int64_t K, int64_t E, int64_t C, int dtype,
+                                 hipStream_t stream);
+
+/* moe_combine_backward(d_routed_out, expert_outputs, topk_idx, topk_weights, token_to_slot)
+ *   -> (d_expert_outputs [E,C,D], d_topk_weights bf16 [N,K])
+ * Replaces csrc/pulsar_cuda.cpp:220-222 / csrc/kernels.cu:1666-1711.
+ * Rows of d_expert_outputs no kept assignment names are zero; dropped assignments get
+ * d_topk_weights = 0. Weights are bf16 words. */
+int pulsar_moe_combine_backward(const void* d_routed_out, const void* expert_outputs,
+                                const int64_t* topk_idx, const uint16_t* topk_w_bf16,
+                                const int32_t* slots, void* d_expert_outputs,
+                                uint16_t* d_topk_w_bf16, int64_t N, int64_t D, int64_t K,
+                                int64_t E, int64_t C, int dtype, hipStream_t stream);
+
+/* moe_router_topk_backward(d_topk_weights, logits, topk_idx, z_loss_weight, d_z_loss,
+ *                          d_probs_mean) -> d_logits (logits' dtype)
+ * Replaces csrc/pulsar_cuda.cpp:267-269 / csrc/kernels.cu:2493-2578.
+ * Adjoint of pulsar_moe_router_topk_forward with the selection held fixed: through the
+ * weight normalisation, the z-loss (scaled by d_z_loss[0] when given) and probs_mean
+ * (d_probs_mean fp32 [E], nullable), then the centring. E <= 32, K <= 8. */
+int pulsar_moe_router_topk_backward(const uint16_t* d_topk_w_bf16, const void* logits,
+                                    int logits_dtype, const int64_t* topk_idx,
+                                    float z_loss_weight, const float* d_z_loss,
+                                    const float* d_probs_mean, void* d_logits, int64_t N,
+                                    int64_t E, int64_t K, hipStream_t stream);
+
+/* causal_depthwise_conv1d_k4_backward(dout, x, weight) -> (dx, dweight)
+ * Replaces csrc/pulsar_cuda.cpp:277-279 / csrc/kernels.cu:3693-3732.
+ * dout, x, dx: contiguous [B,T,D]; w, dw: fp32 [D,4]. */
+int pulsar_causal_conv1d_k4_backward(const void* dout, const void* x, const float* w, void* dx,
+                                     float* dw, int64_t B, int64_t T, int64_t D, int dtype,
+                                     hipStream_t stream);
+
 
 /* ---------------------------------------------------------------------------------
  * Decode engine: prefill + self-speculative decode of a batch of sequences.

@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "pulsar_cuda", "libpulsar_hip.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["ops.hip", "gemm.hip", "rows.hip", "sample.hip", "engine.hip"]
+SOURCES = ["ops.hip", "gemm.hip", "rows.hip", "sample.hip", "engine.hip", "backward.hip"]
 ARCH = os.environ.get("PULSAR_HIP_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

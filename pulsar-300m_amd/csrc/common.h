@@ -194,6 +194,18 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 
+inline unsigned blocks_for(int64_t n, int threads) {
+  return (unsigned)((n + threads - 1) / threads);
+}
+
+// Runs f(float{}) or f(bf16{}) for the activation dtype.
+template <typename F>
+int dispatch_dtype(int dtype, F&& f) {
+  if (dtype == PULSAR_F32) return f(float{});
+  if (dtype == PULSAR_BF16) return f(bf16{});
+  return fail(PULSAR_ERR_INVALID, "dtype must be PULSAR_F32 or PULSAR_BF16");
+}
+
 }  // namespace pulsar
 
 #define PULSAR_CHECK_HIP(expr)                                                      \

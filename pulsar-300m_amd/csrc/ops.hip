@@ -309,16 +309,6 @@ __global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
   if (i < n) p[i] = v;
 }
 
-inline unsigned blocks_for(int64_t n, int threads) {
-  return (unsigned)((n + threads - 1) / threads);
-}
-
-template <typename F>
-int dispatch_dtype(int dtype, F&& f) {
-  if (dtype == PULSAR_F32) return f(float{});
-  if (dtype == PULSAR_BF16) return f(bf16{});
-  return fail(PULSAR_ERR_INVALID, "dtype must be PULSAR_F32 or PULSAR_BF16");
-}
 
 }  // namespace pulsar
 

@@ -6,8 +6,9 @@ GPU, outputs are new tensors allocated on the input's device, invalid arguments 
 RuntimeError (the reference's TORCH_CHECK). Work is enqueued on torch's current stream.
 Beyond the reference, every op also accepts fp32 activations.
 
-Only the forward ops of the decode path are provided; backward and optimizer ops of the
-training path are not part of this module.
+The forward ops of the decode path and the backward ops of the training path through
+model.forward are provided; the loss (softcapped cross-entropy) and optimizer ops are not
+part of this module.
 """
 
 from __future__ import annotations
@@ -21,6 +22,9 @@ __all__ = [
     "rmsnorm_forward", "rope_forward", "qk_rmsnorm_rope_forward", "fused_attn_gate_forward",
     "causal_depthwise_conv1d_k4_forward", "fused_swiglu_forward", "moe_router_topk_forward",
     "moe_dispatch_forward", "moe_combine_forward", "moe_slots_from_order",
+    "rmsnorm_backward", "qk_rmsnorm_rope_backward", "fused_attn_gate_backward",
+    "causal_depthwise_conv1d_k4_backward", "fused_swiglu_backward", "moe_router_topk_backward",
+    "moe_dispatch_backward", "moe_combine_backward",
 ]
 
 _LIB = _lib.load()
@@ -245,3 +249,210 @@ def moe_slots_from_order(flat_e: torch.Tensor, order: torch.Tensor, num_experts:
                                                 _p(counts), M, num_experts, capacity,
                                                 _stream(flat_e)))
     return slots, counts
+
+
+# ---------------------------------------------------------------------------
+# Backward ops (training path)
+# ---------------------------------------------------------------------------
+
+def _same_code(a: torch.Tensor, b: torch.Tensor, na: str, nb: str) -> int:
+    code = _dtype_code(a, na)
+    _req(b.dtype == a.dtype, f"{nb} must have the dtype of {na}")
+    return code
+
+
+def rmsnorm_backward(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                     rsqrt: torch.Tensor):
+    """[dx, dweight] of rmsnorm_forward given its saved rsqrt (csrc/kernels.cu:268-310)."""
+    _cuda(x, "x")
+    _cuda(dy, "dy")
+    _req(x.is_contiguous(), "x must be a contiguous CUDA tensor")
+    _req(weight.dtype == torch.float32, "weight must be float32")
+    code = _same_code(x, dy, "x", "dy")
+    dim = x.shape[-1]
+    rows = x.numel() // dim if dim else 0
+    dx = torch.empty_like(x)
+    dw = torch.zeros_like(weight)
+    if rows == 0:
+        return [dx, dw]
+    _req(dim <= 8192, f"rmsnorm backward supports dim <= 8192, got dim {dim}")
+    dyc = dy.contiguous()
+    rs = rsqrt.float().contiguous()
+    _lib.check(_LIB.pulsar_rmsnorm_backward(_p(dyc), _p(x), _p(weight.contiguous()), _p(rs),
+                                            _p(dx), _p(dw), rows, dim, code, _stream(x)))
+    return [dx, dw]
+
+
+def qk_rmsnorm_rope_backward(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                             rsqrt_in: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                             T: int):
+    """[dx, dweight] of qk_rmsnorm_rope_forward (csrc/kernels.cu:2767-2835). dx takes the
+    layout of a [B,T,H,64] buffer seen as [B,H,T,64] when x is such a view (head stride
+    below time stride), else x's shape, contiguous."""
+    head_dim = x.shape[-1]
+    _req(head_dim == 64, f"qk_rmsnorm_rope requires head_dim == 64, got {head_dim}")
+    _cuda(dy, "dy")
+    _req(dy.is_contiguous(), "dy must be contiguous CUDA")
+    _cuda(x, "x")
+    _req(x.stride(-1) == 1, "x must have stride(-1) == 1")
+    code = _same_code(x, dy, "x", "dy")
+    _req(weight.is_cuda and weight.is_contiguous(), "weight must be contiguous CUDA")
+    _req(weight.dtype == torch.float32, "weight must be float32")
+    H = weight.shape[0]
+    n = x.numel() // head_dim
+    if x.dim() == 4:
+        sB, sH, sT = x.stride(0), x.stride(1), x.stride(2)
+    else:
+        sB, sH, sT = H * T * 64, T * 64, 64
+    B = n // (H * T) if H * T else 0
+    if sH < sT and T > 1:
+        dx = torch.empty((B, T, H, 64), dtype=x.dtype, device=x.device).transpose(1, 2)
+        dB, dH, dT = dx.stride(0), dx.stride(1), dx.stride(2)
+    else:
+        dx = torch.empty_like(x, memory_format=torch.contiguous_format)
+        if dx.dim() == 4:
+            dB, dH, dT = dx.stride(0), dx.stride(1), dx.stride(2)
+        else:
+            dB, dH, dT = H * T * 64, T * 64, 64
+    dw = torch.zeros_like(weight)
+    if n:
+        cf = cos.float().contiguous()
+        sf = sin.float().contiguous()
+        rs = rsqrt_in.float().contiguous()
+        _lib.check(_LIB.pulsar_qk_rmsnorm_rope_backward(
+            _p(dy), _p(x), sB, sH, sT, _p(dx), dB, dH, dT, B, H, T, head_dim, _p(weight), _p(rs),
+            _p(cf), _p(sf), _p(dw), code, _stream(x)))
+    return [dx, dw]
+
+
+def fused_attn_gate_backward(grad_out: torch.Tensor, attn_out: torch.Tensor,
+                             gate_logits: torch.Tensor):
+    """[d_attn_out, d_gate_logits] of fused_attn_gate_forward (csrc/kernels.cu:2960-2992);
+    d_gate_logits in gate_logits' dtype."""
+    B, H, T, D = attn_out.shape
+    _req(D == 64, f"fused_attn_gate requires head_dim == 64, got {D}")
+    _cuda(grad_out, "grad_out")
+    _req(grad_out.is_contiguous(), "grad_out must be contiguous CUDA")
+    _cuda(attn_out, "attn_out")
+    _req(attn_out.is_contiguous(), "attn_out must be contiguous CUDA")
+    code = _same_code(attn_out, grad_out, "attn_out", "grad_out")
+    gl = gate_logits.float().contiguous()
+    d_attn = torch.empty_like(attn_out)
+    d_gate = torch.empty((B, T, H), dtype=torch.float32, device=attn_out.device)
+    if d_attn.numel():
+        _lib.check(_LIB.pulsar_fused_attn_gate_backward(_p(grad_out), _p(attn_out), _p(gl),
+                                                        _p(d_attn), _p(d_gate), B, H, T, D, code,
+                                                        _stream(attn_out)))
+    return [d_attn, d_gate.to(gate_logits.dtype)]
+
+
+def causal_depthwise_conv1d_k4_backward(dout: torch.Tensor, x: torch.Tensor,
+                                        weight: torch.Tensor):
+    """[dx, dweight] of causal_depthwise_conv1d_k4_forward (csrc/kernels.cu:3693-3732)."""
+    _req(dout.is_cuda and x.is_cuda and weight.is_cuda, "Inputs must be CUDA tensors")
+    _req(dout.is_contiguous() and x.is_contiguous() and weight.is_contiguous(),
+         "Inputs must be contiguous")
+    code = _same_code(x, dout, "x", "dout")
+    _req(weight.dtype == torch.float32, "weight must be float32")
+    B, T, D = x.shape
+    dx = torch.empty_like(x)
+    dw = torch.zeros_like(weight)
+    if B * T == 0:
+        return [dx, dw]
+    _lib.check(_LIB.pulsar_causal_conv1d_k4_backward(_p(dout), _p(x), _p(weight), _p(dx), _p(dw),
+                                                      B, T, D, code, _stream(x)))
+    return [dx, dw]
+
+
+def fused_swiglu_backward(dout: torch.Tensor, gu: torch.Tensor, d_ff: int) -> torch.Tensor:
+    """dgu = [d_gate | d_up] of fused_swiglu_forward (csrc/kernels.cu:865-900)."""
+    _cuda(gu, "gu")
+    _req(gu.is_contiguous(), "gu must be a contiguous CUDA tensor")
+    _req(dout.is_contiguous(), "dout must be contiguous")
+    code = _same_code(gu, dout, "gu", "dout")
+    dgu = torch.empty_like(gu)
+    rows = gu.numel() // (2 * d_ff) if d_ff else 0
+    if rows:
+        _lib.check(_LIB.pulsar_fused_swiglu_backward(_p(dout), _p(gu), _p(dgu), rows, d_ff, code,
+                                                     _stream(gu)))
+    return dgu
+
+
+def moe_router_topk_backward(d_topk_weights: torch.Tensor, logits: torch.Tensor,
+                             topk_idx: torch.Tensor, z_loss_weight: float = 1e-4,
+                             d_z_loss=None, d_probs_mean=None) -> torch.Tensor:
+    """d_logits of moe_router_topk_forward with the selection held fixed
+    (csrc/kernels.cu:2493-2578)."""
+    for t, n in ((d_topk_weights, "d_topk_weights"), (logits, "logits"), (topk_idx, "topk_idx")):
+        _cuda(t, n)
+        _req(t.is_contiguous(), f"{n} must be contiguous")
+    _req(d_topk_weights.dtype == torch.bfloat16, "d_topk_weights must be bfloat16")
+    _req(topk_idx.dtype == torch.int64, "topk_idx must be int64")
+    _req(logits.dtype in (torch.float32, torch.bfloat16), "logits must be float32 or bfloat16")
+    N, E = logits.shape
+    K = topk_idx.shape[1]
+    _req(E <= 32, f"moe_router_topk_backward_cuda supports E <= 32, got {E}")
+    _req(0 < K <= 8 and K <= E, f"top_k must be in [1, min(8, E)], got {K}")
+    _req(tuple(d_topk_weights.shape) == (N, K), "d_topk_weights shape mismatch")
+    if d_z_loss is not None:
+        _cuda(d_z_loss, "d_z_loss")
+        _req(d_z_loss.dtype == torch.float32, "d_z_loss must be float32")
+    if d_probs_mean is not None:
+        _cuda(d_probs_mean, "d_probs_mean")
+        _req(d_probs_mean.dtype == torch.float32, "d_probs_mean must be float32")
+        _req(d_probs_mean.numel() == E, "d_probs_mean numel must match E")
+        d_probs_mean = d_probs_mean.contiguous()
+    d_logits = torch.empty_like(logits)
+    if N:
+        _lib.check(_LIB.pulsar_moe_router_topk_backward(
+            _p(d_topk_weights), _p(logits), _dtype_code(logits, "logits"), _p(topk_idx),
+            float(z_loss_weight), _p(d_z_loss), _p(d_probs_mean), _p(d_logits), N, E, K,
+            _stream(logits)))
+    return d_logits
+
+
+def moe_dispatch_backward(d_expert_inputs: torch.Tensor, topk_idx: torch.Tensor,
+                          token_to_slot: torch.Tensor, N: int, D: int) -> torch.Tensor:
+    """dx [N, D]: per token, the sum of its kept slots' gradients (csrc/kernels.cu:1607-1631)."""
+    for t, n in ((d_expert_inputs, "d_expert_inputs"), (topk_idx, "topk_idx"),
+                 (token_to_slot, "token_to_slot")):
+        _cuda(t, n)
+        _req(t.is_contiguous(), f"{n} must be contiguous")
+    _req(topk_idx.dtype == torch.int64, "topk_idx must be int64")
+    _req(token_to_slot.dtype == torch.int32, "token_to_slot must be int32")
+    E, C, D_ = d_expert_inputs.shape
+    _req(D_ == D, "d_expert_inputs last dimension must be D")
+    K = topk_idx.shape[1]
+    code = _dtype_code(d_expert_inputs, "d_expert_inputs")
+    dx = torch.empty((N, D), dtype=d_expert_inputs.dtype, device=d_expert_inputs.device)
+    if N:
+        _lib.check(_LIB.pulsar_moe_dispatch_backward(
+            _p(d_expert_inputs), _p(topk_idx), _p(token_to_slot), _p(dx), N, D, K, E, C, code,
+            _stream(d_expert_inputs)))
+    return dx
+
+
+def moe_combine_backward(d_routed_out: torch.Tensor, expert_outputs: torch.Tensor,
+                         topk_idx: torch.Tensor, topk_weights: torch.Tensor,
+                         token_to_slot: torch.Tensor, expert_counts=None):
+    """[d_expert_outputs, d_topk_weights] of moe_combine_forward (csrc/kernels.cu:1666-1711).
+    expert_counts is accepted for signature parity: every slot a kept assignment does not
+    name is zeroed either way."""
+    E, C, D = expert_outputs.shape
+    N, K = topk_idx.shape
+    for t, n in ((d_routed_out, "d_routed_out"), (expert_outputs, "expert_outputs"),
+                 (topk_idx, "topk_idx"), (token_to_slot, "token_to_slot")):
+        _cuda(t, n)
+        _req(t.is_contiguous(), f"{n} must be contiguous")
+    if expert_counts is not None:
+        _cuda(expert_counts, "expert_counts")
+        _req(expert_counts.dtype == torch.int64, "expert_counts must be int64")
+        _req(expert_counts.numel() >= E, "expert_counts must have at least E elements")
+    code = _same_code(expert_outputs, d_routed_out, "expert_outputs", "d_routed_out")
+    w = topk_weights.to(torch.bfloat16).contiguous()
+    d_eo = torch.empty_like(expert_outputs)
+    d_w = torch.empty((N, K), dtype=torch.bfloat16, device=expert_outputs.device)
+    _lib.check(_LIB.pulsar_moe_combine_backward(
+        _p(d_routed_out), _p(expert_outputs), _p(topk_idx), _p(w), _p(token_to_slot), _p(d_eo),
+        _p(d_w), N, D, K, E, C, code, _stream(expert_outputs)))
+    return [d_eo, d_w.to(topk_weights.dtype)]

@@ -88,6 +88,21 @@ _PROTOS = {
     "pulsar_moe_combine_forward": [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
                                    _c_i64, ctypes.c_int, _vp],
     "pulsar_moe_slots_from_order": [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp],
+    "pulsar_rmsnorm_backward": [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, ctypes.c_int, _vp],
+    "pulsar_qk_rmsnorm_rope_backward": [_vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64,
+                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp,
+                                        _vp, _vp, ctypes.c_int, _vp],
+    "pulsar_fused_attn_gate_backward": [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                                        ctypes.c_int, _vp],
+    "pulsar_fused_swiglu_backward": [_vp, _vp, _vp, _c_i64, _c_i64, ctypes.c_int, _vp],
+    "pulsar_moe_dispatch_backward": [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                     ctypes.c_int, _vp],
+    "pulsar_moe_combine_backward": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64,
+                                    _c_i64, _c_i64, ctypes.c_int, _vp],
+    "pulsar_moe_router_topk_backward": [_vp, _vp, ctypes.c_int, _vp, _c_f32, _vp, _vp, _vp,
+                                        _c_i64, _c_i64, _c_i64, _vp],
+    "pulsar_causal_conv1d_k4_backward": [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64,
+                                         ctypes.c_int, _vp],
     "pulsar_engine_create": [ctypes.POINTER(PulsarModelDesc), ctypes.POINTER(PulsarEngineConfig),
                              ctypes.POINTER(_vp)],
     "pulsar_engine_destroy": [_vp],
