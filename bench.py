@@ -215,12 +215,19 @@ def verify_microbench(model, cfg, es, args):
     att_ms, att_n = prof["attention"]
     att_bytes = by_class["attention"] / max(att_n, 1)
     att_s = att_ms / max(att_n, 1) / 1e3
-    # query columns of a unit (4 per row) and 64-key blocks per wave (4 for caches past
-    # 16 splits of 256 keys)
+    # query columns of a unit (4 per row) and 64-key blocks per wave: caches past 16 splits
+    # of 256 keys take 4 in sliding-window layers and 8 in global layers, 1 otherwise
     cols = 8 if n <= 2 else 16 if n <= 4 else 32
-    bpw = 4 if (ctx + 16 + 63 + 255) // 256 > 16 else 1
-    att_kernel = f"attn_decode_unit_kernel<{cols}, {bpw}>"
-    att_traffic = recorded_traffic([att_kernel], VERIFY_TRAFFIC_PROFILE)
+    lng = (ctx + 16 + 63 + 255) // 256 > 16
+    n_loc = sum(1 for i in range(cfg.n_core) if cfg.is_local(i))
+    n_glob = cfg.n_core - n_loc
+    k_loc = f"attn_decode_unit_kernel<{cols}, {4 if lng else 1}>"
+    k_glob = f"attn_decode_unit_kernel<{cols}, {8 if lng else 1}>"
+    att_kernels = sorted({k_loc, k_glob})
+    t_loc = recorded_traffic([k_loc], VERIFY_TRAFFIC_PROFILE)
+    t_glob = recorded_traffic([k_glob], VERIFY_TRAFFIC_PROFILE)
+    att_traffic = ((n_loc * t_loc + n_glob * t_glob) / cfg.n_core
+                   if t_loc is not None and t_glob is not None else None)
     per_class = {c: {"ms": round(v[0], 3), "launches": v[1],
                      "us_per_launch": round(v[0] / v[1] * 1e3, 2),
                      "GB_per_s": round(by_class.get(c, 0.0) / max(v[0], 1e-9) / 1e6, 1)}
@@ -236,13 +243,14 @@ def verify_microbench(model, cfg, es, args):
         "kv_bytes": int(by_class["attention"]),
         "hbm_frac": round(total / (ms / 1e3) / HBM_PEAK, 4),
         "roofline": {"bound": "hbm", "kernel": "attention",
-                     "kernels": [att_kernel],
+                     "kernels": att_kernels,
                      "achieved": round(att_bytes / att_s / 1e9, 1), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(att_bytes / att_s / HBM_PEAK, 4),
                      "bytes_per_launch": int(att_bytes), "avg_launch_us": round(att_s * 1e6, 2),
                      "traffic": round(att_traffic / 1e6, 3) if att_traffic else None,
                      "traffic_unit": "MB per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
-                                     "copy-calibrated)"},
+                                     "copy-calibrated, averaged over the layer types by "
+                                     "launch count)"},
         "kernel_profile": per_class,
     }
 

@@ -67,11 +67,15 @@ struct Engine {
 
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
+  hipGraphExec_t exec_multi = nullptr;  // kGraphSteps steps in one graph
+  hipGraph_t graph_multi = nullptr;
   hipStream_t capture_stream = nullptr;  // graphs are captured here (never the legacy stream)
 
   ~Engine() {
     if (exec) hipGraphExecDestroy(exec);
     if (graph) hipGraphDestroy(graph);
+    if (exec_multi) hipGraphExecDestroy(exec_multi);
+    if (graph_multi) hipGraphDestroy(graph_multi);
     if (vexec) hipGraphExecDestroy(vexec);
     if (vgraph) hipGraphDestroy(vgraph);
     if (capture_stream) hipStreamDestroy(capture_stream);
@@ -1104,11 +1108,18 @@ int verify(Engine& e, const int32_t* host_tokens, int n, int use_graph, hipStrea
   return PULSAR_OK;
 }
 
-// Capture one step into a graph (on the engine's own stream; launched on the caller's).
-int capture_step(Engine& e, hipGraph_t* graph, hipGraphExec_t* exec) {
+// Steps per graph launch of runs of steps. A step is about 70 kernel nodes; the host cost
+// of launching a graph can approach the step's GPU time on a slow host, so runs of steps
+// launch kGraphSteps of them per graph (the step's work is decided on the device, so
+// consecutive steps capture into one graph unchanged).
+constexpr int kGraphSteps = 4;
+
+// Capture n_steps steps into a graph (on the engine's own stream; launched on the caller's).
+int capture_step(Engine& e, int n_steps, hipGraph_t* graph, hipGraphExec_t* exec) {
   hipStream_t cs = e.capture_stream;
   PULSAR_CHECK_HIP(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
-  const int rc = enqueue_step(e, cs);
+  int rc = PULSAR_OK;
+  for (int i = 0; i < n_steps && rc == PULSAR_OK; ++i) rc = enqueue_step(e, cs);
   hipGraph_t gr = nullptr;
   const hipError_t ce = hipStreamEndCapture(cs, &gr);
   if (rc != PULSAR_OK) {
@@ -1131,8 +1142,14 @@ int step(Engine& e, int n, int use_graph, hipStream_t s) {
     }
     return PULSAR_OK;
   }
-  if (!e.exec) PULSAR_TRY(capture_step(e, &e.graph, &e.exec));
-  for (int i = 0; i < n; ++i) PULSAR_CHECK_HIP(hipGraphLaunch(e.exec, s));
+  if (!e.exec) PULSAR_TRY(capture_step(e, 1, &e.graph, &e.exec));
+  int i = 0;
+  if (n >= kGraphSteps) {
+    if (!e.exec_multi) PULSAR_TRY(capture_step(e, kGraphSteps, &e.graph_multi, &e.exec_multi));
+    for (; i + kGraphSteps <= n; i += kGraphSteps)
+      PULSAR_CHECK_HIP(hipGraphLaunch(e.exec_multi, s));
+  }
+  for (; i < n; ++i) PULSAR_CHECK_HIP(hipGraphLaunch(e.exec, s));
   return PULSAR_OK;
 }
 

@@ -133,10 +133,37 @@ struct QKPostArgs {
   KVDesc kv;
 };
 
+// One layer's caches, resolved on the host (the kernel reads them straight from its
+// arguments instead of indexing the per-layer pointer arrays by layer).
+struct KVLayer {
+  const void* k;
+  const void* v;
+  int lcap, max_pages;
+};
+
+__device__ __forceinline__ KVBlock kv_block_layer(const KVLayer& c, bool local, int Hkv, int b,
+                                                  int g, int kb) {
+  KVBlock r;
+  if (local) {
+    const int64_t bg = (int64_t)b * Hkv + g;
+    const int ring = kb % c.lcap;
+    r.k0 = (bg * c.lcap + ring) * kHeadDim;
+    r.v0 = bg * kHeadDim * c.lcap + ring;
+    r.vstride = c.lcap;
+  } else {
+    const int64_t pg = ((int64_t)b * c.max_pages + kb / kPage) * Hkv + g;
+    r.k0 = pg * kPage * kHeadDim;
+    r.v0 = pg * kHeadDim * kPage;
+    r.vstride = kPage;
+  }
+  return r;
+}
+
 struct AttnArgs {
   const StepCtl* ctl;
   const RowDesc* rows;
   const AttnUnit* units;  // decode, matrix-core path: units of the step (ctl->n_units)
+  KVLayer kl;             // decode, matrix-core path: set by launch_attn_decode
   const void* qkv;
   int64_t ldq;
   const void* gate;  // [rows][H] T

@@ -539,7 +539,7 @@ __device__ __forceinline__ int unit_row(const AttnUnit& un, int z) {
 // Last split block of (unit u, kv head g): merge the split partials (device-coherent loads),
 // normalise, round as the SDPA output and apply the head gate. Query column c = 4 z + h
 // (unit row z, head h of the group); a thread takes two dims of one column at a time.
-constexpr int kMergeChunk = 8;  // split partials loaded per round trip
+constexpr int kMergeChunk = 16;  // split partials loaded per round trip
 template <int COLS>
 __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int g,
                                                   const AttnUnit& un, int nsplit) {
@@ -638,8 +638,17 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   __shared__ float wm[kUnitWaves][COLS], wl[kUnitWaves][COLS];
   __shared__ float wo[kUnitWaves][COLS][65];
   const int u = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
-  if (u >= a.ctl->n_units) return;
+  // the unit descriptor is read together with the unit count (grid.x never exceeds the
+  // units array), so the two loads share one round trip; the empty asm keeps the compiler
+  // from sinking the descriptor load below the exit branch
+  const int n_units = a.ctl->n_units;
   const AttnUnit un = a.units[u];
+  asm volatile("" ::"s"(un.seq), "s"(un.n), "s"(un.pos0), "s"(un.row[0]), "s"(un.row[1]),
+               "s"(un.row[2]), "s"(un.row[3]), "s"(un.row[4]), "s"(un.row[5]), "s"(un.row[6]),
+               "s"(un.row[7]));
+  asm volatile("" ::"s"(a.kl.k), "s"(a.kl.v), "s"(a.kl.lcap), "s"(a.kl.max_pages),
+               "s"(a.is_local), "s"(a.window), "s"(a.Hkv), "s"(a.qkv), "s"(a.ldq));
+  if (u >= n_units) return;
   int base, uhi;
   unit_range(a, un, base, uhi);
   const int nsplit = (uhi + 1 - base + SPLIT - 1) / SPLIT;
@@ -647,8 +656,8 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m16 = lane & 15, kq = lane >> 4;
   const attn_bf16x8 zero = {};
-  const bf16* Kc = reinterpret_cast<const bf16*>(a.kv.k[a.layer]);
-  const bf16* Vc = reinterpret_cast<const bf16*>(a.kv.v[a.layer]);
+  const bf16* Kc = reinterpret_cast<const bf16*>(a.kl.k);
+  const bf16* Vc = reinterpret_cast<const bf16*>(a.kl.v);
   const int s_lo = base + s * SPLIT;
   const int s_hi = min(uhi, s_lo + SPLIT - 1);
   constexpr int kStride = kUnitWaves * 64;
@@ -684,7 +693,8 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   const int full_hi = un.pos0;
   const int kb0 = s_lo + wv * 64;
   for (int kb = kb0; kb <= s_hi; kb += kStride) {
-    attn_load_block(Kc, Vc, kv_block(a.kv, a.layer, un.seq, g, kb), m16, kq, cur);
+    attn_load_block(Kc, Vc, kv_block_layer(a.kl, a.is_local, a.Hkv, un.seq, g, kb), m16, kq,
+                    cur);
     const auto& kk = cur.k;
     const auto& vl = cur.vl;
     const auto& vh = cur.vh;
@@ -1568,14 +1578,21 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
       if (local_splits < splits) splits = local_splits;
     }
     const dim3 grid(a.max_units, a.Hkv, (splits + bpw - 1) / bpw);
+    AttnArgs b = a;
+    b.kl.k = a.kv.k[a.layer];
+    b.kl.v = a.kv.v[a.layer];
+    b.kl.lcap = a.kv.lcap;
+    b.kl.max_pages = a.kv.max_pages;
+    if (((a.kv.local_mask >> a.layer) & 1u) != (a.is_local ? 1u : 0u))
+      return fail(PULSAR_ERR_INVALID, "decode attention: layer type mismatch");
 #define PULSAR_ATTN_UNIT(C)                                                         \
   do {                                                                              \
     if (bpw == 8)                                                                   \
-      attn_decode_unit_kernel<C, 8><<<grid, 64 * kUnitWaves, 0, s>>>(a);            \
+      attn_decode_unit_kernel<C, 8><<<grid, 64 * kUnitWaves, 0, s>>>(b);            \
     else if (bpw == 4)                                                              \
-      attn_decode_unit_kernel<C, 4><<<grid, 64 * kUnitWaves, 0, s>>>(a);            \
+      attn_decode_unit_kernel<C, 4><<<grid, 64 * kUnitWaves, 0, s>>>(b);            \
     else                                                                            \
-      attn_decode_unit_kernel<C, 1><<<grid, 64 * kUnitWaves, 0, s>>>(a);            \
+      attn_decode_unit_kernel<C, 1><<<grid, 64 * kUnitWaves, 0, s>>>(b);            \
   } while (0)
     if (a.unit_rows <= 2)
       PULSAR_ATTN_UNIT(8);
