@@ -4,6 +4,7 @@
 // activation dtype, norm / conv weights in fp32. Weight gradients are summed with fp32
 // atomics (one per element per workgroup), so their rounding depends on scheduling order,
 // as the reference's does.
+#include <algorithm>
 #include <string>
 
 #include "common.h"
@@ -92,31 +93,38 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(const T* __restrict__ 
 //   dn = rope^T(dy) (rotation by -theta: dn_i = dy_i c + dy_{i+32} s,
 //        dn_{i+32} = dy_{i+32} c - dy_i s)
 //   dx = r * w * dn - x * r^3 * sum(dn * x * w) / 64 ;  dw[h] = sum dn * x * r
+// Grid (workgroups per head, H): the waves of head h stride over its B*T vectors, keep
+// their dw partial in a register and add it once.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ void __launch_bounds__(256) qk_norm_rope_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ x, int64_t sB, int64_t sH, int64_t sT,
-    int64_t dB, int64_t dH, int64_t dT, int H, int T_, int64_t nvec,
+    int64_t dB, int64_t dH, int64_t dT, int H, int T_, int64_t per_head,
     const float* __restrict__ w, const float* __restrict__ rsq, const float* __restrict__ cs,
     const float* __restrict__ sn, T* __restrict__ dx, float* __restrict__ dw) {
-  const int64_t v = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
-  if (v >= nvec) return;
+  const int h = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int t = (int)(v % T_);
-  const int h = (int)((v / T_) % H);
-  const int64_t b = v / ((int64_t)T_ * H);
-  const float g = to_f(dy[v * 64 + lane]);
-  const float gp = __shfl_xor(g, 32, 64);
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / 64);
   const int j = lane & 31;
-  const float c = cs[t * 32 + j], s = sn[t * 32 + j];
-  const float dn = lane < 32 ? g * c + gp * s : g * c - gp * s;
-  const float xv = to_f(x[b * sB + h * sH + (int64_t)t * sT + lane]);
   const float wv = w[h * 64 + lane];
-  const float r = rsq[v];
-  const float tot = wave_sum(dn * xv * wv);
-  dx[b * dB + h * dH + (int64_t)t * dT + lane] =
-      from_f<T>(r * wv * dn - xv * r * r * r * tot * (1.0f / 64.0f));
-  atomicAdd(&dw[h * 64 + lane], dn * xv * r);
+  float dwacc = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); i < per_head;
+       i += nwaves) {
+    const int64_t b = i / T_;
+    const int t = (int)(i % T_);
+    const int64_t v = (b * H + h) * T_ + t;  // vector index in [B, H, T] order
+    const float g = to_f(dy[v * 64 + lane]);
+    const float gp = __shfl_xor(g, 32, 64);
+    const float c = cs[t * 32 + j], s = sn[t * 32 + j];
+    const float dn = lane < 32 ? g * c + gp * s : g * c - gp * s;
+    const float xv = to_f(x[b * sB + h * sH + (int64_t)t * sT + lane]);
+    const float r = rsq[v];
+    const float tot = wave_sum(dn * xv * wv);
+    dx[b * dB + h * dH + (int64_t)t * dT + lane] =
+        from_f<T>(r * wv * dn - xv * r * r * r * tot * (1.0f / 64.0f));
+    dwacc += dn * xv * r;
+  }
+  atomicAdd(&dw[h * 64 + lane], dwacc);
 }
 
 // ---------------------------------------------------------------------------
@@ -356,13 +364,16 @@ int pulsar_qk_rmsnorm_rope_backward(const void* dy, const void* x, int64_t sB, i
     return fail(PULSAR_ERR_INVALID,
                 "qk_rmsnorm_rope requires head_dim == 64, got " + std::to_string(head_dim));
   PULSAR_REQUIRE(B >= 0 && H > 0 && T > 0, "qk_rmsnorm_rope backward: bad shape");
+  PULSAR_REQUIRE(H <= 65535, "qk_rmsnorm_rope backward: at most 65535 heads");
   PULSAR_TRY_STATUS(zero_f32(dw, H * 64, stream));
-  const int64_t nvec = B * H * T;
-  if (nvec == 0) return PULSAR_OK;
+  const int64_t per_head = B * T;
+  if (per_head == 0) return PULSAR_OK;
+  // up to 64 workgroups (256 waves) per head; each wave adds its dw partial once
+  const unsigned gx = (unsigned)std::min<int64_t>(64, (per_head + 3) / 4);
   return dispatch_dtype(dtype, [&](auto tag) {
     using T_ = decltype(tag);
-    qk_norm_rope_bwd_kernel<T_><<<blocks_for(nvec, 4), 256, 0, stream>>>(
-        (const T_*)dy, (const T_*)x, sB, sH, sT, dB, dH, dT, (int)H, (int)T, nvec, w, rsqrt,
+    qk_norm_rope_bwd_kernel<T_><<<dim3(gx, (unsigned)H), 256, 0, stream>>>(
+        (const T_*)dy, (const T_*)x, sB, sH, sT, dB, dH, dT, (int)H, (int)T, per_head, w, rsqrt,
         cos, sin, (T_*)dx, dw);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;

@@ -109,6 +109,20 @@ def test_qk_rmsnorm_rope_backward(pc, dtype, layout):
     _check(dw, ow, torch.float32, "qk dw")
 
 
+def test_qk_rmsnorm_rope_backward_long_sequence(pc):
+    """Training-sized sequence: 2 x 2048 vectors per head summed into each weight row."""
+    B, H, T = 2, 16, 2048
+    x = _rand(B, T, H, 64, seed=13).transpose(1, 2)
+    w = torch.rand(H, 64, device="cuda") + 0.5
+    cos, sin = _tables(T)
+    y, rs = pc.qk_rmsnorm_rope_forward(x, w, cos, sin, T)
+    dy = _rand(*y.shape, seed=14)
+    dx, dw = pc.qk_rmsnorm_rope_backward(dy, x, w, rs, cos, sin, T)
+    ox, ow = BW.qk_rmsnorm_rope_bwd(_np(dy), _np(x), _np(w), _np(rs), _np(cos), _np(sin))
+    _check(dx, ox, torch.bfloat16, "qk dx (T=2048)")
+    _check(dw, ow, torch.float32, "qk dw (T=2048)")
+
+
 def test_qk_rmsnorm_rope_backward_rejects_head_dim(pc):
     x = torch.zeros(1, 2, 3, 32, device="cuda", dtype=torch.bfloat16)
     cos, sin = _tables(3)
