@@ -214,3 +214,35 @@ def test_prefill_capacity_drops_match_oracle(full_state, dtype, tol):
         print(f"{dtype} sequence {b}: {err:.3e}")
         assert err <= tol, (b, err)
     eng.close()
+
+
+@pytest.mark.parametrize("draft_len", [0, 4])
+def test_multi_step_graphs_equal_single_steps_and_eager(models, full_state, draft_len):
+    """Runs of steps launch four steps per graph: the same sampled decode stepped one graph
+    step at a time, as one 26-step call (six four-step graphs and two single steps) and
+    eagerly gives identical tokens and per-sequence state."""
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+
+    cfg = full_state[0]
+    B, T_, N, n = 4, 24, 12, 26
+    prompts = np.stack([W.uniform_ids(60 + b, "graph_prompt", T_, cfg.vocab_size)
+                        for b in range(B)])
+    eng = HipEngine(models[torch.bfloat16], batch=B, max_prompt=T_, max_new=N, speculative=True,
+                    temperature=0.8, top_p=0.95, repetition_penalty=1.15, stop_ids=[], seed=7,
+                    draft_len=draft_len)
+    eng.prefill(prompts)
+    runs = []
+    for mode in ("single", "multi", "eager"):
+        eng.rewind(11)
+        if mode == "single":
+            for _ in range(n):
+                eng.step(1, graph=True)
+        else:
+            eng.step(n, graph=mode == "multi")
+        runs.append((eng.tokens(), eng.state().copy()))
+    assert all(len(t) > 0 for t in runs[0][0])
+    for toks, st in runs[1:]:
+        assert toks == runs[0][0]
+        np.testing.assert_array_equal(st, runs[0][1])
+    eng.close()
