@@ -232,6 +232,22 @@ def verify_microbench(model, cfg, es, args):
                      "us_per_launch": round(v[0] / v[1] * 1e3, 2),
                      "GB_per_s": round(by_class.get(c, 0.0) / max(v[0], 1e-9) / 1e6, 1)}
                  for c, v in prof.items() if v[1] and c != "event_pair"}
+    # secondary: matrix-core use of the verify's GEMMs (rows of one pass each launch; top-k
+    # assignments plus the shared expert over every row), against the dense bf16 peak
+    D, R = cfg.d_model, B * n
+    gemm_flops = {
+        "qkv_gate_gemm": 2.0 * R * D * (cfg.qkv_dim + cfg.n_heads),
+        "wo_gemm": 2.0 * R * cfg.q_dim * D,
+        "routed_gate_up": 2.0 * D * (R * cfg.top_k * 2 * cfg.d_expert + R * 2 * cfg.d_shared),
+        "routed_down": 2.0 * D * (R * cfg.top_k * cfg.d_expert + R * cfg.d_shared),
+    }
+    gemm_mfma = {}
+    for c, fl in gemm_flops.items():
+        c_ms, c_n = prof.get(c, (0.0, 0))
+        if c_n:
+            tf = fl / (c_ms / c_n / 1e3) / 1e12
+            gemm_mfma[c] = {"gflop_per_launch": round(fl / 1e9, 3), "TFLOP_per_s": round(tf, 1),
+                            "frac": round(tf * 1e12 / MFMA_BF16_PEAK, 4)}
     eng.close()
     return {
         "workload": f"verify of {n} tokens (4 drafts + 1) for each of {B} sequences over a "
@@ -252,6 +268,7 @@ def verify_microbench(model, cfg, es, args):
                                      "copy-calibrated, averaged over the layer types by "
                                      "launch count)"},
         "kernel_profile": per_class,
+        "gemm_mfma": gemm_mfma,
     }
 
 
