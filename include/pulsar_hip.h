@@ -286,7 +286,16 @@ typedef struct PulsarEngineConfig {
    * reference's equal-draw rule (src/infer.py:704-725). Needs max_ctx >= max_prompt +
    * max_new + 2 + draft_len. */
   int32_t draft_len;
-  int32_t reserved;
+  /* Adaptive early exit (the reference's set_early_exit_threshold, src/infer.py:198-232,
+   * :536-547). early_exit = 1: a token run by decode_step (every decoded token in plain
+   * mode, an accepted draft in speculative mode) stops after pulse k < n_pulses - 1 when
+   * the top-1 probability of softmax(its pulse-k logits), rounded to the activation dtype,
+   * is >= early_exit_threshold; it then keeps pulse k's keys/values and the next token is
+   * drawn from pulse k's logits. Exits are counted per pulse (PULSAR_BUF_EXIT_COUNTS). In
+   * plain mode the last emitted token still runs its pulses, as the reference's loop does,
+   * so that its exit is counted. Exact schedule only (draft_len = 0). */
+  int32_t early_exit;
+  double early_exit_threshold;
 } PulsarEngineConfig;
 
 /* Buffers readable with pulsar_engine_read. */
@@ -302,6 +311,14 @@ typedef struct PulsarEngineConfig {
 #define PULSAR_BUF_LAST_ROWS 5 /* int32 [n_rows][8] rows of the last executed step */
 #define PULSAR_BUF_LAST_CTL 6  /* int32 [16] control block of the last executed step */
 #define PULSAR_BUF_EXPERT_COUNTS 7 /* int32 [n_layers][E] rows routed to each expert, last step */
+#define PULSAR_BUF_EXIT_COUNTS 8   /* int32 [B][4] tokens that left after pulse k (early exit),
+                                      since the last prefill or rewind */
+#define PULSAR_BUF_TOPK_IDX 9      /* int32 [n_layers][max_rows][top_k] router top-k expert ids
+                                      of each row of the last executed step, in that step's row
+                                      order (PULSAR_BUF_LAST_ROWS), in the router's ranking
+                                      order */
+#define PULSAR_BUF_TOKEN_KINDS 10  /* int32 [B][max_new] per emitted token: 1 = an accepted
+                                      draft, 0 = a drawn token */
 
 /* Kernel classes of the per-class timing (pulsar_engine_profile_read). */
 #define PULSAR_PROF_CLASSES 17

@@ -293,6 +293,14 @@ class RefEngine:
         self.dtype = model.dtype
         self.stop_ids = set(stop_ids) if stop_ids is not None else {self.cfg.eos_token_id}
         self.trace: Optional[list] = None  # optional per-pass record for tests
+        # adaptive early exit (src/infer.py:198-200): off when the threshold is None
+        self.early_exit_threshold: Optional[float] = None
+        self.early_exit_counts = [0] * self.cfg.default_pulses
+
+    def set_early_exit_threshold(self, threshold: Optional[float]) -> None:
+        """src/infer.py:210-213: set the threshold and clear the per-pulse exit counts."""
+        self.early_exit_threshold = threshold
+        self.early_exit_counts = [0] * self.cfg.default_pulses
 
     # -- pulse input -------------------------------------------------------
     def _stem(self, ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -377,7 +385,11 @@ class RefEngine:
         idx, wts = router_decode(xf, m.w(pre + "router_weight")[pulse], self._bias(layer, pulse),
                                  cfg.top_k, x.dtype)
         if self.trace is not None:
-            self.trace.append(("router", layer, pulse, idx.clone()))
+            # the biased scores ranked by top-k, for the size of each decision's margin
+            biased = torch.sigmoid((lambda lg: lg - lg.mean(dim=-1, keepdim=True))(
+                F.linear(xf.float(), m.w(pre + "router_weight")[pulse].float())))
+            biased = biased + self._bias(layer, pulse)
+            self.trace.append(("router", layer, pulse, idx.clone(), biased.clone()))
         shared = self._shared_expert(layer, xf)
         routed = torch.zeros_like(xf)
         for i in range(cfg.top_k):
@@ -488,12 +500,42 @@ class RefEngine:
         return logits, h_out, e
 
     def decode_step(self, token: int, pos: int, cache: RefKVCache) -> torch.Tensor:
-        """All pulses of one token (src/infer.py:526-549, early exit off)."""
+        """The pulses of one token with the optional adaptive early exit (src/infer.py:526-549).
+
+        After pulse k < last, when a threshold is set, the top-1 probability of softmax(logits)
+        (the softcapped logits in the model dtype, so rounded to bf16 in bf16 mode) is compared
+        with it; at or above it the token stops at pulse k: its cache entry keeps pulse k's
+        keys/values and pulse k's logits are returned. Exits are counted per pulse; a token that
+        runs every pulse counts at the last one."""
         h, e, logits = None, None, None
-        for k in range(self.cfg.default_pulses):
+        P = self.cfg.default_pulses
+        thr = self.early_exit_threshold
+        for k in range(P):
             logits, h, e = self.decode_pulse_pass(token, pos, cache, k, h, e)
+            if thr is not None and k < P - 1:
+                max_prob = F.softmax(logits, dim=-1).max(dim=-1).values.item()
+                if self.trace is not None:
+                    self.trace.append(("exit_check", token, pos, k, max_prob))
+                if max_prob >= thr:
+                    self.early_exit_counts[k] += 1
+                    break
+        else:
+            if thr is not None:
+                self.early_exit_counts[P - 1] += 1
         cache.seq_len = pos + 1
         return logits
+
+    def get_early_exit_stats(self) -> dict:
+        """Exit distribution over the counted tokens (src/infer.py:215-232); the reference
+        weighs pulses 1-3 as 8, 16 and 24 layers."""
+        c = self.early_exit_counts
+        total = sum(c)
+        if total == 0:
+            return {}
+        eff = (8 * c[0] + 16 * c[1] + 24 * c[2]) / total
+        return {"total_tokens": total, "pulse_counts": list(c),
+                "pulse_pcts": [c[0] / total * 100.0, c[1] / total * 100.0, c[2] / total * 100.0],
+                "effective_layers": eff, "compute_speedup": 24.0 / eff}
 
     # -- sampling (src/infer.py:658-685) ----------------------------------------
     @staticmethod
@@ -556,6 +598,7 @@ class RefEngine:
             stats.setdefault("tests", 0)
             stats.setdefault("accepted", 0)
             stats.setdefault("p_accept", [])
+            stats.setdefault("kinds", [])
         smp = lambda lg: self.sample(lg, seen, temperature, top_p, repetition_penalty, generator)  # noqa: E731
         while produced < max_new_tokens:
             t = smp(logits)
@@ -564,6 +607,8 @@ class RefEngine:
             seen.append(t)
             pos += 1
             produced += 1
+            if stats is not None:
+                stats["kinds"].append(0)
             yield t
             if produced >= max_new_tokens:
                 break
@@ -580,6 +625,7 @@ class RefEngine:
             if draft == true and draft not in self.stop_ids:
                 if stats is not None:
                     stats["accepted"] += 1
+                    stats["kinds"].append(1)
                 seen.append(draft)
                 pos += 1
                 produced += 1
@@ -776,6 +822,102 @@ class RefEngine:
             produced += 1
             yield nxt
             t = nxt
+
+
+def replay_acceptance(engine: "RefEngine", prompt_ids, emitted, kinds, temperature: float,
+                      top_p: float, repetition_penalty: float) -> list:
+    """The reference's self-speculative loop (src/infer.py:688-731) driven along a given
+    emitted stream instead of its own draws: emitted[i] is the i-th output token, kinds[i]
+    is 1 when it was an accepted draft (then emitted[i-1] was tested and accepted) and 0
+    when it was drawn. Returns, for each draft test, (P(accept), accepted) with
+    P(accept) = sum_x p_draft(x) p_verify(x) from the oracle's own pulse-0 and pulse-2
+    logits of the tested token over the oracle's own cache."""
+    ids = torch.as_tensor(prompt_ids, dtype=torch.long).view(1, -1)
+    cache = RefKVCache(engine.cfg)
+    engine.prefill(ids, cache)
+    seen = ids[0].tolist()
+    pos = len(seen) - 1
+    n = len(emitted)
+    out = []
+    i = 0
+    while i < n:
+        if kinds[i] != 0:
+            raise ValueError(f"token {i} marked as an accepted draft without a test before it")
+        t = int(emitted[i])
+        seen.append(t)
+        pos += 1
+        if i == n - 1:
+            break
+        d_logits, h, e = engine.decode_pulse_pass(t, pos, cache, 0)
+        _, h, _ = engine.decode_pulse_pass(t, pos, cache, 1, h, e)
+        v_logits, h, _ = engine.decode_pulse_pass(t, pos, cache, 2, h, e)
+        cache.seq_len = pos + 1
+        acc = kinds[i + 1] == 1
+        out.append((accept_probability(d_logits, v_logits, seen, temperature, top_p,
+                                       repetition_penalty), bool(acc)))
+        if acc:
+            d = int(emitted[i + 1])
+            seen.append(d)
+            pos += 1
+            if i + 1 < n - 1:
+                engine.decode_step(d, pos, cache)
+            i += 2
+        else:
+            i += 1
+    return out
+
+
+def spec_token_marginals(engine: "RefEngine", prompt_ids, temperature: float, top_p: float,
+                         repetition_penalty: float, prune: float = 1e-7) -> list:
+    """Exact distributions (fp64 [V] each) of the first three tokens self_speculative_ids
+    emits (src/infer.py:688-731), with no stop ids and max_new_tokens >= 3.
+
+    Token 1 is a draw from the prefill logits and is tested: its draft d ~ p_d (pulse 0)
+    and check v ~ p_v (pulse 2) are independent, so token 2 = x with probability
+    p_d(x) p_v(x) (accepted draft) + (1 - sum_y p_d(y) p_v(y)) p_v(x) (fresh draw from the
+    verify logits). An accepted token 2 runs decode_step and token 3 is a plain draw from
+    its pulse-2 logits; a drawn token 2 is tested in turn, like token 1. Branches of
+    probability below `prune` are not expanded; their mass is missing from the token-3
+    (and, below prune at token 1, token-2) distributions."""
+    import copy
+
+    cfg = engine.cfg
+    dist = lambda lg, seen: sampling_distribution(lg, seen, temperature, top_p,  # noqa: E731
+                                                  repetition_penalty)
+    ids = torch.as_tensor(prompt_ids, dtype=torch.long).view(1, -1)
+    cache0 = RefKVCache(cfg)
+    logits0 = engine.prefill(ids, cache0)[:, -1, :].clone()
+    seen0 = ids[0].tolist()
+    pos0 = len(seen0) - 1
+    V = cfg.vocab_size
+    m1 = dist(logits0, seen0)
+    m2 = torch.zeros(V, dtype=torch.float64)
+    m3 = torch.zeros(V, dtype=torch.float64)
+
+    def tested(token, pos, cache, seen):
+        ld, h, e = engine.decode_pulse_pass(token, pos, cache, 0)
+        _, h, _ = engine.decode_pulse_pass(token, pos, cache, 1, h, e)
+        lv, h, _ = engine.decode_pulse_pass(token, pos, cache, 2, h, e)
+        cache.seq_len = pos + 1
+        return dist(ld, seen), dist(lv, seen)
+
+    for t1 in torch.nonzero(m1 > prune).view(-1).tolist():
+        w1 = float(m1[t1])
+        c1 = copy.deepcopy(cache0)
+        seen1 = seen0 + [t1]
+        pd, pv = tested(t1, pos0 + 1, c1, seen1)
+        acc = pd * pv
+        rej = (1.0 - float(acc.sum())) * pv
+        m2 += w1 * (acc + rej)
+        for t2 in torch.nonzero(w1 * (acc + rej) > prune).view(-1).tolist():
+            c2 = copy.deepcopy(c1)
+            seen2 = seen1 + [t2]
+            pd2, pv2 = tested(t2, pos0 + 2, c2, seen2)
+            # accepted token 2: decode_step's logits are its pulse-2 logits (no early exit)
+            m3 += w1 * float(acc[t2]) * pv2
+            acc2 = pd2 * pv2
+            m3 += w1 * float(rej[t2]) * (acc2 + (1.0 - float(acc2.sum())) * pv2)
+    return [m1, m2, m3]
 
 
 def sampling_distribution(lgt: torch.Tensor, seen: list, temperature: float, top_p: float,

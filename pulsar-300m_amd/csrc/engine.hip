@@ -33,6 +33,7 @@ struct Engine {
   int32_t *lrow_seq = nullptr, *lrow_extra = nullptr, *argmax = nullptr, *draw = nullptr;
   uint32_t* lrow_ctr = nullptr;  // draft-block mode: per logits row draw counter
   int32_t *tokens = nullptr, *stop_ids = nullptr;
+  int32_t* kinds = nullptr;  // [B][max_new] 1 = emitted as an accepted draft
   uint32_t* seen = nullptr;
   void *e_state = nullptr, *hout_state = nullptr;
   void *h_in = nullptr, *h = nullptr, *xn = nullptr, *qkvbuf = nullptr, *gate = nullptr;
@@ -49,6 +50,9 @@ struct Engine {
   double prof_ms[PULSAR_PROF_CLASSES] = {};
   int64_t prof_n[PULSAR_PROF_CLASSES] = {};
   int32_t *topk_idx = nullptr, *keep = nullptr;
+  int32_t* dec_topk = nullptr;     // decode router top-k ids per layer [L][max_rows][K]
+  float* maxprob = nullptr;        // early exit: top-1 probability per logits row
+  int32_t* exit_counts = nullptr;  // early exit: [B][4] exits per pulse
   int32_t *lists = nullptr, *list_count = nullptr;      // decode: [L][E][max_rows*K], [L][E]
   int32_t *p_lists = nullptr, *p_lcount = nullptr;  // prefill
   int32_t* p_ids = nullptr;
@@ -56,6 +60,7 @@ struct Engine {
   StepCtl* p_ctl = nullptr;   // [P]
   KVDesc kv{};
   int prompt_len = 0;
+  int v_n = 0;  // rows per sequence of the uploaded verify block (0: none since prefill/fill_kv)
   bool prefilled = false;
   bool kv_ready = false;  // the cache holds positions [0, prompt_len) (prefill or fill_kv)
   // block verify: host-built rows, control blocks and units of its passes
@@ -126,6 +131,12 @@ int validate(const PulsarModelDesc& m, const PulsarEngineConfig& c) {
                  "max_ctx < max_prompt + max_new + 2 + draft_len");
   PULSAR_REQUIRE(m.rope_len >= c.max_ctx, "rope tables shorter than max_ctx");
   PULSAR_REQUIRE(c.n_stop >= 0 && c.n_stop <= 8, "n_stop must be 0..8");
+  PULSAR_REQUIRE(c.early_exit == 0 || c.early_exit == 1, "early_exit must be 0 or 1");
+  if (c.early_exit) {
+    PULSAR_REQUIRE(c.draft_len == 0,
+                   "early exit applies to the exact schedule only (draft_len == 0)");
+    PULSAR_REQUIRE(std::isfinite(c.early_exit_threshold), "early_exit_threshold must be finite");
+  }
   return PULSAR_OK;
 }
 
@@ -259,6 +270,7 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.argmax, 4 * MR));
   PULSAR_TRY(x.alloc(&x.draw, 8 * MR));
   PULSAR_TRY(x.alloc(&x.tokens, 4 * (size_t)x.B * std::max(1, c.max_new)));
+  PULSAR_TRY(x.alloc(&x.kinds, 4 * (size_t)x.B * std::max(1, c.max_new)));
   PULSAR_TRY(x.alloc(&x.stop_ids, 4 * 8));
   PULSAR_TRY(x.alloc(&x.seen, 4 * (size_t)x.B * (x.V / 32)));
   PULSAR_TRY(x.alloc(&x.e_state, es * R * D));
@@ -281,6 +293,11 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.topk_idx, 4 * R * x.K));
   PULSAR_TRY(x.alloc(&x.topk_w, 4 * R * x.K));
   PULSAR_TRY(x.alloc(&x.keep, 4 * R * x.K));
+  PULSAR_TRY(x.alloc(&x.dec_topk, 4 * (size_t)x.L * MR * x.K));
+  PULSAR_CHECK_HIP(hipMemset(x.dec_topk, 0xff, 4 * (size_t)x.L * MR * x.K));
+  PULSAR_TRY(x.alloc(&x.maxprob, 4 * std::max<size_t>(MR, x.B)));
+  PULSAR_TRY(x.alloc(&x.exit_counts, 4 * 4 * (size_t)x.B));
+  PULSAR_CHECK_HIP(hipMemset(x.exit_counts, 0, 4 * 4 * (size_t)x.B));
   // split partials: fp32 path per (row, kv head, split, head); bf16 path per (unit, kv
   // head, split, query column), up to 32 columns per unit (8 rows x 4 heads)
   PULSAR_TRY(x.alloc(&x.part, 4 * std::max<size_t>(MR * 4, (size_t)x.B * 4 * kMaxBlock) * x.Hkv *
@@ -454,7 +471,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     ra.E = e.E;
     ra.K = e.K;
     ra.D = D;
-    ra.topk_idx = e.topk_idx;
+    ra.topk_idx = e.dec_topk + (int64_t)l * MR * e.K;
     ra.topk_w = e.topk_w;
     ra.lists = e.lists + (int64_t)l * e.E * lstride;
     ra.list_count = e.list_count + (int64_t)l * e.E;
@@ -603,6 +620,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   sa.seed = e.d_seed;
   sa.out_argmax = e.argmax;
   sa.out_draw = e.draw;
+  sa.out_maxprob = e.cfg.early_exit ? e.maxprob : nullptr;
   PULSAR_TIMED(PC_SAMPLE, launch_sample(sa, e.dtype, e.max_rows, s));
   PULSAR_TRY(prof_delay(e, s));
   const int _pc = prof_mark(e, s);
@@ -619,6 +637,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   co.draft_len = e.G;
   co.seen = e.seen;
   co.out_tokens = e.tokens;
+  co.out_kinds = e.kinds;
   co.argmax = e.argmax;
   co.draw = e.draw;
   co.stop_ids = e.stop_ids;
@@ -630,6 +649,10 @@ int enqueue_step(Engine& e, hipStream_t s) {
   co.speculative = e.cfg.speculative;
   co.all_logits = e.cfg.all_logits;
   co.prompt_len = e.prompt_len;
+  co.early_exit = e.cfg.early_exit;
+  co.maxprob = e.maxprob;
+  co.exit_counts = e.exit_counts;
+  co.exit_thr = e.cfg.early_exit_threshold;
   PULSAR_TRY(launch_controller(co, s));
   prof_span(e, PC_CONTROL, _pc, prof_mark(e, s));
   return PULSAR_OK;
@@ -641,6 +664,7 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   const int T = e.prompt_len, BT = e.B * T;
   PULSAR_CHECK_HIP(hipMemcpyAsync(e.d_seed, &seed, 8, hipMemcpyHostToDevice, s));
   PULSAR_CHECK_HIP(hipMemsetAsync(e.state, 0, sizeof(SeqState) * e.B, s));
+  PULSAR_CHECK_HIP(hipMemsetAsync(e.exit_counts, 0, 4 * 4 * (size_t)e.B, s));
   PULSAR_CHECK_HIP(hipMemsetAsync(e.seen, 0, 4 * (size_t)e.B * (e.V / 32), s));
   set_seen_kernel<<<(BT + 255) / 256, 256, 0, s>>>(e.p_ids, e.seen, T, e.V, BT);
   PULSAR_LAUNCH_CHECK();
@@ -680,6 +704,7 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   co.draft_len = e.G;
   co.seen = e.seen;
   co.out_tokens = e.tokens;
+  co.out_kinds = e.kinds;
   co.argmax = e.argmax;
   co.draw = e.draw;
   co.stop_ids = e.stop_ids;
@@ -692,6 +717,10 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   co.all_logits = e.cfg.all_logits;
   co.init = 1;
   co.prompt_len = T;
+  co.early_exit = e.cfg.early_exit;
+  co.maxprob = e.maxprob;
+  co.exit_counts = e.exit_counts;
+  co.exit_thr = e.cfg.early_exit_threshold;
   PULSAR_TRY(launch_controller(co, s));
   // host vectors above are read by the async copies: finish before they go out of scope
   PULSAR_CHECK_HIP(hipStreamSynchronize(s));
@@ -706,9 +735,14 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   PULSAR_REQUIRE(T >= 1 && T <= e.cfg.max_prompt, "prompt length out of range");
   const int D = e.D, dt = e.dtype, P = e.P;
   const int BT = Bq * T;
-  e.prompt_len = T;
   for (int i = 0; i < BT; ++i)
     PULSAR_REQUIRE(host_ids[i] >= 0 && host_ids[i] < e.V, "prompt id out of vocabulary");
+  // from here on the cache and the saved prefill state are being replaced: a prefill that
+  // fails part way leaves nothing to step, rewind or verify
+  e.prefilled = false;
+  e.kv_ready = false;
+  e.v_n = 0;
+  e.prompt_len = T;
   // graph of a previous generation refers to the same buffers; it stays valid.
   PULSAR_CHECK_HIP(hipMemcpyAsync(e.p_ids, host_ids, 4 * (size_t)BT, hipMemcpyHostToDevice, s));
   std::vector<RowDesc> rows((size_t)P * BT);
@@ -1003,6 +1037,9 @@ __global__ void __launch_bounds__(256) fill_normal_kernel(T* p, int64_t n, uint6
 
 int fill_kv(Engine& e, int ctx, uint64_t seed, hipStream_t s) {
   PULSAR_REQUIRE(ctx >= 1 && ctx + 1 <= e.cfg.max_ctx, "engine_fill_kv: 1 <= ctx < max_ctx");
+  e.prefilled = false;
+  e.kv_ready = false;
+  e.v_n = 0;
   const size_t local_elems = (size_t)e.B * e.Hkv * e.lcap * kHeadDim;
   const size_t global_elems = (size_t)e.B * e.max_pages * e.Hkv * kPage * kHeadDim;
   for (int l = 0; l < e.L; ++l) {
@@ -1023,6 +1060,7 @@ int fill_kv(Engine& e, int ctx, uint64_t seed, hipStream_t s) {
   e.prompt_len = ctx;
   e.kv_ready = true;
   e.prefilled = false;  // no prefill logits: decoding needs a prefill
+  e.v_n = 0;
   return PULSAR_OK;
 }
 
@@ -1036,6 +1074,12 @@ int fill_kv(Engine& e, int ctx, uint64_t seed, hipStream_t s) {
 int verify(Engine& e, const int32_t* host_tokens, int n, int use_graph, hipStream_t s) {
   PULSAR_REQUIRE(e.kv_ready, "engine_verify: prefill or fill_kv first");
   const int P = e.P, B = e.B, MR = e.max_rows;
+  // re-running needs a block uploaded since the last prefill / fill_kv: the row, control
+  // and unit buffers are uninitialised (or describe other positions) until then
+  PULSAR_REQUIRE(host_tokens || e.v_n > 0,
+                 "engine_verify: no block uploaded since the last prefill or fill_kv");
+  PULSAR_REQUIRE(host_tokens || e.prompt_len + e.v_n <= e.cfg.max_ctx,
+                 "engine_verify: block past max_ctx");
   if (host_tokens) {
     PULSAR_REQUIRE(n >= 1 && n <= e.S,
                    "engine_verify: 1 <= n <= rows per sequence (draft_len + 1, or 2)");
@@ -1078,6 +1122,7 @@ int verify(Engine& e, const int32_t* host_tokens, int n, int use_graph, hipStrea
                                     hipMemcpyHostToDevice, s));
     // the host vectors must outlive the copies
     PULSAR_CHECK_HIP(hipStreamSynchronize(s));
+    e.v_n = n;
   }
   auto passes = [&](hipStream_t st) -> int {
     for (int k = 0; k < P; ++k)
@@ -1285,6 +1330,18 @@ int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes
     case PULSAR_BUF_EXPERT_COUNTS:
       src = e.list_count;
       cap = 4ll * e.L * e.E;
+      break;
+    case PULSAR_BUF_EXIT_COUNTS:
+      src = e.exit_counts;
+      cap = 16ll * e.B;
+      break;
+    case PULSAR_BUF_TOKEN_KINDS:
+      src = e.kinds;
+      cap = 4ll * e.B * std::max(1, e.cfg.max_new);
+      break;
+    case PULSAR_BUF_TOPK_IDX:
+      src = e.dec_topk;
+      cap = 4ll * e.L * e.max_rows * e.K;
       break;
     default:
       return fail(PULSAR_ERR_INVALID, "engine_read: unknown buffer");

@@ -813,6 +813,17 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
     }
   }
   if (nsplit == 1) return;
+  // Hand-off to the merging block without a release/acquire pair. Every partial is written
+  // and read with agent-scope atomics, which gfx950 issues as `global_store ... sc1` /
+  // `global_load ... sc1`: coherent at device scope on their own (written through and read
+  // past the XCD's L2). What the memory model would add with acq_rel on the counter is
+  // ordering against *other* accesses, as `buffer_wbl2 sc1` before and `buffer_inv sc1`
+  // after the add: a write-back and invalidate of the whole L2, measured slower. The order
+  // that matters is kept in hardware and by the compiler: `s_waitcnt vmcnt(0)` below waits
+  // for every partial store of this workgroup to be acknowledged before the barrier, so all
+  // of them complete before thread 0's counter add is issued; the merging block issues its
+  // partial loads only after the add has returned (through LDS and a barrier, which the
+  // compiler does not move memory operations across).
   __builtin_amdgcn_s_waitcnt(0);
   __shared__ int s_last;
   __syncthreads();

@@ -28,7 +28,8 @@ struct SeqState {
   int32_t tests, accepted;
   int32_t row_c, row_s, lrow_c, lrow_s;
   uint32_t ctr;
-  int32_t pad[2];
+  int32_t tail;  // plain mode with early exit: the last emitted token runs for its exit count
+  int32_t pad;
   // draft-block mode: block tokens (blk[0] = the round's emitted token at position c_pos),
   // tokens known, phase (0 draft, 1 verify), step within the phase (draft index or verify
   // pulse), drafts wanted this round
@@ -51,6 +52,8 @@ struct SampleArgs {
   int32_t* out_argmax;  // [lrows]
   int32_t* out_draw;    // [lrows][2]
   int n_seq;            // > 0: rows naming a sequence outside [0, n_seq) output -1
+  float* out_maxprob;   // nullable: [lrows] top-1 probability of softmax(raw logits), rounded
+                        // to the activation dtype (the early-exit test)
 };
 
 struct ControllerArgs {
@@ -65,11 +68,18 @@ struct ControllerArgs {
   uint32_t* lrow_ctr;   // draft-block mode: per logits row draw counter
   uint32_t* seen;
   int32_t* out_tokens;  // [B][max_new]
+  int32_t* out_kinds;   // nullable: [B][max_new] 1 = accepted draft, 0 = drawn token
   const int32_t* argmax;
   const int32_t* draw;
   const int32_t* stop_ids;
   int n_stop, B, V, n_pulses, max_new, speculative, all_logits, init, prompt_len;
   int draft_len;        // > 0: draft-block mode with up to draft_len drafts per round
+  // adaptive early exit (exact schedule): per logits row top-1 probability, per-sequence
+  // exit counts [B][4], threshold
+  int early_exit;
+  const float* maxprob;
+  int32_t* exit_counts;
+  double exit_thr;
 };
 
 int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s);

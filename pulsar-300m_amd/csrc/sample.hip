@@ -135,6 +135,20 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
     l[i + 2] = v.z;
     l[i + 3] = v.w;
   }
+  if (a.out_maxprob) {
+    // early-exit test (src/infer.py:540-541): max of softmax(logits) = 1 / sum exp(l - max),
+    // on the logits before penalty and temperature, rounded like the reference's softmax
+    // output in the activation dtype
+    float rm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) rm = fmaxf(rm, l[i]);
+    rm = block_max(rm, red);
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) z += expf(l[i] - rm);
+    z = block_sum(z, red);
+    if (threadIdx.x == 0) a.out_maxprob[lr] = rnd<T>(1.0f / z);
+  }
   if (a.rep_penalty != 1.0f) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -269,8 +283,10 @@ __device__ bool is_stop(const ControllerArgs& a, int tok) {
   return false;
 }
 
-__device__ void emit(const ControllerArgs& a, SeqState& s, int b, int tok) {
+// Append tok to the sequence's output; kind 1 marks an accepted draft, 0 a drawn token.
+__device__ void emit(const ControllerArgs& a, SeqState& s, int b, int tok, int kind = 0) {
   a.out_tokens[(int64_t)b * a.max_new + s.produced] = tok;
+  if (a.out_kinds) a.out_kinds[(int64_t)b * a.max_new + s.produced] = kind;
   s.produced += 1;
   a.seen[(int64_t)b * (a.V / 32) + (tok >> 5)] |= 1u << (tok & 31);
   if (s.produced >= s.max_new) s.done = 1;
@@ -308,12 +324,40 @@ __device__ void fresh(SeqState& s, int tok) {
 
 }  // namespace
 
+// Tokens whose pulses the reference runs through decode_step, the only place its early
+// exit applies: every decoded token in plain mode (src/infer.py:620), an accepted draft in
+// speculative mode (:728); the tested tokens' draft/verify passes never exit (:700-714).
+__device__ bool exit_eligible(const ControllerArgs& a, const SeqState& s) {
+  return a.early_exit && (!a.speculative || s.c_kind == KIND_PLAIN);
+}
+
+// Plain decode with early exit: the reference's loop runs decode_step on the last emitted
+// token as well (src/infer.py:619-620), and counts its exit; keep the sequence running for
+// that token's pulses (it emits nothing after them).
+__device__ void keep_for_tail(const ControllerArgs& a, SeqState& s) {
+  if (s.done && a.early_exit && !a.speculative) {
+    s.done = 0;
+    s.tail = 1;
+  }
+}
+
 // Advance one sequence's state after the step whose rows it ran.
 __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
   const int P = a.n_pulses;
   s.ctr += 1;
   const int pulse_ran = s.c_pulse;
-  if (pulse_ran < P - 1) {
+  bool last = pulse_ran >= P - 1;
+  if (exit_eligible(a, s)) {
+    // exit after pulse_ran when the top-1 probability of its logits reaches the threshold
+    // (src/infer.py:536-543); a token that runs every pulse counts at the last (:546-547)
+    if (!last && (double)a.maxprob[s.lrow_c] >= a.exit_thr) last = true;
+    if (last) a.exit_counts[b * 4 + pulse_ran] += 1;
+  }
+  if (last && s.tail) {
+    s.done = 1;
+    return;
+  }
+  if (!last) {
     if (pulse_ran == 0 && a.speculative) {
       const int lr = s.lrow_c;
       if (s.c_kind == KIND_TESTED) {
@@ -336,7 +380,7 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
     s.tests += 1;
     if (s.d_tok == v && !is_stop(a, s.d_tok)) {
       s.accepted += 1;
-      emit(a, s, b, s.d_tok);
+      emit(a, s, b, s.d_tok, 1);
       if (!s.done) promote(a, s, KIND_PLAIN);
     } else {
       const int t = a.draw[lr * 2 + 1];
@@ -358,6 +402,7 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
       s.done = 1;
     } else {
       emit(a, s, b, t);
+      keep_for_tail(a, s);
       if (!s.done) {
         if (a.speculative && s_ran && s.s_tok == t)
           promote(a, s, KIND_TESTED);
@@ -413,11 +458,16 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
       s.max_new = a.max_new;
       s.c_pos = a.prompt_len - 1;
       s.c_slot = 1;
+      // the first token was drawn with counter 0 (state cleared before that draw); step
+      // draws use counters 2 * ctr (+1 for the speculative row), so ctr starts at 1 and no
+      // later draw reuses the first token's uniform
+      s.ctr = 1;
       const int t = a.draw[b * 2];
       if (is_stop(a, t) || s.max_new <= 0) {
         s.done = 1;
       } else {
         emit(a, s, b, t);
+        keep_for_tail(a, s);
         fresh(s, t);
       }
     } else if (!s.done) {
@@ -428,7 +478,11 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
   const bool live = act && !s.done;
   const bool crow = live;
   const bool srow = live && a.speculative && s.c_pulse == P - 1 && s.s_valid;
-  const bool cwant = crow && (a.all_logits || s.c_pulse == P - 1 || (a.speculative && s.c_pulse == 0));
+  // logits of c: at its last pulse (the next draw; not for a tail token, which draws
+  // nothing), at pulse 0 when it drafts, and after every earlier pulse when it may exit
+  const bool cwant = crow && (a.all_logits || (s.c_pulse == P - 1 && !s.tail) ||
+                              (a.speculative && s.c_pulse == 0) ||
+                              (exit_eligible(a, s) && s.c_pulse < P - 1));
   int v[5] = {0, 0, 0, 0, 0};  // rows of pulse 0, 1, 2; logits rows; attention units
   if (crow) v[s.c_pulse] += 1;
   if (srow) v[0] += 1;
@@ -555,7 +609,7 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
       s.tests += 1;
       if (v == s.blk[i + 1] && !is_stop(a, v)) {
         s.accepted += 1;
-        emit(a, s, b, v);
+        emit(a, s, b, v, 1);
         acc = i + 1;
         if (s.done) return;
         continue;

@@ -217,10 +217,31 @@ def moe_dispatch_forward(x: torch.Tensor, topk_idx: torch.Tensor, token_to_slot:
 
 def moe_combine_forward(expert_outputs: torch.Tensor, topk_idx: torch.Tensor,
                         topk_weights: torch.Tensor, token_to_slot: torch.Tensor, shared_out=None):
-    """out[t] = shared[t] + sum_k w[t,k] * expert_out[e, slot] (csrc/kernels.cu:1633-1664)."""
+    """out[t] = shared[t] + sum_k w[t,k] * expert_out[e, slot] (csrc/kernels.cu:1633-1664).
+
+    The reference reads these through typed data_ptr calls, which raise on a wrong dtype;
+    here every operand the kernel dereferences is checked before the launch."""
+    for t, n in ((expert_outputs, "expert_outputs"), (topk_idx, "topk_idx"),
+                 (topk_weights, "topk_weights"), (token_to_slot, "token_to_slot")):
+        _cuda(t, n)
+        _req(t.device == expert_outputs.device, f"{n} must be on the device of expert_outputs")
+    _req(expert_outputs.dim() == 3, "expert_outputs must be [E, C, D]")
+    _req(topk_idx.dim() == 2, "topk_idx must be [N, K]")
+    _req(topk_idx.dtype == torch.int64, "topk_idx must be int64")
+    _req(token_to_slot.dtype == torch.int32, "token_to_slot must be int32")
     E, C, D = expert_outputs.shape
     N, K = topk_idx.shape
+    _req(tuple(token_to_slot.shape) == (N, K), "token_to_slot must be [N, K]")
+    _req(tuple(topk_weights.shape) == (N, K), "topk_weights must be [N, K]")
     code = _dtype_code(expert_outputs, "expert_outputs")
+    if shared_out is not None and shared_out.numel():
+        _cuda(shared_out, "shared_out")
+        _req(shared_out.device == expert_outputs.device,
+             "shared_out must be on the device of expert_outputs")
+        _req(shared_out.dtype == expert_outputs.dtype,
+             "shared_out must have the dtype of expert_outputs")
+        _req(shared_out.numel() == N * D and shared_out.shape[-1] == D,
+             "shared_out must be [N, D]")
     w = topk_weights.to(torch.bfloat16).contiguous()
     sh = shared_out.contiguous() if shared_out is not None and shared_out.numel() else None
     out = torch.empty((N, D), dtype=expert_outputs.dtype, device=expert_outputs.device)
@@ -240,7 +261,10 @@ def moe_slots_from_order(flat_e: torch.Tensor, order: torch.Tensor, num_experts:
     (csrc/kernels.cu:3058-3095)."""
     _cuda(flat_e, "flat_e")
     _req(flat_e.is_contiguous(), "flat_e must be contiguous CUDA")
+    _req(flat_e.dtype == torch.int64, "flat_e must be int64")
     _req(order.is_cuda and order.is_contiguous(), "order must be contiguous CUDA")
+    _req(order.device == flat_e.device, "order must be on the device of flat_e")
+    _req(order.numel() == flat_e.numel(), "order must have as many elements as flat_e")
     M = flat_e.numel()
     slots = torch.empty(M, dtype=torch.int32, device=flat_e.device)
     counts = torch.zeros(num_experts, dtype=torch.int64, device=flat_e.device)
@@ -444,6 +468,11 @@ def moe_combine_backward(d_routed_out: torch.Tensor, expert_outputs: torch.Tenso
                  (topk_idx, "topk_idx"), (token_to_slot, "token_to_slot")):
         _cuda(t, n)
         _req(t.is_contiguous(), f"{n} must be contiguous")
+    _req(topk_idx.dtype == torch.int64, "topk_idx must be int64")
+    _req(token_to_slot.dtype == torch.int32, "token_to_slot must be int32")
+    _req(tuple(token_to_slot.shape) == (N, K), "token_to_slot must be [N, K]")
+    _req(tuple(topk_weights.shape) == (N, K), "topk_weights must be [N, K]")
+    _req(d_routed_out.numel() == N * D, "d_routed_out must be [N, D]")
     if expert_counts is not None:
         _cuda(expert_counts, "expert_counts")
         _req(expert_counts.dtype == torch.int64, "expert_counts must be int64")

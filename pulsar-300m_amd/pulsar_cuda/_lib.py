@@ -20,6 +20,10 @@ BUF_CTL = 4
 BUF_LAST_ROWS = 5
 BUF_LAST_CTL = 6
 BUF_EXPERT_COUNTS = 7
+BUF_EXIT_COUNTS = 8
+BUF_TOPK_IDX = 9
+BUF_TOKEN_KINDS = 10
+ABI_VERSION = 3
 SEQSTATE_INTS = 32
 ROW_INTS = 8
 CTL_INTS = 16
@@ -66,7 +70,7 @@ class PulsarEngineConfig(ctypes.Structure):
         ("speculative", _c_i32), ("all_logits", _c_i32),
         ("temperature", _c_f32), ("top_p", _c_f32), ("repetition_penalty", _c_f32),
         ("n_stop", _c_i32), ("stop_ids", _c_i32 * 8), ("seed", ctypes.c_uint64),
-        ("draft_len", _c_i32), ("reserved", _c_i32),
+        ("draft_len", _c_i32), ("early_exit", _c_i32), ("early_exit_threshold", ctypes.c_double),
     ]
 
 

@@ -37,9 +37,11 @@ class HipEngine:
                  speculative: bool = True, temperature: float = 0.7, top_p: float = 0.9,
                  repetition_penalty: float = 1.15, stop_ids: Iterable[int] = (0,),
                  seed: int = 0, all_logits: bool = False, max_ctx: Optional[int] = None,
-                 draft_len: int = 0):
+                 draft_len: int = 0, early_exit_threshold: Optional[float] = None):
         """draft_len = 0 runs the reference's exact self-speculation; 1..7 the draft-block
-        mode (up to draft_len pulse-0 drafts per round, one all-pulse verify of the block)."""
+        mode (up to draft_len pulse-0 drafts per round, one all-pulse verify of the block).
+        early_exit_threshold (exact schedule only): the reference's adaptive early exit
+        (src/infer.py:536-547); None switches it off."""
         self.lib = _lib.load()
         self.model = model
         self.batch = batch
@@ -64,6 +66,9 @@ class HipEngine:
         for i, s in enumerate(stops):
             c.stop_ids[i] = s
         c.seed = seed & 0xFFFFFFFFFFFFFFFF
+        c.early_exit = int(early_exit_threshold is not None)
+        c.early_exit_threshold = float(early_exit_threshold) if early_exit_threshold is not None else 0.0
+        self.early_exit_threshold = early_exit_threshold
         model.ensure_rope(c.max_ctx)
         self.cfg = c
         h = ctypes.c_void_p()
@@ -191,6 +196,28 @@ class HipEngine:
         st = self.state()
         return int(st[:, ST_TESTS].sum()), int(st[:, ST_ACCEPTED].sum())
 
+    def token_kinds(self) -> list[list[int]]:
+        """Per emitted token: 1 when it was an accepted draft, 0 when drawn (the first token,
+        a plain draw, or the fresh draw after a rejected draft)."""
+        st = self.state()
+        k = self._read(_lib.BUF_TOKEN_KINDS, np.zeros((self.batch, max(1, self.max_new)), np.int32))
+        return [k[b, : st[b, ST_PRODUCED]].tolist() for b in range(self.batch)]
+
+    def exit_counts(self) -> np.ndarray:
+        """Early exit: tokens of each sequence that left after pulse k, [batch, n_pulses],
+        since the last prefill or rewind."""
+        c = self._read(_lib.BUF_EXIT_COUNTS, np.zeros((self.batch, 4), np.int32))
+        return c[:, : self.model.n_pulses]
+
+    def topk_idx(self) -> np.ndarray:
+        """Router top-k expert ids of every row of the last executed step in every layer,
+        [layers, rows, top_k] in the router's ranking order (rows as in rows())."""
+        c = self.model.cfg
+        buf = np.zeros((c.n_core, self.slots * self.batch, c.top_k), np.int32)
+        self._read(_lib.BUF_TOPK_IDX, buf)
+        n = int(self.last_ctl()[0])
+        return buf[:, :n]
+
 
 def sample_rows(logits: torch.Tensor, seen: Sequence[Iterable[int]], row_seq: Sequence[int],
                 row_extra: Sequence[int], ctr: Sequence[int], seed: int, temperature: float,
@@ -227,6 +254,29 @@ def sample_rows(logits: torch.Tensor, seen: Sequence[Iterable[int]], row_seq: Se
     return am.cpu().numpy(), dr.cpu().numpy()
 
 
+def early_exit_stats(counts: Sequence[int]) -> dict:
+    """Distribution of exit pulses (src/infer.py:215-232): per-pulse counts and shares, the
+    effective depth with pulses weighed as 8, 16 and 24 layers, and 24 / depth."""
+    c = [int(x) for x in counts]
+    total = sum(c)
+    if total == 0:
+        return {}
+    eff = (8 * c[0] + 16 * c[1] + 24 * c[2]) / total
+    return {"total_tokens": total, "pulse_counts": c,
+            "pulse_pcts": [c[0] / total * 100.0, c[1] / total * 100.0, c[2] / total * 100.0],
+            "effective_layers": eff, "compute_speedup": 24.0 / eff}
+
+
+def format_early_exit_stats(threshold: float, stats: dict) -> str:
+    """The block generate() prints after the text when early exit is on (src/infer.py:775-780)."""
+    p = stats["pulse_pcts"]
+    return (f"\n[Adaptive Early-Exit Stats | Threshold: {threshold:.2f}]\n"
+            f"  Tokens: {stats['total_tokens']} | P1 (8L): {p[0]:.1f}% | P2 (16L): {p[1]:.1f}% "
+            f"| P3 (24L): {p[2]:.1f}%\n"
+            f"  Effective Depth: {stats['effective_layers']:.1f} layers | "
+            f"Speedup: {stats['compute_speedup']:.2f}x\n")
+
+
 def stop_ids_for(cfg, tokenizer=None) -> set[int]:
     """{eos} plus the tokenizer ids of the reference's stop strings (src/infer.py:649-656)."""
     ids = {cfg.eos_token_id}
@@ -251,29 +301,82 @@ class PulsarInferenceEngine:
         self.dtype = model.dtype
         self.stop_token_ids = {self.cfg.eos_token_id}
         self.last_engine: Optional[HipEngine] = None
+        # adaptive early exit (src/infer.py:198-200): off until a threshold is set; the
+        # counts add up over generations until the threshold is set again
+        self.early_exit_threshold: Optional[float] = None
+        self.early_exit_counts = [0] * model.n_pulses
+        # engines (KV cache, buffers, captured graphs) kept for reuse, keyed by batch shape
+        # and generation settings
+        self._engines: dict = {}
+        self.max_cached_engines = 4
+
+    def set_early_exit_threshold(self, threshold: Optional[float]) -> None:
+        """Confidence threshold of the adaptive early exit; clears the counts
+        (src/infer.py:210-213)."""
+        self.early_exit_threshold = threshold
+        self.early_exit_counts = [0] * self.model.n_pulses
+
+    def get_early_exit_stats(self) -> dict:
+        """src/infer.py:215-232."""
+        return early_exit_stats(self.early_exit_counts)
+
+    def _engine(self, batch: int, prompt_len: int, max_new: int, speculative: bool,
+                temperature: float, top_p: float, repetition_penalty: float, stops, seed: int,
+                draft_len: int) -> HipEngine:
+        key = (batch, prompt_len, max_new, bool(speculative), float(temperature), float(top_p),
+               float(repetition_penalty), tuple(stops), int(draft_len),
+               self.early_exit_threshold)
+        eng = self._engines.get(key)
+        if eng is None or eng.handle is None:
+            while len(self._engines) >= self.max_cached_engines:
+                self._engines.pop(next(iter(self._engines))).close()
+            eng = HipEngine(self.model, batch=batch, max_prompt=prompt_len, max_new=max_new,
+                            speculative=speculative, temperature=temperature, top_p=top_p,
+                            repetition_penalty=repetition_penalty, stop_ids=stops, seed=seed,
+                            draft_len=draft_len, early_exit_threshold=self.early_exit_threshold)
+            self._engines[key] = eng
+        return eng
+
+    def _decode(self, eng: HipEngine, ids: np.ndarray, seed: int) -> None:
+        """Prefill (first token drawn with the engine's creation seed) and, for another seed,
+        redraw the first token from the kept prefill logits."""
+        eng.prefill(ids)
+        if (seed & 0xFFFFFFFFFFFFFFFF) != eng.cfg.seed:
+            eng.rewind(seed)
+
+    def _count_exits(self, eng: HipEngine) -> None:
+        if self.early_exit_threshold is not None:
+            c = eng.exit_counts().sum(axis=0)
+            self.early_exit_counts = [a + int(b) for a, b in zip(self.early_exit_counts, c)]
 
     def generate_ids(self, prompt_ids: Sequence[Sequence[int]], max_new_tokens: int = 512,
                      temperature: float = 0.7, top_p: float = 0.9,
                      repetition_penalty: float = 1.15, speculative: bool = True,
                      stop_ids: Optional[Iterable[int]] = None, seed: int = 0,
                      draft_len: int = 0) -> list[list[int]]:
-        """Batched id-level generation; prompts must share one length. draft_len > 0 selects
-        the draft-block mode (no reference counterpart; see HipEngine)."""
-        ids = np.asarray(prompt_ids, dtype=np.int32)
-        if ids.ndim == 1:
-            ids = ids[None, :]
+        """Batched id-level generation. Prompts of different lengths run as one batch per
+        length (results in prompt order). draft_len > 0 selects the draft-block mode (no
+        reference counterpart; see HipEngine)."""
+        if len(prompt_ids) and np.ndim(prompt_ids[0]) == 0:
+            prompt_ids = [prompt_ids]
+        prompts = [np.asarray(p, dtype=np.int32).reshape(-1) for p in prompt_ids]
         stops = sorted(stop_ids if stop_ids is not None else self.stop_token_ids)
-        eng = HipEngine(self.model, batch=ids.shape[0], max_prompt=ids.shape[1],
-                        max_new=max_new_tokens, speculative=speculative,
-                        temperature=temperature, top_p=top_p,
-                        repetition_penalty=repetition_penalty, stop_ids=stops, seed=seed,
-                        draft_len=draft_len)
-        try:
-            eng.prefill(ids)
-            eng.run()
-            out = eng.tokens()
-        finally:
+        groups: dict[int, list[int]] = {}
+        for i, p in enumerate(prompts):
+            if p.size == 0:
+                raise ValueError("empty prompt")
+            groups.setdefault(p.size, []).append(i)
+        out: list = [None] * len(prompts)
+        for T, members in groups.items():
+            ids = np.stack([prompts[i] for i in members])
+            eng = self._engine(len(members), T, max_new_tokens, speculative, temperature, top_p,
+                               repetition_penalty, stops, seed, draft_len)
             self.last_engine = eng
+            self._decode(eng, ids, seed)
+            eng.run()
+            self._count_exits(eng)
+            for i, toks in zip(members, eng.tokens()):
+                out[i] = toks
         return out
 
     def _stream(self, tokenizer, prompt: str, max_new_tokens, temperature, top_p,
@@ -281,11 +384,10 @@ class PulsarInferenceEngine:
         ids = tokenizer.encode(prompt, return_tensors="pt")
         ids = np.asarray(ids.reshape(1, -1).cpu().numpy(), dtype=np.int32)
         stops = stop_ids_for(self.cfg, tokenizer)
-        eng = HipEngine(self.model, batch=1, max_prompt=ids.shape[1], max_new=max_new_tokens,
-                        speculative=speculative, temperature=temperature, top_p=top_p,
-                        repetition_penalty=repetition_penalty, stop_ids=sorted(stops))
+        eng = self._engine(1, ids.shape[1], max_new_tokens, speculative, temperature, top_p,
+                           repetition_penalty, sorted(stops), 0, 0)
         self.last_engine = eng
-        eng.prefill(ids)
+        self._decode(eng, ids, 0)
         sent = 0
         limit = 4 * (max_new_tokens + 2) * self.model.n_pulses
         while True:
@@ -296,6 +398,7 @@ class PulsarInferenceEngine:
             if eng.state()[0, ST_DONE] or eng.steps >= limit:
                 break
             eng.step(8, graph=True)
+        self._count_exits(eng)
 
     def stream_generate(self, tokenizer, prompt: str, max_new_tokens: int = 512,
                         temperature: float = 0.7, top_p: float = 0.9,
@@ -329,4 +432,8 @@ class PulsarInferenceEngine:
         if stream:
             sys.stdout.write("\n")
             sys.stdout.flush()
+        if self.early_exit_threshold is not None:
+            stats = self.get_early_exit_stats()
+            if stats:
+                print(format_early_exit_stats(self.early_exit_threshold, stats), end="")
         return prompt + "".join(pieces)

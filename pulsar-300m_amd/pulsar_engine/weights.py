@@ -211,6 +211,20 @@ def synthetic_state(cfg: PulsarConfig, seed: int = 0, std: float = 0.02,
     return out
 
 
+def exit_probe_state(cfg: PulsarConfig, seed: int = 0) -> dict[str, np.ndarray]:
+    """synthetic_state with pulse 0's harmonic residual scale x3 and pulse 1's x0.
+
+    With the plain init the top-1 probability falls from pulse to pulse, so an early-exit
+    threshold never sends a token out after pulse 1; with these scales it rises from pulse
+    0 to pulse 1 and every exit pulse can be exercised."""
+    st = synthetic_state(cfg, seed=seed)
+    rs = st["pulse_res_scale"].copy()
+    rs[0] *= np.float32(3.0)
+    rs[1] *= np.float32(0.0)
+    st["pulse_res_scale"] = rs
+    return st
+
+
 def state_digest(state: dict[str, np.ndarray]) -> str:
     """SHA-256 over names, shapes and fp32 bytes in sorted-name order."""
     h = hashlib.sha256()

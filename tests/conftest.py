@@ -80,3 +80,38 @@ def max_abs_rel(actual, expected) -> float:
     a = torch.as_tensor(actual).float()
     e = torch.as_tensor(expected).float()
     return ((a - e).abs().max() / e.abs().max().clamp_min(1e-12)).item()
+
+
+def poisson_binomial_pvalue(ps, k: int) -> float:
+    """Two-sided p-value of observing k successes among independent Bernoulli(p_i) trials:
+    the total probability of outcomes no more likely than k (exact, by dynamic programming
+    over the trials)."""
+    dist = np.zeros(len(ps) + 1)
+    dist[0] = 1.0
+    for i, p in enumerate(ps):
+        nxt = dist * (1.0 - p)
+        nxt[1:i + 2] += dist[:i + 1] * p
+        dist = nxt
+    return float(dist[dist <= dist[k] * (1 + 1e-9)].sum())
+
+
+def chi_square_pvalue(samples, probs, min_expected: float = 5.0) -> float:
+    """Goodness of fit of integer samples to a distribution over [0, len(probs)): Pearson's
+    chi-square over the categories expected >= min_expected times, the rest (and any
+    probability mass missing from probs) pooled into one category."""
+    from scipy.stats import chi2
+
+    n = len(samples)
+    p = np.asarray(probs, dtype=np.float64)
+    allc = np.bincount(np.asarray(samples, dtype=np.int64), minlength=len(p)).astype(np.float64)
+    counts, beyond = allc[: len(p)], allc[len(p):].sum()
+    exp = n * p
+    big = exp >= min_expected
+    obs_b, exp_b = list(counts[big]), list(exp[big])
+    rest_o, rest_e = counts[~big].sum() + beyond, n - exp[big].sum()
+    if rest_e > 0 or rest_o > 0:
+        obs_b.append(rest_o)
+        exp_b.append(max(rest_e, 1e-12))
+    obs_b, exp_b = np.asarray(obs_b), np.asarray(exp_b)
+    stat = float(((obs_b - exp_b) ** 2 / exp_b).sum())
+    return float(chi2.sf(stat, max(1, len(obs_b) - 1)))

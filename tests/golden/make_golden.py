@@ -20,6 +20,11 @@ Outputs (``tests/golden/*.npz`` plus ``index.json``):
   pulse logits of the first decode step, 64-token greedy self-speculative stream with
   per-step top-5 ids/logits of the draft (pulse 0) and verify (pulse 2) passes, and a
   penalty-10 greedy stream whose tokens are not dominated by the self-logit.
+* ``early_exit.npz`` — adaptive early exit: tiny config (weights of ``weights.exit_probe_state``)
+  in fp32 and bf16 at three thresholds, plain and self-speculative, greedy and seeded
+  sampled: id streams and per-pulse exit counts, and the text and statistics generate()
+  prints; full-size fp32 model at threshold 0.9978: plain and self-speculative greedy
+  streams and counts. Written alone with ``--only early_exit``.
 """
 
 from __future__ import annotations
@@ -192,13 +197,98 @@ def full_goldens(ref_root: str, out_dir: str) -> dict:
             "weights_sha256": digest, "dtype": "fp32"}
 
 
+def run_exit(engine, tok, prompt_key, n, temperature, top_p, rp, speculative, thr, seed=None):
+    """One generation with early exit at `thr`; returns (ids, per-pulse exit counts)."""
+    engine.set_early_exit_threshold(thr)
+    ids = run(engine, tok, prompt_key, n, temperature, top_p, rp, speculative, seed=seed)
+    return ids, list(engine.early_exit_counts)
+
+
+def early_exit_goldens(ref_root: str, out_dir: str, skip_full: bool) -> dict:
+    """Adaptive early exit (src/infer.py:198-232, :526-549, :775-780): id streams and per-pulse
+    exit counts of plain and self-speculative generation, and the stats text generate()
+    prints. Tiny config in fp32 and bf16 with weights.exit_probe_state weights; full-size fp32 model
+    with the plain synthetic weights."""
+    import contextlib
+    import io
+
+    out = {}
+    cfg = tiny_config()
+    state = W.exit_probe_state(cfg)
+    prompt = W.uniform_ids(0, "tiny_prompt", 24, cfg.vocab_size).tolist()
+    tok = IdTokenizer({"p": prompt})
+    # the last threshold of each dtype lies between the top-1 probabilities after pulse 0
+    # (fp32 0.0162719, bf16 0.0162354) and pulse 1 (0.0162895, 0.0163574) of the first
+    # decoded token, which therefore leaves after pulse 1
+    thr_by = {"fp32": [0.0140, 0.0155, 0.01628], "bf16": [0.0140, 0.0155, 0.0163]}
+    out["tiny_prompt"] = np.array(prompt, dtype=np.int64)
+    for dtype, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        thrs = thr_by[tag]
+        out[f"tiny_{tag}_thresholds"] = np.array(thrs, dtype=np.float64)
+        eng = build_reference(ref_root, cfg, state, dtype)
+        for i, thr in enumerate(thrs):
+            cases = {
+                "greedy_plain": (20, 0.0, 1.0, 10.0, False, None),
+                "greedy_spec": (20, 0.0, 1.0, 10.0, True, None),
+                "sampled_spec": (20, 0.8, 0.95, 10.0, True, 1234),
+                "sampled_plain": (20, 0.8, 0.95, 10.0, False, 1234),
+                "greedy_spec_rp115": (20, 0.0, 1.0, 1.15, True, None),
+            }
+            for name, (n, T, tp, rp, spec, seed) in cases.items():
+                ids, counts = run_exit(eng, tok, "p", n, T, tp, rp, spec, thr, seed)
+                out[f"tiny_{tag}_{name}_{i}_ids"] = np.array(ids, dtype=np.int64)
+                out[f"tiny_{tag}_{name}_{i}_counts"] = np.array(counts, dtype=np.int64)
+        # generate() with the threshold set prints the exit statistics after the text
+        eng.set_early_exit_threshold(thrs[2])
+        buf = io.StringIO()
+        with contextlib.redirect_stdout(buf):
+            text = eng.generate(tok, "p", max_new_tokens=12, temperature=0.0, top_p=1.0,
+                                repetition_penalty=10.0, stream=False, speculative=False)
+        out[f"tiny_{tag}_generate_text"] = np.array(text)
+        out[f"tiny_{tag}_generate_stdout"] = np.array(buf.getvalue())
+        out[f"tiny_{tag}_generate_counts"] = np.array(eng.early_exit_counts, dtype=np.int64)
+    meta = {"tiny_config": cfg.to_dict(), "tiny_weights_sha256": W.state_digest(state),
+            "tiny_weights": "weights.exit_probe_state (pulse_res_scale[0] x3, [1] x0)"}
+    if not skip_full:
+        fcfg = PulsarConfig()
+        fstate = W.synthetic_state(fcfg, seed=0)
+        fprompt = W.uniform_ids(0, "prompt", 128, fcfg.vocab_size).tolist()
+        ftok = IdTokenizer({"p": fprompt})
+        eng = build_reference(ref_root, fcfg, fstate, torch.float32)
+        out["full_prompt"] = np.array(fprompt, dtype=np.int64)
+        out["full_threshold"] = np.array(0.9978, dtype=np.float64)
+        ids, counts = run_exit(eng, ftok, "p", 32, 0.0, 1.0, 10.0, False, 0.9978)
+        out["full_greedy_plain_ids"] = np.array(ids, dtype=np.int64)
+        out["full_greedy_plain_counts"] = np.array(counts, dtype=np.int64)
+        ids, counts = run_exit(eng, ftok, "p", 32, 0.0, 1.0, 10.0, True, 0.9978)
+        out["full_greedy_spec_ids"] = np.array(ids, dtype=np.int64)
+        out["full_greedy_spec_counts"] = np.array(counts, dtype=np.int64)
+        meta["full_weights_sha256"] = W.state_digest(fstate)
+    path = os.path.join(out_dir, "early_exit.npz")
+    np.savez_compressed(path, **out)
+    meta.update({"file": os.path.basename(path), "seed": 0})
+    return meta
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
     ap.add_argument("--out", default=HERE)
     ap.add_argument("--skip-full", action="store_true")
+    ap.add_argument("--only", choices=["early_exit"], default=None,
+                    help="write only this golden file and add its entry to index.json")
     args = ap.parse_args()
     torch.set_num_threads(max(1, min(8, os.cpu_count() or 1)))
+    if args.only == "early_exit":
+        path = os.path.join(args.out, "index.json")
+        with open(path) as f:
+            index = json.load(f)
+        entry = early_exit_goldens(args.ref, args.out, args.skip_full)
+        index["entries"] = [e for e in index["entries"] if e["file"] != entry["file"]] + [entry]
+        with open(path, "w") as f:
+            json.dump(index, f, indent=1)
+        print("[golden] wrote", entry["file"])
+        return
     index = {"generator": "tests/golden/make_golden.py", "torch": torch.__version__,
              "rope_tables": "fp32 (reference HAS_PULSAR_CUDA=True, CPU tensors)",
              "numpy": np.__version__, "stop_ids": [0, 2], "entries": []}

@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     assert set(_declared()) == set(_lib.EXPORTED)
     lib.pulsar_abi_version.restype = ctypes.c_int
-    assert lib.pulsar_abi_version() == 2
+    assert lib.pulsar_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_struct_layouts_match_the_c_header(tmp_path):
@@ -50,7 +50,8 @@ def test_struct_layouts_match_the_c_header(tmp_path):
     src = tmp_path / "layout.cpp"
     fields_m = ["vocab", "dtype", "local_mask", "rms_eps", "rope_len", "tok_emb", "rope_sin_global",
                 "attn_norm", "wqkvg", "routed_scale"]
-    fields_c = ["max_batch", "temperature", "n_stop", "stop_ids", "seed", "draft_len"]
+    fields_c = ["max_batch", "temperature", "n_stop", "stop_ids", "seed", "draft_len",
+                "early_exit", "early_exit_threshold"]
     lines = ["#include <cstdio>", "#include <cstddef>", f'#include "{HEADER}"', "int main() {",
              'printf("%zu %zu\\n", sizeof(PulsarModelDesc), sizeof(PulsarEngineConfig));']
     lines += [f'printf("%zu\\n", offsetof(PulsarModelDesc, {f}));' for f in fields_m]

@@ -1,0 +1,211 @@
+"""GPU: router indices of the engine, the sampled-token distribution, random streams and
+verify-entry guards.
+
+* Router: the engine's per-layer top-4 expert ids of every row of every step (readable
+  buffer) against the oracle's decode router trace (src/infer.py:324-333), rank by rank.
+  fp32: identical everywhere. bf16: identical wherever the oracle's biased scores separate
+  consecutive ranks (through rank 5) by more than 1e-2 (the router input differs from the
+  oracle's by bf16 rounding of the layer stack); at least 95 % of all decisions compared.
+  Shapes: a 40-token prompt, and the skewed-routing shape (256 x 512 Zipf prompts, router
+  weights x4; sequences 0 and 255 compared).
+* Sampled self-speculation: 2048 runs (256 slots x 8 seeds) of the first three emitted
+  tokens against the exact distributions the oracle enumerates from its own logits
+  (oracle.spec_token_marginals), chi-square per token.
+* The first token's draw and its draft's draw use different random numbers (the draft is
+  the engine's sampler at the step counter, not the first token's).
+* verify() without a block uploaded since the last prefill / fill_kv, and stepping or
+  rewinding after a failed prefill, are refused before any launch.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import chi_square_pvalue
+
+pytestmark = pytest.mark.gpu
+
+
+def _router_by_pass(trace):
+    """{(token, pos, pulse): [layer -> (idx [K], biased scores [E])]} from an oracle trace."""
+    out, pending = {}, []
+    for t in trace:
+        if t[0] == "router":
+            pending.append((t[3][0].tolist(), t[4][0].double()))
+        elif t[0] == "pulse":
+            out[(t[1], t[2], t[3])] = pending
+            pending = []
+    return out
+
+
+def _compare_router(model, cfg, st, dtype, prompts, n_new, check):
+    from oracle import pulsar_ref as R
+    from pulsar_engine.engine import HipEngine
+
+    ref_pass, ref_ids = {}, {}
+    for b in check:
+        ref = R.load_ref(cfg, st, dtype, stop_ids=set())
+        ref.trace = []
+        ref_ids[b] = list(ref.stream_generate_ids(prompts[b], n_new, 0.0, 1.0, 10.0))
+        ref_pass[b] = _router_by_pass(ref.trace)
+    K = cfg.top_k
+    strict = same = total = 0
+    with HipEngine(model, batch=len(prompts), max_prompt=len(prompts[0]), max_new=n_new,
+                   speculative=False, temperature=0.0, repetition_penalty=10.0,
+                   stop_ids=[]) as eng:
+        eng.prefill(np.asarray(prompts))
+        for _ in range(4 * n_new + 8):
+            if eng.state()[:, 0].all():
+                break
+            emitted = eng.tokens()
+            eng.step(1)
+            rows, tk = eng.rows(last=True), eng.topk_idx()
+            for i, r in enumerate(rows):
+                b, key = int(r[0]), (int(r[4]), int(r[3]), int(r[2]))
+                if b not in ref_pass or emitted[b] != ref_ids[b][:len(emitted[b])]:
+                    continue  # compared while the streams agree
+                if key not in ref_pass[b]:
+                    continue
+                for L, (want, sc) in enumerate(ref_pass[b][key]):
+                    got = tk[L, i].tolist()
+                    total += 1
+                    same += got == want
+                    if dtype == torch.float32:
+                        assert got == want, (b, key, L, got, want)
+                        continue
+                    top = torch.sort(sc, descending=True).values[: K + 1]
+                    if float((top[:-1] - top[1:]).min()) > 1e-2:
+                        strict += 1
+                        assert got == want, (b, key, L, got, want, top.tolist())
+    print(f"[router] {dtype}: {total} decisions, {same} identical, {strict} with clear margins",
+          flush=True)
+    assert total >= len(check) * cfg.n_core * 3
+    assert same >= 0.95 * total
+    return total
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_engine_router_indices_equal_oracle(models, full_state, dtype):
+    from pulsar_engine import weights as W
+
+    cfg, st = full_state
+    prompts = [W.uniform_ids(s, "router_prompt", 40, cfg.vocab_size).tolist() for s in range(2)]
+    _compare_router(models[dtype], cfg, st, dtype, prompts, 6, check=[0, 1])
+
+
+@pytest.fixture(scope="module")
+def skewed(full_state):
+    from pulsar_engine import weights as W
+
+    cfg = full_state[0]
+    return W.synthetic_state(cfg, seed=0, router_scale=4.0)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_engine_router_indices_equal_oracle_skewed_256x512(full_state, skewed, dtype):
+    from pulsar_engine import weights as W
+    from pulsar_engine.model import DeviceModel
+
+    cfg = full_state[0]
+    model = DeviceModel(cfg, skewed, dtype)
+    prompts = [W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size).tolist() for b in range(256)]
+    _compare_router(model, cfg, skewed, dtype, prompts, 3, check=[0, 255])
+    del model
+    torch.cuda.empty_cache()
+
+
+@pytest.fixture(scope="module")
+def small_fp32():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from pulsar_engine import weights as W
+    from pulsar_engine.config import small_config
+    from pulsar_engine.model import DeviceModel
+
+    cfg = small_config()
+    st = W.synthetic_state(cfg, seed=0)
+    return cfg, st, DeviceModel(cfg, st, torch.float32)
+
+
+def test_sampled_first_three_tokens_follow_the_oracle_distribution(small_fp32):
+    from oracle import pulsar_ref as R
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+
+    cfg, st, model = small_fp32
+    prompt = W.uniform_ids(0, "dist_prompt", 24, cfg.vocab_size)
+    T_, TP, RP = 0.05, 0.95, 10.0
+    marg = R.spec_token_marginals(R.load_ref(cfg, st, torch.float32, stop_ids=set()), prompt,
+                                  T_, TP, RP, prune=1e-4)
+    draws = []
+    with HipEngine(model, batch=256, max_prompt=24, max_new=3, speculative=True,
+                   temperature=T_, top_p=TP, repetition_penalty=RP, stop_ids=[],
+                   seed=1000) as eng:
+        eng.prefill(np.tile(prompt, (256, 1)))
+        for rep in range(8):
+            if rep:
+                eng.rewind(1000 + rep)
+            eng.run()
+            draws += eng.tokens()
+    draws = np.asarray(draws)
+    assert draws.shape == (2048, 3)
+    pvals = [chi_square_pvalue(draws[:, k], marg[k].numpy()) for k in range(3)]
+    print(f"[sampling] chi-square p-values of tokens 1-3: {pvals}", flush=True)
+    assert min(pvals) > 1e-4
+
+
+def test_first_draft_draw_is_independent_of_the_first_token_draw(small_fp32):
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine, sample_rows
+
+    cfg, st, model = small_fp32
+    prompt = W.uniform_ids(4, "dist_prompt", 24, cfg.vocab_size)
+    kw = dict(temperature=0.8, top_p=0.95, repetition_penalty=1.15)
+    with HipEngine(model, batch=1, max_prompt=24, max_new=8, speculative=True, stop_ids=[],
+                   seed=77, all_logits=True, **kw) as eng:
+        eng.prefill(prompt[None])
+        pre = torch.from_numpy(eng.logits(1)).cuda()
+        first = eng.tokens()[0][0]
+        eng.step(1)
+        rows = eng.rows(last=True)
+        c = [r for r in rows if int(r[4]) == first and int(r[2]) == 0][0]
+        lg = torch.from_numpy(eng.logits(len(rows))[int(c[5])][None]).cuda()
+        d_tok = int(eng.state()[0, 10])
+    _, dr0 = sample_rows(pre, [prompt.tolist()], [0], [-1], [0], 77, dtype=torch.float32, **kw)
+    assert int(dr0[0, 0]) == first  # the first token: counter 0
+    seen = [prompt.tolist() + [first]]
+    _, dr1 = sample_rows(lg, seen, [0], [-1], [1], 77, dtype=torch.float32, **kw)
+    assert int(dr1[0, 0]) == d_tok  # its draft: the step counter (1), not counter 0
+
+
+def test_verify_and_stepping_guards(small_fp32):
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+
+    cfg, st, model = small_fp32
+    prompts = np.stack([W.uniform_ids(s, "guard", 8, cfg.vocab_size) for s in range(2)])
+    with HipEngine(model, batch=2, max_prompt=8, max_new=4, draft_len=4, stop_ids=[]) as eng:
+        with pytest.raises(RuntimeError, match="prefill or fill_kv first"):
+            eng.verify(None)
+        eng.prefill(prompts)
+        with pytest.raises(RuntimeError, match="no block uploaded"):
+            eng.verify(None)
+        eng.verify(prompts[:, :3])
+        eng.verify(None)
+        eng.fill_kv(8)
+        with pytest.raises(RuntimeError, match="no block uploaded"):
+            eng.verify(None)
+        bad = prompts.copy()
+        bad[1, 3] = cfg.vocab_size
+        with pytest.raises(RuntimeError, match="out of vocabulary"):
+            eng.prefill(bad)
+        with pytest.raises(RuntimeError, match="prefill before stepping"):
+            eng.step(1)
+        with pytest.raises(RuntimeError, match="prefill first"):
+            eng.rewind(3)
+        eng.prefill(prompts)
+        eng.run()
+        assert all(len(t) == 4 for t in eng.tokens())

@@ -149,3 +149,88 @@ def test_prefill_flops_count_each_query_key_pair(T):
             + cfg.top_k * (2 * cfg.d_expert * D + D * cfg.d_expert))
     assert f["projections"] == 2 * macs * cfg.n_core * cfg.default_pulses * 2 * T
     assert f["total"] == sum(v for k, v in f.items() if k != "total")
+
+
+def test_poisson_binomial_pvalue_against_binomial_and_brute_force():
+    from scipy.stats import binomtest
+
+    from conftest import poisson_binomial_pvalue
+
+    # equal probabilities: the binomial test with the same two-sided rule
+    for n, p, k in ((40, 0.3, 5), (40, 0.3, 12), (64, 0.95, 64), (64, 0.95, 55)):
+        want = binomtest(k, n, p, alternative="two-sided").pvalue
+        assert abs(poisson_binomial_pvalue([p] * n, k) - want) < 1e-9, (n, p, k)
+    # unequal probabilities: enumerate all 2^n outcomes
+    import itertools
+
+    ps = [0.1, 0.5, 0.9, 0.7, 0.2]
+    dist = [0.0] * 6
+    for bits in itertools.product((0, 1), repeat=5):
+        pr = 1.0
+        for b, p in zip(bits, ps):
+            pr *= p if b else 1 - p
+        dist[sum(bits)] += pr
+    for k in range(6):
+        want = sum(d for d in dist if d <= dist[k] * (1 + 1e-9))
+        assert abs(poisson_binomial_pvalue(ps, k) - want) < 1e-12
+
+
+def test_chi_square_pvalue_detects_a_shifted_distribution():
+    import numpy as np
+
+    from conftest import chi_square_pvalue
+
+    rng = np.random.default_rng(0)
+    p = np.array([0.5, 0.3, 0.15, 0.04, 0.01])
+    good = rng.choice(5, size=3000, p=p)
+    assert chi_square_pvalue(good, p) > 1e-3
+    bad = rng.choice(5, size=3000, p=[0.45, 0.35, 0.15, 0.04, 0.01])
+    assert chi_square_pvalue(bad, p) < 1e-4
+    # mass missing from probs is pooled: samples there count against the rest category
+    assert chi_square_pvalue(good, p[:4]) > 1e-3
+
+
+def test_op_wrappers_check_operands_before_the_library_is_called(monkeypatch):
+    """moe_combine_forward / moe_combine_backward / moe_slots_from_order reject operands the
+    kernels would read out of bounds (wrong dtype, shape or device) with RuntimeError and
+    never reach the library. Device checks are stubbed so that CPU tensors stand in."""
+    import torch
+
+    import pulsar_cuda as pc
+
+    class NoLib:
+        def __getattr__(self, name):
+            raise AssertionError(f"library called: {name}")
+
+    monkeypatch.setattr(pc, "_LIB", NoLib())
+    monkeypatch.setattr(pc, "_cuda", lambda t, n: None)
+    monkeypatch.setattr(pc, "_stream", lambda t: 0)
+    E, C, D, N, K = 4, 8, 16, 5, 2
+    eo = torch.zeros(E, C, D, dtype=torch.bfloat16)
+    idx = torch.zeros(N, K, dtype=torch.int64)
+    w = torch.zeros(N, K, dtype=torch.bfloat16)
+    slots = torch.zeros(N, K, dtype=torch.int32)
+    sh = torch.zeros(N, D, dtype=torch.bfloat16)
+    cases = {
+        "topk_idx must be int64": dict(topk_idx=idx.int()),
+        "token_to_slot must be int32": dict(token_to_slot=slots.long()),
+        "token_to_slot must be \\[N, K\\]": dict(token_to_slot=slots[:3]),
+        "topk_weights must be \\[N, K\\]": dict(topk_weights=w[:, :1]),
+        "shared_out must have the dtype": dict(shared_out=sh.float()),
+        "shared_out must be \\[N, D\\]": dict(shared_out=sh[:2]),
+    }
+    for msg, over in cases.items():
+        args = dict(expert_outputs=eo, topk_idx=idx, topk_weights=w, token_to_slot=slots,
+                    shared_out=sh)
+        args.update(over)
+        with pytest.raises(RuntimeError, match=msg):
+            pc.moe_combine_forward(**args)
+    dro = torch.zeros(N, D, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="topk_idx must be int64"):
+        pc.moe_combine_backward(dro, eo, idx.int(), w, slots)
+    with pytest.raises(RuntimeError, match="token_to_slot must be int32"):
+        pc.moe_combine_backward(dro, eo, idx, w, slots.long())
+    with pytest.raises(RuntimeError, match="d_routed_out must be \\[N, D\\]"):
+        pc.moe_combine_backward(dro[:2], eo, idx, w, slots)
+    with pytest.raises(RuntimeError, match="flat_e must be int64"):
+        pc.moe_slots_from_order(idx.view(-1).int(), idx.view(-1), E, C)

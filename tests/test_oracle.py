@@ -289,3 +289,186 @@ def test_full_size_fp32_goldens(full_state):
     eng.trace = None
     ids = list(eng.self_speculative_ids(g["prompt"], 32, 0.0, 1.0, 10.0))
     assert ids == g["greedy_rp10_spec_ids"].tolist()
+
+
+# -- adaptive early exit (src/infer.py:198-232, :526-549) -------------------------------
+
+@pytest.mark.parametrize("tag,dtype", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_early_exit_tiny_goldens(tag, dtype):
+    """Streams and per-pulse exit counts equal the reference's at three thresholds (the
+    last sends the first decoded token out after pulse 1), plain and self-speculative,
+    greedy and seeded sampled."""
+    from pulsar_engine import weights as W
+    from pulsar_engine.config import tiny_config
+
+    cfg = tiny_config()
+    st = W.exit_probe_state(cfg)
+    g = golden("early_exit.npz")
+    prompt = g["tiny_prompt"]
+    eng = R.load_ref(cfg, st, dtype, stop_ids={0, 2})
+    cases = {
+        "greedy_plain": (0.0, 1.0, 10.0, False, None),
+        "greedy_spec": (0.0, 1.0, 10.0, True, None),
+        "sampled_spec": (0.8, 0.95, 10.0, True, 1234),
+        "sampled_plain": (0.8, 0.95, 10.0, False, 1234),
+        "greedy_spec_rp115": (0.0, 1.0, 1.15, True, None),
+    }
+    seen_exit_pulses = set()
+    for i, thr in enumerate(g[f"tiny_{tag}_thresholds"].tolist()):
+        for name, (T, tp, rp, spec, seed) in cases.items():
+            eng.set_early_exit_threshold(thr)
+            if seed is not None:
+                torch.manual_seed(seed)
+            gen = eng.self_speculative_ids if spec else eng.stream_generate_ids
+            ids = list(gen(prompt, 20, T, tp, rp))
+            assert ids == g[f"tiny_{tag}_{name}_{i}_ids"].tolist(), (name, thr)
+            assert eng.early_exit_counts == g[f"tiny_{tag}_{name}_{i}_counts"].tolist(), (name, thr)
+            seen_exit_pulses |= {k for k, c in enumerate(eng.early_exit_counts) if c}
+    assert seen_exit_pulses == {0, 1, 2}
+    # set_early_exit_threshold clears the counts; None switches the exit off
+    eng.set_early_exit_threshold(None)
+    assert eng.early_exit_counts == [0, 0, 0] and eng.get_early_exit_stats() == {}
+    assert list(eng.stream_generate_ids(prompt, 6, 0.0, 1.0, 10.0)) == \
+        list(R.load_ref(cfg, st, dtype, stop_ids={0, 2}).stream_generate_ids(prompt, 6, 0.0, 1.0, 10.0))
+    assert eng.early_exit_counts == [0, 0, 0]
+
+
+def test_early_exit_stats_text_matches_reference():
+    """generate()'s statistics block (src/infer.py:775-780) from the counts of the golden
+    run, formatted by the host mirror, equals what the reference printed."""
+    from pulsar_engine.engine import early_exit_stats, format_early_exit_stats
+
+    g = golden("early_exit.npz")
+    for tag in ("fp32", "bf16"):
+        thr = float(g[f"tiny_{tag}_thresholds"][2])
+        stats = early_exit_stats(g[f"tiny_{tag}_generate_counts"].tolist())
+        assert format_early_exit_stats(thr, stats) == str(g[f"tiny_{tag}_generate_stdout"])
+        # the oracle's statistics agree with the host mirror's
+        eng = R.RefEngine.__new__(R.RefEngine)
+        eng.early_exit_counts = g[f"tiny_{tag}_generate_counts"].tolist()
+        assert R.RefEngine.get_early_exit_stats(eng) == stats
+    assert early_exit_stats([0, 0, 0]) == {}
+    s = early_exit_stats([1, 1, 2])
+    # closed form: (8 + 16 + 2 * 24) / 4 = 18 layers, 24 / 18 speedup
+    assert s["effective_layers"] == 18.0 and abs(s["compute_speedup"] - 24 / 18) < 1e-12
+    assert s["pulse_pcts"] == [25.0, 25.0, 50.0]
+
+
+def test_early_exit_full_fp32_golden(full_state):
+    """Full-size fp32 model at threshold 0.9978: streams and exit counts of the reference."""
+    cfg, st = full_state
+    g = golden("early_exit.npz")
+    eng = R.load_ref(cfg, st, torch.float32, stop_ids={0, 2})
+    thr = float(g["full_threshold"])
+    for name, spec in (("greedy_plain", False), ("greedy_spec", True)):
+        eng.set_early_exit_threshold(thr)
+        gen = eng.self_speculative_ids if spec else eng.stream_generate_ids
+        assert list(gen(g["full_prompt"], 32, 0.0, 1.0, 10.0)) == g[f"full_{name}_ids"].tolist()
+        assert eng.early_exit_counts == g[f"full_{name}_counts"].tolist()
+
+
+def test_early_exit_rule_on_hand_built_passes():
+    """decode_step's exit rule with stubbed pulse passes: after pulse k < 2 the token leaves
+    when softmax's top-1 probability >= threshold, returns pulse k's logits and counts at
+    k; a token running every pulse counts at pulse 2; no threshold, no counting."""
+    V = 8
+
+    def logits_with_top(p):
+        # softmax of [a, 0, ..., 0] has top-1 probability e^a / (e^a + V - 1) = p
+        lg = torch.zeros(1, V)
+        lg[0, 5] = math.log(p * (V - 1) / (1.0 - p))
+        return lg
+
+    probs = {0: 0.50, 1: 0.80, 2: 0.30}
+    eng = R.RefEngine.__new__(R.RefEngine)
+    eng.cfg = type("C", (), {"default_pulses": 3})()
+    eng.trace = None
+    ran = []
+
+    def fake_pass(token, pos, cache, pulse, h=None, e=None):
+        ran.append(pulse)
+        return logits_with_top(probs[pulse]), None, None
+
+    eng.decode_pulse_pass = fake_pass
+    cache = type("K", (), {})()
+    for thr, want_pulses, want_counts in ((0.45, [0], [1, 0, 0]), (0.75, [0, 1], [0, 1, 0]),
+                                          (0.85, [0, 1, 2], [0, 0, 1]), (None, [0, 1, 2], [0, 0, 0])):
+        R.RefEngine.set_early_exit_threshold(eng, thr)
+        ran.clear()
+        out = R.RefEngine.decode_step(eng, 3, 10, cache)
+        assert ran == want_pulses and eng.early_exit_counts == want_counts, thr
+        top = F.softmax(out, dim=-1).max().item()
+        assert abs(top - probs[want_pulses[-1]]) < 1e-6
+        assert cache.seq_len == 11
+
+
+def test_replay_acceptance_reproduces_the_generators_own_tests(tiny_state):
+    """Driving the loop along the generator's own emitted stream gives back, test for test,
+    the acceptance probabilities and outcomes the generator recorded."""
+    cfg, st = tiny_state
+    for dtype, T, rp, seed in ((torch.float32, 0.02, 10.0, 3), (torch.bfloat16, 0.05, 10.0, 3)):
+        eng = R.load_ref(cfg, st, dtype, stop_ids=set())
+        stats = {}
+        torch.manual_seed(seed)
+        ids = list(eng.self_speculative_ids(W_prompt(cfg), 30, T, 0.95, rp, stats=stats))
+        assert len(ids) == 30 and stats["accepted"] > 0 and stats["tests"] > stats["accepted"]
+        rep = R.replay_acceptance(R.load_ref(cfg, st, dtype, stop_ids=set()), W_prompt(cfg),
+                                  ids, stats["kinds"], T, 0.95, rp)
+        assert [p for p, _ in rep] == stats["p_accept"]
+        assert sum(a for _, a in rep) == stats["accepted"] and len(rep) == stats["tests"]
+
+
+def W_prompt(cfg):
+    from pulsar_engine import weights as W
+
+    return W.uniform_ids(0, "tiny_prompt", 24, cfg.vocab_size)
+
+
+def test_spec_token_marginals_match_monte_carlo():
+    """The exact first-three-token distributions of the self-speculative loop against 1500
+    seeded runs of the generator itself (small config, temperature 0.05, penalty 10)."""
+    import copy
+
+    from conftest import chi_square_pvalue
+    from pulsar_engine import weights as W
+    from pulsar_engine.config import small_config
+
+    cfg = small_config()
+    st = W.synthetic_state(cfg, seed=0)
+    prompt = W.uniform_ids(0, "dist_prompt", 24, cfg.vocab_size)
+    m = R.spec_token_marginals(R.load_ref(cfg, st, torch.float32, stop_ids=set()), prompt,
+                               0.05, 0.95, 10.0, prune=1e-4)
+    assert abs(m[0].sum().item() - 1) < 1e-9 and abs(m[1].sum().item() - 1) < 1e-6
+    assert m[2].sum().item() > 0.99
+    eng = R.load_ref(cfg, st, torch.float32, stop_ids=set())
+    # every run starts from the same prompt: keep one prefill and hand out copies of it
+    saved = {}
+    real_prefill = eng.prefill
+
+    def prefill_once(ids, cache):
+        if not saved:
+            saved["logits"] = real_prefill(ids, cache)
+            saved["cache"] = copy.deepcopy(cache)
+        cache.__dict__.update(copy.deepcopy(saved["cache"]).__dict__)
+        return saved["logits"].clone()
+
+    eng.prefill = prefill_once
+    g = torch.Generator().manual_seed(2024)
+    draws = np.array([list(eng.self_speculative_ids(prompt, 3, 0.05, 0.95, 10.0, generator=g))
+                      for _ in range(1500)])
+    for k in range(3):
+        pv = chi_square_pvalue(draws[:, k], m[k].numpy())
+        assert pv > 1e-4, (k, pv)
+    # a plausible mistake fails: token 2 drawn from the verify logits alone (no draft mix)
+    ref2 = R.load_ref(cfg, st, torch.float32, stop_ids=set())
+    cache = R.RefKVCache(cfg)
+    lg = ref2.prefill(torch.as_tensor(prompt).view(1, -1), cache)[:, -1, :]
+    p1 = R.sampling_distribution(lg, prompt.tolist(), 0.05, 0.95, 10.0)
+    wrong = torch.zeros_like(m[1])
+    for t1 in torch.nonzero(p1 > 1e-4).view(-1).tolist():
+        c = copy.deepcopy(cache)
+        _, h, e = ref2.decode_pulse_pass(t1, 24, c, 0)
+        _, h, _ = ref2.decode_pulse_pass(t1, 24, c, 1, h, e)
+        lv, _, _ = ref2.decode_pulse_pass(t1, 24, c, 2, h, e)
+        wrong += p1[t1] * R.sampling_distribution(lv, prompt.tolist() + [t1], 0.05, 0.95, 10.0)
+    assert (wrong - m[1]).abs().sum() > 0.05
