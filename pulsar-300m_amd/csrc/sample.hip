@@ -341,6 +341,24 @@ __device__ void keep_for_tail(const ControllerArgs& a, SeqState& s) {
   }
 }
 
+// The current token is done without a draft test (plain mode, an accepted draft, or an
+// early exit): the next token is a draw from logits row lr; a speculative row that ran
+// with that very token is kept.
+__device__ void finish_untested(const ControllerArgs& a, SeqState& s, int b, int lr, bool s_ran) {
+  const int t = a.draw[lr * 2];
+  if (is_stop(a, t)) {
+    s.done = 1;
+    return;
+  }
+  emit(a, s, b, t);
+  keep_for_tail(a, s);
+  if (s.done) return;
+  if (a.speculative && s_ran && s.s_tok == t)
+    promote(a, s, KIND_TESTED);
+  else
+    fresh(s, t);
+}
+
 // Advance one sequence's state after the step whose rows it ran.
 __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
   const int P = a.n_pulses;
@@ -351,7 +369,7 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
     // exit after pulse_ran when the top-1 probability of its logits reaches the threshold
     // (src/infer.py:536-543); a token that runs every pulse counts at the last (:546-547)
     if (!last && (double)a.maxprob[s.lrow_c] >= a.exit_thr) last = true;
-    if (last) a.exit_counts[b * 4 + pulse_ran] += 1;
+    if (last) a.exit_counts[b * 4 + min(pulse_ran, P - 1)] += 1;
   }
   if (last && s.tail) {
     s.done = 1;
@@ -381,7 +399,16 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
     if (s.d_tok == v && !is_stop(a, s.d_tok)) {
       s.accepted += 1;
       emit(a, s, b, s.d_tok, 1);
-      if (!s.done) promote(a, s, KIND_PLAIN);
+      if (!s.done) {
+        const int lr_s = s.lrow_s;
+        promote(a, s, KIND_PLAIN);
+        // the accepted draft's pulse 0 ran as this step's speculative row, so the exit
+        // test after its pulse 0 (src/infer.py:536-543) reads that row's logits
+        if (exit_eligible(a, s) && P > 1 && (double)a.maxprob[lr_s] >= a.exit_thr) {
+          a.exit_counts[b * 4] += 1;
+          finish_untested(a, s, b, lr_s, false);
+        }
+      }
     } else {
       const int t = a.draw[lr * 2 + 1];
       if (is_stop(a, t)) {
@@ -397,19 +424,7 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
       }
     }
   } else {
-    const int t = a.draw[lr * 2];
-    if (is_stop(a, t)) {
-      s.done = 1;
-    } else {
-      emit(a, s, b, t);
-      keep_for_tail(a, s);
-      if (!s.done) {
-        if (a.speculative && s_ran && s.s_tok == t)
-          promote(a, s, KIND_TESTED);
-        else
-          fresh(s, t);
-      }
-    }
+    finish_untested(a, s, b, lr, s_ran);
   }
 }
 

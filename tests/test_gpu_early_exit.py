@@ -100,7 +100,7 @@ def test_bf16_exit_decisions_follow_the_rule_on_the_engines_logits():
     cfg = small_config(n_heads=16, n_kv_heads=4)
     model = DeviceModel(cfg, W.exit_probe_state(cfg), torch.bfloat16)
     prompts = np.stack([W.uniform_ids(s, "exit_prompt", 24, cfg.vocab_size) for s in range(4)])
-    thr = 0.0400
+    thr = 0.034
     checked = exits = 0
     with HipEngine(model, batch=4, max_prompt=24, max_new=16, speculative=False,
                    temperature=0.0, repetition_penalty=10.0, stop_ids=[], all_logits=True,
