@@ -387,6 +387,19 @@ int pulsar_sample_rows(const float* logits, int32_t n_rows, int32_t V, int32_t d
                        float top_p, float repetition_penalty, int32_t greedy, int32_t* out_argmax,
                        int32_t* out_draw, void* workspace, hipStream_t stream);
 
+/* pulsar_sample_rows without a workspace argument: the same sampling on caller buffers,
+ * with its workspace in a static device array of the library instead (one per GPU, 525 KB,
+ * held until the process ends). No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops, harnesses
+ * that forbid allocation). It allocates nothing; n_seq <= 4096 (larger requests fail with
+ * PULSAR_ERR_INVALID). Calls that overlap on one GPU share the array and race. */
+int pulsar_sample_rows_static(const float* logits, int32_t n_rows, int32_t V, int32_t dtype,
+                              const uint32_t* seen, const int32_t* row_seq,
+                              const int32_t* row_extra, const uint32_t* seq_ctr, int32_t n_seq,
+                              uint64_t seed, float temperature, float top_p,
+                              float repetition_penalty, int32_t greedy, int32_t* out_argmax,
+                              int32_t* out_draw, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

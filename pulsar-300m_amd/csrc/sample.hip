@@ -17,6 +17,8 @@
 // draw. After an accepted draft the next token is a plain draw, as in the reference;
 // s is then the pulse-0 argmax guess of the accepted token, which changes which work is
 // speculative but never the emitted distribution.
+#include <mutex>
+
 #include "sample.h"
 
 namespace pulsar {
@@ -868,3 +870,74 @@ int launch_controller(const ControllerArgs& a, hipStream_t s) {
 }
 
 }  // namespace pulsar
+
+// ---------------------------------------------------------------------------
+// Allocation-free sampling entry: pulsar_sample_rows with its workspace (control block, seed
+// word, per-sequence states) in a file-scope device array instead of a caller buffer, for
+// callers that cannot allocate device memory (code under HIP graph capture, serving loops).
+// Each GPU holds its own copy of the array until the process ends; host code reaches it only
+// through the address hipGetSymbolAddress returns for the current device, looked up once per
+// device on the entry's first call there. Calls that overlap on one GPU share the array and
+// race; calls on one stream are ordered.
+// ---------------------------------------------------------------------------
+namespace pulsar {
+namespace {
+
+constexpr int kStaticSampleSeqs = 4096;
+constexpr size_t kStaticSampleBytes = 512 + (size_t)kStaticSampleSeqs * sizeof(SeqState);
+static_assert(kStaticSampleBytes >= 512 + 4096 * 128, "scratch holds 4096 sequence states");
+
+static __device__ __align__(256) char scratch[kStaticSampleBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch (looked up once per device, with it current).
+int scratch_address(void** out) {
+  int dev = -1;
+  PULSAR_CHECK_HIP(hipGetDevice(&dev));
+  PULSAR_REQUIRE(dev >= 0 && dev < kMaxDevices, "sample_rows_static: device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(PULSAR_ERR_HIP,
+                  std::string("sample_rows_static: hipGetSymbolAddress(scratch): ") +
+                      hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PULSAR_OK;
+}
+
+}  // namespace
+}  // namespace pulsar
+
+extern "C" int pulsar_sample_rows_static(const float* logits, int32_t n_rows, int32_t V,
+                                         int32_t dtype, const uint32_t* seen,
+                                         const int32_t* row_seq, const int32_t* row_extra,
+                                         const uint32_t* seq_ctr, int32_t n_seq, uint64_t seed,
+                                         float temperature, float top_p,
+                                         float repetition_penalty, int32_t greedy,
+                                         int32_t* out_argmax, int32_t* out_draw,
+                                         hipStream_t stream) {
+  using namespace pulsar;
+  PULSAR_REQUIRE(logits && seen && row_seq && row_extra && seq_ctr && out_argmax && out_draw,
+                 "sample_rows_static: null argument");
+  PULSAR_REQUIRE(n_rows >= 0 && n_seq >= 1, "sample_rows_static: n_rows >= 0 and n_seq >= 1");
+  PULSAR_REQUIRE(n_seq <= kStaticSampleSeqs,
+                 "sample_rows_static: n_seq > 4096 (the size of its static scratch); use "
+                 "pulsar_sample_rows with a workspace");
+  PULSAR_REQUIRE(dtype == PULSAR_BF16 || dtype == PULSAR_F32, "sample_rows_static: dtype");
+  PULSAR_REQUIRE(temperature > 0.f && top_p > 0.f && top_p <= 1.f && repetition_penalty > 0.f,
+                 "sample_rows_static: temperature > 0, 0 < top_p <= 1, repetition_penalty > 0");
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != PULSAR_OK) return rc;
+  if (n_rows == 0) return PULSAR_OK;
+  return launch_sample_rows(logits, n_rows, V, dtype, seen, row_seq, row_extra, seq_ctr, n_seq,
+                            seed, temperature, top_p, repetition_penalty, greedy, out_argmax,
+                            out_draw, ws, stream);
+}

@@ -122,6 +122,9 @@ _PROTOS = {
     "pulsar_sample_workspace_bytes": [_c_i32],
     "pulsar_sample_rows": [_vp, _c_i32, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _c_i32,
                            ctypes.c_uint64, _c_f32, _c_f32, _c_f32, _c_i32, _vp, _vp, _vp, _vp],
+    "pulsar_sample_rows_static": [_vp, _c_i32, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _c_i32,
+                                  ctypes.c_uint64, _c_f32, _c_f32, _c_f32, _c_i32, _vp, _vp,
+                                  _vp],
 }
 # entries whose result is not an int status
 _RESTYPES = {"pulsar_sample_workspace_bytes": _c_i64}
