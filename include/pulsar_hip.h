@@ -317,6 +317,10 @@ typedef struct PulsarEngineConfig {
                                       of each row of the last executed step, in that step's row
                                       order (PULSAR_BUF_LAST_ROWS), in the router's ranking
                                       order */
+#define PULSAR_BUF_KV_LAYOUT 11    /* int32 [4] cache layout: ring positions of a sliding-
+                                      window layer (lcap), pages per sequence of a global
+                                      layer, positions per page, kv heads (host copy, no
+                                      device access) */
 #define PULSAR_BUF_TOKEN_KINDS 10  /* int32 [B][max_new] per emitted token: 1 = an accepted
                                       draft, 0 = a drawn token */
 

@@ -953,3 +953,60 @@ def accept_probability(d_logits, v_logits, seen, temperature, top_p, repetition_
 def load_ref(cfg: PulsarConfig, state: dict, dtype=torch.float32, rope_tables_fp32=True,
              stop_ids=None) -> RefEngine:
     return RefEngine(RefModel(cfg, state, dtype, rope_tables_fp32), stop_ids=stop_ids)
+
+
+# ---------------------------------------------------------------------------
+# Synthetic caches of the HIP engine's pulsar_engine_fill_kv, restated on the CPU so that a
+# verify over a long pre-filled cache can be compared with block_verify on the same keys
+# and values. (This follows the engine's test generator, not the reference.)
+# ---------------------------------------------------------------------------
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def _mix64(z: np.ndarray) -> np.ndarray:
+    """SplitMix64 finaliser on uint64 arrays (wrapping arithmetic)."""
+    with np.errstate(over="ignore"):
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def _fill_values(seed: int, layer: int, kv: int, idx: np.ndarray) -> np.ndarray:
+    """Element values of the engine's fill kernel for flat indices idx of one layer's K
+    (kv = 0) or V (kv = 1) buffer: Box-Muller in fp32 of a counter-based uniform pair."""
+    sd = _mix64(np.array([np.uint64(seed) ^ np.uint64(2 * layer + kv + 1)], dtype=np.uint64))[0]
+    with np.errstate(over="ignore"):
+        h = _mix64(sd + np.uint64(0x9E3779B97F4A7C15) * (idx.astype(np.uint64) + np.uint64(1)))
+    u1 = ((h >> np.uint64(40)) + np.uint64(1)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+    u2 = ((h >> np.uint64(16)) & np.uint64(0xFFFFFF)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+    return (np.sqrt(np.float32(-2.0) * np.log(u1)) *
+            np.cos(np.float32(6.28318530718) * u2)).astype(np.float32)
+
+
+def fill_kv_cache(cfg: PulsarConfig, layout: dict, ctx: int, seed: int, b: int, batch: int,
+                  dtype=torch.bfloat16) -> RefKVCache:
+    """RefKVCache of sequence b holding positions [0, ctx) of an engine cache filled by
+    pulsar_engine_fill_kv(ctx, seed): sliding-window layers keep the last window positions
+    (ring slot = position mod lcap), global layers every position (page = b * max_pages +
+    position / page). K is position-major, V dimension-major in the engine's buffers."""
+    Hkv, hd, lcap, mp, pg = layout["hkv"], cfg.head_dim, layout["lcap"], layout["max_pages"], layout["page"]
+    cache = RefKVCache(cfg)
+    g = np.arange(Hkv, dtype=np.int64)[:, None, None]
+    d = np.arange(hd, dtype=np.int64)[None, None, :]
+    for L in range(cfg.n_core):
+        if cfg.is_local(L):
+            pos = np.arange(max(0, ctx - cfg.sliding_window), ctx, dtype=np.int64)[None, :, None]
+            slot = pos % lcap
+            ik = ((b * Hkv + g) * lcap + slot) * hd + d
+            iv = ((b * Hkv + g) * hd + d) * lcap + slot
+        else:
+            pos = np.arange(ctx, dtype=np.int64)[None, :, None]
+            page = b * mp + pos // pg
+            ik = ((page * Hkv + g) * pg + pos % pg) * hd + d
+            iv = ((page * Hkv + g) * hd + d) * pg + pos % pg
+        k = torch.from_numpy(_fill_values(seed, L, 0, ik)).to(dtype)
+        v = torch.from_numpy(_fill_values(seed, L, 1, iv)).to(dtype)
+        cache.k[L], cache.v[L] = k.unsqueeze(0).contiguous(), v.unsqueeze(0).contiguous()
+    cache.seq_len = ctx
+    return cache

@@ -1335,6 +1335,12 @@ int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes
       src = e.exit_counts;
       cap = 16ll * e.B;
       break;
+    case PULSAR_BUF_KV_LAYOUT: {
+      const int32_t layout[4] = {e.lcap, e.max_pages, kPage, e.Hkv};
+      PULSAR_REQUIRE(bytes <= (int64_t)sizeof(layout), "engine_read: more bytes than the buffer holds");
+      std::memcpy(host_dst, layout, bytes);
+      return PULSAR_OK;
+    }
     case PULSAR_BUF_TOKEN_KINDS:
       src = e.kinds;
       cap = 4ll * e.B * std::max(1, e.cfg.max_new);

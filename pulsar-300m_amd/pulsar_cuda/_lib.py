@@ -23,6 +23,7 @@ BUF_EXPERT_COUNTS = 7
 BUF_EXIT_COUNTS = 8
 BUF_TOPK_IDX = 9
 BUF_TOKEN_KINDS = 10
+BUF_KV_LAYOUT = 11
 ABI_VERSION = 3
 SEQSTATE_INTS = 32
 ROW_INTS = 8

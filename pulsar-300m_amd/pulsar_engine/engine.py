@@ -203,6 +203,12 @@ class HipEngine:
         k = self._read(_lib.BUF_TOKEN_KINDS, np.zeros((self.batch, max(1, self.max_new)), np.int32))
         return [k[b, : st[b, ST_PRODUCED]].tolist() for b in range(self.batch)]
 
+    def kv_layout(self) -> dict:
+        """Cache layout: ring positions of a sliding-window layer, pages per sequence of a
+        global layer, positions per page, kv heads."""
+        v = self._read(_lib.BUF_KV_LAYOUT, np.zeros(4, np.int32))
+        return {"lcap": int(v[0]), "max_pages": int(v[1]), "page": int(v[2]), "hkv": int(v[3])}
+
     def exit_counts(self) -> np.ndarray:
         """Early exit: tokens of each sequence that left after pulse k, [batch, n_pulses],
         since the last prefill or rewind."""
