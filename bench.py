@@ -272,6 +272,77 @@ def verify_microbench(model, cfg, es, args):
     }
 
 
+def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warmup, es=2,
+                 profile=True, draft_len=0, label=""):
+    """Timed generations of a batch from one prefill: each generation rewinds (redraws the
+    first tokens from the saved prefill logits with a new seed) and decodes until every
+    sequence has n_new tokens (no stop ids). Returns accepted tokens/s, acceptance, the
+    whole generation's algorithmic bytes against the HBM peak and, from one eagerly
+    profiled generation, the dominant kernel class's bytes per launch against its
+    event-timed launch duration."""
+    import torch
+
+    from pulsar_engine.engine import HipEngine
+
+    B, T = prompts.shape
+    eng = HipEngine(model, batch=B, max_prompt=T, max_new=n_new, temperature=temperature,
+                    top_p=top_p, repetition_penalty=rp, stop_ids=[], seed=1, draft_len=draft_len)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.prefill(prompts)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+
+    def generation(seed):
+        eng.rewind(seed)
+        n = eng.run(check_every=16)
+        st = eng.state()
+        return n, int(st[:, 1].sum()), int(st[:, 11].sum()), int(st[:, 12].sum())
+
+    for w in range(warmup):
+        generation(1000 + w)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    produced = tests = accepted = nsteps = 0
+    for k in range(steps):
+        s_, p, t, a = generation(2000 + k)
+        nsteps += s_
+        produced += p
+        tests += t
+        accepted += a
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    out = {"value": round(produced / elapsed, 1), "unit": "tokens/s",
+           "ms_per_generation": round(elapsed / steps * 1e3, 2),
+           "pulse_steps_per_generation": round(nsteps / steps, 1),
+           "acceptance_rate": round(accepted / tests, 4) if tests else None,
+           "prefill_ms_first_call": round(prefill_s * 1e3, 1)}
+    log(f"{label}: {steps} timed generations, {produced} tokens in {elapsed:.3f}s, "
+        f"acceptance {accepted}/{tests}")
+    if profile:
+        prof, bytes_by_class, psteps = profile_generation(eng, cfg, es, 3000)
+        pair_ms, pair_n = prof.pop("event_pair")
+        net = {k: v for k, v in prof.items() if v[1]}
+        dom = max(net, key=lambda k: net[k][0])
+        ms, n = net[dom]
+        per_launch = bytes_by_class[dom] / max(n, 1)
+        avg_s = ms / max(n, 1) / 1e3
+        all_bytes = sum(bytes_by_class.values())
+        out["hbm_roofline_frac_generation"] = round(all_bytes / (elapsed / steps) / HBM_PEAK, 4)
+        out["algorithmic_bytes_per_generation"] = int(all_bytes)
+        out["roofline"] = {"bound": "hbm", "kernel": dom,
+                           "achieved": round(per_launch / avg_s / 1e9, 1), "peak": 8000.0,
+                           "unit": "GB/s", "frac": round(per_launch / avg_s / HBM_PEAK, 4),
+                           "bytes_per_launch": int(per_launch),
+                           "avg_launch_us": round(avg_s * 1e6, 2)}
+        out["kernel_profile"] = {
+            k: {"ms": round(v[0], 3), "launches": v[1], "us_per_launch": round(v[0] / v[1] * 1e3, 2),
+                "GB_per_s": round(bytes_by_class[k] / max(v[0], 1e-9) / 1e6, 1)}
+            for k, v in net.items()}
+    eng.close()
+    return out
+
+
 def draft_block_run(model, cfg, prompts, args):
     """The bench workload in draft-block mode (draft length args.draft_len): accepted
     tokens/s over timed generations from the prefilled cache, acceptance rate."""
@@ -319,7 +390,20 @@ def draft_block_run(model, cfg, prompts, args):
     }
 
 
-def cpu_baseline(cfg, state, prompt, n_new, temperature, top_p, rp):
+def _cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        return ""
+
+
+def cpu_baseline(cfg, state, c2_prompt, c2_new, temperature, top_p, rp, c1_prompt, c1_new):
+    """The oracle (PyTorch CPU restatement of src/infer.py, pinned to the reference by the
+    golden vectors) on this host's cores: the headline workload's sequence 0 in bf16 (sampled
+    self-speculative, c2_new tokens after its prefill; the oracle's own acceptance rate
+    beside the measured one), and c1 exactly (fp32, batch 1, greedy self-speculative,
+    c1_new tokens), whose id stream the GPU run is checked against."""
     import torch
 
     from oracle import pulsar_ref as R
@@ -328,29 +412,54 @@ def cpu_baseline(cfg, state, prompt, n_new, temperature, top_p, rp):
     torch.set_num_threads(cores)
     eng = R.load_ref(cfg, state, torch.bfloat16, stop_ids=set())
     torch.manual_seed(0)
-    gen = eng.self_speculative_ids(prompt, n_new, temperature, top_p, rp)
+    stats = {}
+    gen = eng.self_speculative_ids(c2_prompt, c2_new, temperature, top_p, rp, stats=stats)
     t0 = time.perf_counter()
-    first = next(gen)  # includes the prefill
+    next(gen)  # the prefill and the first token
     t1 = time.perf_counter()
     rest = list(gen)
     t2 = time.perf_counter()
     n = len(rest)
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
-    except OSError:
-        pass
+    ref1 = R.load_ref(cfg, state, torch.float32, stop_ids=set())
+    g1 = ref1.self_speculative_ids(c1_prompt, c1_new, 0.0, 1.0, rp)
+    u0 = time.perf_counter()
+    c1_ids = [next(g1)]
+    u1 = time.perf_counter()
+    c1_ids += list(g1)
+    u2 = time.perf_counter()
+    p_acc = stats.get("p_accept", [])
     return {
         "value": round(n / (t2 - t1), 3) if n else None,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"oracle (PyTorch CPU restatement of src/infer.py) in bf16, 1 sequence of the "
-                   f"workload: {len(prompt)}-token prompt prefilled in {t1 - t0:.1f}s (untimed), "
-                   f"then {n} self-speculative tokens after the first timed in {t2 - t1:.1f}s; "
-                   f"cpu '{model}', torch {torch.__version__}"),
+        "sample": (f"oracle in bf16 on sequence 0 of the headline workload: {len(c2_prompt)}-token "
+                   f"prompt prefilled in {t1 - t0:.1f}s (untimed), then {n} sampled "
+                   f"self-speculative tokens after the first in {t2 - t1:.1f}s; the reference "
+                   f"path is batch 1, so batch 16 takes 16x this time; cpu '{_cpu_model_name()}', "
+                   f"torch {torch.__version__}"),
+        "acceptance_rate": round(stats["accepted"] / stats["tests"], 4) if stats.get("tests") else None,
+        "acceptance_expected": round(sum(p_acc) / len(p_acc), 4) if p_acc else None,
+        "tests": stats.get("tests", 0),
+        "c1": {"workload": f"fp32, batch 1, {len(c1_prompt)}-token prompt, greedy "
+                           f"self-speculative, {c1_new} new tokens",
+               "value": round((len(c1_ids) - 1) / (u2 - u1), 3), "unit": "tokens/s",
+               "prefill_and_first_token_s": round(u1 - u0, 2), "ids": c1_ids},
     }
+
+
+def kv_footprint(cfg) -> dict:
+    """KV-cache bytes at batch 1 in bf16 for 1k-32k contexts: the engine's allocation beside the
+    reference's analytic unified-cache figure (src/infer.py:834-846)."""
+    from pulsar_engine import traffic
+
+    out = {}
+    for ctx in (1024, 4096, 8192, 16384, 32768):
+        e = traffic.kv_cache_bytes(cfg, 1, ctx)
+        out[str(ctx)] = {"engine_MB": round(e["total"] / 1e6, 1),
+                         "reference_MB": round(traffic.reference_unified_kv_bytes(ctx) / 1e6, 1),
+                         "rewind_copy_MB": round(e["rewind_copy"] / 1e6, 1)}
+    return out
 
 
 def main() -> int:
@@ -367,7 +476,10 @@ def main() -> int:
     ap.add_argument("--plain", action="store_true", help="plain decode instead of self-speculative")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-new-tokens", type=int, default=12)
+    ap.add_argument("--cpu-new-tokens", type=int, default=24)
+    ap.add_argument("--no-c1", action="store_true", help="skip the c1 run (fp32, batch 1)")
+    ap.add_argument("--no-c4", action="store_true", help="skip the long-context workload")
+    ap.add_argument("--no-c5", action="store_true", help="skip the high-batch workload")
     ap.add_argument("--draft-len", type=int, default=4,
                     help="draft length of the draft-block run (0 skips it)")
     ap.add_argument("--no-verify", action="store_true", help="skip the verify microbenchmark")
@@ -525,10 +637,69 @@ def main() -> int:
     if not args.no_verify:
         verify = verify_microbench(model, cfg, es, args)
         log(f"verify microbenchmark: {json.dumps(verify)}")
+    # c1: fp32, batch 1, 128-token prompt, greedy self-speculative, 64 new tokens (the
+    # reference's CPU-runnable case); its ids are checked against the oracle's below
+    c1_prompt = W.uniform_ids(0, "prompt", 128, cfg.vocab_size)
+    c1 = None
+    if not args.no_c1:
+        from pulsar_engine.engine import PulsarInferenceEngine
+
+        m32 = DeviceModel(cfg, state, torch.float32)
+        pe = PulsarInferenceEngine(m32)
+        pe.generate_ids([c1_prompt.tolist()], max_new_tokens=64, temperature=0.0,
+                        repetition_penalty=1.15, speculative=True, stop_ids=[])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        c1_ids = pe.generate_ids([c1_prompt.tolist()], max_new_tokens=64, temperature=0.0,
+                                 repetition_penalty=1.15, speculative=True, stop_ids=[])[0]
+        torch.cuda.synchronize()
+        c1_s = time.perf_counter() - t0
+        c1 = {"workload": "fp32, batch 1, 128-token uniform prompt, greedy self-speculative, "
+                          "64 new tokens (prefill included)",
+              "value": round(len(c1_ids) / c1_s, 1), "unit": "tokens/s",
+              "ms_per_generation": round(c1_s * 1e3, 2), "ids": c1_ids}
+        for e_ in list(pe._engines.values()):
+            e_.close()
+        del pe, m32
+        torch.cuda.empty_cache()
+        log(f"c1: {c1['value']} tokens/s")
+    # c4: 4 sequences of 32768 uniform-random prompt tokens, 512 new tokens, greedy (the
+    # configuration names no temperature), reference schedule
+    c4 = None
+    if not args.no_c4:
+        p4 = np.stack([W.uniform_ids(90 + b, "c4_prompt", 32768, cfg.vocab_size) for b in range(4)])
+        c4 = run_workload(model, cfg, p4, 512, 0.0, 1.0, args.repetition_penalty, steps=1,
+                          warmup=1, label="c4")
+        c4["workload"] = ("Pulsar-283M bf16, batch 4, 32768-token uniform prompts, greedy "
+                          "self-speculative decode of 512 tokens (reference schedule)")
+        log(f"c4: {json.dumps({k: v for k, v in c4.items() if k != 'kernel_profile'})}")
+    # c5: 256 sequences of 512 Zipf(1.1) prompt tokens, router weights x4, greedy, 512 new
+    # tokens; reference schedule, and the draft-block mode at draft length 6 beside it
+    c5 = None
+    if not args.no_c5:
+        # the skewed-routing weights: synthetic_state(router_scale=4) without regenerating
+        st5 = {k: (v * np.float32(4.0)).astype(np.float32) if k.endswith("router_weight") else v
+               for k, v in state.items()}
+        m5 = DeviceModel(cfg, st5, torch.bfloat16)
+        p5 = np.stack([W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size) for b in range(256)])
+        c5 = run_workload(m5, cfg, p5, 512, 0.0, 1.0, args.repetition_penalty, steps=1,
+                          warmup=1, label="c5")
+        c5["workload"] = ("Pulsar-283M bf16 with router weights x4, batch 256, 512-token "
+                          "Zipf(1.1) prompts, greedy self-speculative decode of 512 tokens "
+                          "(reference schedule)")
+        c5["draft_block_6"] = run_workload(m5, cfg, p5, 512, 0.0, 1.0, args.repetition_penalty,
+                                           steps=1, warmup=1, profile=False, draft_len=6,
+                                           label="c5 draft-block 6")
+        log(f"c5: {json.dumps({k: v for k, v in c5.items() if k != 'kernel_profile'})}")
+        del m5, st5
+        torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, state, prompts[0], args.cpu_new_tokens, args.temperature,
-                           args.top_p, args.repetition_penalty)
+                           args.top_p, args.repetition_penalty, c1_prompt, 64)
+        if c1 is not None:
+            c1["token_identical_to_cpu_oracle"] = c1["ids"] == cpu["c1"]["ids"]
+        log(f"cpu baseline: {json.dumps({k: v for k, v in cpu.items() if k != 'c1'})}")
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -559,6 +730,10 @@ def main() -> int:
         "kernel_profile": prof_detail,
         "draft_block": block,
         "verify": verify,
+        "c1": c1,
+        "c4": c4,
+        "c5": c5,
+        "kv_cache_batch1_bf16": kv_footprint(cfg),
     }
     print(json.dumps(line), flush=True)
     return 0

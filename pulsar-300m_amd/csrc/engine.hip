@@ -59,6 +59,8 @@ struct Engine {
   RowDesc* p_rows = nullptr;  // [P][R]
   StepCtl* p_ctl = nullptr;   // [P]
   KVDesc kv{};
+  void* ring_save_k[kMaxLayers] = {};  // sliding-window rings as the last prefill left them
+  void* ring_save_v[kMaxLayers] = {};
   int prompt_len = 0;
   int v_n = 0;  // rows per sequence of the uploaded verify block (0: none since prefill/fill_kv)
   bool prefilled = false;
@@ -240,10 +242,11 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   e->max_rows = e->S * c.max_batch;
   e->R = std::max(e->max_rows, c.max_batch * c.max_prompt);
   e->max_pages = (c.max_ctx + kPage - 1) / kPage;
-  // ring capacity: the prompt's last `window` positions stay intact while max_new tokens
-  // (+ speculative or draft rows, at most kMaxBlock) are appended, so a rewound decode sees
-  // the prefill state unchanged
-  e->lcap = (m.window + c.max_new + 2 * kPage - 1) / kPage * kPage;
+  // ring capacity: the window plus the rows one step writes (at most kMaxBlock), so that a
+  // step's writes never overwrite a key some row of it still attends (the reference keeps
+  // the newest `window` entries, src/infer.py:142-148); rewind restores the ring from the
+  // copy prefill leaves (ring_save)
+  e->lcap = (m.window + kMaxBlock + kPage - 1) / kPage * kPage;
   static_assert(kMaxBlock <= kPage, "ring slack holds a draft block");
   // decode splits start at a 64-aligned position at most 63 keys before the first key
   e->max_splits = (c.max_ctx + kPage - 1 + kSplitLen - 1) / kSplitLen;
@@ -317,6 +320,10 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
     const size_t n = loc ? local_elems : global_elems;
     PULSAR_TRY(x.alloc(&x.kv.k[l], es * n));
     PULSAR_TRY(x.alloc(&x.kv.v[l], es * n));
+    if (loc) {
+      PULSAR_TRY(x.alloc(&x.ring_save_k[l], es * n));
+      PULSAR_TRY(x.alloc(&x.ring_save_v[l], es * n));
+    }
     // never-written positions are read (masked) by the block-wise decode attention: keep
     // them finite
     PULSAR_CHECK_HIP(hipMemset(x.kv.k[l], 0, es * n));
@@ -441,6 +448,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     aa.part = e.part;
     aa.max_splits = e.max_splits;
     aa.max_splits_unit = e.max_splits_unit;
+    aa.max_ctx = e.cfg.max_ctx;
     aa.H = e.H;
     aa.Hkv = e.Hkv;
     aa.layer = l;
@@ -655,6 +663,22 @@ int enqueue_step(Engine& e, hipStream_t s) {
   co.exit_thr = e.cfg.early_exit_threshold;
   PULSAR_TRY(launch_controller(co, s));
   prof_span(e, PC_CONTROL, _pc, prof_mark(e, s));
+  return PULSAR_OK;
+}
+
+// Copy the sliding-window rings to their saved copies (restore = false) or back (restore =
+// true). Decoding overwrites ring slots of prompt positions; the global layers' prompt
+// positions are never written after prefill.
+int save_rings(Engine& e, hipStream_t s, bool restore) {
+  const size_t bytes = (size_t)e.es * e.B * e.Hkv * e.lcap * kHeadDim;
+  for (int l = 0; l < e.L; ++l) {
+    if (!((e.m.local_mask >> l) & 1u)) continue;
+    void* ring[2] = {e.kv.k[l], e.kv.v[l]};
+    void* save[2] = {e.ring_save_k[l], e.ring_save_v[l]};
+    for (int i = 0; i < 2; ++i)
+      PULSAR_CHECK_HIP(hipMemcpyAsync(restore ? ring[i] : save[i], restore ? save[i] : ring[i], bytes,
+                                      hipMemcpyDeviceToDevice, s));
+  }
   return PULSAR_OK;
 }
 
@@ -1009,6 +1033,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   // the prefill logits are also the readable "last logits" until the first step runs
   PULSAR_CHECK_HIP(hipMemcpyAsync(e.logits, e.plogits, 4 * (size_t)Bq * e.V,
                                   hipMemcpyDeviceToDevice, s));
+  PULSAR_TRY(save_rings(e, s, false));
   PULSAR_TRY(first_token(e, e.cfg.seed, s));
   PULSAR_CHECK_HIP(hipStreamSynchronize(s));
   e.prefilled = true;
@@ -1264,6 +1289,7 @@ int pulsar_engine_rewind(void* handle, uint64_t seed, hipStream_t stream) {
   PULSAR_REQUIRE(handle, "engine_rewind: null handle");
   Engine& e = *reinterpret_cast<Engine*>(handle);
   PULSAR_REQUIRE(e.prefilled, "engine_rewind: prefill first");
+  PULSAR_TRY(save_rings(e, stream, true));
   return first_token(e, seed, stream);
 }
 

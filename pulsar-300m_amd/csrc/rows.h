@@ -174,6 +174,7 @@ struct AttnArgs {
   int max_splits_unit;  // bf16 path: splits of kUnitSplit keys
   int max_units;
   int unit_rows;        // bf16 path: most rows a unit of this launch holds (1..kMaxBlock)
+  int max_ctx;          // positions per sequence of the engine (bounds a unit's key range)
   int H, Hkv, layer, is_local, window, prefill_T;
   float scale;
   KVDesc kv;

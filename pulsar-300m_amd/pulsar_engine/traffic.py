@@ -91,3 +91,36 @@ def prefill_flops(cfg: PulsarConfig, batch: int, prompt_len: int) -> dict:
     }
     out["total"] = sum(out.values())
     return out
+
+
+# Rows one sequence may hold in a step (a draft block plus the next round's first row), the
+# positions per global page, and the ring of a sliding-window layer: the window plus one
+# step's rows, rounded to whole pages (mirrors the engine's allocation in csrc/engine.hip).
+MAX_BLOCK = 8
+PAGE = 64
+
+
+def ring_positions(cfg: PulsarConfig) -> int:
+    return (cfg.sliding_window + MAX_BLOCK + PAGE - 1) // PAGE * PAGE
+
+
+def kv_cache_bytes(cfg: PulsarConfig, batch: int, max_ctx: int, es: int = 2) -> dict:
+    """Device bytes of the engine's KV cache for `batch` sequences of up to max_ctx positions:
+    sliding-window layers hold a ring of ring_positions() positions, global layers whole
+    pages up to max_ctx; K and V, kv heads x head_dim elements of es bytes each. The copy of
+    the rings prefill leaves for rewind is reported apart."""
+    per_pos = cfg.n_kv_heads * cfg.head_dim * 2 * es
+    n_local = sum(1 for L in range(cfg.n_core) if cfg.is_local(L))
+    n_global = cfg.n_core - n_local
+    pages = (max_ctx + PAGE - 1) // PAGE
+    local = n_local * batch * ring_positions(cfg) * per_pos
+    glob = n_global * batch * pages * PAGE * per_pos
+    return {"local": local, "global": glob, "total": local + glob, "rewind_copy": local}
+
+
+def reference_unified_kv_bytes(context: int) -> int:
+    """The reference's analytic figure for its unified cache at batch 1 in bf16
+    (src/infer.py:840-843): six sliding-window layers at min(context, 1024) positions and two
+    global layers at `context`, 4 kv heads of 64, K and V, two bytes."""
+    loc = min(context, 1024)
+    return 6 * 2 * 4 * 64 * loc * 2 + 2 * 2 * 4 * 64 * context * 2

@@ -234,3 +234,18 @@ def test_op_wrappers_check_operands_before_the_library_is_called(monkeypatch):
         pc.moe_combine_backward(dro[:2], eo, idx, w, slots)
     with pytest.raises(RuntimeError, match="flat_e must be int64"):
         pc.moe_slots_from_order(idx.view(-1).int(), idx.view(-1), E, C)
+
+
+def test_kv_cache_bytes_against_the_reference_table():
+    """The reference's published unified-cache table (src/infer.py:834-846):
+    73.4 MB at 32k; the engine's footprint differs only by the ring's one-block slack and
+    page rounding."""
+    cfg = PulsarConfig()
+    want = {1024: 8.4, 4096: 14.7, 8192: 23.1, 16384: 39.8, 32768: 73.4}
+    for ctx, mb in want.items():
+        assert round(traffic.reference_unified_kv_bytes(ctx) / 1e6, 1) == mb
+        got = traffic.kv_cache_bytes(cfg, 1, ctx)["total"]
+        ref = traffic.reference_unified_kv_bytes(ctx)
+        slack = 6 * (traffic.ring_positions(cfg) - min(ctx, 1024)) * 4 * 64 * 2 * 2
+        assert got - ref == slack + 2 * (-ctx % 64) * 4 * 64 * 2 * 2
+    assert traffic.ring_positions(cfg) == 1088
