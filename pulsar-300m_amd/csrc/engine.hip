@@ -349,6 +349,8 @@ GemmArgs gemm_base(const Engine& e) {
   return g;
 }
 
+constexpr int kWideLogitsRows = 128;
+
 // One pass over a row set (the rows of a step, or of one pulse of a block verify): pulse
 // input, every layer, pulse output and the logits of the rows that need them.
 // Per layer: qkv+gate GEMM, qk-norm/RoPE/KV write, attention (+ split combine), wo GEMM with
@@ -602,7 +604,15 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
   g.row_mode = ROWS_LOGITS;
   g.ctl = ctl;
   g.softcap = m.softcap;
-  PULSAR_TIMED(PC_LMHEAD, launch_gemm(g, dt, EPI_LOGITS, 1, MR, s));
+  // Engines whose steps hold kWideLogitsRows rows or more (verify blocks, batches of 64+)
+  // compute the output head in 128 x 256 tiles staged through LDS (the head's 64 MiB read
+  // once per 128 rows instead of once per 32); below that the weight-streaming row tiles.
+  // The two sum K in different orders, so logits can differ in the last fp32 bit (before
+  // their bf16 rounding) between engines on either side of the threshold.
+  if (dt == PULSAR_BF16 && MR >= kWideLogitsRows)
+    PULSAR_TIMED(PC_LMHEAD, launch_gemm_wide(g, dt, EPI_LOGITS, 1, MR, s));
+  else
+    PULSAR_TIMED(PC_LMHEAD, launch_gemm(g, dt, EPI_LOGITS, 1, MR, s));
   return PULSAR_OK;
 }
 

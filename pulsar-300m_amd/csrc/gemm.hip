@@ -440,6 +440,24 @@ __device__ __forceinline__ void epilogue4(const GemmArgs& g, int epi, int group,
       for (int j = 0; j < 4; ++j) o[j] = (__bf16)(rnd<bf16>(v[j]) * (float)sc[j]);
       break;
     }
+    case EPI_LOGITS:
+    case EPI_LOGITS_RAW: {
+      // fp32 store of bf16-rounded logits, softcapped with the scalar epilogue's roundings
+      float4 lv;
+      float* lp = &lv.x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float l = rnd<bf16>(v[j]);
+        if (epi == EPI_LOGITS && g.softcap > 0.f) {
+          float t = rnd<bf16>(l / g.softcap);
+          t = rnd<bf16>(tanhf(t));
+          l = rnd<bf16>(g.softcap * t);
+        }
+        lp[j] = l;
+      }
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(Cv) + (int64_t)crow * ldc + col0) = lv;
+      return;
+    }
     default:  // EPI_QKVG: q/k/v columns stored, gate columns through the scalar epilogue
       if (col0 >= g.n_main) {
 #pragma unroll
@@ -659,6 +677,12 @@ int launch_wide(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
     case ROWS_PULSE: gemm_bf16_lds_kernel<EPI, ROWS_PULSE><<<grid, 256, 0, s>>>(a); break;
     case ROWS_LIST: gemm_bf16_lds_kernel<EPI, ROWS_LIST><<<grid, 256, 0, s>>>(a); break;
     case ROWS_ALL: gemm_bf16_lds_kernel<EPI, ROWS_ALL><<<grid, 256, 0, s>>>(a); break;
+    case ROWS_LOGITS:
+      if constexpr (EPI == EPI_LOGITS || EPI == EPI_LOGITS_RAW) {
+        gemm_bf16_lds_kernel<EPI, ROWS_LOGITS><<<grid, 256, 0, s>>>(a);
+        break;
+      }
+      return fail(PULSAR_ERR_INVALID, "gemm: logits rows take a logits epilogue");
     default: return fail(PULSAR_ERR_INVALID, "gemm: row mode of a wide launch");
   }
   PULSAR_LAUNCH_CHECK();
@@ -669,7 +693,7 @@ int launch_wide(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
 
 int launch_gemm_wide(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
                      hipStream_t s) {
-  if (dtype != PULSAR_BF16 || a.has_g0 || a.row_mode == ROWS_LOGITS)
+  if (dtype != PULSAR_BF16 || a.has_g0)
     return launch_gemm(a, dtype, epi, groups, max_rows, s);
   if (groups <= 0) return PULSAR_OK;
   if (a.K % 256 != 0 || a.N % 16 != 0 || (epi == EPI_SWIGLU && a.N % 128 != 0))
@@ -681,6 +705,8 @@ int launch_gemm_wide(const GemmArgs& a, int dtype, int epi, int groups, int max_
     case EPI_RESID: return launch_wide<EPI_RESID>(a, groups, max_rows, s);
     case EPI_SWIGLU: return launch_wide<EPI_SWIGLU>(a, groups, max_rows, s);
     case EPI_SCALE: return launch_wide<EPI_SCALE>(a, groups, max_rows, s);
+    case EPI_LOGITS: return launch_wide<EPI_LOGITS>(a, groups, max_rows, s);
+    case EPI_LOGITS_RAW: return launch_wide<EPI_LOGITS_RAW>(a, groups, max_rows, s);
   }
   return launch_gemm(a, dtype, epi, groups, max_rows, s);
 }

@@ -518,11 +518,17 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
 typedef __bf16 attn_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float attn_f32x4 __attribute__((ext_vector_type(4)));
 
+// Splits of SPLIT keys start at multiples of SPLIT, so the 64-key blocks a row's keys fall
+// in, the wave and split that compute each block, and the order of every sum (within a wave,
+// across the waves, across the splits) are fixed by the row's own position: a row gives the
+// same result alone or in a unit with other rows (the speculative row of the exact schedule,
+// the rows of a draft block).
+template <int SPLIT>
 __device__ __forceinline__ void unit_range(const AttnArgs& a, const AttnUnit& un, int& base,
                                            int& uhi) {
   const int lo0 = a.is_local ? max(0, un.pos0 - a.window + 1) : 0;
   uhi = un.pos0 + un.n - 1;
-  base = lo0 & ~63;
+  base = lo0 / SPLIT * SPLIT;
 }
 
 // Row of unit row z (z < NZ), -1 past the unit's rows: a select chain, so the unit stays
@@ -662,7 +668,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
                "s"(a.is_local), "s"(a.window), "s"(a.Hkv), "s"(a.qkv), "s"(a.ldq));
   if (u >= n_units) return;
   int base, uhi;
-  unit_range(a, un, base, uhi);
+  unit_range<SPLIT>(a, un, base, uhi);
   const int nsplit = (uhi + 1 - base + SPLIT - 1) / SPLIT;
   if (s >= nsplit) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -924,7 +930,7 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_lds_kernel(AttnArgs a) {
                "s"(un.row[7]));
   if (u >= n_units) return;
   int base, uhi;
-  unit_range(a, un, base, uhi);
+  unit_range<SPLIT>(a, un, base, uhi);
   const int nsplit = (uhi + 1 - base + SPLIT - 1) / SPLIT;
   if (s >= nsplit) return;
   const int lane = threadIdx.x & 63;
@@ -1932,8 +1938,9 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     const bool local = a.is_local;
     const AttnLdsCfg c = attn_lds_cfg(local, a.max_splits_unit > kLongCacheSplits, a.unit_rows);
     const int split = c.nw * c.bpw * 64;
-    const int range = local ? std::min(a.window + a.unit_rows - 1, max_ctx) + 63 : max_ctx + 63;
-    const dim3 grid(a.max_units, a.Hkv, (range + split - 1) / split);
+    int zs = (max_ctx + split - 1) / split;
+    if (local) zs = std::min(zs, (a.window + a.unit_rows - 1 + split - 1) / split + 1);
+    const dim3 grid(a.max_units, a.Hkv, zs);
     AttnArgs b = a;
     b.kl.k = a.kv.k[a.layer];
     b.kl.v = a.kv.v[a.layer];
@@ -1955,12 +1962,12 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     // take 256-key splits (one block per wave, many workgroups in parallel).
     const bool lng = a.max_splits_unit > kLongCacheSplits;
     const int bpw = !lng ? 1 : (a.is_local ? 4 : 8);
-    int splits = a.max_splits_unit;
-    if (a.is_local) {
-      const int local_splits = (a.window + a.unit_rows - 1 + 63 + kUnitSplit - 1) / kUnitSplit;
-      if (local_splits < splits) splits = local_splits;
-    }
-    const dim3 grid(a.max_units, a.Hkv, (splits + bpw - 1) / bpw);
+    const int split = kUnitSplit * bpw;
+    // a unit's keys [lo, hi] lie in the splits from lo's to hi's: at most max_ctx keys, and in
+    // sliding-window layers window + rows - 1 keys, which can straddle one more split
+    int zs = (a.max_ctx + split - 1) / split;
+    if (a.is_local) zs = std::min(zs, (a.window + a.unit_rows - 1 + split - 1) / split + 1);
+    const dim3 grid(a.max_units, a.Hkv, zs);
     AttnArgs b = a;
     b.kl.k = a.kv.k[a.layer];
     b.kl.v = a.kv.v[a.layer];

@@ -228,7 +228,8 @@ def test_bf16_block_sampled_acceptance_matches_draft_verify_overlap(models, full
 
 def test_verify_microbench_shape_batch_consistent(models, full_state):
     """64 sequences over 8192 cached N(0,1) positions, 5-token blocks: sequence 0 of the
-    batch gives the same logits as the same cache and block alone; all logits finite."""
+    batch gives the same logits as the same cache and block alone, to one bf16 rounding of
+    the output head; all logits finite."""
     from pulsar_engine import weights as W
     from pulsar_engine.engine import HipEngine
 
@@ -247,5 +248,14 @@ def test_verify_microbench_shape_batch_consistent(models, full_state):
     one = HipEngine(models[torch.bfloat16], batch=1, **kw)
     one.fill_kv(ctx, seed=11)
     one.verify(blocks[:1])
-    np.testing.assert_array_equal(one.logits(n), first)
+    alone = one.logits(n)
     one.close()
+    # engines of 128+ rows per step compute the output head in 128-row tiles, which sum K in
+    # another order than the single sequence's row tiles: a logit may then round to the
+    # neighbouring bf16 value, nothing more
+    diff = np.abs(alone - first)
+    ulp = np.abs(first) * 2.0 ** -7 + 1e-6
+    print(f"[verify] batch 64 vs alone: {(diff > 0).sum()} of {diff.size} logits differ, "
+          f"max {diff.max():.3e}", flush=True)
+    assert (diff <= ulp).all()
+    assert (diff > 0).mean() < 1e-3
