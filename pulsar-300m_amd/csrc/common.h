@@ -154,13 +154,33 @@ __device__ __forceinline__ void stv(float* p, const float* v) {
 }
 template <int N>
 __device__ __forceinline__ void stv(bf16* p, const float* v) {
+  if constexpr (N % 8 == 0) {
 #pragma unroll
-  for (int i = 0; i < N; i += 4) {
-    uint2 u;
-    u.x = (uint32_t)f2bf(v[i]).u | ((uint32_t)f2bf(v[i + 1]).u << 16);
-    u.y = (uint32_t)f2bf(v[i + 2]).u | ((uint32_t)f2bf(v[i + 3]).u << 16);
-    *reinterpret_cast<uint2*>(p + i) = u;
+    for (int i = 0; i < N; i += 8) {
+      uint4 u;
+      u.x = (uint32_t)f2bf(v[i]).u | ((uint32_t)f2bf(v[i + 1]).u << 16);
+      u.y = (uint32_t)f2bf(v[i + 2]).u | ((uint32_t)f2bf(v[i + 3]).u << 16);
+      u.z = (uint32_t)f2bf(v[i + 4]).u | ((uint32_t)f2bf(v[i + 5]).u << 16);
+      u.w = (uint32_t)f2bf(v[i + 6]).u | ((uint32_t)f2bf(v[i + 7]).u << 16);
+      *reinterpret_cast<uint4*>(p + i) = u;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      uint2 u;
+      u.x = (uint32_t)f2bf(v[i]).u | ((uint32_t)f2bf(v[i + 1]).u << 16);
+      u.y = (uint32_t)f2bf(v[i + 2]).u | ((uint32_t)f2bf(v[i + 3]).u << 16);
+      *reinterpret_cast<uint2*>(p + i) = u;
+    }
   }
+}
+
+// Elements of T in 16 bytes (the vector width of the op kernels' loads and stores).
+template <typename T>
+constexpr int kVec = 16 / (int)sizeof(T);
+
+__host__ __device__ __forceinline__ bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` needs 16 floats.

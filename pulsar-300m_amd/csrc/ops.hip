@@ -60,8 +60,8 @@ __global__ void rope_kernel(const T* __restrict__ x, T* __restrict__ y,
   const int64_t t = row % T_;
   const float c = cs[t * half + i], s = sn[t * half + i];
   const float a = to_f(x[row * hd + i]), b = to_f(x[row * hd + i + half]);
-  y[row * hd + i] = from_f<T>(a * c - b * s);
-  y[row * hd + i + half] = from_f<T>(b * c + a * s);
+  y[row * hd + i] = from_f<T>(fmaf(a, c, -(b * s)));
+  y[row * hd + i + half] = from_f<T>(fmaf(b, c, a * s));
 }
 
 // ---------------------------------------------------------------------------
@@ -86,7 +86,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(
   const float partner = __shfl_xor(n, 32, 64);
   const int j = lane & 31;
   const float c = cs[t * 32 + j], s = sn[t * 32 + j];
-  const float out = (lane < 32) ? (n * c - partner * s) : (n * c + partner * s);
+  const float out = (lane < 32) ? fmaf(n, c, -(partner * s)) : fmaf(n, c, partner * s);
   y[v * 64 + lane] = from_f<T>(out);
 }
 
@@ -110,6 +110,12 @@ __global__ void attn_gate_kernel(const T* __restrict__ a, const float* __restric
 // ---------------------------------------------------------------------------
 // Causal depthwise conv k=4 with residual, fp32 arithmetic.
 // ---------------------------------------------------------------------------
+// The elementwise ops spell their multiply-adds as fmaf so that the scalar and 16-byte
+// kernels round identically whatever the compiler would contract.
+__device__ __forceinline__ float conv4(const float* w, float x0, float x1, float x2, float x3) {
+  return fmaf(w[3], x3, fmaf(w[2], x2, fmaf(w[1], x1, w[0] * x0)));
+}
+
 template <typename T>
 __global__ void conv_k4_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                T* __restrict__ y, int64_t T_, int64_t D, int64_t total) {
@@ -122,7 +128,7 @@ __global__ void conv_k4_kernel(const T* __restrict__ x, const float* __restrict_
   const float x2 = t >= 2 ? to_f(x[idx - 2 * D]) : 0.f;
   const float x3 = t >= 3 ? to_f(x[idx - 3 * D]) : 0.f;
   const float* wd = w + d * 4;
-  y[idx] = from_f<T>(x0 + (wd[0] * x0 + wd[1] * x1 + wd[2] * x2 + wd[3] * x3));
+  y[idx] = from_f<T>(x0 + conv4(wd, x0, x1, x2, x3));
 }
 
 // ---------------------------------------------------------------------------
@@ -137,6 +143,166 @@ __global__ void swiglu_kernel(const T* __restrict__ gu, T* __restrict__ out, int
   const float g = to_f(gu[r * 2 * dff + c]);
   const float u = to_f(gu[r * 2 * dff + dff + c]);
   out[idx] = from_f<T>(g * sigmoidf_(g) * u);
+}
+
+
+// ---------------------------------------------------------------------------
+// 16-byte forms of the elementwise ops (kVec<T> elements per thread and access), used when
+// the row lengths are multiples of kVec<T> and the tensors 16-byte aligned; the arithmetic
+// per element is the scalar kernels'.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(256) rmsnorm_vec_kernel(const T* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          T* __restrict__ y,
+                                                          float* __restrict__ rsq, int dim,
+                                                          float eps) {
+  constexpr int V = kVec<T>;
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * dim;
+  T* yr = y + row * dim;
+  const int nc = dim / V;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < nc; c += blockDim.x) {
+    float v[V];
+    ldv<V>(xr + c * V, v);
+#pragma unroll
+    for (int j = 0; j < V; ++j) ss += v[j] * v[j];
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+  if (threadIdx.x == 0 && rsq) rsq[row] = inv;
+  for (int c = threadIdx.x; c < nc; c += blockDim.x) {
+    float v[V], wv[V], o[V];
+    ldv<V>(xr + c * V, v);
+    ldv<V>(w + c * V, wv);
+#pragma unroll
+    for (int j = 0; j < V; ++j) o[j] = rnd<T>(v[j] * inv * wv[j]);
+    stv<V>(yr + c * V, o);
+  }
+}
+
+// Thread = 8 consecutive pairs (i, i + half) of one row.
+template <typename T>
+__global__ void rope_vec_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                const float* __restrict__ cs, const float* __restrict__ sn,
+                                int64_t rows, int64_t T_, int hd) {
+  const int half = hd / 2, per_row = half / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = idx / per_row;
+  if (row >= rows) return;
+  const int i = (int)(idx % per_row) * 8;
+  const int64_t t = row % T_;
+  float a[8], b[8], c[8], s[8], o1[8], o2[8];
+  ldv<8>(x + row * hd + i, a);
+  ldv<8>(x + row * hd + half + i, b);
+  ldv<8>(cs + t * half + i, c);
+  ldv<8>(sn + t * half + i, s);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    o1[j] = rnd<T>(fmaf(a[j], c[j], -(b[j] * s[j])));
+    o2[j] = rnd<T>(fmaf(b[j], c[j], a[j] * s[j]));
+  }
+  stv<8>(y + row * hd + i, o1);
+  stv<8>(y + row * hd + half + i, o2);
+}
+
+// 8 lanes per 64-element head vector, 8 elements per lane: lanes 0-3 of a group hold the
+// first half, lanes 4-7 the second, so a lane's rotate-half partners sit in lane ^ 4.
+template <typename T>
+__global__ void __launch_bounds__(256) qk_norm_rope_vec_kernel(
+    const T* __restrict__ x, int64_t sB, int64_t sH, int64_t sT, int H, int T_, int64_t nvec,
+    const float* __restrict__ w, const float* __restrict__ cs, const float* __restrict__ sn,
+    T* __restrict__ y, float* __restrict__ rsq, float eps) {
+  const int64_t v = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
+  const int j = threadIdx.x & 7;
+  const bool ok = v < nvec;
+  const int64_t vv = ok ? v : 0;
+  const int t = (int)(vv % T_);
+  const int h = (int)((vv / T_) % H);
+  const int64_t b = vv / ((int64_t)T_ * H);
+  float xv[8];
+  ldv<8>(x + b * sB + h * sH + (int64_t)t * sT + j * 8, xv);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  ss += __shfl_xor(ss, 4, 64);
+  const float inv = 1.0f / sqrtf(ss / 64.0f + eps);
+  float wv[8], n[8], p[8], c[8], s[8], o[8];
+  ldv<8>(w + h * 64 + j * 8, wv);
+  ldv<8>(cs + t * 32 + (j & 3) * 8, c);
+  ldv<8>(sn + t * 32 + (j & 3) * 8, s);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) n[e] = xv[e] * inv * wv[e];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(n[e], 4, 64);
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    o[e] = rnd<T>(j < 4 ? fmaf(n[e], c[e], -(p[e] * s[e])) : fmaf(n[e], c[e], p[e] * s[e]));
+  if (!ok) return;
+  if (j == 0 && rsq) rsq[v] = inv;
+  stv<8>(y + v * 64 + j * 8, o);
+}
+
+// Thread = kVec<T> consecutive dims of one (b, t, h) output head.
+template <typename T>
+__global__ void attn_gate_vec_kernel(const T* __restrict__ a, const float* __restrict__ gl,
+                                     T* __restrict__ out, int H, int T_, int hd, int64_t total) {
+  constexpr int V = kVec<T>;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx * V >= total) return;
+  const int d = (int)((idx * V) % hd);
+  const int64_t hv = (idx * V) / hd;
+  const int h = (int)(hv % H);
+  const int t = (int)((hv / H) % T_);
+  const int64_t b = hv / ((int64_t)H * T_);
+  const float g = sigmoidf_(gl[hv]);
+  float v[V];
+  ldv<V>(a + ((b * H + h) * T_ + t) * hd + d, v);
+#pragma unroll
+  for (int j = 0; j < V; ++j) v[j] = rnd<T>(v[j] * g);
+  stv<V>(out + idx * V, v);
+}
+
+template <typename T>
+__global__ void conv_k4_vec_kernel(const T* __restrict__ x, const float* __restrict__ w,
+                                   T* __restrict__ y, int64_t T_, int64_t D, int64_t total) {
+  constexpr int V = kVec<T>;
+  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
+  if (i0 >= total) return;
+  const int64_t d = i0 % D;
+  const int64_t t = (i0 / D) % T_;
+  float x0[V], x1[V], x2[V], x3[V], wd[4 * V], o[V];
+  ldv<V>(x + i0, x0);
+#pragma unroll
+  for (int j = 0; j < V; ++j) x1[j] = x2[j] = x3[j] = 0.f;
+  if (t >= 1) ldv<V>(x + i0 - D, x1);
+  if (t >= 2) ldv<V>(x + i0 - 2 * D, x2);
+  if (t >= 3) ldv<V>(x + i0 - 3 * D, x3);
+  ldv<4 * V>(w + d * 4, wd);
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    o[j] = rnd<T>(x0[j] + conv4(wd + 4 * j, x0[j], x1[j], x2[j], x3[j]));
+  }
+  stv<V>(y + i0, o);
+}
+
+template <typename T>
+__global__ void swiglu_vec_kernel(const T* __restrict__ gu, T* __restrict__ out, int64_t dff,
+                                  int64_t total) {
+  constexpr int V = kVec<T>;
+  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
+  if (i0 >= total) return;
+  const int64_t r = i0 / dff, c = i0 % dff;
+  float g[V], u[V], o[V];
+  ldv<V>(gu + r * 2 * dff + c, g);
+  ldv<V>(gu + r * 2 * dff + dff + c, u);
+#pragma unroll
+  for (int j = 0; j < V; ++j) o[j] = rnd<T>(g[j] * sigmoidf_(g[j]) * u[j]);
+  stv<V>(out + i0, o);
 }
 
 // ---------------------------------------------------------------------------
@@ -194,7 +360,9 @@ __global__ void router_topk_kernel(const L* __restrict__ logits, const float* __
   }
 }
 
-// Deterministic z-loss and probs_mean: one block loops over all tokens.
+// Deterministic z-loss and probs_mean: block e < E sums expert e's score over all tokens,
+// block E the squared logsumexp; each in a fixed order (threads stride the tokens, then one
+// block reduction), so the statistics do not depend on scheduling.
 template <typename L>
 __global__ void __launch_bounds__(256) router_stats_kernel(const L* __restrict__ logits,
                                                            const float* __restrict__ bias,
@@ -202,29 +370,29 @@ __global__ void __launch_bounds__(256) router_stats_kernel(const L* __restrict__
                                                            float* __restrict__ probs_mean,
                                                            int64_t N, int E, float zw) {
   __shared__ float red[16];
+  const int target = blockIdx.x;
   float c[32], s[32], b[32];
-  float pm[32];
-  for (int e = 0; e < E; ++e) pm[e] = 0.f;
-  float zsum = 0.f;
+  float acc = 0.f;
   for (int64_t t = threadIdx.x; t < N; t += blockDim.x) {
     router_scores(logits + t * E, bias, E, c, s, b);
+    if (target < E) {
+      acc += s[target];
+      continue;
+    }
     float mx = -INFINITY;
     for (int e = 0; e < E; ++e) mx = fmaxf(mx, c[e]);
     float se = 0.f;
-    for (int e = 0; e < E; ++e) {
-      se += expf(c[e] - mx);
-      pm[e] += s[e];
-    }
+    for (int e = 0; e < E; ++e) se += expf(c[e] - mx);
     const float lse = mx + logf(se);
-    zsum += lse * lse;
+    acc += lse * lse;
   }
   const float inv_n = N > 0 ? 1.0f / (float)N : 0.f;
-  const float zt = block_sum(zsum, red);
-  if (threadIdx.x == 0) z_loss[0] = zw > 0.f ? zw * zt * inv_n : 0.f;
-  for (int e = 0; e < E; ++e) {
-    const float v = block_sum(pm[e], red);
-    if (threadIdx.x == 0) probs_mean[e] = v * inv_n;
-  }
+  const float v = block_sum(acc, red);
+  if (threadIdx.x != 0) return;
+  if (target < E)
+    probs_mean[target] = v * inv_n;
+  else
+    z_loss[0] = zw > 0.f ? zw * v * inv_n : 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -276,9 +444,75 @@ __global__ void moe_combine_kernel(const T* __restrict__ eo, const int64_t* __re
       if (slot < 0 || slot >= C || e < 0 || e >= E) continue;
       bf16 wb;
       wb.u = wts[tok * K + k];
-      acc += bf2f(wb) * to_f(eo[(e * C + slot) * D + i]);
+      acc = fmaf(bf2f(wb), to_f(eo[(e * C + slot) * D + i]), acc);
     }
     out[tok * D + i] = from_f<T>(acc);
+  }
+}
+
+// 16-byte forms of zero / dispatch / combine for 16-byte-aligned tensors whose rows are a
+// multiple of 16 bytes (dispatch and zero move bytes; combine keeps the scalar kernel's
+// per-element order: shared output first, then the k terms in order).
+__global__ void moe_zero_vec_kernel(uint4* __restrict__ buf, const int64_t* __restrict__ counts,
+                                    int C, int64_t row_q) {
+  const int e = blockIdx.y;
+  int64_t start = 0;
+  if (counts) {
+    const int64_t n = counts[e];
+    start = n < 0 ? 0 : (n > C ? C : n);
+  }
+  const int64_t len = (C - start) * row_q;
+  uint4* base = buf + ((int64_t)e * C + start) * row_q;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+       i += (int64_t)gridDim.x * blockDim.x)
+    base[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+__global__ void moe_dispatch_vec_kernel(const uint4* __restrict__ x,
+                                        const int64_t* __restrict__ idx,
+                                        const int32_t* __restrict__ slots,
+                                        uint4* __restrict__ dst, int64_t row_q, int K, int E,
+                                        int C) {
+  const int64_t tok = blockIdx.x;
+  for (int k = 0; k < K; ++k) {
+    const int slot = slots[tok * K + k];
+    const int64_t e = idx[tok * K + k];
+    if (slot < 0 || slot >= C || e < 0 || e >= E) continue;
+    uint4* d = dst + (e * C + slot) * row_q;
+    for (int64_t i = threadIdx.x; i < row_q; i += blockDim.x) d[i] = x[tok * row_q + i];
+  }
+}
+
+template <typename T>
+__global__ void moe_combine_vec_kernel(const T* __restrict__ eo, const int64_t* __restrict__ idx,
+                                       const uint16_t* __restrict__ wts,
+                                       const int32_t* __restrict__ slots,
+                                       const T* __restrict__ shared, T* __restrict__ out,
+                                       int64_t D, int K, int E, int C) {
+  constexpr int V = kVec<T>;
+  const int64_t tok = blockIdx.x;
+  for (int64_t i = (int64_t)threadIdx.x * V; i < D; i += (int64_t)blockDim.x * V) {
+    float acc[V], v[V];
+    if (shared) {
+      ldv<V>(shared + tok * D + i, acc);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] = 0.f;
+    }
+    for (int k = 0; k < K; ++k) {
+      const int slot = slots[tok * K + k];
+      const int64_t e = idx[tok * K + k];
+      if (slot < 0 || slot >= C || e < 0 || e >= E) continue;
+      bf16 wb;
+      wb.u = wts[tok * K + k];
+      const float w = bf2f(wb);
+      ldv<V>(eo + (e * C + slot) * D + i, v);
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] = fmaf(w, v[j], acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) acc[j] = rnd<T>(acc[j]);
+    stv<V>(out + tok * D + i, acc);
   }
 }
 
@@ -328,8 +562,12 @@ int pulsar_rmsnorm_forward(const void* x, const float* w, void* y, float* rsqrt_
   PULSAR_REQUIRE(x && w && y, "rmsnorm: null pointer");
   return dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    rmsnorm_kernel<T><<<(unsigned)rows, 256, 0, stream>>>((const T*)x, w, (T*)y, rsqrt_out,
-                                                          (int)dim, eps);
+    if (dim % kVec<T> == 0 && aligned16(x) && aligned16(w) && aligned16(y))
+      rmsnorm_vec_kernel<T><<<(unsigned)rows, 256, 0, stream>>>((const T*)x, w, (T*)y,
+                                                                rsqrt_out, (int)dim, eps);
+    else
+      rmsnorm_kernel<T><<<(unsigned)rows, 256, 0, stream>>>((const T*)x, w, (T*)y, rsqrt_out,
+                                                            (int)dim, eps);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   });
@@ -343,9 +581,16 @@ int pulsar_rope_forward(const void* x, void* y, const float* cos, const float* s
   if (rows == 0) return PULSAR_OK;
   return dispatch_dtype(dtype, [&](auto tag) {
     using T_ = decltype(tag);
-    const int64_t n = rows * (head_dim / 2);
-    rope_kernel<T_><<<blocks_for(n, 256), 256, 0, stream>>>((const T_*)x, (T_*)y, cos, sin, rows,
-                                                            T, (int)head_dim);
+    if ((head_dim / 2) % 8 == 0 && aligned16(x) && aligned16(y) && aligned16(cos) &&
+        aligned16(sin)) {
+      const int64_t n = rows * (head_dim / 16);
+      rope_vec_kernel<T_><<<blocks_for(n, 256), 256, 0, stream>>>(
+          (const T_*)x, (T_*)y, cos, sin, rows, T, (int)head_dim);
+    } else {
+      const int64_t n = rows * (head_dim / 2);
+      rope_kernel<T_><<<blocks_for(n, 256), 256, 0, stream>>>((const T_*)x, (T_*)y, cos, sin,
+                                                              rows, T, (int)head_dim);
+    }
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   });
@@ -364,8 +609,14 @@ int pulsar_qk_rmsnorm_rope_forward(const void* x, int64_t sB, int64_t sH, int64_
   PULSAR_REQUIRE(T > 0 && H > 0, "qk_rmsnorm_rope: H and T must be positive");
   return dispatch_dtype(dtype, [&](auto tag) {
     using T_ = decltype(tag);
-    qk_norm_rope_kernel<T_><<<blocks_for(nvec, 4), 256, 0, stream>>>(
-        (const T_*)x, sB, sH, sT, (int)H, (int)T, nvec, w, cos, sin, (T_*)y, rsqrt_out, eps);
+    constexpr int V = kVec<T_>;
+    if (sB % V == 0 && sH % V == 0 && sT % V == 0 && aligned16(x) && aligned16(w) &&
+        aligned16(cos) && aligned16(sin) && aligned16(y))
+      qk_norm_rope_vec_kernel<T_><<<blocks_for(nvec * 8, 256), 256, 0, stream>>>(
+          (const T_*)x, sB, sH, sT, (int)H, (int)T, nvec, w, cos, sin, (T_*)y, rsqrt_out, eps);
+    else
+      qk_norm_rope_kernel<T_><<<blocks_for(nvec, 4), 256, 0, stream>>>(
+          (const T_*)x, sB, sH, sT, (int)H, (int)T, nvec, w, cos, sin, (T_*)y, rsqrt_out, eps);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   });
@@ -381,8 +632,12 @@ int pulsar_fused_attn_gate_forward(const void* attn, const float* gate_logits, v
   if (total == 0) return PULSAR_OK;
   return dispatch_dtype(dtype, [&](auto tag) {
     using T_ = decltype(tag);
-    attn_gate_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>(
-        (const T_*)attn, gate_logits, (T_*)out, (int)H, (int)T, (int)head_dim, total);
+    if (aligned16(attn) && aligned16(out))  // head_dim 64 is a multiple of kVec
+      attn_gate_vec_kernel<T_><<<blocks_for(total / kVec<T_>, 256), 256, 0, stream>>>(
+          (const T_*)attn, gate_logits, (T_*)out, (int)H, (int)T, (int)head_dim, total);
+    else
+      attn_gate_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>(
+          (const T_*)attn, gate_logits, (T_*)out, (int)H, (int)T, (int)head_dim, total);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   });
@@ -395,8 +650,12 @@ int pulsar_causal_conv1d_k4_forward(const void* x, const float* w, void* y, int6
   if (total == 0) return PULSAR_OK;
   return dispatch_dtype(dtype, [&](auto tag) {
     using T_ = decltype(tag);
-    conv_k4_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>((const T_*)x, w, (T_*)y, T,
-                                                                   D, total);
+    if (D % kVec<T_> == 0 && aligned16(x) && aligned16(w) && aligned16(y))
+      conv_k4_vec_kernel<T_><<<blocks_for(total / kVec<T_>, 256), 256, 0, stream>>>(
+          (const T_*)x, w, (T_*)y, T, D, total);
+    else
+      conv_k4_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>((const T_*)x, w, (T_*)y,
+                                                                     T, D, total);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   });
@@ -409,8 +668,12 @@ int pulsar_fused_swiglu_forward(const void* gu, void* out, int64_t rows, int64_t
   if (total == 0) return PULSAR_OK;
   return dispatch_dtype(dtype, [&](auto tag) {
     using T_ = decltype(tag);
-    swiglu_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>((const T_*)gu, (T_*)out, d_ff,
-                                                                  total);
+    if (d_ff % kVec<T_> == 0 && aligned16(gu) && aligned16(out))
+      swiglu_vec_kernel<T_><<<blocks_for(total / kVec<T_>, 256), 256, 0, stream>>>(
+          (const T_*)gu, (T_*)out, d_ff, total);
+    else
+      swiglu_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>((const T_*)gu, (T_*)out,
+                                                                    d_ff, total);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   });
@@ -434,7 +697,7 @@ int pulsar_moe_router_topk_forward(const void* logits, int logits_dtype, const f
           (const L*)logits, bias, topk_idx, topk_w_bf16, N, (int)E, (int)K);
     PULSAR_LAUNCH_CHECK();
     if (z_loss && probs_mean) {
-      router_stats_kernel<L><<<1, 256, 0, stream>>>((const L*)logits, bias, z_loss, probs_mean,
+      router_stats_kernel<L><<<(unsigned)(E + 1), 256, 0, stream>>>((const L*)logits, bias, z_loss, probs_mean,
                                                     N, (int)E, z_loss_weight);
       PULSAR_LAUNCH_CHECK();
     }
@@ -452,14 +715,25 @@ int pulsar_moe_dispatch_forward(const void* x, const int64_t* topk_idx, const in
   PULSAR_REQUIRE(N >= 0 && K >= 0 && E > 0 && C >= 0, "dispatch: bad shape");
   return dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
+    const bool vec = aligned16(x) && aligned16(expert_inputs);  // rows: D % 8 == 0
+    const int64_t row_q = D * (int64_t)sizeof(T) / 16;
     if (C > 0) {
       dim3 g(64, (unsigned)E);
-      moe_zero_kernel<T><<<g, 256, 0, stream>>>((T*)expert_inputs, expert_counts, (int)C, D);
+      if (vec)
+        moe_zero_vec_kernel<<<g, 256, 0, stream>>>((uint4*)expert_inputs, expert_counts,
+                                                   (int)C, row_q);
+      else
+        moe_zero_kernel<T><<<g, 256, 0, stream>>>((T*)expert_inputs, expert_counts, (int)C, D);
       PULSAR_LAUNCH_CHECK();
     }
     if (N > 0 && K > 0 && C > 0) {
-      moe_dispatch_kernel<T><<<(unsigned)N, 128, 0, stream>>>(
-          (const T*)x, topk_idx, slots, (T*)expert_inputs, D, (int)K, (int)E, (int)C);
+      if (vec)
+        moe_dispatch_vec_kernel<<<(unsigned)N, 128, 0, stream>>>(
+            (const uint4*)x, topk_idx, slots, (uint4*)expert_inputs, row_q, (int)K, (int)E,
+            (int)C);
+      else
+        moe_dispatch_kernel<T><<<(unsigned)N, 128, 0, stream>>>(
+            (const T*)x, topk_idx, slots, (T*)expert_inputs, D, (int)K, (int)E, (int)C);
       PULSAR_LAUNCH_CHECK();
     }
     return PULSAR_OK;
@@ -474,9 +748,15 @@ int pulsar_moe_combine_forward(const void* expert_outputs, const int64_t* topk_i
   if (N == 0) return PULSAR_OK;
   return dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    moe_combine_kernel<T><<<(unsigned)N, 128, 0, stream>>>(
-        (const T*)expert_outputs, topk_idx, topk_w_bf16, slots, (const T*)shared_out, (T*)out, D,
-        (int)K, (int)E, (int)C);
+    if (D % kVec<T> == 0 && aligned16(expert_outputs) && aligned16(out) &&
+        (!shared_out || aligned16(shared_out)))
+      moe_combine_vec_kernel<T><<<(unsigned)N, 128, 0, stream>>>(
+          (const T*)expert_outputs, topk_idx, topk_w_bf16, slots, (const T*)shared_out,
+          (T*)out, D, (int)K, (int)E, (int)C);
+    else
+      moe_combine_kernel<T><<<(unsigned)N, 128, 0, stream>>>(
+          (const T*)expert_outputs, topk_idx, topk_w_bf16, slots, (const T*)shared_out,
+          (T*)out, D, (int)K, (int)E, (int)C);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   });

@@ -100,7 +100,7 @@ constexpr int kSampleThreads = PULSAR_SAMPLE_THREADS;
 
 template <typename T, int PER, int NT>
 __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
-  __shared__ float red[16];
+  __shared__ float red[32];
   __shared__ ArgMax ared[16];
   const int lr = blockIdx.x;
   if (lr >= a.ctl->n_lrows) return;
@@ -192,18 +192,53 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
   uint32_t kw[PER / kPack];
 #pragma unroll
   for (int i = 0; i < PER / kPack; ++i) kw[i] = 0u;
-  float zl = 0.f;
+  float zl = 0.f, at_max = 0.f;
+  const uint32_t kmax = order_key(mx) >> kLow;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     pr[i] = expf(l[i] - mx);
     const uint32_t k = order_key(l[i]) >> kLow;
     kw[i / kPack] |= kPack == 2 ? k << (16 * (i & 1)) : k;
     zl += pr[i];
+    at_max += k == kmax ? 1.f : 0.f;
   }
 #define KEY(i) (kPack == 2 ? (kw[(i) / kPack] >> (16 * ((i) & 1))) & 0xffffu : kw[(i) / kPack])
-  const float Z = block_sum(zl, red);
+  // Z, and the number of scores at the maximum (each with probability weight exp(0) = 1):
+  // one reduction, Z summed in the same order as a reduction of its own
+  float Z, n_max;
+  {
+    const float zw = wave_sum(zl), cw = wave_sum(at_max);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+      red[w] = zw;
+      red[16 + w] = cw;
+    }
+    __syncthreads();
+    Z = 0.f;
+    n_max = 0.f;
+    for (int i = 0; i < nw; ++i) {
+      Z += red[i];
+      n_max += red[16 + i];
+    }
+  }
   uint32_t kstar = 0;
-  if (a.top_p < 1.0f) {
+  // When the scores tied at the maximum hold more than top_p of the mass (mass above any
+  // lower key >= n_max > top_p Z, mass above the maximum's key 0), the threshold search
+  // would end at the maximum's key: take it directly. A single such score is then the only
+  // token kept, and both draws are the argmax.
+  const bool max_only = a.top_p < 1.0f && n_max > a.top_p * Z;
+  if (max_only && n_max == 1.f) {
+    if (threadIdx.x == 0) {
+      a.out_argmax[lr] = am.i;
+      a.out_draw[lr * 2] = am.i;
+      a.out_draw[lr * 2 + 1] = am.i;
+    }
+    return;
+  }
+  if (max_only) {
+    kstar = kmax;
+  } else if (a.top_p < 1.0f) {
     // smallest m with mass(key > m) <= top_p * Z; the maximum's key always qualifies.
     // Bisection (per-step cost is the 32-element pass, so wider probes do not pay); one
     // barrier per step: partials alternate between two LDS buffers.

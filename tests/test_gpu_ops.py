@@ -184,3 +184,74 @@ def test_slots_dispatch_combine(pc):
             if s >= 0:
                 ref[n] += w[n, k].float() * eo[idx[n, k], s].float()
     assert_close(out, ref, atol=3e-2, rtol=8e-3)
+
+
+def _misaligned(t: torch.Tensor) -> torch.Tensor:
+    """The same values in a contiguous view one element past a 16-byte boundary, which sends
+    an op to its scalar kernel instead of the 16-byte one."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    v = buf[1:].view(t.shape)
+    v.copy_(t)
+    assert v.data_ptr() % 16 != 0 and v.is_contiguous()
+    return v
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_vector_and_scalar_kernels_agree(pc, dtype):
+    """Each elementwise op's 16-byte kernel (aligned inputs) and scalar kernel (misaligned
+    copy) compute every element by the same expression: equal outputs. RMSNorm's sum of
+    squares runs in another order: within one rounding of the output dtype."""
+    # bf16: one rounding step; fp32: a few ulp from the reordered 768-term sum
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -20
+    x = _rand(8, 768, seed=21, dtype=dtype)
+    w = torch.rand(768, device="cuda") + 0.5
+    (ya, ra), (yb, rb) = pc.rmsnorm_forward(x, w, 1e-6), pc.rmsnorm_forward(_misaligned(x), w, 1e-6)
+    assert ((ya.float() - yb.float()).abs() <= ulp * yb.float().abs() + 1e-30).all()
+    assert_close(ra, rb, atol=0, rtol=1e-6)
+
+    q = _rand(2, 4, 13, 64, seed=22, dtype=dtype)
+    cos, sin = _tables(13)
+    assert torch.equal(pc.rope_forward(q, cos, sin), pc.rope_forward(_misaligned(q), cos, sin))
+
+    B, T, H = 2, 7, 4
+    qkv = _rand(B, T, H * 64 * 3, seed=23, dtype=dtype)
+    xs = qkv[..., : H * 64].view(B, T, H, 64).transpose(1, 2)
+    xm = _misaligned(qkv)[..., : H * 64].view(B, T, H, 64).transpose(1, 2)
+    wq = torch.rand(H, 64, device="cuda") + 0.5
+    cq, sq = _tables(T)
+    (y1, r1), (y2, r2) = (pc.qk_rmsnorm_rope_forward(xs, wq, cq, sq, T, 1e-6),
+                          pc.qk_rmsnorm_rope_forward(xm, wq, cq, sq, T, 1e-6))
+    # the rotation's differences may cancel: bound by the head's largest output
+    assert ((y1.float() - y2.float()).abs()
+            <= 2 * ulp * y2.float().abs().amax(-1, keepdim=True)).all()
+    assert_close(r1, r2, atol=0, rtol=1e-6)
+
+    a = _rand(2, 16, 5, 64, seed=24, dtype=dtype)
+    gl = _rand(2, 5, 16, seed=25, dtype=torch.float32)
+    assert torch.equal(pc.fused_attn_gate_forward(a, gl),
+                       pc.fused_attn_gate_forward(_misaligned(a), gl))
+
+    xc = _rand(2, 11, 256, seed=26, dtype=dtype)
+    wc = _rand(256, 4, seed=27, dtype=torch.float32, scale=0.3)
+    assert torch.equal(pc.causal_depthwise_conv1d_k4_forward(xc, wc),
+                       pc.causal_depthwise_conv1d_k4_forward(_misaligned(xc), wc))
+
+    gu = _rand(7, 1024, seed=28, dtype=dtype)
+    assert torch.equal(pc.fused_swiglu_forward(gu, 512),
+                       pc.fused_swiglu_forward(_misaligned(gu), 512))
+
+    N, K, E, C, D = 32, 2, 8, 10, 256
+    g = torch.Generator().manual_seed(29)
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(N)]).cuda()
+    wt = torch.rand(N, K, generator=g).cuda().to(torch.bfloat16)
+    flat_e = idx.reshape(-1).contiguous()
+    slots, counts = pc.moe_slots_from_order(flat_e, torch.argsort(flat_e, stable=True), E, C)
+    slots = slots.view(N, K).contiguous()
+    xd = _rand(N, D, seed=30, dtype=dtype)
+    (b1,) = pc.moe_dispatch_forward(xd, idx, slots, E, C, counts)
+    (b2,) = pc.moe_dispatch_forward(_misaligned(xd), idx, slots, E, C, counts)
+    assert torch.equal(b1, b2)
+    eo = _rand(E, C, D, seed=31, dtype=dtype)
+    sh = _rand(N, D, seed=32, dtype=dtype)
+    assert torch.equal(pc.moe_combine_forward(eo, idx, wt, slots, sh),
+                       pc.moe_combine_forward(_misaligned(eo), idx, wt, slots, sh))

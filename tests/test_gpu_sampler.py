@@ -60,6 +60,7 @@ def test_argmax_exact_and_draws_inside_top_p(dtype):
     rows[::4] = np.round(rows[::4] * 4) / 4          # many exact ties
     rows[1::8, 77] = 40.0                              # one dominant token
     rows[2::8, :] = 0.0                                # a flat row: every token tied
+    rows[3::8, 4100] = rows[3::8, 9000] = 40.0         # two tied dominant tokens
     seen = [set(rng.integers(0, V, 120).tolist()) | {77} for _ in range(n_seq)]
     row_seq = [i % n_seq for i in range(n)]
     row_extra = [int(rng.integers(0, V)) if i % 3 == 0 else -1 for i in range(n)]
