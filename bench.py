@@ -87,18 +87,37 @@ def _csv(directory: str, suffix: str) -> list:
         return list(csv.DictReader(f))
 
 
+def _busy_launches(v: list) -> list:
+    """The launches of a kernel that did work: kernels whose row set can be empty (the output
+    head and the sampler on steps without logits rows, exact schedule) exit at once there.
+    When a kernel's durations split into such a cluster under 4 us and one at least 3 times
+    longer (10th against 90th percentile), the launches above the geometric mean of the two
+    percentiles; otherwise all of them."""
+    s = sorted(v)
+    if len(s) < 8:
+        return v
+    lo, hi = s[len(s) // 10], s[(9 * len(s)) // 10]
+    if hi < 3 * lo or lo > 4000:
+        return v
+    cut = (lo * hi) ** 0.5
+    return [x for x in v if x >= cut]
+
+
 def rocprof_summary(directory: str, phase: str = "decode") -> str:
-    """Markdown table of one phase's kernel durations from a rocprofv3 kernel trace (csv)."""
+    """Markdown table of one phase's kernel durations from a rocprofv3 kernel trace (csv):
+    all dispatches, and the dispatches that did work (`_busy_launches`)."""
     from collections import defaultdict
     rows = _phase_rows(_csv(directory, "kernel_trace.csv"), phase)
     agg = defaultdict(list)
     for r in rows:
         agg[_short_kernel(r["Kernel_Name"])].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
     total = sum(sum(v) for v in agg.values())
-    out = ["| kernel | dispatches | avg us | total ms | share |", "|---|---|---|---|---|"]
+    out = ["| kernel | dispatches | avg us | total ms | share | busy dispatches | busy avg us |",
+           "|---|---|---|---|---|---|---|"]
     for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        b = _busy_launches(v)
         out.append(f"| `{k}` | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | {sum(v) / 1e6:.2f} | "
-                   f"{100 * sum(v) / total:.1f}% |")
+                   f"{100 * sum(v) / total:.1f}% | {len(b)} | {sum(b) / len(b) / 1e3:.2f} |")
     out.append(f"\n{phase.capitalize()} kernel time {total / 1e6:.2f} ms over {len(rows)} dispatches.")
     return "\n".join(out)
 
@@ -462,6 +481,49 @@ def kv_footprint(cfg) -> dict:
     return out
 
 
+def run_c4(model, cfg, args, profile: bool = True) -> dict:
+    """4 sequences of 32768 uniform-random prompt tokens, 512 new tokens, greedy (the
+    configuration names no temperature), reference schedule."""
+    import numpy as np
+
+    from pulsar_engine import weights as W
+    p4 = np.stack([W.uniform_ids(90 + b, "c4_prompt", 32768, cfg.vocab_size) for b in range(4)])
+    c4 = run_workload(model, cfg, p4, 512, 0.0, 1.0, args.repetition_penalty, steps=1,
+                      warmup=1, label="c4", profile=profile)
+    c4["workload"] = ("Pulsar-283M bf16, batch 4, 32768-token uniform prompts, greedy "
+                      "self-speculative decode of 512 tokens (reference schedule)")
+    log(f"c4: {json.dumps({k: v for k, v in c4.items() if k != 'kernel_profile'})}")
+    return c4
+
+
+def run_c5(cfg, state, args, profile: bool = True, draft_block: bool = True) -> dict:
+    """256 sequences of 512 Zipf(1.1) prompt tokens, router weights x4, greedy, 512 new
+    tokens; reference schedule, and the draft-block mode at draft length 6 beside it."""
+    import numpy as np
+    import torch
+
+    from pulsar_engine import weights as W
+    from pulsar_engine.model import DeviceModel
+    # the skewed-routing weights: synthetic_state(router_scale=4) without regenerating
+    st5 = {k: (v * np.float32(4.0)).astype(np.float32) if k.endswith("router_weight") else v
+           for k, v in state.items()}
+    m5 = DeviceModel(cfg, st5, torch.bfloat16)
+    p5 = np.stack([W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size) for b in range(256)])
+    c5 = run_workload(m5, cfg, p5, 512, 0.0, 1.0, args.repetition_penalty, steps=1,
+                      warmup=1, label="c5", profile=profile)
+    c5["workload"] = ("Pulsar-283M bf16 with router weights x4, batch 256, 512-token "
+                      "Zipf(1.1) prompts, greedy self-speculative decode of 512 tokens "
+                      "(reference schedule)")
+    if draft_block:
+        c5["draft_block_6"] = run_workload(m5, cfg, p5, 512, 0.0, 1.0, args.repetition_penalty,
+                                           steps=1, warmup=1, profile=False, draft_len=6,
+                                           label="c5 draft-block 6")
+    log(f"c5: {json.dumps({k: v for k, v in c5.items() if k != 'kernel_profile'})}")
+    del m5, st5
+    torch.cuda.empty_cache()
+    return c5
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -483,6 +545,8 @@ def main() -> int:
     ap.add_argument("--draft-len", type=int, default=4,
                     help="draft length of the draft-block run (0 skips it)")
     ap.add_argument("--no-verify", action="store_true", help="skip the verify microbenchmark")
+    ap.add_argument("--only", choices=("c4", "c5"),
+                    help="run only that workload, unprofiled (kernel traces)")
     ap.add_argument("--verify-only", action="store_true",
                     help="run only the verify microbenchmark (profiling)")
     ap.add_argument("--verify-batch", type=int, default=64)
@@ -541,6 +605,13 @@ def main() -> int:
     if args.verify_only:
         vr = verify_microbench(model, cfg, es, args)
         print(json.dumps({"verify": vr}), flush=True)
+        return 0
+    if args.only == "c4":
+        print(json.dumps({"c4": run_c4(model, cfg, args, profile=False)}), flush=True)
+        return 0
+    if args.only == "c5":
+        print(json.dumps({"c5": run_c5(cfg, state, args, profile=False, draft_block=False)}),
+              flush=True)
         return 0
     prompts = np.stack([W.uniform_ids(0, f"bench_prompt_{b}", T, cfg.vocab_size) for b in range(B)])
     eng = HipEngine(model, batch=B, max_prompt=T, max_new=N, speculative=not args.plain,
@@ -663,36 +734,8 @@ def main() -> int:
         del pe, m32
         torch.cuda.empty_cache()
         log(f"c1: {c1['value']} tokens/s")
-    # c4: 4 sequences of 32768 uniform-random prompt tokens, 512 new tokens, greedy (the
-    # configuration names no temperature), reference schedule
-    c4 = None
-    if not args.no_c4:
-        p4 = np.stack([W.uniform_ids(90 + b, "c4_prompt", 32768, cfg.vocab_size) for b in range(4)])
-        c4 = run_workload(model, cfg, p4, 512, 0.0, 1.0, args.repetition_penalty, steps=1,
-                          warmup=1, label="c4")
-        c4["workload"] = ("Pulsar-283M bf16, batch 4, 32768-token uniform prompts, greedy "
-                          "self-speculative decode of 512 tokens (reference schedule)")
-        log(f"c4: {json.dumps({k: v for k, v in c4.items() if k != 'kernel_profile'})}")
-    # c5: 256 sequences of 512 Zipf(1.1) prompt tokens, router weights x4, greedy, 512 new
-    # tokens; reference schedule, and the draft-block mode at draft length 6 beside it
-    c5 = None
-    if not args.no_c5:
-        # the skewed-routing weights: synthetic_state(router_scale=4) without regenerating
-        st5 = {k: (v * np.float32(4.0)).astype(np.float32) if k.endswith("router_weight") else v
-               for k, v in state.items()}
-        m5 = DeviceModel(cfg, st5, torch.bfloat16)
-        p5 = np.stack([W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size) for b in range(256)])
-        c5 = run_workload(m5, cfg, p5, 512, 0.0, 1.0, args.repetition_penalty, steps=1,
-                          warmup=1, label="c5")
-        c5["workload"] = ("Pulsar-283M bf16 with router weights x4, batch 256, 512-token "
-                          "Zipf(1.1) prompts, greedy self-speculative decode of 512 tokens "
-                          "(reference schedule)")
-        c5["draft_block_6"] = run_workload(m5, cfg, p5, 512, 0.0, 1.0, args.repetition_penalty,
-                                           steps=1, warmup=1, profile=False, draft_len=6,
-                                           label="c5 draft-block 6")
-        log(f"c5: {json.dumps({k: v for k, v in c5.items() if k != 'kernel_profile'})}")
-        del m5, st5
-        torch.cuda.empty_cache()
+    c4 = None if args.no_c4 else run_c4(model, cfg, args)
+    c5 = None if args.no_c5 else run_c5(cfg, state, args)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, state, prompts[0], args.cpu_new_tokens, args.temperature,

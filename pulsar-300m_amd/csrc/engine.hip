@@ -356,9 +356,10 @@ constexpr int kWideLogitsRows = 128;
 // Per layer: qkv+gate GEMM, qk-norm/RoPE/KV write, attention (+ split combine), wo GEMM with
 // residual, mlp-norm + router, shared+routed gate/up GEMM, shared+routed down GEMM, MoE
 // combine with residual and the next layer's attn-norm (the first layer's attn-norm is
-// fused into the pulse-input kernel).
+// fused into the pulse-input kernel). `head` false leaves out the output head, for passes
+// the host knows to have no logits rows.
 int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnUnit* units,
-                 hipStream_t s) {
+                 hipStream_t s, bool head = true) {
   const PulsarModelDesc& m = e.m;
   const int D = e.D, MR = e.max_rows, dt = e.dtype;
   // at two or more assignments per expert on average, nearly every expert has rows: the
@@ -592,6 +593,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
   po.final_norm = m.final_norm;
   po.xn_final = e.xn_final;
   PULSAR_TIMED(PC_OUTPUT, launch_pulse_output(po, dt, MR, s));
+  if (!head) return PULSAR_OK;
   GemmArgs g = gemm_base(e);
   g.A = e.xn_final;
   g.lda = D;
@@ -1162,7 +1164,7 @@ int verify(Engine& e, const int32_t* host_tokens, int n, int use_graph, hipStrea
   auto passes = [&](hipStream_t st) -> int {
     for (int k = 0; k < P; ++k)
       PULSAR_TRY(enqueue_pass(e, e.v_ctl + k, e.v_rows + (size_t)k * MR, e.v_units + (size_t)k * B,
-                              st));
+                              st, k == P - 1));  // logits rows: the last pulse's only
     return PULSAR_OK;
   };
   if (!use_graph || e.prof_on) {
