@@ -496,9 +496,22 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   const int wr = wv >> 1, wc = wv & 1;
   const int m16 = lane & 15, kq = lane >> 4;
   const int cnt = group_rows<MODE>(g, group);
-  const int r_wg = (int)blockIdx.z * kTileRows;
+  int bx = (int)blockIdx.x, bz = (int)blockIdx.z;
+  if constexpr (MODE == ROWS_LOGITS) {
+    // output head (one group): workgroup L runs on XCD L % 8; give each XCD a contiguous
+    // range of column tiles with their row tiles one after another, so the row tiles of a
+    // column tile read its weights through one L2
+    const int nz = (int)gridDim.z, total = (int)gridDim.x * nz;
+    if (nz > 1 && total % 8 == 0) {
+      const int L = bx + (int)gridDim.x * bz;
+      const int w = (L & 7) * (total >> 3) + (L >> 3);
+      bx = w / nz;
+      bz = w % nz;
+    }
+  }
+  const int r_wg = bz * kTileRows;
   if (r_wg >= cnt) return;
-  const int ct_wg = (int)blockIdx.x * (kPair ? 8 : 16);  // first (gate) column tile
+  const int ct_wg = bx * (kPair ? 8 : 16);  // first (gate) column tile
   if (ct_wg * 16 >= N) return;
   const bf16* A = reinterpret_cast<const bf16*>(g.A);
   const bf16* W = reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;

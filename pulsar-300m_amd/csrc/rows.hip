@@ -608,7 +608,9 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
 // layers and 4 in the sliding-window layers. Holding the next block in registers while
 // computing the current one (64 more registers: one wave per SIMD) and touching the next
 // blocks' lines ahead of their loads were both measured slower at 64 x 8192 positions, and
-// so was staging the blocks through LDS (attn_decode_lds_kernel below).
+// so was staging the blocks through LDS with direct global-to-LDS loads (2-stage rings of
+// 16 KB per wave, 4-8 waves): slower at batch 16 x 2048 and 64 x 8192, 3 % faster only at
+// 4 x 8192.
 // ---------------------------------------------------------------------------
 typedef __bf16 attn_bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -842,302 +844,6 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   // of them complete before thread 0's counter add is issued; the merging block issues its
   // partial loads only after the add has returned (through LDS and a barrier, which the
   // compiler does not move memory operations across).
-  __builtin_amdgcn_s_waitcnt(0);
-  __shared__ int s_last;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int32_t* cnt = a.split_done + (int64_t)u * a.Hkv + g;
-    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == nsplit - 1;
-    if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  attn_merge_splits<COLS>(a, u, g, un, nsplit);
-}
-
-// ---------------------------------------------------------------------------
-// Decode attention with LDS-staged key/value blocks (bf16 caches, gfx950).
-//
-// Workgroup = (unit, kv head, split of NW * BPW 64-key blocks); wave w takes blocks
-// w, w + NW, ... of the split. Each block is fetched with direct global-to-LDS loads
-// (global_load_lds_dwordx4: 16 bytes per lane, no staging registers) into a per-wave ring
-// of STAGES slots of 16 KB, so a wave has up to STAGES blocks in flight while it computes
-// one; only the block being computed occupies registers.
-//
-// Key order. Row m of S^T tile kt is key kperm(kt, m) = 32 (kt >> 1) + 8 (m >> 2) +
-// 4 (kt & 1) + (m & 3) of the block. With it the 8 P values a lane contributes to the B
-// operand of the s2-th O^T = V^T P^T product (rows 4 kq + j of tiles 2 s2 and 2 s2 + 1 of
-// its S^T registers) are keys 32 s2 + 8 kq .. + 7, consecutive, so the V^T operand of the
-// dimension-major V block is one 16-byte run per lane, like the K operand.
-//
-// Each lane stages exactly the 16-byte chunks it later reads back (ds_read_b128 at the
-// same LDS offset), so a slot needs no barrier between its fill and its use, only the
-// wave's own vmcnt wait. Products, softmax, the wave merge in LDS and the split merge are
-// those of attn_decode_unit_kernel.
-// ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void* lds_vptr;
-typedef __attribute__((address_space(1))) void* glb_vptr;
-
-__device__ __forceinline__ int attn_kperm(int kt, int m) {
-  return 32 * (kt >> 1) + 8 * (m >> 2) + 4 * (kt & 1) + (m & 3);
-}
-
-// Issue one 64-key block into an LDS slot of 16 KB: K chunks (kt, ks) at (kt * 2 + ks) KB,
-// V chunks (mt, s2) at 8 + (mt * 2 + s2) KB; lane l's chunk at +16 l.
-__device__ __forceinline__ void attn_stage_block(const bf16* Kc, const bf16* Vc, const KVBlock& blk,
-                                                 int m16, int kq, char* slot) {
-#pragma unroll
-  for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      __builtin_amdgcn_global_load_lds(
-          (glb_vptr)(Kc + blk.k0 + attn_kperm(kt, m16) * 64 + ks * 32 + kq * 8),
-          (lds_vptr)(slot + (kt * 2 + ks) * 1024), 16, 0, 0);
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-      __builtin_amdgcn_global_load_lds(
-          (glb_vptr)(Vc + blk.v0 + (int64_t)(mt * 16 + m16) * blk.vstride + s2 * 32 + kq * 8),
-          (lds_vptr)(slot + 8192 + (mt * 2 + s2) * 1024), 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima), n <= 63.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-template <int COLS, int NW, int BPW, int STAGES>
-__global__ void __launch_bounds__(64 * NW) attn_decode_lds_kernel(AttnArgs a) {
-  constexpr int NQT = (COLS + 15) / 16;
-  constexpr int NZ = COLS / 4;
-  constexpr int SPLIT = NW * BPW * 64;
-  constexpr int SLOT = 16384;
-  constexpr int QBYTES = NQT * 2 * 1024;  // a wave's staged query chunks
-  constexpr int kStageBytes = NW * (STAGES * SLOT + QBYTES);
-  constexpr int kMergeBytes = NW * COLS * (2 + 65) * 4;
-  static_assert(kStageBytes >= kMergeBytes, "the wave merge reuses the staging slots");
-  static_assert(kStageBytes <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(16))) char lds[kStageBytes];
-  const int u = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
-  const int n_units = a.ctl->n_units;
-  const AttnUnit un = a.units[u];
-  asm volatile("" ::"s"(un.seq), "s"(un.n), "s"(un.pos0), "s"(un.row[0]), "s"(un.row[1]),
-               "s"(un.row[2]), "s"(un.row[3]), "s"(un.row[4]), "s"(un.row[5]), "s"(un.row[6]),
-               "s"(un.row[7]));
-  if (u >= n_units) return;
-  int base, uhi;
-  unit_range<SPLIT>(a, un, base, uhi);
-  const int nsplit = (uhi + 1 - base + SPLIT - 1) / SPLIT;
-  if (s >= nsplit) return;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int m16 = lane & 15, kq = lane >> 4;
-  const bf16* Kc = reinterpret_cast<const bf16*>(a.kl.k);
-  const bf16* Vc = reinterpret_cast<const bf16*>(a.kl.v);
-  const int s_lo = base + s * SPLIT;
-  const int s_hi = min(uhi, s_lo + SPLIT - 1);
-  // this wave's blocks: kb(i) = s_lo + (wv + NW i) 64, i < nb
-  const int first = s_lo + wv * 64;
-  const int nb = first > s_hi ? 0 : (s_hi - first) / (NW * 64) + 1;
-  char* ring = lds + wv * (STAGES * SLOT + QBYTES);
-  char* qst = ring + STAGES * SLOT;
-  const attn_bf16x8 zero = {};
-  int qlo[NQT], qhi[NQT];
-  bool qok[NQT];
-  // the query chunks go through LDS like the blocks (a register load would make the
-  // compiler wait for every staged block before the loop); columns without a row stage row
-  // 0's chunk and are zeroed after the read
-#pragma unroll
-  for (int t = 0; t < NQT; ++t) {
-    const int c = t * 16 + m16, z = c >> 2;
-    const int qrow = c < COLS ? unit_row<NZ>(un, z) : -1;
-    const int qpos = un.pos0 + z;
-    qlo[t] = a.is_local ? max(0, qpos - a.window + 1) : 0;
-    qhi[t] = qrow < 0 ? -1 : qpos;
-    qok[t] = qrow >= 0;
-    const bf16* qp = reinterpret_cast<const bf16*>(a.qkv) + (int64_t)(qrow < 0 ? un.row[0] : qrow) * a.ldq +
-                     (g * 4 + (c & 3)) * 64 + kq * 8;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      __builtin_amdgcn_global_load_lds((glb_vptr)(qp + ks * 32), (lds_vptr)(qst + (t * 2 + ks) * 1024),
-                                       16, 0, 0);
-  }
-  // prologue: the first STAGES blocks in flight
-#pragma unroll
-  for (int i = 0; i < STAGES; ++i)
-    if (i < nb)
-      attn_stage_block(Kc, Vc, kv_block_layer(a.kl, a.is_local, a.Hkv, un.seq, g, first + i * NW * 64),
-                       m16, kq, ring + i * SLOT);
-  // the queries landed once at most the prologue's loads are pending
-  attn_bf16x8 qb[NQT][2];
-  if (nb >= STAGES)
-    wait_vmcnt<16 * STAGES>();
-  else
-    wait_vmcnt<0>();
-#pragma unroll
-  for (int t = 0; t < NQT; ++t)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const attn_bf16x8 v = *reinterpret_cast<const attn_bf16x8*>(qst + (t * 2 + ks) * 1024 + lane * 16);
-      qb[t][ks] = qok[t] ? v : zero;
-    }
-  float mrun[NQT], lrun[NQT];
-  attn_f32x4 o[NQT][4];
-#pragma unroll
-  for (int t = 0; t < NQT; ++t) {
-    mrun[t] = -INFINITY;
-    lrun[t] = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) o[t][mt] = attn_f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  const float scale2 = a.scale * 1.4426950408889634f;
-  const int full_lo = a.is_local ? max(0, uhi - a.window + 1) : 0;
-  const int full_hi = un.pos0;
-  for (int i = 0; i < nb; ++i) {
-    const int kb = first + i * NW * 64;
-    const char* slot = ring + (i % STAGES) * SLOT;
-    // block i has landed once at most (blocks in flight after it) * 16 loads are pending
-    if (i + STAGES <= nb)
-      wait_vmcnt<16 * (STAGES - 1)>();
-    else
-      wait_vmcnt<0>();
-    attn_bf16x8 kk[4][2], vv[4][2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        kk[kt][ks] = *reinterpret_cast<const attn_bf16x8*>(slot + (kt * 2 + ks) * 1024 + lane * 16);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-        vv[mt][s2] = *reinterpret_cast<const attn_bf16x8*>(slot + 8192 + (mt * 2 + s2) * 1024 + lane * 16);
-    // the slot is free again once its reads have returned: refill it with block i + STAGES
-    if (i + STAGES < nb) {
-      __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
-      attn_stage_block(Kc, Vc,
-                       kv_block_layer(a.kl, a.is_local, a.Hkv, un.seq, g, kb + STAGES * NW * 64),
-                       m16, kq, ring + (i % STAGES) * SLOT);
-    }
-#pragma unroll
-    for (int t = 0; t < NQT; ++t) {
-      attn_f32x4 sv[4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][0], qb[t][0], acc, 0, 0, 0);
-        sv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kk[kt][1], qb[t][1], acc, 0, 0, 0);
-      }
-      // lane holds keys kb + kperm(kt, 4 kq + j) of query column 16 t + m16
-      float mx = -INFINITY;
-      if (kb >= full_lo && kb + 63 <= full_hi) {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            sv[kt][j] *= scale2;
-            mx = fmaxf(mx, sv[kt][j]);
-          }
-      } else {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int key = kb + attn_kperm(kt, kq * 4 + j);
-            const float v = (key >= qlo[t] && key <= qhi[t]) ? sv[kt][j] * scale2 : -INFINITY;
-            sv[kt][j] = v;
-            mx = fmaxf(mx, v);
-          }
-      }
-      mx = fmaxf(mx, swz_xor16(mx));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(mrun[t], mx);
-      const float muse = mnew == -INFINITY ? 0.f : mnew;
-      const float f = __builtin_amdgcn_exp2f(mrun[t] - muse);
-      mrun[t] = mnew;
-      lrun[t] *= f;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) o[t][mt] *= f;
-      attn_bf16x8 ph[2], pl[2];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float p = __builtin_amdgcn_exp2f(sv[kt][j] - muse);
-          lrun[t] += p;
-          const __bf16 hi = (__bf16)p;
-          ph[kt >> 1][(kt & 1) * 4 + j] = hi;
-          pl[kt >> 1][(kt & 1) * 4 + j] = (__bf16)(p - (float)hi);
-        }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          o[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[mt][s2], ph[s2], o[t][mt], 0, 0, 0);
-          o[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[mt][s2], pl[s2], o[t][mt], 0, 0, 0);
-        }
-    }
-  }
-  // wave merge in LDS (the staging slots are reused once every wave is past its loop)
-  __syncthreads();
-  float* wm = reinterpret_cast<float*>(lds);
-  float* wl = wm + NW * COLS;
-  float* wo = wl + NW * COLS;  // [NW][COLS][65]
-#pragma unroll
-  for (int t = 0; t < NQT; ++t) {
-    float lr = lrun[t];
-    lr += swz_xor16(lr);
-    lr += __shfl_xor(lr, 32, 64);
-    const int c = t * 16 + m16;
-    if (c < COLS) {
-      if (kq == 0) {
-        wm[wv * COLS + c] = mrun[t];
-        wl[wv * COLS + c] = lr;
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wo[(wv * COLS + c) * 65 + mt * 16 + kq * 4 + j] = o[t][mt][j];
-    }
-  }
-  __syncthreads();
-  for (int t = threadIdx.x; t < COLS * 64; t += blockDim.x) {
-    const int hr = t >> 6, d = t & 63;
-    const int row = unit_row<NZ>(un, hr >> 2);
-    if (row < 0) continue;
-    float M = -INFINITY, L = 0.f, O = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w * COLS + hr]);
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float mw = wm[w * COLS + hr];
-        if (mw == -INFINITY) continue;
-        const float f = __builtin_amdgcn_exp2f(mw - M);
-        L += wl[w * COLS + hr] * f;
-        O += wo[(w * COLS + hr) * 65 + d] * f;
-      }
-    }
-    if (nsplit == 1) {
-      const int head = g * 4 + (hr & 3);
-      const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
-      reinterpret_cast<bf16*>(a.out)[(int64_t)row * a.H * 64 + head * 64 + d] =
-          f2bf(rnd<bf16>(O / L) * gate);
-    } else {
-      float* out = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits + s) * COLS + hr) * 66;
-      __hip_atomic_store(out + 2 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (d == 0) {
-        __hip_atomic_store(out, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(out + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  if (nsplit == 1) return;
-  // hand-off to the merging block: as in attn_decode_unit_kernel
   __builtin_amdgcn_s_waitcnt(0);
   __shared__ int s_last;
   __syncthreads();
@@ -1887,72 +1593,7 @@ int launch_norm_rows(const NormArgs& a, int dtype, int max_rows, hipStream_t s) 
 int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s) {
   PULSAR_DISPATCH(dtype, qk_post_kernel, dim3(max_rows, (a.H + a.Hkv + 3) / 4), 256, a);
 }
-// LDS-staged decode attention: (waves, 64-key blocks per wave per split, staged blocks per
-// wave) by layer type; the split of a unit's keys then follows from the key range alone.
-struct AttnLdsCfg {
-  int nw, bpw, stages;
-};
-#ifndef PULSAR_ATTN_VARIANT
-#define PULSAR_ATTN_VARIANT -1
-#endif
-__host__ AttnLdsCfg attn_lds_cfg(bool local, bool long_ctx, int unit_rows) {
-  switch (PULSAR_ATTN_VARIANT) {
-    case 1:
-      if (unit_rows <= 4) return local ? AttnLdsCfg{8, 3, 1} : AttnLdsCfg{8, 2, 1};
-      return local ? AttnLdsCfg{4, 5, 2} : AttnLdsCfg{4, 4, 2};
-    case 2: return local ? AttnLdsCfg{4, 5, 2} : AttnLdsCfg{4, 8, 2};
-    case 3: return local ? AttnLdsCfg{4, 1, 1} : AttnLdsCfg{4, 1, 1};
-    case 4: return local ? AttnLdsCfg{4, 5, 2} : (long_ctx ? AttnLdsCfg{4, 8, 2} : AttnLdsCfg{4, 2, 2});
-    default: return local ? AttnLdsCfg{4, 5, 2} : AttnLdsCfg{4, 4, 2};
-  }
-}
-
-template <int C>
-int launch_attn_lds_cols(const AttnArgs& b, const AttnLdsCfg& c, dim3 grid, hipStream_t s) {
-#define PULSAR_ATTN_LDS(NW, BPW, ST)                                                  \
-  if (c.nw == NW && c.bpw == BPW && c.stages == ST) {                                 \
-    attn_decode_lds_kernel<C, NW, BPW, ST><<<grid, 64 * NW, 0, s>>>(b);               \
-    PULSAR_LAUNCH_CHECK();                                                            \
-    return PULSAR_OK;                                                                 \
-  }
-  PULSAR_ATTN_LDS(4, 5, 2)
-  PULSAR_ATTN_LDS(4, 4, 2)
-#if PULSAR_ATTN_VARIANT != 0
-  if constexpr (C <= 16) {
-    PULSAR_ATTN_LDS(8, 3, 1)
-    PULSAR_ATTN_LDS(8, 2, 1)
-  }
-  PULSAR_ATTN_LDS(4, 8, 2)
-  PULSAR_ATTN_LDS(4, 1, 1)
-  PULSAR_ATTN_LDS(4, 2, 2)
-#endif
-#undef PULSAR_ATTN_LDS
-  return fail(PULSAR_ERR_UNSUPPORTED, "decode attention: no kernel for this split shape");
-}
-
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s) {
-  if (dtype == PULSAR_BF16 && PULSAR_ATTN_VARIANT >= 0) {
-    // keys a unit reads: a 64-aligned range of at most window + rows - 1 (+ 63) keys in the
-    // sliding-window layers, max_ctx (+ 63) in the global ones
-    const int max_ctx = a.max_ctx;
-    const bool local = a.is_local;
-    const AttnLdsCfg c = attn_lds_cfg(local, a.max_splits_unit > kLongCacheSplits, a.unit_rows);
-    const int split = c.nw * c.bpw * 64;
-    int zs = (max_ctx + split - 1) / split;
-    if (local) zs = std::min(zs, (a.window + a.unit_rows - 1 + split - 1) / split + 1);
-    const dim3 grid(a.max_units, a.Hkv, zs);
-    AttnArgs b = a;
-    b.kl.k = a.kv.k[a.layer];
-    b.kl.v = a.kv.v[a.layer];
-    b.kl.lcap = a.kv.lcap;
-    b.kl.max_pages = a.kv.max_pages;
-    if (((a.kv.local_mask >> a.layer) & 1u) != (local ? 1u : 0u))
-      return fail(PULSAR_ERR_INVALID, "decode attention: layer type mismatch");
-    if (a.unit_rows <= 2) return launch_attn_lds_cols<8>(b, c, grid, s);
-    if (a.unit_rows <= 4) return launch_attn_lds_cols<16>(b, c, grid, s);
-    if (a.unit_rows <= kMaxBlock) return launch_attn_lds_cols<32>(b, c, grid, s);
-    return fail(PULSAR_ERR_UNSUPPORTED, "decode attention: at most 8 rows per unit");
-  }
   if (dtype == PULSAR_BF16) {
     // Key split per launch, from the layer type and the engine's context length only (never
     // the batch). Engines whose context needs more than kLongCacheSplits 256-key splits
