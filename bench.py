@@ -257,9 +257,14 @@ def verify_microbench(model, cfg, es, args):
     gemm_flops = {
         "qkv_gate_gemm": 2.0 * R * D * (cfg.qkv_dim + cfg.n_heads),
         "wo_gemm": 2.0 * R * cfg.q_dim * D,
-        "routed_gate_up": 2.0 * D * (R * cfg.top_k * 2 * cfg.d_expert + R * 2 * cfg.d_shared),
-        "routed_down": 2.0 * D * (R * cfg.top_k * cfg.d_expert + R * cfg.d_shared),
+        "routed_gate_up": 2.0 * D * R * cfg.top_k * 2 * cfg.d_expert,
+        "routed_down": 2.0 * D * R * cfg.top_k * cfg.d_expert,
+        "shared_gate_up": 2.0 * D * R * 2 * cfg.d_shared,
+        "shared_down": 2.0 * D * R * cfg.d_shared,
     }
+    for sh, ro in (("shared_gate_up", "routed_gate_up"), ("shared_down", "routed_down")):
+        if not prof.get(sh, (0.0, 0))[1]:  # the shared expert rode in the routed launch
+            gemm_flops[ro] += gemm_flops.pop(sh)
     gemm_mfma = {}
     for c, fl in gemm_flops.items():
         c_ms, c_n = prof.get(c, (0.0, 0))

@@ -175,6 +175,42 @@ __device__ __forceinline__ void stv(bf16* p, const float* v) {
   }
 }
 
+// Address-space pointers of the direct global-to-LDS load builtin.
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) void* glb_vptr;
+
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima), n <= 63.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane l's
+// bytes land at lds + 16 l; `lds` must be the same for the whole wave. Issued as inline
+// assembly so that the compiler neither waits for it before unrelated LDS reads nor counts
+// it: the caller waits with wait_vmcnt (these loads count in vmcnt and complete in order)
+// and publishes the data to the other waves with lds_barrier.
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_vptr)lds)));
+  // one wait state between the M0 write and the load that reads it
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(m0), "v"(g)
+               : "memory", "m0");
+}
+
+// Workgroup barrier for data exchanged through LDS only: s_barrier without the release
+// fence of __syncthreads (which waits for every outstanding global load, including loads
+// still in flight for later steps). The asm statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Elements of T in 16 bytes (the vector width of the op kernels' loads and stores).
 template <typename T>
 constexpr int kVec = 16 / (int)sizeof(T);

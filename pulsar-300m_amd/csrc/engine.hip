@@ -349,7 +349,16 @@ GemmArgs gemm_base(const Engine& e) {
   return g;
 }
 
-constexpr int kWideLogitsRows = 128;
+// Engines whose steps hold kWideHeadRows rows or more (verify blocks, batches of 64+) run
+// the output head in the 128 x 256 LDS tiles of the prefill GEMMs (its 64 MiB of weights
+// read once per 128 rows instead of once per 32); from kWideRows rows (the draft-block
+// mode at batch 256) the decode projections too. Below that the row-tile GEMMs are faster:
+// 128 x 256 tiles leave most CUs idle at a few hundred rows (320-row verify: 3.78 against
+// 5.35 ms with every projection in wide tiles). The two kinds sum K in different orders,
+// so an engine's logits can differ from an engine's on the other side of a threshold by
+// bf16 rounding; engines on the same side agree exactly.
+constexpr int kWideHeadRows = 128;
+constexpr int kWideRows = 1024;
 
 // One pass over a row set (the rows of a step, or of one pulse of a block verify): pulse
 // input, every layer, pulse output and the logits of the rows that need them.
@@ -366,6 +375,8 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
   // routed gate/up GEMM then streams weights and rows without first waiting for each
   // expert's row count (12.2 -> 11.5 us at batch 16; the down GEMM measured no gain)
   const int eager_experts = (int64_t)MR * e.K >= 2 * (int64_t)e.E ? 1 : 0;
+  const bool wide = dt == PULSAR_BF16 && MR >= kWideRows;
+  const bool wide_head = dt == PULSAR_BF16 && MR >= kWideHeadRows;
   if (e.prof_on) {
     // an empty timed group: the fixed cost of an event pair around a kernel launch
     PULSAR_TRY(prof_delay(e, s));
@@ -416,7 +427,8 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     g.ldc2 = e.H;
     g.bias = m.gate_bias[l];
     g.bias_group_stride = e.H;
-    PULSAR_TIMED(PC_QKVG, launch_gemm(g, dt, EPI_QKVG, e.P, MR, s));
+    PULSAR_TIMED(PC_QKVG, wide ? launch_gemm_wide(g, dt, EPI_QKVG, e.P, MR, s)
+                               : launch_gemm(g, dt, EPI_QKVG, e.P, MR, s));
     QKPostArgs qa{};
     qa.ctl = ctl;
     qa.rows = rows;
@@ -472,7 +484,8 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     g.N = D;
     g.row_mode = ROWS_PULSE;
     g.ctl = ctl;
-    PULSAR_TIMED(PC_WO, launch_gemm(g, dt, EPI_RESID, e.P, MR, s));
+    PULSAR_TIMED(PC_WO, wide ? launch_gemm_wide(g, dt, EPI_RESID, e.P, MR, s)
+                             : launch_gemm(g, dt, EPI_RESID, e.P, MR, s));
     RouterArgs ra{};
     ra.ctl = ctl;
     ra.rows = rows;
@@ -511,16 +524,33 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     g.eager_w = eager_experts;
     g.a_rows = MR;
     g.a_rows0 = MR;
-    g.has_g0 = 1;
-    g.K0 = D;
-    g.A0 = e.xn;
-    g.lda0 = D;
-    g.W0 = m.shared_gu[l];
-    g.ldw0 = D;
-    g.C0 = e.act_s;
-    g.ldc0 = e.ds;
-    g.N0 = e.ds;
-    PULSAR_TIMED(PC_ROUTED_GU, launch_gemm(g, dt, EPI_SWIGLU, e.E, MR, s));
+    if (wide) {
+      // wide tiles: the shared expert over all rows, then the routed experts' lists
+      GemmArgs gs = gemm_base(e);
+      gs.A = e.xn;
+      gs.lda = D;
+      gs.W = m.shared_gu[l];
+      gs.ldw = D;
+      gs.C = e.act_s;
+      gs.ldc = e.ds;
+      gs.K = D;
+      gs.N = e.ds;
+      gs.row_mode = ROWS_ALL;
+      gs.ctl = ctl;
+      PULSAR_TIMED(PC_SHARED_GU, launch_gemm_wide(gs, dt, EPI_SWIGLU, 1, MR, s));
+      PULSAR_TIMED(PC_ROUTED_GU, launch_gemm_wide(g, dt, EPI_SWIGLU, e.E, MR, s));
+    } else {
+      g.has_g0 = 1;
+      g.K0 = D;
+      g.A0 = e.xn;
+      g.lda0 = D;
+      g.W0 = m.shared_gu[l];
+      g.ldw0 = D;
+      g.C0 = e.act_s;
+      g.ldc0 = e.ds;
+      g.N0 = e.ds;
+      PULSAR_TIMED(PC_ROUTED_GU, launch_gemm(g, dt, EPI_SWIGLU, e.E, MR, s));
+    }
     // shared + routed down projections
     g = gemm_base(e);
     g.A = e.act_r;
@@ -538,7 +568,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     g.list_stride = lstride;
     g.a_div = 1;
     g.ctl = ctl;
-    if (e.ds == e.de || e.ds == 2 * e.de) {
+    if (!wide && (e.ds == e.de || e.ds == 2 * e.de)) {
       g.has_g0 = 1;
       g.K0 = e.ds;
       g.A0 = e.act_s;
@@ -550,8 +580,10 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
       g.N0 = D;
       PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
     } else {
-      // the fused launch takes K0 = K or 2K for the shared group; other widths: two launches
-      PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
+      // the fused launch takes K0 = K or 2K for the shared group; other widths and wide
+      // tiles: two launches
+      PULSAR_TIMED(PC_ROUTED_DOWN, wide ? launch_gemm_wide(g, dt, EPI_STORE, e.E, MR, s)
+                                        : launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
       GemmArgs gs = gemm_base(e);
       gs.A = e.act_s;
       gs.lda = e.ds;
@@ -563,7 +595,8 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
       gs.N = D;
       gs.row_mode = ROWS_ALL;
       gs.ctl = ctl;
-      PULSAR_TIMED(PC_SHARED_DOWN, launch_gemm(gs, dt, EPI_STORE, 1, MR, s));
+      PULSAR_TIMED(PC_SHARED_DOWN, wide ? launch_gemm_wide(gs, dt, EPI_STORE, 1, MR, s)
+                                        : launch_gemm(gs, dt, EPI_STORE, 1, MR, s));
     }
     CombineArgs ca{};
     ca.ctl = ctl;
@@ -606,12 +639,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
   g.row_mode = ROWS_LOGITS;
   g.ctl = ctl;
   g.softcap = m.softcap;
-  // Engines whose steps hold kWideLogitsRows rows or more (verify blocks, batches of 64+)
-  // compute the output head in 128 x 256 tiles staged through LDS (the head's 64 MiB read
-  // once per 128 rows instead of once per 32); below that the weight-streaming row tiles.
-  // The two sum K in different orders, so logits can differ in the last fp32 bit (before
-  // their bf16 rounding) between engines on either side of the threshold.
-  if (dt == PULSAR_BF16 && MR >= kWideLogitsRows)
+  if (wide_head)
     PULSAR_TIMED(PC_LMHEAD, launch_gemm_wide(g, dt, EPI_LOGITS, 1, MR, s));
   else
     PULSAR_TIMED(PC_LMHEAD, launch_gemm(g, dt, EPI_LOGITS, 1, MR, s));

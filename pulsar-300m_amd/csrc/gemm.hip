@@ -474,21 +474,25 @@ __device__ __forceinline__ void epilogue4(const GemmArgs& g, int epi, int group,
 // LDS-staged tiles for wide row sets: a workgroup of 4 waves owns 128 rows x 256 output
 // columns (SwiGLU: 128 gate columns and their 128 up-projection twins); wave (wr, wc)
 // computes 64 rows x 128 columns as 4 x 8 MFMA tiles (128 accumulators). Per 32-wide k
-// step the workgroup stages the A tile (gathered rows, written in MFMA lane order) and
-// 16 weight tiles (1 KB each, stored in lane order) in LDS, double-buffered: the next
-// step's global loads are in flight while this step's 32 MFMAs per wave run, and one
-// barrier per step separates the buffers. Each staged byte feeds 2 waves from LDS, and
-// each wave's 12 fragment reads feed 32 products. The weights go in as the A operand and
-// the rows as B, so a lane ends with 4 consecutive output columns of its own row: 8-byte
-// epilogue loads and stores, and the C row is an entry the lane loads itself. Gathered
-// expert rows cost nothing extra: each staging thread fetches 16 bytes of its own row.
+// step the workgroup stages the A tile (8 row tiles of 16 rows, gathered rows in MFMA lane
+// order) and 16 weight tiles (1 KB each, stored in lane order) in LDS with direct
+// global-to-LDS loads (16 bytes per lane, no staging registers): a wave's load instruction
+// fills one 1 KB tile, lane l at +16 l, which is the lane's own MFMA operand. A ring of
+// kWideStages buffers keeps kWideStages - 1 k steps in flight while one is computed; one
+// barrier per step both publishes the step's tiles to all waves and frees the buffer the
+// next load overwrites. Each staged byte feeds 2 waves from LDS, and each wave's 12
+// fragment reads feed 32 products. The weights go in as the A operand and the rows as B,
+// so a lane ends with 4 consecutive output columns of its own row: 8-byte epilogue loads
+// and stores, and the C row is an entry the lane loads itself.
 constexpr int kTileRows = 128;
+constexpr int kWideStages = 3;
 
 template <int EPI, int MODE>
 __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
-  __shared__ bf16x8_t sA[2][8][64];   // [buffer][row tile][lane]
-  __shared__ bf16x8_t sW[2][16][64];  // [buffer][column tile][lane]
+  constexpr int S = kWideStages;
+  __shared__ bf16x8_t sA[S][8][64];   // [buffer][row tile][lane]
+  __shared__ bf16x8_t sW[S][16][64];  // [buffer][column tile][lane]
   const int group = (int)blockIdx.y + g.group_offset;
   const int N = g.N;
   const int KT = g.K / 32;
@@ -516,21 +520,20 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   const bf16* A = reinterpret_cast<const bf16*>(g.A);
   const bf16* W = reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
 
-  // staging: A chunks q = tid + 256 h (h < 2): row q / 4, k chunk q % 4; weight chunks
-  // q = tid + 256 h (h < 4): tile q / 64, lane q % 64
+  // staging: wave wv fills row tiles wv + 4 h (h < 2) and weight tiles wv + 4 h (h < 4);
+  // lane l of a row tile's load carries row 16 t + (l & 15), k chunk l >> 4
   const bf16* ga[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int r = (tid >> 2) + 64 * h;
+    const int r = (wv + 4 * h) * 16 + m16;
     const int i = min(r_wg + r, cnt - 1);
     const int e = entry_load<MODE>(g, group, i);
-    ga[h] = A + (int64_t)a_row_of<MODE>(g, group, e) * g.lda + (tid & 3) * 8;
+    ga[h] = A + (int64_t)a_row_of<MODE>(g, group, e) * g.lda + kq * 8;
   }
-  const int sa_tile = (tid >> 2) >> 4, sa_lane = (tid & 3) * 16 + ((tid >> 2) & 15);
   const bf16* gw[4];
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
-    const int c = (tid >> 6) + 4 * h;
+    const int c = wv + 4 * h;
     int ct;
     if constexpr (kPair)
       ct = c < 8 ? ct_wg + c : N / 16 + ct_wg + (c - 8);
@@ -538,18 +541,12 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
       ct = min(ct_wg + c, N / 16 - 1);  // tiles past N re-read the last one (never stored)
     gw[h] = W + ((int64_t)ct * KT * 64 + lane) * 8;
   }
-  bf16x8_t ra[2], rw[4];
-  auto fetch = [&](int kt) {
+  // k step kt into ring buffer b: 6 loads per wave, counted by vmcnt
+  auto fetch = [&](int kt, int b) {
 #pragma unroll
-    for (int h = 0; h < 4; ++h) rw[h] = load_bf16x8(gw[h] + (int64_t)kt * 512);
+    for (int h = 0; h < 4; ++h) load_lds16(gw[h] + (int64_t)kt * 512, &sW[b][wv + 4 * h][0]);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) ra[h] = load_bf16x8(ga[h] + kt * 32);
-  };
-  auto stage = [&](int buf) {
-#pragma unroll
-    for (int h = 0; h < 4; ++h) sW[buf][(tid >> 6) + 4 * h][lane] = rw[h];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) sA[buf][sa_tile + 4 * h][sa_lane] = ra[h];
+    for (int h = 0; h < 2; ++h) load_lds16(ga[h] + kt * 32, &sA[b][wv + 4 * h][0]);
   };
   // this wave's column tiles in the staged set: 8 of 16 (SwiGLU: 4 gate + their 4 up)
   int wcol[8];
@@ -561,12 +558,20 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  fetch(0);
-  stage(0);
-  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < S - 1; ++k)
+    if (k < KT) fetch(k, k);
+  int buf = 0;
   for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) fetch(kt + 1);
+    // this wave's loads of step kt are done once at most the S - 2 younger steps' loads
+    // are outstanding (all of them near the end); the barrier then makes every wave's
+    // tiles of step kt visible and retires step kt - 1, whose buffer the next fetch fills
+    if (kt + S - 2 < KT)
+      wait_vmcnt<6 * (S - 2)>();
+    else
+      wait_vmcnt<0>();
+    lds_barrier();
+    if (kt + S - 1 < KT) fetch(kt + S - 1, buf == 0 ? S - 1 : buf - 1);
     bf16x8_t fa[4], fw[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) fa[i] = sA[buf][wr * 4 + i][lane];
@@ -577,8 +582,7 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[j], fa[i], acc[i][j], 0, 0, 0);
-    if (kt + 1 < KT) stage(buf ^ 1);
-    __syncthreads();
+    buf = buf == S - 1 ? 0 : buf + 1;
   }
   // lane holds columns 4 kq + e of column tile wcol[j] for row m16 of row tile wr * 4 + i
 #pragma unroll

@@ -34,8 +34,8 @@ def _alone(eng, prompts, i, sub, **kw):
 def _spec_plain_single(model, prompts, n_new, singles, sub=1):
     """Greedy self-speculative == plain over the batch, and sequences `singles` decode the same
     in a sub-batch of `sub` prompts (1: alone). Batches of 64+ sequences hold 128+ rows per
-    step and compute the output head in 128-row tiles, so they are compared with sub-batches
-    on the same side of that threshold."""
+    step and run the output head in 128-row tiles (1024+ rows: the projections too), so
+    they are compared with sub-batches on the same side of those thresholds."""
     from pulsar_engine.engine import PulsarInferenceEngine
 
     eng = PulsarInferenceEngine(model)
@@ -129,7 +129,9 @@ def test_c5_batch_256_draft6_batch_equals_single(full_state, c5_model):
 
     cfg = full_state[0]
     prompts = [W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size).tolist() for b in range(256)]
-    out = _block_batch_single(c5_model[1], prompts, 512, 6, singles=[0, 255], sub=64)
+    # 256 x 7 rows per step run the projections in wide tiles from 1024 rows: a sub-batch
+    # of 160 (1120 rows) is on the same side
+    out = _block_batch_single(c5_model[1], prompts, 512, 6, singles=[0, 255], sub=160)
     print("c5 draft-block first tokens", [s[:4] for s in out[:4]])
 
 

@@ -1,6 +1,8 @@
 """GPU: block verify over long pre-filled caches against the oracle, at the verify
-microbenchmark's shape (64 sequences x 8192 cached positions) and the long-context shape
-(4 sequences x 32768 cached positions, YaRN in the global layers, 513 pages per sequence).
+microbenchmark's shape (64 sequences x 8192 cached positions), the long-context shape
+(4 sequences x 32768 cached positions, YaRN in the global layers, 513 pages per sequence)
+and a wide one (224 sequences x 1024 positions: 1120 rows per pass, so the projections
+run in the 128 x 256 LDS tiles).
 
 The engine's synthetic cache (pulsar_engine_fill_kv: every key/value element ~ N(0,1) from
 a counter-based generator) is regenerated on the CPU for the compared sequences
@@ -21,7 +23,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.timeout(900)
-@pytest.mark.parametrize("B,ctx,check", [(64, 8192, [0, 63]), (4, 32768, [0, 3])])
+@pytest.mark.parametrize("B,ctx,check", [(64, 8192, [0, 63]), (4, 32768, [0, 3]),
+                                         (224, 1024, [0, 223])])
 def test_verify_over_prefilled_cache_matches_oracle(models, full_state, B, ctx, check):
     from oracle import pulsar_ref as R
     from pulsar_engine import weights as W
