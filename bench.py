@@ -485,6 +485,98 @@ def cpu_baseline(cfg, state, c2_prompts, c2_new, temperature, top_p, rp, c1_prom
     }
 
 
+def op_surface_bench(cfg, reps: int = 20) -> dict:
+    """Secondary figure for the pulsar_cuda op surface (the drop-in for src/model.py's fused
+    functions): each forward op at a training micro-batch of 8 x 2048 tokens in bf16,
+    HIP-event timed on the current stream over `reps` graph-replayed calls after 3 warm
+    ones, with its algorithmic bytes (every input read once, every output written once)
+    against the HBM peak."""
+    import torch
+
+    import pulsar_cuda as pc
+
+    dev, bf = "cuda", torch.bfloat16
+    B, T, D, H, Hkv = 8, 2048, cfg.d_model, cfg.n_heads, cfg.n_kv_heads
+    E, K, ds = cfg.n_routed_experts, cfg.top_k, cfg.d_shared
+    N = B * T
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rnd(*shape, dtype=bf):
+        return torch.randn(*shape, generator=g, device=dev).to(dtype)
+
+    x = rnd(B, T, D)
+    w = torch.rand(D, generator=g, device=dev) + 0.5
+    qkv = rnd(B, T, (H + 2 * Hkv) * 64)
+    q = qkv[..., : H * 64].view(B, T, H, 64).transpose(1, 2)
+    wq = torch.rand(H, 64, generator=g, device=dev) + 0.5
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2, device=dev).float() / 64))
+    f = torch.outer(torch.arange(T, device=dev).float(), inv)
+    cos, sin = f.cos().contiguous(), f.sin().contiguous()
+    attn = rnd(B, H, T, 64)
+    gl = rnd(B, T, H, dtype=torch.float32)
+    cw = rnd(D, 4, dtype=torch.float32) * 0.3
+    gu = rnd(N, 2 * ds)
+    logits = rnd(N, E) * 2
+    bias = torch.zeros(E, device=dev)
+    idx, tw, _, _ = pc.moe_router_topk_forward(logits, bias, K, 1e-3)
+    flat = idx.reshape(-1).contiguous()
+    C = int(-(-N * K * 1.25 // E))
+    slots, counts = pc.moe_slots_from_order(flat, torch.argsort(flat, stable=True), E, C)
+    slots = slots.view(N, K).contiguous()
+    xr = x.view(N, D)
+    kept = int((slots >= 0).sum())
+    eo = rnd(E, C, D)
+    sh = rnd(N, D)
+    es = 2
+    ops = {
+        "rmsnorm": (lambda: pc.rmsnorm_forward(x, w, 1e-6), 2 * N * D * es + N * 4 + D * 4),
+        "qk_rmsnorm_rope": (lambda: pc.qk_rmsnorm_rope_forward(q, wq, cos, sin, T, 1e-6),
+                            2 * N * H * 64 * es + N * H * 4 + 2 * T * 32 * 4 + H * 64 * 4),
+        "fused_attn_gate": (lambda: pc.fused_attn_gate_forward(attn, gl),
+                            2 * N * H * 64 * es + N * H * 4),
+        "causal_conv1d_k4": (lambda: pc.causal_depthwise_conv1d_k4_forward(x, cw),
+                             2 * N * D * es + D * 16),
+        "fused_swiglu": (lambda: pc.fused_swiglu_forward(gu, ds), 3 * N * ds * es),
+        "moe_router_topk": (lambda: pc.moe_router_topk_forward(logits, bias, K, 1e-3),
+                            N * E * es + N * K * (8 + 2)),
+        "moe_dispatch": (lambda: pc.moe_dispatch_forward(xr, idx, slots, E, C, counts),
+                         N * D * es + E * C * D * es + N * K * 12),
+        "moe_combine": (lambda: pc.moe_combine_forward(eo, idx, tw, slots, sh),
+                        kept * D * es + 2 * N * D * es + N * K * 14),
+    }
+    out = {}
+    for name, (fn, nbytes) in ops.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        # device time: `reps` calls captured in one graph and replayed, so the host's
+        # per-call cost (argument checks, output allocation) is not in the figure;
+        # `us_eager` is the same calls launched one by one
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        graph.replay()
+        t1.record()
+        t1.synchronize()
+        us = t0.elapsed_time(t1) / reps * 1e3
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        t1.synchronize()
+        us_eager = t0.elapsed_time(t1) / reps * 1e3
+        del graph
+        out[name] = {"us": round(us, 2), "us_eager": round(us_eager, 2), "bytes": int(nbytes),
+                     "GB_per_s": round(nbytes / us / 1e3, 1),
+                     "hbm_frac": round(nbytes / (us * 1e-6) / HBM_PEAK, 4)}
+    return {"workload": f"bf16, {B} x {T} tokens, d_model {D}, {H} heads of 64, {E} experts "
+                        f"top-{K} (capacity {C}), shared d_ff {ds}", "ops": out}
+
+
 def kv_footprint(cfg) -> dict:
     """KV-cache bytes at batch 1 in bf16 for 1k-32k contexts: the engine's allocation beside the
     reference's analytic unified-cache figure (src/infer.py:834-846)."""
@@ -564,6 +656,7 @@ def main() -> int:
     ap.add_argument("--draft-len", type=int, default=4,
                     help="draft length of the draft-block run (0 skips it)")
     ap.add_argument("--no-verify", action="store_true", help="skip the verify microbenchmark")
+    ap.add_argument("--no-ops", action="store_true", help="skip the op-surface figures")
     ap.add_argument("--only", choices=("c4", "c5"),
                     help="run only that workload, unprofiled (kernel traces)")
     ap.add_argument("--verify-only", action="store_true",
@@ -755,6 +848,10 @@ def main() -> int:
         log(f"c1: {c1['value']} tokens/s")
     c4 = None if args.no_c4 else run_c4(model, cfg, args)
     c5 = None if args.no_c5 else run_c5(cfg, state, args)
+    ops = None
+    if not args.no_ops:
+        ops = op_surface_bench(cfg)
+        log(f"op surface: {json.dumps(ops)}")
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, state, prompts, args.cpu_new_tokens, args.temperature,
@@ -797,6 +894,7 @@ def main() -> int:
         "c4": c4,
         "c5": c5,
         "kv_cache_batch1_bf16": kv_footprint(cfg),
+        "op_surface": ops,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -101,6 +101,19 @@ int pulsar_moe_router_topk_forward(const void* logits, int logits_dtype, const f
                                    float* probs_mean, int64_t N, int64_t E, int64_t K,
                                    float z_loss_weight, hipStream_t stream);
 
+/* The same with a caller workspace of pulsar_moe_router_workspace_bytes(N, E) bytes (device
+ * memory, any contents): the statistics are then summed per workgroup of 128 tokens inside
+ * the top-k launch and the partials merged in workgroup order (deterministic), instead of
+ * one workgroup reading every token again. Same results up to the summation order of the
+ * statistics; the indices and weights are identical. The Python op surface uses this entry.
+ * pulsar_moe_router_workspace_bytes returns -1 for E outside [1, 32] or N < 0. */
+int64_t pulsar_moe_router_workspace_bytes(int64_t N, int64_t E);
+int pulsar_moe_router_topk_forward_ws(const void* logits, int logits_dtype, const float* bias,
+                                      int64_t* topk_idx, uint16_t* topk_w_bf16, float* z_loss,
+                                      float* probs_mean, int64_t N, int64_t E, int64_t K,
+                                      float z_loss_weight, float* workspace,
+                                      hipStream_t stream);
+
 /* moe_dispatch_forward(x, topk_idx, token_to_slot, E, C, expert_counts) -> [E,C,D]
  * Replaces csrc/pulsar_cuda.cpp:213-215 / csrc/kernels.cu:1548-1605.
  * Slots >= count[e] (or all unused slots when expert_counts is NULL) are zeroed. */

@@ -231,59 +231,84 @@ __global__ void __launch_bounds__(256) combine_bwd_kernel(
 //       + dpm_e s_e (1 - s_e) / N                               (probs_mean)
 //   d_l = g - mean(g)                                           (centring)
 // ---------------------------------------------------------------------------
-template <typename L>
+// EM (16 or 32) >= E register slots in unrolled loops: every register-array index is a
+// compile-time constant (runtime indices would move the arrays to scratch memory).
+template <typename L, int EM>
 __global__ void router_bwd_kernel(const uint16_t* __restrict__ dtw, const L* __restrict__ logits,
                                   const int64_t* __restrict__ idx, L* __restrict__ dl,
                                   float zw, const float* __restrict__ dz,
                                   const float* __restrict__ dpm, int64_t N, int E, int K) {
   const int64_t tok = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (tok >= N) return;
-  float c[32], s[32], g[32];
+  float c[EM], s[EM], g[EM];
   float mean = 0.f;
-  for (int e = 0; e < E; ++e) {
-    c[e] = to_f(logits[tok * E + e]);
-    mean += c[e];
+#pragma unroll
+  for (int e = 0; e < EM; ++e) {
+    c[e] = e < E ? to_f(logits[tok * E + e]) : 0.f;
+    if (e < E) mean += c[e];
   }
   mean /= (float)E;
   float mx = -INFINITY;
-  for (int e = 0; e < E; ++e) {
+#pragma unroll
+  for (int e = 0; e < EM; ++e) {
     c[e] -= mean;
     s[e] = sigmoidf_(c[e]);
-    mx = fmaxf(mx, c[e]);
+    if (e < E) mx = fmaxf(mx, c[e]);
     g[e] = 0.f;
   }
   const float zeff = zw * (dz ? dz[0] : 1.0f);
   if (zeff > 0.f) {
     float se = 0.f;
-    for (int e = 0; e < E; ++e) se += expf(c[e] - mx);
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+      if (e < E) se += expf(c[e] - mx);
     se = fmaxf(se, 1e-20f);
     const float lse = mx + logf(se);
     const float f = 2.0f * zeff * lse / (float)N;
-    for (int e = 0; e < E; ++e) g[e] = f * expf(c[e] - mx) / se;
+#pragma unroll
+    for (int e = 0; e < EM; ++e) g[e] = f * expf(c[e] - mx) / se;
   }
   float den = 1e-6f, sdu = 0.f;
   int ek[8];
-  float d[8];
-  for (int k = 0; k < K; ++k) {
+  float d[8], us[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    ek[k] = -1;
+    d[k] = us[k] = 0.f;
+    if (k >= K) continue;
     ek[k] = (int)idx[tok * K + k];
     d[k] = bf2f(bf16{dtw[tok * K + k]});
-    const float u = (ek[k] >= 0 && ek[k] < E) ? s[ek[k]] : 0.f;
+    float u = 0.f;
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+      if (e < E && e == ek[k]) u = s[e];
+    us[k] = u;
     den += u;
     sdu += d[k] * u;
   }
   const float dbar = sdu / den;
-  for (int k = 0; k < K; ++k) {
-    if (ek[k] < 0 || ek[k] >= E) continue;
-    const float u = s[ek[k]];
-    g[ek[k]] += (d[k] - dbar) / den * u * (1.0f - u);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k >= K) continue;
+    const float u = us[k];
+    const float add = (d[k] - dbar) / den * u * (1.0f - u);
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+      if (e < E && e == ek[k]) g[e] += add;
   }
   if (dpm) {
-    for (int e = 0; e < E; ++e) g[e] += dpm[e] / (float)N * s[e] * (1.0f - s[e]);
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+      if (e < E) g[e] += dpm[e] / (float)N * s[e] * (1.0f - s[e]);
   }
   float gm = 0.f;
-  for (int e = 0; e < E; ++e) gm += g[e];
+#pragma unroll
+  for (int e = 0; e < EM; ++e)
+    if (e < E) gm += g[e];
   gm /= (float)E;
-  for (int e = 0; e < E; ++e) dl[tok * E + e] = from_f<L>(g[e] - gm);
+#pragma unroll
+  for (int e = 0; e < EM; ++e)
+    if (e < E) dl[tok * E + e] = from_f<L>(g[e] - gm);
 }
 
 // ---------------------------------------------------------------------------
@@ -465,9 +490,14 @@ int pulsar_moe_router_topk_backward(const uint16_t* d_topk_w_bf16, const void* l
   if (N == 0) return PULSAR_OK;
   return dispatch_dtype(logits_dtype, [&](auto tag) {
     using L = decltype(tag);
-    router_bwd_kernel<L><<<blocks_for(N, 128), 128, 0, stream>>>(
-        d_topk_w_bf16, (const L*)logits, topk_idx, (L*)d_logits, z_loss_weight, d_z_loss,
-        d_probs_mean, N, (int)E, (int)K);
+    if (E <= 16)
+      router_bwd_kernel<L, 16><<<blocks_for(N, 128), 128, 0, stream>>>(
+          d_topk_w_bf16, (const L*)logits, topk_idx, (L*)d_logits, z_loss_weight, d_z_loss,
+          d_probs_mean, N, (int)E, (int)K);
+    else
+      router_bwd_kernel<L, 32><<<blocks_for(N, 128), 128, 0, stream>>>(
+          d_topk_w_bf16, (const L*)logits, topk_idx, (L*)d_logits, z_loss_weight, d_z_loss,
+          d_probs_mean, N, (int)E, (int)K);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   });

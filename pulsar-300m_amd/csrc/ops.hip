@@ -3,7 +3,9 @@
 // Each kernel is one pass over its tensors with 128-bit loads where the row length
 // allows; reductions are wave64 shuffles. Every entry validates shapes on the host and
 // returns a status code instead of throwing.
+#include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "common.h"
 
@@ -267,27 +269,48 @@ __global__ void attn_gate_vec_kernel(const T* __restrict__ a, const float* __res
   stv<V>(out + idx * V, v);
 }
 
+// Thread = kVec<T> channels of one sequence over kConvTokens consecutive tokens: the three
+// previous rows ride along in registers, so each row of x is read once and the channels'
+// weights once per thread.
+constexpr int kConvTokens = 16;
 template <typename T>
-__global__ void conv_k4_vec_kernel(const T* __restrict__ x, const float* __restrict__ w,
-                                   T* __restrict__ y, int64_t T_, int64_t D, int64_t total) {
+__global__ void __launch_bounds__(256) conv_k4_vec_kernel(const T* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          T* __restrict__ y, int64_t B,
+                                                          int64_t T_, int64_t D) {
   constexpr int V = kVec<T>;
-  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
-  if (i0 >= total) return;
-  const int64_t d = i0 % D;
-  const int64_t t = (i0 / D) % T_;
-  float x0[V], x1[V], x2[V], x3[V], wd[4 * V], o[V];
-  ldv<V>(x + i0, x0);
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nc = D / V, ntc = (T_ + kConvTokens - 1) / kConvTokens;
+  const int64_t cv = idx % nc, rest = idx / nc;
+  const int64_t tc = rest % ntc, b = rest / ntc;
+  if (b >= B) return;
+  const int64_t d0 = cv * V, t0 = tc * kConvTokens;
+  const T* xb = x + b * T_ * D + d0;
+  T* yb = y + b * T_ * D + d0;
+  float wd[4 * V], h1[V], h2[V], h3[V], x0[kConvTokens][V], o[V];
+  ldv<4 * V>(w + d0 * 4, wd);
 #pragma unroll
-  for (int j = 0; j < V; ++j) x1[j] = x2[j] = x3[j] = 0.f;
-  if (t >= 1) ldv<V>(x + i0 - D, x1);
-  if (t >= 2) ldv<V>(x + i0 - 2 * D, x2);
-  if (t >= 3) ldv<V>(x + i0 - 3 * D, x3);
-  ldv<4 * V>(w + d * 4, wd);
+  for (int j = 0; j < V; ++j) h1[j] = h2[j] = h3[j] = 0.f;
+  if (t0 >= 1) ldv<V>(xb + (t0 - 1) * D, h1);
+  if (t0 >= 2) ldv<V>(xb + (t0 - 2) * D, h2);
+  if (t0 >= 3) ldv<V>(xb + (t0 - 3) * D, h3);
 #pragma unroll
-  for (int j = 0; j < V; ++j) {
-    o[j] = rnd<T>(x0[j] + conv4(wd + 4 * j, x0[j], x1[j], x2[j], x3[j]));
+  for (int i = 0; i < kConvTokens; ++i)
+    if (t0 + i < T_) ldv<V>(xb + (t0 + i) * D, x0[i]);
+#pragma unroll
+  for (int i = 0; i < kConvTokens; ++i) {
+    if (t0 + i >= T_) break;
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      o[j] = rnd<T>(x0[i][j] + conv4(wd + 4 * j, x0[i][j], h1[j], h2[j], h3[j]));
+    stv<V>(yb + (t0 + i) * D, o);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      h3[j] = h2[j];
+      h2[j] = h1[j];
+      h1[j] = x0[i][j];
+    }
   }
-  stv<V>(y + i0, o);
 }
 
 template <typename T>
@@ -306,91 +329,196 @@ __global__ void swiglu_vec_kernel(const T* __restrict__ gu, T* __restrict__ out,
 }
 
 // ---------------------------------------------------------------------------
-// Router top-k: one lane per token. Scores in registers (E <= 32).
+// Router top-k: one lane per token. Scores in registers: EM (16 or 32) >= E slots in
+// unrolled loops, so every register-array index is a compile-time constant (a runtime index
+// would move the arrays to scratch memory).
 // ---------------------------------------------------------------------------
-template <typename L>
-__device__ __forceinline__ void router_scores(const L* lt, const float* bias, int E, float* c,
-                                              float* s, float* b) {
-  float sum = 0.f;
-  for (int e = 0; e < E; ++e) {
-    c[e] = to_f(lt[e]);
-    sum += c[e];
-  }
-  const float mean = sum / (float)E;
-  for (int e = 0; e < E; ++e) {
-    c[e] = c[e] - mean;
-    s[e] = sigmoidf_(c[e]);
-    b[e] = s[e] + bias[e];
+// One token's logits into c[0..EM) (zero past E): 16-byte loads when VEC (rows a multiple
+// of 16 bytes, 16-byte aligned), element loads otherwise.
+template <typename L, int EM, bool VEC>
+__device__ __forceinline__ void router_row(const L* lt, int E, float* c) {
+  if constexpr (VEC) {
+    constexpr int V = kVec<L>;
+#pragma unroll
+    for (int q = 0; q < EM / V; ++q) {
+      if (q * V < E) {
+        ldv<V>(lt + q * V, c + q * V);
+      } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) c[q * V + j] = 0.f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EM; ++e) c[e] = e < E ? to_f(lt[e]) : 0.f;
   }
 }
 
-template <typename L>
-__global__ void router_topk_kernel(const L* __restrict__ logits, const float* __restrict__ bias,
-                                   int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out,
-                                   int64_t N, int E, int K) {
+// Centred logits c[e] = l[e] - mean (mean summed in expert order, as the reference kernel).
+template <typename L, int EM, bool VEC>
+__device__ __forceinline__ void router_centred(const L* lt, int E, float* c) {
+  router_row<L, EM, VEC>(lt, E, c);
+  float sum = 0.f;
+#pragma unroll
+  for (int e = 0; e < EM; ++e)
+    if (e < E) sum += c[e];
+  const float mean = sum / (float)E;
+#pragma unroll
+  for (int e = 0; e < EM; ++e) c[e] -= mean;
+}
+
+// PART: the workgroup also sums its tokens' E + 1 statistics (each expert's score, the
+// squared logsumexp) in a fixed order and writes them to part[blockIdx.x][0..E].
+constexpr int kRouterTopkThreads = 128;
+template <typename L, int EM, bool VEC, bool PART>
+__global__ void __launch_bounds__(kRouterTopkThreads) router_topk_kernel(
+    const L* __restrict__ logits, const float* __restrict__ bias, int64_t* __restrict__ idx_out,
+    uint16_t* __restrict__ w_out, float* __restrict__ part, int64_t N, int E, int K) {
   const int64_t tok = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (tok >= N) return;
-  float c[32], s[32], b[32];
-  router_scores(logits + tok * E, bias, E, c, s, b);
-  int bi[8];
-  float bv[8];
-  for (int k = 0; k < K; ++k) {
-    bi[k] = -1;
-    bv[k] = -INFINITY;
+  const bool valid = tok < N;
+  if (!PART && !valid) return;
+  float c[EM], s[EM], b[EM];
+  router_centred<L, EM, VEC>(logits + (valid ? tok : N - 1) * E, E, c);
+#pragma unroll
+  for (int e = 0; e < EM; ++e) {
+    s[e] = e < E ? sigmoidf_(c[e]) : 0.f;
+    b[e] = e < E ? s[e] + bias[e] : -INFINITY;
   }
-  for (int e = 0; e < E; ++e) {
-    const float v = b[e];
-    if (v > bv[K - 1]) {
-      int p = K - 1;
-      while (p > 0 && v > bv[p - 1]) {
-        bv[p] = bv[p - 1];
-        bi[p] = bi[p - 1];
-        --p;
-      }
-      bv[p] = v;
-      bi[p] = e;
+  if constexpr (PART) {
+    __shared__ float red[kRouterTopkThreads / 64][EM + 1];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+      if (e < E) mx = fmaxf(mx, c[e]);
+    float se = 0.f;
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+      if (e < E) se += expf(c[e] - mx);
+    const float lse = mx + logf(se);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int e = 0; e <= EM; ++e) {
+      const float v = wave_sum(valid ? (e < EM ? s[e] : lse * lse) : 0.f);
+      if (lane == 0) red[w][e] = v;
     }
+    __syncthreads();
+    const int i = threadIdx.x;
+    if (i < E || i == EM) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < kRouterTopkThreads / 64; ++k) v += red[k][i];
+      part[(int64_t)blockIdx.x * (EM + 1) + i] = v;
+    }
+    if (!valid) return;
+  }
+  // K rounds of argmax over the experts not taken yet, ties to the lower index: the order
+  // and tie rule of the reference's insertion top-k with strict '>' (csrc/kernels.cu:2181-2200)
+  int sel[8];
+  float sv[8];
+  uint32_t taken = 0u;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    sel[k] = 0;
+    sv[k] = 0.f;
+    if (k >= K) continue;
+    int bi = -1;
+    float best = -INFINITY, bs = 0.f;
+#pragma unroll
+    for (int e = 0; e < EM; ++e) {
+      const bool free = e < E && !((taken >> e) & 1u);
+      if (free && (bi < 0 || b[e] > best)) {
+        bi = e;
+        best = b[e];
+        bs = s[e];
+      }
+    }
+    taken |= 1u << bi;
+    sel[k] = bi;
+    sv[k] = bs;
   }
   float tot = 0.f;
-  for (int k = 0; k < K; ++k) tot += s[bi[k]];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < K) tot += sv[k];
   tot += 1e-6f;
-  for (int k = 0; k < K; ++k) {
-    idx_out[tok * K + k] = bi[k];
-    w_out[tok * K + k] = f2bf(s[bi[k]] / tot).u;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k >= K) continue;
+    idx_out[tok * K + k] = sel[k];
+    w_out[tok * K + k] = f2bf(sv[k] / tot).u;
   }
 }
 
-// Deterministic z-loss and probs_mean: block e < E sums expert e's score over all tokens,
-// block E the squared logsumexp; each in a fixed order (threads stride the tokens, then one
-// block reduction), so the statistics do not depend on scheduling.
-template <typename L>
-__global__ void __launch_bounds__(256) router_stats_kernel(const L* __restrict__ logits,
-                                                           const float* __restrict__ bias,
-                                                           float* __restrict__ z_loss,
-                                                           float* __restrict__ probs_mean,
-                                                           int64_t N, int E, float zw) {
-  __shared__ float red[16];
-  const int target = blockIdx.x;
-  float c[32], s[32], b[32];
-  float acc = 0.f;
-  for (int64_t t = threadIdx.x; t < N; t += blockDim.x) {
-    router_scores(logits + t * E, bias, E, c, s, b);
-    if (target < E) {
-      acc += s[target];
-      continue;
-    }
-    float mx = -INFINITY;
-    for (int e = 0; e < E; ++e) mx = fmaxf(mx, c[e]);
-    float se = 0.f;
-    for (int e = 0; e < E; ++e) se += expf(c[e] - mx);
-    const float lse = mx + logf(se);
-    acc += lse * lse;
-  }
+// The workgroups' partial statistics summed in workgroup order (one thread per statistic).
+template <int EM>
+__global__ void router_stats_merge_kernel(const float* __restrict__ part, int nblk,
+                                          float* __restrict__ z_loss,
+                                          float* __restrict__ probs_mean, int64_t N, int E,
+                                          float zw) {
+  const int i = threadIdx.x;
+  if (i > EM || (i < EM && i >= E)) return;
+  float v = 0.f;
+  for (int k = 0; k < nblk; ++k) v += part[(int64_t)k * (EM + 1) + i];
   const float inv_n = N > 0 ? 1.0f / (float)N : 0.f;
-  const float v = block_sum(acc, red);
-  if (threadIdx.x != 0) return;
-  if (target < E)
-    probs_mean[target] = v * inv_n;
+  if (i < EM)
+    probs_mean[i] = v * inv_n;
+  else
+    z_loss[0] = zw > 0.f ? zw * v * inv_n : 0.f;
+}
+
+// Deterministic z-loss and probs_mean in one workgroup: a thread takes tokens tid,
+// tid + 1024, ... in increasing order and keeps E + 1 sums (each expert's score, the
+// squared logsumexp); waves then reduce each sum in a fixed order, so the statistics do
+// not depend on scheduling. U tokens per thread are loaded before any is used (one memory
+// round trip per U tokens).
+constexpr int kRouterStatThreads = 1024;
+template <typename L, int EM, int U, bool VEC>
+__global__ void __launch_bounds__(kRouterStatThreads) router_stats_kernel(
+    const L* __restrict__ logits, float* __restrict__ z_loss, float* __restrict__ probs_mean,
+    int64_t N, int E, float zw) {
+  __shared__ float red[kRouterStatThreads / 64][EM + 1];
+  float acc[EM + 1];
+#pragma unroll
+  for (int e = 0; e <= EM; ++e) acc[e] = 0.f;
+  for (int64_t t0 = threadIdx.x; t0 < N; t0 += (int64_t)U * kRouterStatThreads) {
+    float c[U][EM];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = min(t0 + (int64_t)u * kRouterStatThreads, N - 1);
+      router_centred<L, EM, VEC>(logits + t * E, E, c[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (t0 + (int64_t)u * kRouterStatThreads >= N) break;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < EM; ++e)
+        if (e < E) {
+          acc[e] += sigmoidf_(c[u][e]);
+          mx = fmaxf(mx, c[u][e]);
+        }
+      float se = 0.f;
+#pragma unroll
+      for (int e = 0; e < EM; ++e)
+        if (e < E) se += expf(c[u][e] - mx);
+      const float lse = mx + logf(se);
+      acc[EM] += lse * lse;
+    }
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int e = 0; e <= EM; ++e) {
+    const float v = wave_sum(acc[e]);
+    if (lane == 0) red[w][e] = v;
+  }
+  __syncthreads();
+  const int i = threadIdx.x;
+  if (i > EM || (i < EM && i >= E)) return;
+  float v = 0.f;
+  for (int k = 0; k < kRouterStatThreads / 64; ++k) v += red[k][i];
+  const float inv_n = N > 0 ? 1.0f / (float)N : 0.f;
+  if (i < EM)
+    probs_mean[i] = v * inv_n;
   else
     z_loss[0] = zw > 0.f ? zw * v * inv_n : 0.f;
 }
@@ -544,6 +672,54 @@ __global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
 }
 
 
+// Router entry: top-k, and the statistics either through per-workgroup partials in a
+// caller workspace or (no workspace) one workgroup over all tokens.
+int router_topk_forward(const void* logits, int logits_dtype, const float* bias,
+                        int64_t* topk_idx, uint16_t* topk_w_bf16, float* z_loss,
+                        float* probs_mean, int64_t N, int64_t E, int64_t K,
+                        float z_loss_weight, float* workspace, hipStream_t stream) {
+  if (E < 1 || E > 32)
+    return fail(PULSAR_ERR_INVALID,
+                "moe_router_topk_forward supports E <= 32, got " + std::to_string(E));
+  if (K < 1 || K > 8 || K > E)
+    return fail(PULSAR_ERR_INVALID,
+                "top_k must be in [1, min(8, E)], got " + std::to_string(K));
+  PULSAR_REQUIRE(N >= 0, "router: N must be >= 0");
+  return dispatch_dtype(logits_dtype, [&](auto tag) {
+    using L = decltype(tag);
+    const bool vec = E % kVec<L> == 0 && aligned16(logits);
+    const bool stats = z_loss && probs_mean;
+    const unsigned nblk = blocks_for(N, kRouterTopkThreads);
+    auto run = [&](auto em, auto v) {
+      constexpr int EM = decltype(em)::value;
+      constexpr bool VEC = decltype(v)::value;
+      if (stats && workspace && N > 0) {
+        // per-workgroup partials, then their fixed-order sum
+        router_topk_kernel<L, EM, VEC, true><<<nblk, kRouterTopkThreads, 0, stream>>>(
+            (const L*)logits, bias, topk_idx, topk_w_bf16, workspace, N, (int)E, (int)K);
+        router_stats_merge_kernel<EM><<<1, 64, 0, stream>>>(workspace, (int)nblk, z_loss,
+                                                            probs_mean, N, (int)E,
+                                                            z_loss_weight);
+        return;
+      }
+      if (N > 0)
+        router_topk_kernel<L, EM, VEC, false><<<nblk, kRouterTopkThreads, 0, stream>>>(
+            (const L*)logits, bias, topk_idx, topk_w_bf16, nullptr, N, (int)E, (int)K);
+      if (stats)
+        router_stats_kernel<L, EM, EM == 16 ? 4 : 2, VEC><<<1, kRouterStatThreads, 0, stream>>>(
+            (const L*)logits, z_loss, probs_mean, N, (int)E, z_loss_weight);
+    };
+    using T16 = std::integral_constant<int, 16>;
+    using T32 = std::integral_constant<int, 32>;
+    if (E <= 16)
+      vec ? run(T16{}, std::true_type{}) : run(T16{}, std::false_type{});
+    else
+      vec ? run(T32{}, std::true_type{}) : run(T32{}, std::false_type{});
+    PULSAR_LAUNCH_CHECK();
+    return PULSAR_OK;
+  });
+}
+
 }  // namespace pulsar
 
 using namespace pulsar;
@@ -552,7 +728,7 @@ extern "C" {
 
 const char* pulsar_last_error(void) { return g_last_error.c_str(); }
 
-int pulsar_abi_version(void) { return 3; }
+int pulsar_abi_version(void) { return 4; }
 
 int pulsar_rmsnorm_forward(const void* x, const float* w, void* y, float* rsqrt_out,
                            int64_t rows, int64_t dim, float eps, int dtype,
@@ -562,9 +738,13 @@ int pulsar_rmsnorm_forward(const void* x, const float* w, void* y, float* rsqrt_
   PULSAR_REQUIRE(x && w && y, "rmsnorm: null pointer");
   return dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    if (dim % kVec<T> == 0 && aligned16(x) && aligned16(w) && aligned16(y))
-      rmsnorm_vec_kernel<T><<<(unsigned)rows, 256, 0, stream>>>((const T*)x, w, (T*)y,
-                                                                rsqrt_out, (int)dim, eps);
+    if (dim % kVec<T> == 0 && aligned16(x) && aligned16(w) && aligned16(y)) {
+      // one 16-byte chunk per thread where the row allows (a multiple of 64 threads, <= 256)
+      const int64_t nc = dim / kVec<T>;
+      const int threads = (int)std::min<int64_t>(256, std::max<int64_t>(64, (nc + 63) / 64 * 64));
+      rmsnorm_vec_kernel<T><<<(unsigned)rows, threads, 0, stream>>>((const T*)x, w, (T*)y,
+                                                                    rsqrt_out, (int)dim, eps);
+    }
     else
       rmsnorm_kernel<T><<<(unsigned)rows, 256, 0, stream>>>((const T*)x, w, (T*)y, rsqrt_out,
                                                             (int)dim, eps);
@@ -651,8 +831,9 @@ int pulsar_causal_conv1d_k4_forward(const void* x, const float* w, void* y, int6
   return dispatch_dtype(dtype, [&](auto tag) {
     using T_ = decltype(tag);
     if (D % kVec<T_> == 0 && aligned16(x) && aligned16(w) && aligned16(y))
-      conv_k4_vec_kernel<T_><<<blocks_for(total / kVec<T_>, 256), 256, 0, stream>>>(
-          (const T_*)x, w, (T_*)y, T, D, total);
+      conv_k4_vec_kernel<T_><<<blocks_for(B * ((T + kConvTokens - 1) / kConvTokens) *
+                                              (D / kVec<T_>), 256), 256, 0, stream>>>(
+          (const T_*)x, w, (T_*)y, B, T, D);
     else
       conv_k4_kernel<T_><<<blocks_for(total, 256), 256, 0, stream>>>((const T_*)x, w, (T_*)y,
                                                                      T, D, total);
@@ -683,26 +864,25 @@ int pulsar_moe_router_topk_forward(const void* logits, int logits_dtype, const f
                                    int64_t* topk_idx, uint16_t* topk_w_bf16, float* z_loss,
                                    float* probs_mean, int64_t N, int64_t E, int64_t K,
                                    float z_loss_weight, hipStream_t stream) {
-  if (E < 1 || E > 32)
-    return fail(PULSAR_ERR_INVALID,
-                "moe_router_topk_forward supports E <= 32, got " + std::to_string(E));
-  if (K < 1 || K > 8 || K > E)
-    return fail(PULSAR_ERR_INVALID,
-                "top_k must be in [1, min(8, E)], got " + std::to_string(K));
-  PULSAR_REQUIRE(N >= 0, "router: N must be >= 0");
-  return dispatch_dtype(logits_dtype, [&](auto tag) {
-    using L = decltype(tag);
-    if (N > 0)
-      router_topk_kernel<L><<<blocks_for(N, 128), 128, 0, stream>>>(
-          (const L*)logits, bias, topk_idx, topk_w_bf16, N, (int)E, (int)K);
-    PULSAR_LAUNCH_CHECK();
-    if (z_loss && probs_mean) {
-      router_stats_kernel<L><<<(unsigned)(E + 1), 256, 0, stream>>>((const L*)logits, bias, z_loss, probs_mean,
-                                                    N, (int)E, z_loss_weight);
-      PULSAR_LAUNCH_CHECK();
-    }
-    return PULSAR_OK;
-  });
+  return router_topk_forward(logits, logits_dtype, bias, topk_idx, topk_w_bf16, z_loss,
+                             probs_mean, N, E, K, z_loss_weight, nullptr, stream);
+}
+
+int64_t pulsar_moe_router_workspace_bytes(int64_t N, int64_t E) {
+  if (N < 0 || E < 1 || E > 32) return -1;
+  const int64_t em = E <= 16 ? 16 : 32;
+  return (int64_t)blocks_for(N, kRouterTopkThreads) * (em + 1) * (int64_t)sizeof(float);
+}
+
+int pulsar_moe_router_topk_forward_ws(const void* logits, int logits_dtype, const float* bias,
+                                      int64_t* topk_idx, uint16_t* topk_w_bf16, float* z_loss,
+                                      float* probs_mean, int64_t N, int64_t E, int64_t K,
+                                      float z_loss_weight, float* workspace,
+                                      hipStream_t stream) {
+  PULSAR_REQUIRE(workspace || !(z_loss && probs_mean) || N == 0,
+                 "moe_router_topk_forward_ws: workspace required for the statistics");
+  return router_topk_forward(logits, logits_dtype, bias, topk_idx, topk_w_bf16, z_loss,
+                             probs_mean, N, E, K, z_loss_weight, workspace, stream);
 }
 
 int pulsar_moe_dispatch_forward(const void* x, const int64_t* topk_idx, const int32_t* slots,

@@ -184,9 +184,12 @@ def moe_router_topk_forward(logits: torch.Tensor, expert_bias: torch.Tensor, top
     w = torch.empty((N, top_k), dtype=torch.bfloat16, device=dev)
     z = torch.zeros((), dtype=torch.float32, device=dev)
     pm = torch.zeros(E, dtype=torch.float32, device=dev)
-    _lib.check(_LIB.pulsar_moe_router_topk_forward(
+    # per-workgroup partial statistics (merged in a fixed order inside the library)
+    ws = torch.empty(max(1, _LIB.pulsar_moe_router_workspace_bytes(N, E) // 4),
+                     dtype=torch.float32, device=dev)
+    _lib.check(_LIB.pulsar_moe_router_topk_forward_ws(
         _p(logits), _dtype_code(logits, "logits"), _p(expert_bias), _p(idx), _p(w), _p(z), _p(pm),
-        N, E, top_k, float(z_loss_weight), _stream(logits)))
+        N, E, top_k, float(z_loss_weight), _p(ws), _stream(logits)))
     return idx, w, z, pm
 
 

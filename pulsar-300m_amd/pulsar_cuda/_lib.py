@@ -24,7 +24,7 @@ BUF_EXIT_COUNTS = 8
 BUF_TOPK_IDX = 9
 BUF_TOKEN_KINDS = 10
 BUF_KV_LAYOUT = 11
-ABI_VERSION = 3
+ABI_VERSION = 4
 SEQSTATE_INTS = 32
 ROW_INTS = 8
 CTL_INTS = 16
@@ -88,6 +88,9 @@ _PROTOS = {
     "pulsar_fused_swiglu_forward": [_vp, _vp, _c_i64, _c_i64, ctypes.c_int, _vp],
     "pulsar_moe_router_topk_forward": [_vp, ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
                                        _c_i64, _c_f32, _vp],
+    "pulsar_moe_router_workspace_bytes": [_c_i64, _c_i64],
+    "pulsar_moe_router_topk_forward_ws": [_vp, ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _c_i64,
+                                          _c_i64, _c_i64, _c_f32, _vp, _vp],
     "pulsar_moe_dispatch_forward": [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
                                     _c_i64, ctypes.c_int, _vp],
     "pulsar_moe_combine_forward": [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
@@ -128,7 +131,7 @@ _PROTOS = {
                                   _vp],
 }
 # entries whose result is not an int status
-_RESTYPES = {"pulsar_sample_workspace_bytes": _c_i64}
+_RESTYPES = {"pulsar_sample_workspace_bytes": _c_i64, "pulsar_moe_router_workspace_bytes": _c_i64}
 
 EXPORTED = tuple(["pulsar_last_error", *_PROTOS])
 

@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     assert set(_declared()) == set(_lib.EXPORTED)
     lib.pulsar_abi_version.restype = ctypes.c_int
-    assert lib.pulsar_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.pulsar_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_struct_layouts_match_the_c_header(tmp_path):
@@ -105,3 +105,21 @@ def test_sample_rows_validates_before_touching_the_device():
         rc = lib.pulsar_sample_rows(*a)
         assert rc != 0, name
         assert b"sample_rows" in lib.pulsar_last_error(), name
+
+
+def test_router_workspace_entry_validates_without_a_device():
+    """The router's workspace size for 128-token workgroups, and the workspace entry's refusal
+    to compute statistics without one (checked before any launch)."""
+    from pulsar_cuda import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libpulsar_hip.so not built")
+    lib = _lib.load()
+    assert lib.pulsar_moe_router_workspace_bytes(16384, 16) == 128 * 17 * 4
+    assert lib.pulsar_moe_router_workspace_bytes(129, 32) == 2 * 33 * 4
+    assert lib.pulsar_moe_router_workspace_bytes(10, 33) == -1
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    rc = lib.pulsar_moe_router_topk_forward_ws(p, _lib.PULSAR_BF16, p, p, p, p, p, 8, 16, 4,
+                                               1e-3, None, None)
+    assert rc != 0 and b"workspace" in lib.pulsar_last_error()

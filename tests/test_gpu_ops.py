@@ -133,6 +133,42 @@ def test_router_topk_bit_exact_indices(pc, N, dtype):
     assert_close(z, 1e-3 * lse.pow(2).mean(), atol=1e-6, rtol=1e-4)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,E", [(4096, 16), (1000, 24), (300, 7)])
+def test_router_statistics_with_and_without_workspace(pc, N, E, dtype):
+    """The workspace entry (per-workgroup partials) and the plain entry (one workgroup over
+    every token): identical indices and weights, statistics equal up to summation order."""
+    from pulsar_cuda import _lib
+
+    lib = _lib.load()
+    K = 4
+    logits = _rand(N, E, seed=N + E, dtype=dtype, scale=2.0)
+    bias = (torch.rand(E, device="cuda") - 0.5) * 0.1
+    outs = []
+    for ws in (True, False):
+        idx = torch.empty(N, K, dtype=torch.int64, device="cuda")
+        w = torch.empty(N, K, dtype=torch.bfloat16, device="cuda")
+        z = torch.zeros((), device="cuda")
+        pm = torch.zeros(E, device="cuda")
+        code = 1 if dtype == torch.bfloat16 else 0
+        stream = torch.cuda.current_stream().cuda_stream
+        if ws:
+            buf = torch.empty(lib.pulsar_moe_router_workspace_bytes(N, E) // 4, device="cuda")
+            rc = lib.pulsar_moe_router_topk_forward_ws(
+                logits.data_ptr(), code, bias.data_ptr(), idx.data_ptr(), w.data_ptr(),
+                z.data_ptr(), pm.data_ptr(), N, E, K, 1e-3, buf.data_ptr(), stream)
+        else:
+            rc = lib.pulsar_moe_router_topk_forward(
+                logits.data_ptr(), code, bias.data_ptr(), idx.data_ptr(), w.data_ptr(),
+                z.data_ptr(), pm.data_ptr(), N, E, K, 1e-3, stream)
+        assert rc == 0, lib.pulsar_last_error()
+        outs.append((idx, w, z, pm))
+    (i1, w1, z1, p1), (i2, w2, z2, p2) = outs
+    assert torch.equal(i1, i2) and torch.equal(w1, w2)
+    assert_close(p1, p2, atol=0, rtol=1e-5)
+    assert_close(z1, z2, atol=0, rtol=1e-5)
+
+
 def test_router_three_argument_overload(pc):
     logits = _rand(8, 8, seed=9, dtype=torch.float32)
     idx, w, z, pm = pc.moe_router_topk_forward(logits, torch.zeros(8, device="cuda"), 0.0)
