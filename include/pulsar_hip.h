@@ -309,6 +309,14 @@ typedef struct PulsarEngineConfig {
    * so that its exit is counted. Exact schedule only (draft_len = 0). */
   int32_t early_exit;
   double early_exit_threshold;
+  /* Pages of 64 positions in the global layers' KV pool, shared by the batch (0: enough for
+   * every sequence to reach max_ctx). Prefill (and fill_kv) give each sequence the pages of
+   * its prompt; decoding takes one more page from the pool when a sequence first writes a
+   * position in it. A sequence that finds the pool spent stops there (PULSAR_BUF_KV_PAGES
+   * reports it); a prompt set that does not fit fails prefill with an error. No reference
+   * counterpart: the reference grows each global layer's cache tensor by concatenation
+   * (src/infer.py:139-150). */
+  int32_t kv_pages;
 } PulsarEngineConfig;
 
 /* Buffers readable with pulsar_engine_read. */
@@ -331,9 +339,12 @@ typedef struct PulsarEngineConfig {
                                       order (PULSAR_BUF_LAST_ROWS), in the router's ranking
                                       order */
 #define PULSAR_BUF_KV_LAYOUT 11    /* int32 [4] cache layout: ring positions of a sliding-
-                                      window layer (lcap), pages per sequence of a global
-                                      layer, positions per page, kv heads (host copy, no
+                                      window layer (lcap), page-table entries per sequence
+                                      of a global layer, positions per page, kv heads (host copy, no
                                       device access) */
+#define PULSAR_BUF_KV_PAGES 12     /* int32 [3] global KV pages: pool size, pages handed out
+                                      (at most the pool size), 1 if a request found the pool
+                                      spent since the last prefill, fill_kv or rewind */
 #define PULSAR_BUF_TOKEN_KINDS 10  /* int32 [B][max_new] per emitted token: 1 = an accepted
                                       draft, 0 = a drawn token */
 

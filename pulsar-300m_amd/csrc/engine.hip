@@ -59,6 +59,13 @@ struct Engine {
   RowDesc* p_rows = nullptr;  // [P][R]
   StepCtl* p_ctl = nullptr;   // [P]
   KVDesc kv{};
+  // global-layer KV pages: pool size, page table [B][max_pages] (unassigned entries name
+  // the spare page pool_pages, never written by a sequence), pages per sequence [B], pool
+  // counter and spent flag [2]; the *_save copies hold the state the last prefill or
+  // fill_kv left, which rewind restores
+  int pool_pages = 0;
+  int32_t *page_table = nullptr, *page_count = nullptr, *pool = nullptr;
+  int32_t *page_table_save = nullptr, *page_count_save = nullptr, *pool_save = nullptr;
   void* ring_save_k[kMaxLayers] = {};  // sliding-window rings as the last prefill left them
   void* ring_save_v[kMaxLayers] = {};
   int prompt_len = 0;
@@ -134,6 +141,7 @@ int validate(const PulsarModelDesc& m, const PulsarEngineConfig& c) {
   PULSAR_REQUIRE(m.rope_len >= c.max_ctx, "rope tables shorter than max_ctx");
   PULSAR_REQUIRE(c.n_stop >= 0 && c.n_stop <= 8, "n_stop must be 0..8");
   PULSAR_REQUIRE(c.early_exit == 0 || c.early_exit == 1, "early_exit must be 0 or 1");
+  PULSAR_REQUIRE(c.kv_pages >= 0, "kv_pages must be >= 0 (0: every sequence up to max_ctx)");
   if (c.early_exit) {
     PULSAR_REQUIRE(c.draft_len == 0,
                    "early exit applies to the exact schedule only (draft_len == 0)");
@@ -155,6 +163,7 @@ void kv_desc(Engine& e) {
   e.kv.Hkv = e.Hkv;
   e.kv.lcap = e.lcap;
   e.kv.max_pages = e.max_pages;
+  e.kv.page_table = e.page_table;
 }
 
 int prof_mark(Engine& e, hipStream_t s) {
@@ -312,9 +321,27 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   PULSAR_TRY(x.alloc(&x.p_ids, 4 * (size_t)x.B * c.max_prompt));
   PULSAR_TRY(x.alloc(&x.p_rows, sizeof(RowDesc) * x.P * (size_t)x.B * c.max_prompt));
   PULSAR_TRY(x.alloc(&x.p_ctl, sizeof(StepCtl) * x.P));
-  // KV cache
+  // KV cache; the global layers' pool holds one spare page past pool_pages, which the
+  // page-table entries not assigned yet name
+  x.pool_pages = c.kv_pages > 0 ? c.kv_pages : x.B * x.max_pages;
+  const size_t pt = (size_t)x.B * x.max_pages;
+  PULSAR_TRY(x.alloc(&x.page_table, 4 * pt));
+  PULSAR_TRY(x.alloc(&x.page_table_save, 4 * pt));
+  PULSAR_TRY(x.alloc(&x.page_count, 4 * (size_t)x.B));
+  PULSAR_TRY(x.alloc(&x.page_count_save, 4 * (size_t)x.B));
+  PULSAR_TRY(x.alloc(&x.pool, 8));
+  PULSAR_TRY(x.alloc(&x.pool_save, 8));
+  {
+    const std::vector<int32_t> spare(pt, x.pool_pages);
+    PULSAR_CHECK_HIP(hipMemcpy(x.page_table, spare.data(), 4 * pt, hipMemcpyHostToDevice));
+    PULSAR_CHECK_HIP(hipMemcpy(x.page_table_save, spare.data(), 4 * pt, hipMemcpyHostToDevice));
+    PULSAR_CHECK_HIP(hipMemset(x.page_count, 0, 4 * (size_t)x.B));
+    PULSAR_CHECK_HIP(hipMemset(x.page_count_save, 0, 4 * (size_t)x.B));
+    PULSAR_CHECK_HIP(hipMemset(x.pool, 0, 8));
+    PULSAR_CHECK_HIP(hipMemset(x.pool_save, 0, 8));
+  }
   const size_t local_elems = (size_t)x.B * x.Hkv * x.lcap * kHeadDim;
-  const size_t global_elems = (size_t)x.B * x.max_pages * x.Hkv * kPage * kHeadDim;
+  const size_t global_elems = ((size_t)x.pool_pages + 1) * x.Hkv * kPage * kHeadDim;
   for (int l = 0; l < x.L; ++l) {
     const bool loc = (m.local_mask >> l) & 1u;
     const size_t n = loc ? local_elems : global_elems;
@@ -701,9 +728,73 @@ int enqueue_step(Engine& e, hipStream_t s) {
   co.maxprob = e.maxprob;
   co.exit_counts = e.exit_counts;
   co.exit_thr = e.cfg.early_exit_threshold;
+  co.page_table = e.page_table;
+  co.page_count = e.page_count;
+  co.pool = e.pool;
+  co.pool_pages = e.pool_pages;
+  co.max_pages = e.max_pages;
   PULSAR_TRY(launch_controller(co, s));
   prof_span(e, PC_CONTROL, _pc, prof_mark(e, s));
   return PULSAR_OK;
+}
+
+// Global-layer pages of a fresh cache holding positions [0, npos) of every sequence:
+// sequence b gets pool pages [b * need, (b + 1) * need), need = ceil(npos / 64), the rest of
+// its table names the spare page; the same state goes to the saved copies rewind restores.
+int assign_prompt_pages(Engine& e, int npos, hipStream_t s) {
+  const int need = (npos + kPage - 1) / kPage;
+  PULSAR_REQUIRE((int64_t)e.B * need <= e.pool_pages,
+                 "KV page pool too small for the prompts: " + std::to_string(e.B) + " x " +
+                     std::to_string(need) + " pages > kv_pages " +
+                     std::to_string(e.pool_pages));
+  const size_t pt = (size_t)e.B * e.max_pages;
+  std::vector<int32_t> table(pt, e.pool_pages), count(e.B, need);
+  for (int b = 0; b < e.B; ++b)
+    for (int p = 0; p < need; ++p) table[(size_t)b * e.max_pages + p] = b * need + p;
+  const int32_t pool[2] = {e.B * need, 0};
+  for (int32_t* dst : {e.page_table, e.page_table_save})
+    PULSAR_CHECK_HIP(hipMemcpyAsync(dst, table.data(), 4 * pt, hipMemcpyHostToDevice, s));
+  for (int32_t* dst : {e.page_count, e.page_count_save})
+    PULSAR_CHECK_HIP(hipMemcpyAsync(dst, count.data(), 4 * (size_t)e.B, hipMemcpyHostToDevice, s));
+  for (int32_t* dst : {e.pool, e.pool_save})
+    PULSAR_CHECK_HIP(hipMemcpyAsync(dst, pool, 8, hipMemcpyHostToDevice, s));
+  // the host vectors must outlive the copies
+  PULSAR_CHECK_HIP(hipStreamSynchronize(s));
+  return PULSAR_OK;
+}
+
+// Back to the pages the last prefill or fill_kv left (pages decoding took return to the
+// pool).
+int restore_pages(Engine& e, hipStream_t s) {
+  const size_t pt = (size_t)e.B * e.max_pages;
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.page_table, e.page_table_save, 4 * pt,
+                                  hipMemcpyDeviceToDevice, s));
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.page_count, e.page_count_save, 4 * (size_t)e.B,
+                                  hipMemcpyDeviceToDevice, s));
+  PULSAR_CHECK_HIP(hipMemcpyAsync(e.pool, e.pool_save, 8, hipMemcpyDeviceToDevice, s));
+  return PULSAR_OK;
+}
+
+// Pages for the positions of the block verify's units (unit b: sequence b's block), taken
+// in order of request; when the pool is spent the entries keep naming the spare page and
+// the spent flag is set. Reads the positions from the uploaded units, so a captured verify
+// follows later uploads.
+__global__ void kv_ensure_pages_kernel(const AttnUnit* units, int32_t* table, int32_t* count,
+                                       int32_t* pool, int pool_pages, int max_pages, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const AttnUnit un = units[b];
+  const int need = (un.pos0 + un.n - 1) / kPage + 1;
+  const int have = count[un.seq];
+  if (have >= need) return;
+  const int n = need - have;
+  const int first = atomicAdd(&pool[0], n);
+  if (first + n > pool_pages) {
+    atomicOr(&pool[1], 1);
+    return;
+  }
+  for (int i = 0; i < n; ++i) table[(int64_t)un.seq * max_pages + have + i] = first + i;
+  count[un.seq] = need;
 }
 
 // Copy the sliding-window rings to their saved copies (restore = false) or back (restore =
@@ -785,6 +876,11 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   co.maxprob = e.maxprob;
   co.exit_counts = e.exit_counts;
   co.exit_thr = e.cfg.early_exit_threshold;
+  co.page_table = e.page_table;
+  co.page_count = e.page_count;
+  co.pool = e.pool;
+  co.pool_pages = e.pool_pages;
+  co.max_pages = e.max_pages;
   PULSAR_TRY(launch_controller(co, s));
   // host vectors above are read by the async copies: finish before they go out of scope
   PULSAR_CHECK_HIP(hipStreamSynchronize(s));
@@ -806,6 +902,7 @@ int prefill(Engine& e, const int32_t* host_ids, int Bq, int T, hipStream_t s) {
   e.prefilled = false;
   e.kv_ready = false;
   e.v_n = 0;
+  PULSAR_TRY(assign_prompt_pages(e, T, s));
   e.prompt_len = T;
   // graph of a previous generation refers to the same buffers; it stays valid.
   PULSAR_CHECK_HIP(hipMemcpyAsync(e.p_ids, host_ids, 4 * (size_t)BT, hipMemcpyHostToDevice, s));
@@ -1100,24 +1197,53 @@ __global__ void __launch_bounds__(256) fill_normal_kernel(T* p, int64_t n, uint6
   }
 }
 
+// Global layers: the value of element `inner` of sequence b's page p is keyed by its
+// position in a per-sequence layout, ((b * max_pages + p) * page_elems + inner), whichever
+// pool page holds it (fill_kv assigns sequence b the pool pages [b * need, (b + 1) * need)).
+template <typename T>
+__global__ void __launch_bounds__(256) fill_pages_kernel(T* p, int64_t n, int need,
+                                                         int max_pages, int64_t page_elems,
+                                                         uint64_t seed) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t pool_page = i / page_elems, inner = i % page_elems;
+    const int64_t b = pool_page / need, pg = pool_page % need;
+    const int64_t key = (b * max_pages + pg) * page_elems + inner;
+    const uint64_t h = fill_mix64(seed + 0x9E3779B97F4A7C15ull * (uint64_t)(key + 1));
+    const float u1 = (float)((h >> 40) + 1) * (1.0f / 16777216.0f);  // (0, 1]
+    const float u2 = (float)((h >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    p[i] = from_f<T>(sqrtf(-2.0f * logf(u1)) * cosf(6.28318530718f * u2));
+  }
+}
+
 int fill_kv(Engine& e, int ctx, uint64_t seed, hipStream_t s) {
   PULSAR_REQUIRE(ctx >= 1 && ctx + 1 <= e.cfg.max_ctx, "engine_fill_kv: 1 <= ctx < max_ctx");
   e.prefilled = false;
   e.kv_ready = false;
   e.v_n = 0;
+  PULSAR_TRY(assign_prompt_pages(e, ctx, s));
+  const int need = (ctx + kPage - 1) / kPage;
+  const int64_t page_elems = (int64_t)e.Hkv * kPage * kHeadDim;
   const size_t local_elems = (size_t)e.B * e.Hkv * e.lcap * kHeadDim;
-  const size_t global_elems = (size_t)e.B * e.max_pages * e.Hkv * kPage * kHeadDim;
   for (int l = 0; l < e.L; ++l) {
     const bool loc = (e.m.local_mask >> l) & 1u;
-    const int64_t n = (int64_t)(loc ? local_elems : global_elems);
+    const int64_t n = loc ? (int64_t)local_elems : (int64_t)e.B * need * page_elems;
     for (int kvi = 0; kvi < 2; ++kvi) {
       void* p = kvi == 0 ? e.kv.k[l] : e.kv.v[l];
       const uint64_t sd = fill_mix64(seed ^ (uint64_t)(2 * l + kvi + 1));
       const unsigned grid = (unsigned)std::min<int64_t>(8192, (n + 255) / 256);
-      if (e.dtype == PULSAR_BF16)
-        fill_normal_kernel<bf16><<<grid, 256, 0, s>>>(reinterpret_cast<bf16*>(p), n, sd);
-      else
-        fill_normal_kernel<float><<<grid, 256, 0, s>>>(reinterpret_cast<float*>(p), n, sd);
+      if (loc) {
+        if (e.dtype == PULSAR_BF16)
+          fill_normal_kernel<bf16><<<grid, 256, 0, s>>>(reinterpret_cast<bf16*>(p), n, sd);
+        else
+          fill_normal_kernel<float><<<grid, 256, 0, s>>>(reinterpret_cast<float*>(p), n, sd);
+      } else if (e.dtype == PULSAR_BF16) {
+        fill_pages_kernel<bf16><<<grid, 256, 0, s>>>(reinterpret_cast<bf16*>(p), n, need,
+                                                     e.max_pages, page_elems, sd);
+      } else {
+        fill_pages_kernel<float><<<grid, 256, 0, s>>>(reinterpret_cast<float*>(p), n, need,
+                                                      e.max_pages, page_elems, sd);
+      }
       PULSAR_LAUNCH_CHECK();
     }
   }
@@ -1190,6 +1316,11 @@ int verify(Engine& e, const int32_t* host_tokens, int n, int use_graph, hipStrea
     e.v_n = n;
   }
   auto passes = [&](hipStream_t st) -> int {
+    // pages for the block's positions (a no-op once taken)
+    kv_ensure_pages_kernel<<<(B + 63) / 64, 64, 0, st>>>(e.v_units, e.page_table,
+                                                         e.page_count, e.pool, e.pool_pages,
+                                                         e.max_pages, B);
+    PULSAR_LAUNCH_CHECK();
     for (int k = 0; k < P; ++k)
       PULSAR_TRY(enqueue_pass(e, e.v_ctl + k, e.v_rows + (size_t)k * MR, e.v_units + (size_t)k * B,
                               st, k == P - 1));  // logits rows: the last pulse's only
@@ -1330,6 +1461,7 @@ int pulsar_engine_rewind(void* handle, uint64_t seed, hipStream_t stream) {
   Engine& e = *reinterpret_cast<Engine*>(handle);
   PULSAR_REQUIRE(e.prefilled, "engine_rewind: prefill first");
   PULSAR_TRY(save_rings(e, stream, true));
+  PULSAR_TRY(restore_pages(e, stream));
   return first_token(e, seed, stream);
 }
 
@@ -1405,6 +1537,15 @@ int pulsar_engine_read(void* handle, int32_t what, void* host_dst, int64_t bytes
       const int32_t layout[4] = {e.lcap, e.max_pages, kPage, e.Hkv};
       PULSAR_REQUIRE(bytes <= (int64_t)sizeof(layout), "engine_read: more bytes than the buffer holds");
       std::memcpy(host_dst, layout, bytes);
+      return PULSAR_OK;
+    }
+    case PULSAR_BUF_KV_PAGES: {
+      int32_t pool[2] = {0, 0};
+      PULSAR_CHECK_HIP(hipMemcpyAsync(pool, e.pool, 8, hipMemcpyDeviceToHost, stream));
+      PULSAR_CHECK_HIP(hipStreamSynchronize(stream));
+      const int32_t info[3] = {e.pool_pages, std::min(pool[0], e.pool_pages), pool[1]};
+      PULSAR_REQUIRE(bytes <= (int64_t)sizeof(info), "engine_read: more bytes than the buffer holds");
+      std::memcpy(host_dst, info, bytes);
       return PULSAR_OK;
     }
     case PULSAR_BUF_TOKEN_KINDS:

@@ -728,7 +728,7 @@ extern "C" {
 
 const char* pulsar_last_error(void) { return g_last_error.c_str(); }
 
-int pulsar_abi_version(void) { return 4; }
+int pulsar_abi_version(void) { return 5; }
 
 int pulsar_rmsnorm_forward(const void* x, const float* w, void* y, float* rsqrt_out,
                            int64_t rows, int64_t dim, float eps, int dtype,

@@ -17,21 +17,29 @@ static_assert(kUnitSplit >= kSplitLen, "split partial slots are sized for kSplit
 constexpr int kMaxRank = 16;    // re-injection gate rank bound
 
 // KV cache addressing. Local (sliding-window) layers: a per-sequence ring of `lcap`
-// positions (a multiple of 64). Global layers: pages of 64 positions, sequence b owning
-// the run of pages [b * max_pages, (b + 1) * max_pages), so a page's address is computed,
-// never looked up (no dependent load ahead of the KV loads). K is stored position-major ([..][pos][64]);
-// V is stored transposed, dimension-major ([..][64][pos]), so that the keys of one
-// dimension are contiguous: the layout the P.V matrix-core operand reads.
-//   local  K: [B][Hkv][lcap][64]        V: [B][Hkv][64][lcap]
-//   global K: [pages][Hkv][64 pos][64]  V: [pages][Hkv][64][64 pos]
+// positions (a multiple of 64). Global layers: pages of 64 positions from a pool shared by
+// the batch; page_table[b * max_pages + p] is the pool page holding positions
+// [64 p, 64 p + 64) of sequence b (the same page index in every global layer). Pages are
+// given out when a sequence first writes a position in them (prefill and fill_kv for the
+// prompt, the controller as decoding reaches a new page). K is stored position-major
+// ([..][pos][64]); V is stored transposed, dimension-major ([..][64][pos]), so that the
+// keys of one dimension are contiguous: the layout the P.V matrix-core operand reads.
+//   local  K: [B][Hkv][lcap][64]            V: [B][Hkv][64][lcap]
+//   global K: [pool pages][Hkv][64 pos][64]  V: [pool pages][Hkv][64][64 pos]
 struct KVDesc {
   void* k[kMaxLayers];
   void* v[kMaxLayers];
   uint32_t local_mask;
   int Hkv;
   int lcap;
-  int max_pages;
+  int max_pages;                // page-table entries per sequence
+  const int32_t* page_table;    // [B][max_pages] pool page ids
 };
+
+// Pool page of sequence b's positions [64 p, 64 p + 64) in the global layers.
+__device__ __forceinline__ int64_t kv_page(const int32_t* table, int max_pages, int b, int pos) {
+  return table[(int64_t)b * max_pages + pos / kPage];
+}
 
 __device__ __forceinline__ bool kv_is_local(const KVDesc& c, int layer) {
   return (c.local_mask >> layer) & 1u;
@@ -42,7 +50,7 @@ __device__ __forceinline__ int64_t kv_offset(const KVDesc& c, int layer, int b, 
   if (kv_is_local(c, layer)) {
     return (((int64_t)b * c.Hkv + g) * c.lcap + (pos % c.lcap)) * kHeadDim;
   }
-  const int64_t page = (int64_t)b * c.max_pages + pos / kPage;
+  const int64_t page = kv_page(c.page_table, c.max_pages, b, pos);
   return ((page * c.Hkv + g) * kPage + (pos % kPage)) * kHeadDim;
 }
 
@@ -52,7 +60,7 @@ __device__ __forceinline__ int64_t kv_offset_v(const KVDesc& c, int layer, int b
   if (kv_is_local(c, layer)) {
     return (((int64_t)b * c.Hkv + g) * kHeadDim + dim) * c.lcap + (pos % c.lcap);
   }
-  const int64_t page = (int64_t)b * c.max_pages + pos / kPage;
+  const int64_t page = kv_page(c.page_table, c.max_pages, b, pos);
   return ((page * c.Hkv + g) * kHeadDim + dim) * kPage + (pos % kPage);
 }
 
@@ -71,7 +79,7 @@ __device__ __forceinline__ KVBlock kv_block(const KVDesc& c, int layer, int b, i
     r.v0 = bg * kHeadDim * c.lcap + ring;
     r.vstride = c.lcap;
   } else {
-    const int64_t pg = ((int64_t)b * c.max_pages + kb / kPage) * c.Hkv + g;
+    const int64_t pg = kv_page(c.page_table, c.max_pages, b, kb) * c.Hkv + g;
     r.k0 = pg * kPage * kHeadDim;
     r.v0 = pg * kHeadDim * kPage;
     r.vstride = kPage;
@@ -139,6 +147,7 @@ struct KVLayer {
   const void* k;
   const void* v;
   int lcap, max_pages;
+  const int32_t* page_table;
 };
 
 __device__ __forceinline__ KVBlock kv_block_layer(const KVLayer& c, bool local, int Hkv, int b,
@@ -151,7 +160,7 @@ __device__ __forceinline__ KVBlock kv_block_layer(const KVLayer& c, bool local, 
     r.v0 = bg * kHeadDim * c.lcap + ring;
     r.vstride = c.lcap;
   } else {
-    const int64_t pg = ((int64_t)b * c.max_pages + kb / kPage) * Hkv + g;
+    const int64_t pg = kv_page(c.page_table, c.max_pages, b, kb) * Hkv + g;
     r.k0 = pg * kPage * kHeadDim;
     r.v0 = pg * kHeadDim * kPage;
     r.vstride = kPage;

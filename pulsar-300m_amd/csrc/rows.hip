@@ -667,6 +667,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
                "s"(un.row[2]), "s"(un.row[3]), "s"(un.row[4]), "s"(un.row[5]), "s"(un.row[6]),
                "s"(un.row[7]));
   asm volatile("" ::"s"(a.kl.k), "s"(a.kl.v), "s"(a.kl.lcap), "s"(a.kl.max_pages),
+               "s"(a.kl.page_table),
                "s"(a.is_local), "s"(a.window), "s"(a.Hkv), "s"(a.qkv), "s"(a.ldq));
   if (u >= n_units) return;
   int base, uhi;
@@ -1614,6 +1615,7 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     b.kl.v = a.kv.v[a.layer];
     b.kl.lcap = a.kv.lcap;
     b.kl.max_pages = a.kv.max_pages;
+    b.kl.page_table = a.kv.page_table;
     if (((a.kv.local_mask >> a.layer) & 1u) != (a.is_local ? 1u : 0u))
       return fail(PULSAR_ERR_INVALID, "decode attention: layer type mismatch");
 #define PULSAR_ATTN_UNIT(C)                                                         \

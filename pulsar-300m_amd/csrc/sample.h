@@ -80,6 +80,12 @@ struct ControllerArgs {
   const float* maxprob;
   int32_t* exit_counts;
   double exit_thr;
+  // global-layer KV pages: page table [B][max_pages], pages per sequence [B], pool counter
+  // and spent flag [2], pool size (nullable table: no page allocation)
+  int32_t* page_table;
+  int32_t* page_count;
+  int32_t* pool;
+  int pool_pages, max_pages;
 };
 
 int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s);

@@ -465,6 +465,24 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
   }
 }
 
+// Global-layer KV pages for sequence b's positions up to hi, taken from the pool in order
+// of request; false (and the pool's spent flag set) when the pool cannot cover them.
+__device__ bool ensure_pages(const ControllerArgs& a, int b, int hi) {
+  if (!a.page_table) return true;
+  const int need = hi / kPage + 1;
+  const int have = a.page_count[b];
+  if (have >= need) return true;
+  const int n = need - have;
+  const int first = atomicAdd(&a.pool[0], n);
+  if (first + n > a.pool_pages) {
+    atomicOr(&a.pool[1], 1);
+    return false;
+  }
+  for (int i = 0; i < n; ++i) a.page_table[(int64_t)b * a.max_pages + have + i] = first + i;
+  a.page_count[b] = need;
+  return true;
+}
+
 // Exclusive scan of N counters over the block (blockDim 256) in LDS.
 template <int N>
 __device__ void scan_counts(int* v, int* sh, int* total) {
@@ -525,6 +543,11 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
     } else if (!s.done) {
       update_seq(a, s, b);
     }
+    // pages for the next step's positions: the current token's, and the speculative row's
+    // one position later; a sequence the pool cannot serve stops here
+    if (!s.done && !ensure_pages(a, b, s.c_pos + (a.speculative && s.c_pulse == P - 1 &&
+                                                  s.s_valid ? 1 : 0)))
+      s.done = 1;
   }
   // rows of the next step
   const bool live = act && !s.done;
@@ -724,7 +747,7 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
       update_block(a, s, b);
     }
   }
-  const bool live = act && !s.done;
+  bool live = act && !s.done;
   const bool pipe = block_pipelined(a.draft_len);
   int nrow = 0, pulse = 0, lrows = 0, pos0 = 0, slot0 = 0;
   bool guess_row = false, spec = false;
@@ -744,6 +767,13 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
       spec = pipe && pulse == P - 1 && P > 1 && s.s_valid && s.produced + nrow < s.max_new;
     }
     pos0 = s.c_pos + slot0;
+    // pages for the step's positions; a sequence the pool cannot serve stops here
+    if (!ensure_pages(a, b, spec ? s.c_pos + nrow : pos0 + nrow - 1)) {
+      s.done = 1;
+      live = false;
+      nrow = lrows = 0;
+      guess_row = spec = false;
+    }
   }
   int v[5] = {0, 0, 0, 0, 0};  // rows of pulse 0, 1, 2; logits rows; attention units
   v[pulse] = nrow;

@@ -24,7 +24,8 @@ BUF_EXIT_COUNTS = 8
 BUF_TOPK_IDX = 9
 BUF_TOKEN_KINDS = 10
 BUF_KV_LAYOUT = 11
-ABI_VERSION = 4
+BUF_KV_PAGES = 12
+ABI_VERSION = 5
 SEQSTATE_INTS = 32
 ROW_INTS = 8
 CTL_INTS = 16
@@ -72,6 +73,7 @@ class PulsarEngineConfig(ctypes.Structure):
         ("temperature", _c_f32), ("top_p", _c_f32), ("repetition_penalty", _c_f32),
         ("n_stop", _c_i32), ("stop_ids", _c_i32 * 8), ("seed", ctypes.c_uint64),
         ("draft_len", _c_i32), ("early_exit", _c_i32), ("early_exit_threshold", ctypes.c_double),
+        ("kv_pages", _c_i32),
     ]
 
 

@@ -37,11 +37,15 @@ class HipEngine:
                  speculative: bool = True, temperature: float = 0.7, top_p: float = 0.9,
                  repetition_penalty: float = 1.15, stop_ids: Iterable[int] = (0,),
                  seed: int = 0, all_logits: bool = False, max_ctx: Optional[int] = None,
-                 draft_len: int = 0, early_exit_threshold: Optional[float] = None):
+                 draft_len: int = 0, early_exit_threshold: Optional[float] = None,
+                 kv_pages: Optional[int] = None):
         """draft_len = 0 runs the reference's exact self-speculation; 1..7 the draft-block
         mode (up to draft_len pulse-0 drafts per round, one all-pulse verify of the block).
         early_exit_threshold (exact schedule only): the reference's adaptive early exit
-        (src/infer.py:536-547); None switches it off."""
+        (src/infer.py:536-547); None switches it off. kv_pages: pages of 64 positions in the
+        global layers' KV pool shared by the batch (None: enough for every sequence to
+        reach max_ctx); sequences take pages as they reach them, and run() raises when a
+        sequence found the pool spent."""
         self.lib = _lib.load()
         self.model = model
         self.batch = batch
@@ -68,6 +72,7 @@ class HipEngine:
         c.seed = seed & 0xFFFFFFFFFFFFFFFF
         c.early_exit = int(early_exit_threshold is not None)
         c.early_exit_threshold = float(early_exit_threshold) if early_exit_threshold is not None else 0.0
+        c.kv_pages = int(kv_pages or 0)
         self.early_exit_threshold = early_exit_threshold
         model.ensure_rope(c.max_ctx)
         self.cfg = c
@@ -150,6 +155,10 @@ class HipEngine:
         _lib.check(self.lib.pulsar_engine_generate(self.handle, max_steps, check_every, _stream(),
                                                    ctypes.byref(ran)))
         self.steps += ran.value
+        pages = self.kv_pages()
+        if pages["spent"]:
+            raise RuntimeError(f"KV page pool spent ({pages['pool']} pages): sequences that "
+                               f"needed another page stopped early")
         return ran.value
 
     # -- reading ---------------------------------------------------------------
@@ -204,10 +213,16 @@ class HipEngine:
         return [k[b, : st[b, ST_PRODUCED]].tolist() for b in range(self.batch)]
 
     def kv_layout(self) -> dict:
-        """Cache layout: ring positions of a sliding-window layer, pages per sequence of a
-        global layer, positions per page, kv heads."""
+        """Cache layout: ring positions of a sliding-window layer, page-table entries per
+        sequence of a global layer, positions per page, kv heads."""
         v = self._read(_lib.BUF_KV_LAYOUT, np.zeros(4, np.int32))
         return {"lcap": int(v[0]), "max_pages": int(v[1]), "page": int(v[2]), "hkv": int(v[3])}
+
+    def kv_pages(self) -> dict:
+        """Global-layer KV pages: pool size, pages handed out, whether a request found the
+        pool spent (since the last prefill, fill_kv or rewind)."""
+        v = self._read(_lib.BUF_KV_PAGES, np.zeros(3, np.int32))
+        return {"pool": int(v[0]), "used": int(v[1]), "spent": bool(v[2])}
 
     def exit_counts(self) -> np.ndarray:
         """Early exit: tokens of each sequence that left after pulse k, [batch, n_pulses],

@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     assert set(_declared()) == set(_lib.EXPORTED)
     lib.pulsar_abi_version.restype = ctypes.c_int
-    assert lib.pulsar_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.pulsar_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_struct_layouts_match_the_c_header(tmp_path):
