@@ -104,17 +104,19 @@ def ring_positions(cfg: PulsarConfig) -> int:
     return (cfg.sliding_window + MAX_BLOCK + PAGE - 1) // PAGE * PAGE
 
 
-def kv_cache_bytes(cfg: PulsarConfig, batch: int, max_ctx: int, es: int = 2) -> dict:
+def kv_cache_bytes(cfg: PulsarConfig, batch: int, max_ctx: int, es: int = 2,
+                   pool_pages: int = 0) -> dict:
     """Device bytes of the engine's KV cache for `batch` sequences of up to max_ctx positions:
-    sliding-window layers hold a ring of ring_positions() positions, global layers whole
-    pages up to max_ctx; K and V, kv heads x head_dim elements of es bytes each. The copy of
-    the rings prefill leaves for rewind is reported apart."""
+    sliding-window layers hold a ring of ring_positions() positions per sequence, global
+    layers a pool of pool_pages pages of PAGE positions (0: enough for every sequence to
+    reach max_ctx) plus one spare page; K and V, kv heads x head_dim elements of es bytes
+    each. The copy of the rings prefill leaves for rewind is reported apart."""
     per_pos = cfg.n_kv_heads * cfg.head_dim * 2 * es
     n_local = sum(1 for L in range(cfg.n_core) if cfg.is_local(L))
     n_global = cfg.n_core - n_local
-    pages = (max_ctx + PAGE - 1) // PAGE
+    pages = pool_pages or batch * ((max_ctx + PAGE - 1) // PAGE)
     local = n_local * batch * ring_positions(cfg) * per_pos
-    glob = n_global * batch * pages * PAGE * per_pos
+    glob = n_global * (pages + 1) * PAGE * per_pos
     return {"local": local, "global": glob, "total": local + glob, "rewind_copy": local}
 
 

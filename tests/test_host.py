@@ -238,8 +238,8 @@ def test_op_wrappers_check_operands_before_the_library_is_called(monkeypatch):
 
 def test_kv_cache_bytes_against_the_reference_table():
     """The reference's published unified-cache table (src/infer.py:834-846):
-    73.4 MB at 32k; the engine's footprint differs only by the ring's one-block slack and
-    page rounding."""
+    73.4 MB at 32k; the engine's footprint differs only by the ring's one-block slack, page
+    rounding and the pool's spare page."""
     cfg = PulsarConfig()
     want = {1024: 8.4, 4096: 14.7, 8192: 23.1, 16384: 39.8, 32768: 73.4}
     for ctx, mb in want.items():
@@ -247,5 +247,9 @@ def test_kv_cache_bytes_against_the_reference_table():
         got = traffic.kv_cache_bytes(cfg, 1, ctx)["total"]
         ref = traffic.reference_unified_kv_bytes(ctx)
         slack = 6 * (traffic.ring_positions(cfg) - min(ctx, 1024)) * 4 * 64 * 2 * 2
-        assert got - ref == slack + 2 * (-ctx % 64) * 4 * 64 * 2 * 2
+        spare = 2 * 64 * 4 * 64 * 2 * 2
+        assert got - ref == slack + 2 * (-ctx % 64) * 4 * 64 * 2 * 2 + spare
     assert traffic.ring_positions(cfg) == 1088
+    # a pool sized in pages instead of max_ctx
+    assert (traffic.kv_cache_bytes(cfg, 4, 1024, pool_pages=20)["global"]
+            == 2 * 21 * 64 * 4 * 64 * 2 * 2)
