@@ -988,8 +988,10 @@ def fill_kv_cache(cfg: PulsarConfig, layout: dict, ctx: int, seed: int, b: int, 
                   dtype=torch.bfloat16) -> RefKVCache:
     """RefKVCache of sequence b holding positions [0, ctx) of an engine cache filled by
     pulsar_engine_fill_kv(ctx, seed): sliding-window layers keep the last window positions
-    (ring slot = position mod lcap), global layers every position (page = b * max_pages +
-    position / page). K is position-major, V dimension-major in the engine's buffers."""
+    (ring slot = position mod lcap), global layers every position. Each element's value is
+    keyed by its index in a per-sequence layout (rings: the ring buffer; global layers:
+    page b * max_pages + position / page, whichever pool page the engine stores it in); K is
+    position-major, V dimension-major."""
     Hkv, hd, lcap, mp, pg = layout["hkv"], cfg.head_dim, layout["lcap"], layout["max_pages"], layout["page"]
     cache = RefKVCache(cfg)
     g = np.arange(Hkv, dtype=np.int64)[:, None, None]
