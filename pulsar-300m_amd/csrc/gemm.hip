@@ -27,6 +27,11 @@ namespace {
 __device__ __forceinline__ bf16x8_t load_bf16x8(const bf16* p) {
   return *reinterpret_cast<const bf16x8_t*>(p);
 }
+// Non-temporal (streaming) load: for weights a launch reads once, so that they do not push
+// out of the caches what later kernels read again (attention keys/values, activations).
+__device__ __forceinline__ bf16x8_t load_bf16x8_nt(const bf16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(p));
+}
 
 // Resolve the (A row, C row) pairs of this workgroup's 32-row tile into LDS.
 // Returns the number of valid rows (0 => nothing to do).
@@ -246,8 +251,9 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   do {                                                                                   \
     _Pragma("unroll") for (int i = 0; i < KITER; ++i) {                                  \
       const int64_t kt = (int64_t)(pass) * (kKPass / 32) + wv * KITER + i;               \
-      bw[i] = load_bf16x8(w0 + kt * 512);                                                \
-      if constexpr (kPair) bu[i] = load_bf16x8(w1 + kt * 512);                           \
+      bw[i] = XCD ? load_bf16x8(w0 + kt * 512) : load_bf16x8_nt(w0 + kt * 512);         \
+      if constexpr (kPair)                                                               \
+        bu[i] = XCD ? load_bf16x8(w1 + kt * 512) : load_bf16x8_nt(w1 + kt * 512);        \
     }                                                                                    \
   } while (0)
 
