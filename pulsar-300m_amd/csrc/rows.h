@@ -13,6 +13,9 @@ constexpr int kUnitSplit = kUnitWaves * 64;
 // engines whose context needs more 256-key splits than this use 2048-key splits in the
 // global layers
 constexpr int kLongCacheSplits = 16;
+// engines of at least this many sequences (units) take 1024-key splits in the long
+// engines' sliding-window layers, fewer keep 256-key splits
+constexpr int kManyUnits = 16;
 static_assert(kUnitSplit >= kSplitLen, "split partial slots are sized for kSplitLen");
 constexpr int kMaxRank = 16;    // re-injection gate rank bound
 

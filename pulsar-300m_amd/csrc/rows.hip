@@ -1603,7 +1603,10 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     // sliding-window layers (at most window + unit rows keys: two splits); shorter engines
     // take 256-key splits (one block per wave, many workgroups in parallel).
     const bool lng = a.max_splits_unit > kLongCacheSplits;
-    const int bpw = !lng ? 1 : (a.is_local ? 4 : 8);
+    // engines of few sequences keep 256-key splits in the sliding-window layers: 1024-key
+    // splits would leave most CUs idle there (two workgroups per unit and kv head)
+    const bool few = a.max_units < kManyUnits;
+    const int bpw = !lng ? 1 : (a.is_local ? (few ? 1 : 4) : 8);
     const int split = kUnitSplit * bpw;
     // a unit's keys [lo, hi] lie in the splits from lo's to hi's: at most max_ctx keys, and in
     // sliding-window layers window + rows - 1 keys, which can straddle one more split
