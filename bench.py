@@ -297,25 +297,29 @@ def verify_microbench(model, cfg, es, args):
 
 
 def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warmup, es=2,
-                 profile=True, draft_len=0, label=""):
+                 profile=True, draft_len=0, label="", speculative=True,
+                 early_exit_threshold=None):
     """Timed generations of a batch from one prefill: each generation rewinds (redraws the
     first tokens from the saved prefill logits with a new seed) and decodes until every
     sequence has n_new tokens (no stop ids). Returns accepted tokens/s, acceptance, the
     whole generation's algorithmic bytes against the HBM peak and, from one eagerly
     profiled generation, the dominant kernel class's bytes per launch against its
     event-timed launch duration."""
+    import numpy as np
     import torch
 
     from pulsar_engine.engine import HipEngine
 
     B, T = prompts.shape
     eng = HipEngine(model, batch=B, max_prompt=T, max_new=n_new, temperature=temperature,
-                    top_p=top_p, repetition_penalty=rp, stop_ids=[], seed=1, draft_len=draft_len)
+                    top_p=top_p, repetition_penalty=rp, stop_ids=[], seed=1, draft_len=draft_len,
+                    speculative=speculative, early_exit_threshold=early_exit_threshold)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     eng.prefill(prompts)
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
+    exits = np.zeros(cfg.default_pulses, np.int64)
 
     def generation(seed):
         eng.rewind(seed)
@@ -334,6 +338,8 @@ def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warm
         produced += p
         tests += t
         accepted += a
+        if early_exit_threshold is not None:
+            exits += eng.exit_counts().sum(axis=0)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     out = {"value": round(produced / elapsed, 1), "unit": "tokens/s",
@@ -341,6 +347,8 @@ def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warm
            "pulse_steps_per_generation": round(nsteps / steps, 1),
            "acceptance_rate": round(accepted / tests, 4) if tests else None,
            "prefill_ms_first_call": round(prefill_s * 1e3, 1)}
+    if early_exit_threshold is not None:
+        out["exits_per_pulse"] = exits.tolist()
     log(f"{label}: {steps} timed generations, {produced} tokens in {elapsed:.3f}s, "
         f"acceptance {accepted}/{tests}")
     if profile:
@@ -365,6 +373,33 @@ def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warm
             for k, v in net.items()}
     eng.close()
     return out
+
+
+def early_exit_run(model, cfg, prompts, args) -> dict:
+    """The headline workload with the reference's adaptive early exit
+    (set_early_exit_threshold, src/infer.py:536-547): plain decoding without and with the
+    exit, and the self-speculative schedule with it (only accepted drafts can exit there,
+    as in the reference), each one timed generation after a warm one."""
+    kw = dict(steps=1, warmup=1, profile=False)
+    thr = args.early_exit_threshold
+    sampling = (args.temperature, args.top_p, args.repetition_penalty)
+    plain = run_workload(model, cfg, prompts, args.new_tokens, *sampling, speculative=False,
+                         label="plain", **kw)
+    plain_ee = run_workload(model, cfg, prompts, args.new_tokens, *sampling, speculative=False,
+                            early_exit_threshold=thr, label="plain early exit", **kw)
+    spec_ee = run_workload(model, cfg, prompts, args.new_tokens, *sampling,
+                           early_exit_threshold=thr, label="self-speculative early exit", **kw)
+    return {"threshold": thr,
+            "note": "random-init weights: the top-1 probability of every pulse-0 pass lies "
+                    "between 0.99 and 0.999 (the tied-embedding self-logit dominates), so at "
+                    "this threshold every eligible token leaves after pulse 0",
+            "plain": {k: plain[k] for k in ("value", "unit", "pulse_steps_per_generation")},
+            "plain_early_exit": {k: plain_ee[k] for k in ("value", "unit",
+                                                          "pulse_steps_per_generation",
+                                                          "exits_per_pulse")},
+            "self_speculative_early_exit": {k: spec_ee[k] for k in (
+                "value", "unit", "pulse_steps_per_generation", "acceptance_rate",
+                "exits_per_pulse")}}
 
 
 def draft_block_run(model, cfg, prompts, args):
@@ -657,6 +692,8 @@ def main() -> int:
                     help="draft length of the draft-block run (0 skips it)")
     ap.add_argument("--no-verify", action="store_true", help="skip the verify microbenchmark")
     ap.add_argument("--no-ops", action="store_true", help="skip the op-surface figures")
+    ap.add_argument("--no-early-exit", action="store_true", help="skip the early-exit runs")
+    ap.add_argument("--early-exit-threshold", type=float, default=0.99)
     ap.add_argument("--only", choices=("c4", "c5"),
                     help="run only that workload, unprofiled (kernel traces)")
     ap.add_argument("--verify-only", action="store_true",
@@ -816,6 +853,10 @@ def main() -> int:
     if args.draft_len > 0:
         block = draft_block_run(model, cfg, prompts, args)
         log(f"draft-block run: {json.dumps(block)}")
+    early = None
+    if not args.no_early_exit:
+        early = early_exit_run(model, cfg, prompts, args)
+        log(f"early exit: {json.dumps(early)}")
     verify = None
     if not args.no_verify:
         verify = verify_microbench(model, cfg, es, args)
@@ -894,6 +935,7 @@ def main() -> int:
         "c4": c4,
         "c5": c5,
         "kv_cache_batch1_bf16": kv_footprint(cfg),
+        "early_exit": early,
         "op_surface": ops,
     }
     print(json.dumps(line), flush=True)
