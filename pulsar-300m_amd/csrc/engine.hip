@@ -404,6 +404,8 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
   const int eager_experts = (int64_t)MR * e.K >= 2 * (int64_t)e.E ? 1 : 0;
   const bool wide = dt == PULSAR_BF16 && MR >= kWideRows;
   const bool wide_head = dt == PULSAR_BF16 && MR >= kWideHeadRows;
+  // bf16: the decode attention finishes q, k and v itself (no qk_post launch)
+  const bool fuse_post = dt == PULSAR_BF16;
   if (e.prof_on) {
     // an empty timed group: the fixed cost of an event pair around a kernel launch
     PULSAR_TRY(prof_delay(e, s));
@@ -475,7 +477,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     qa.cos = loc ? m.rope_cos_local : m.rope_cos_global;
     qa.sin = loc ? m.rope_sin_local : m.rope_sin_global;
     qa.kv = e.kv;
-    PULSAR_TIMED(PC_QKPOST, launch_qk_post(qa, dt, MR, s));
+    if (!fuse_post) PULSAR_TIMED(PC_QKPOST, launch_qk_post(qa, dt, MR, s));
     AttnArgs aa{};
     aa.ctl = ctl;
     aa.rows = rows;
@@ -498,6 +500,17 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     aa.window = m.window;
     aa.scale = 0.125f;
     aa.kv = e.kv;
+    if (fuse_post) {
+      aa.post = 1;
+      aa.base_seq_len = m.base_seq_len;
+      aa.eps = m.rms_eps;
+      aa.q_norm = m.q_norm[l];
+      aa.k_norm = m.k_norm[l];
+      aa.v_lambda = m.v_lambda[l];
+      aa.v_first = e.v_first;
+      aa.cos = qa.cos;
+      aa.sin = qa.sin;
+    }
     PULSAR_TIMED(PC_ATTN, launch_attn_decode(aa, dt, MR, s));
     g = gemm_base(e);
     g.A = e.attn_out;

@@ -190,6 +190,17 @@ struct AttnArgs {
   int H, Hkv, layer, is_local, window, prefill_T;
   float scale;
   KVDesc kv;
+  // bf16 decode: q/k/v post-processing (what qk_post_kernel does) fused into the attention;
+  // qkv then holds the raw projection (q | k | v columns)
+  int post;
+  int base_seq_len;
+  float eps;
+  const float* q_norm;    // [P][H][64]
+  const float* k_norm;    // [P][Hkv][64]
+  const float* v_lambda;  // [P]
+  void* v_first;          // [rows][Hkv*64]
+  const float* cos;       // [positions][32]
+  const float* sin;
 };
 
 struct RouterArgs {

@@ -288,6 +288,8 @@ __global__ void __launch_bounds__(256) norm_rows_kernel(NormArgs a) {
 // ---------------------------------------------------------------------------
 // QK-norm + RoPE (+YaRN) on q heads, value residual + K-norm + RoPE on kv heads and the
 // cache write. One wave per head vector (lane = element, rotate-half partner = lane^32).
+// Prefill and fp32 decode; bf16 decode does the same arithmetic inside
+// attn_decode_unit_kernel.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ void __launch_bounds__(256) qk_post_kernel(QKPostArgs a) {
@@ -603,6 +605,10 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
 // V block per lane (attn_key_of). P = exp(S - max) in fp32 is split into bf16 hi + lo (hi + lo =
 // P to 2^-16 relative), two products each. The last split block to count in merges the
 // split partials, normalises, rounds as the SDPA output and applies the head gate.
+// The step's q/k/v post-processing is fused in (no separate launch): qkv holds the raw
+// projection; every split finishes the unit's queries, and the split holding a row's own
+// position finishes its key and value, patches them into the loaded block and stores them
+// to the caches at the end (the arithmetic of qk_post_kernel, bit for bit).
 // COLS = 8 serves units of up to 2 rows (exact mode), 16 up to 4, 32 up to 8. BPW = 64-key
 // blocks per wave and split: long caches take BPW = 8 (2048-key splits) in the global
 // layers and 4 in the sliding-window layers. Holding the next block in registers while
@@ -650,8 +656,54 @@ __device__ __forceinline__ void attn_load_block(const bf16* Kc, const bf16* Vc, 
     }
 }
 
+// Pulse of step row `row` from the step's pulse row ranges [ps[q], ps[q] + pc[q]) (rows of
+// a step are sorted by pulse).
+__device__ __forceinline__ int step_row_pulse(const int* ps, const int* pc, int row) {
+  int p = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxPulses; ++q)
+    if (row >= ps[q] && row < ps[q] + pc[q]) p = q;
+  return p;
+}
+
+// Replace, in a loaded block at kb, the keys and values of positions [f_lo, f_hi] (rows
+// z = pos - pos0 of the unit, finished in LDS by this workgroup) by their new values.
+// Lane (m16, kq) holds K rows attn_key_of(kt, m16), dims 32 ks + 8 kq .. + 7, and V^T rows
+// (dims) 16 mt + m16 of keys 32 s2 + 8 kq + e.
+__device__ __forceinline__ void attn_patch_fresh(AttnKV& r, int kb, int f_lo, int f_hi, int pos0,
+                                                 int m16, int kq, const uint16_t (*fk)[64],
+                                                 const uint16_t (*fv)[64]) {
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    const int p = kb + attn_key_of(kt, m16);
+    if (p >= f_lo && p <= f_hi) {
+      const int z = p - pos0;
+      r.k[kt][0] = *reinterpret_cast<const attn_bf16x8*>(&fk[z][kq * 8]);
+      r.k[kt][1] = *reinterpret_cast<const attn_bf16x8*>(&fk[z][32 + kq * 8]);
+    }
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int p = kb + 32 * s2 + 8 * kq + e;
+      if (p >= f_lo && p <= f_hi) {
+        const int z = p - pos0;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const __bf16 v = __builtin_bit_cast(__bf16, fv[z][16 * mt + m16]);
+          if (e < 4)
+            r.vl[mt][s2][e] = v;
+          else
+            r.vh[mt][s2][e - 4] = v;
+        }
+      }
+    }
+}
+
 template <int COLS, int BPW>
-__global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(64 * kUnitWaves)
+__attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel(AttnArgs a) {
   constexpr int NQT = (COLS + 15) / 16;
   constexpr int NZ = COLS / 4;
   constexpr int SPLIT = kUnitSplit * BPW;
@@ -663,9 +715,19 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   // from sinking the descriptor load below the exit branch
   const int n_units = a.ctl->n_units;
   const AttnUnit un = a.units[u];
+  // the step's pulse row ranges and the value-residual weight, read with the unit: scalar
+  // loads ahead of every store and asm statement of the kernel (after either, the compiler
+  // reads them with vector loads, each a round trip)
+  int ps[kMaxPulses], pc[kMaxPulses];
+#pragma unroll
+  for (int q = 0; q < kMaxPulses; ++q) {
+    ps[q] = a.ctl->pulse_start[q];
+    pc[q] = a.ctl->pulse_count[q];
+  }
+  const float lv0 = a.v_lambda[0];
   asm volatile("" ::"s"(un.seq), "s"(un.n), "s"(un.pos0), "s"(un.row[0]), "s"(un.row[1]),
                "s"(un.row[2]), "s"(un.row[3]), "s"(un.row[4]), "s"(un.row[5]), "s"(un.row[6]),
-               "s"(un.row[7]));
+               "s"(un.row[7]), "s"(ps[1]), "s"(ps[2]), "s"(pc[1]), "s"(pc[2]), "s"(lv0));
   asm volatile("" ::"s"(a.kl.k), "s"(a.kl.v), "s"(a.kl.lcap), "s"(a.kl.max_pages),
                "s"(a.kl.page_table),
                "s"(a.is_local), "s"(a.window), "s"(a.Hkv), "s"(a.qkv), "s"(a.ldq));
@@ -682,7 +744,119 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   const int s_lo = base + s * SPLIT;
   const int s_hi = min(uhi, s_lo + SPLIT - 1);
   constexpr int kStride = kUnitWaves * 64;
+  const int kb0 = s_lo + wv * 64;
+  // Post-processing of the step's projections (what qk_post_kernel does, fused): every split
+  // finishes the unit's query columns (wave per column, lane = dimension: RMSNorm over the
+  // head, RoPE, YaRN query scale); the split whose keys hold a unit row's own position
+  // finishes that row's key and value (value residual, cache stores) and patches them into
+  // the block registers it loaded, so no load waits for the stores. Loads first (queries,
+  // fresh rows), then the first key block, then the arithmetic.
+  constexpr int NQ = COLS / kUnitWaves;  // query columns per wave
+  constexpr int NF = NZ / 2;             // fresh (row, key | value) tasks per wave
+  __shared__ __align__(16) uint16_t qs[COLS][64];
+  __shared__ __align__(16) uint16_t fk[NZ][64], fv[NZ][64];
+  const int zlo = max(0, s_lo - un.pos0), zhi = min(un.n - 1, s_hi - un.pos0);
+  const bf16* qkv = reinterpret_cast<const bf16*>(a.qkv);
+  const int H = a.H, Hkv = a.Hkv, jr = lane & 31;
+  // Loads without branches (addresses clamped into range, results unused where invalid): a
+  // load on one side of a branch makes the join wait for every load in flight. Order: the
+  // post operands, then the wave's first block (a wave without blocks loads the split's last
+  // block and does not use it; in global layers its page read waits with the post operands,
+  // all in flight together).
+  const int kbf = min(kb0, s_hi / 64 * 64);
+  float qx[NQ], qw[NQ], qcs[NQ], qsn[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int c = wv + kUnitWaves * i, z = c >> 2, head = g * 4 + (c & 3);
+    const int row = max(unit_row<NZ>(un, z), 0);
+    const int pos = z < un.n ? un.pos0 + z : un.pos0, pulse = step_row_pulse(ps, pc, row);
+    qx[i] = to_f(qkv[(int64_t)row * a.ldq + head * 64 + lane]);
+    qw[i] = a.q_norm[((int64_t)pulse * H + head) * 64 + lane];
+    qcs[i] = a.cos[(int64_t)pos * 32 + jr];
+    qsn[i] = a.sin[(int64_t)pos * 32 + jr];
+  }
+  float fx[NF], fw[NF], fcs[NF], fsn[NF], fvf[NF];
+  int fpg[NF];  // global layers: pool page of the fresh position
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    const int t = wv + kUnitWaves * i, z = min(zlo + (t >> 1), max(zhi, 0));
+    const int row = max(unit_row<NZ>(un, z), 0), pos = un.pos0 + z;
+    const int pulse = step_row_pulse(ps, pc, row);
+    const int col = (t & 1) == 0 ? (H + g) * 64 : (H + Hkv + g) * 64;
+    fx[i] = to_f(qkv[(int64_t)row * a.ldq + col + lane]);
+    fw[i] = a.k_norm[((int64_t)pulse * Hkv + g) * 64 + lane];
+    fcs[i] = a.cos[(int64_t)pos * 32 + jr];
+    fsn[i] = a.sin[(int64_t)pos * 32 + jr];
+    fvf[i] = to_f(reinterpret_cast<const bf16*>(a.v_first)[(int64_t)row * Hkv * 64 + g * 64 + lane]);
+    fpg[i] = a.kl.page_table[(int64_t)un.seq * a.kl.max_pages + pos / kPage];
+  }
   AttnKV cur;
+  attn_load_block(Kc, Vc, kv_block_layer(a.kl, a.is_local, Hkv, un.seq, g, kbf), m16, kq, cur);
+  auto norm_rope = [&](float x, float w, float cs, float sn) {
+    const float ss = wave_sum(x * x);
+    const float inv = 1.0f / sqrtf(ss / 64.0f + a.eps);
+    const float y = rnd<bf16>(w * (x * inv));
+    const float p = __shfl_xor(y, 32, 64);
+    return rnd<bf16>(lane < 32 ? y * cs - p * sn : y * cs + p * sn);
+  };
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int c = wv + kUnitWaves * i, z = c >> 2;
+    float o = 0.f;
+    if (unit_row<NZ>(un, z) >= 0) {
+      o = norm_rope(qx[i], qw[i], qcs[i], qsn[i]);
+      const int pos = un.pos0 + z;
+      if (!a.is_local && pos + 1 > a.base_seq_len) {
+        const double b0 = (double)a.base_seq_len;
+        const double pp = (double)(pos + 1) > b0 ? (double)(pos + 1) : b0;
+        const float sc = (float)(1.0 + 0.1 * log(pp / b0));
+        o = rnd<bf16>(o * sc);
+      }
+    }
+    qs[c][lane] = f2bf(o).u;
+  }
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    const int t = wv + kUnitWaves * i, z = zlo + (t >> 1);
+    if (z > zhi) continue;
+    if ((t & 1) == 0) {
+      fk[z][lane] = f2bf(norm_rope(fx[i], fw[i], fcs[i], fsn[i])).u;
+    } else {
+      float v = fx[i];
+      if (step_row_pulse(ps, pc, unit_row<NZ>(un, z)) == 0 && a.layer > 0)
+        v = rnd<bf16>(rnd<bf16>(rnd<bf16>(1.0f - lv0) * v) + rnd<bf16>(lv0 * fvf[i]));
+      fv[z][lane] = f2bf(v).u;
+    }
+  }
+  // the fresh keys and values go to the caches at the end of the kernel (stores count in
+  // the same counter as loads: issued here, the block loads' wait would include them)
+  auto store_fresh = [&]() {
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+      const int t = wv + kUnitWaves * i, z = zlo + (t >> 1);
+      if (z > zhi) continue;
+      const int pos = un.pos0 + z;
+      if ((t & 1) == 0) {
+        bf16* kc = reinterpret_cast<bf16*>(const_cast<void*>(a.kl.k));
+        const int64_t ko = a.is_local
+            ? (((int64_t)un.seq * Hkv + g) * a.kl.lcap + pos % a.kl.lcap) * kHeadDim
+            : (((int64_t)fpg[i] * Hkv + g) * kPage + pos % kPage) * kHeadDim;
+        kc[ko + lane].u = fk[z][lane];
+      } else {
+        const int row = unit_row<NZ>(un, z);
+        bf16 v;
+        v.u = fv[z][lane];
+        if (a.layer == 0 && step_row_pulse(ps, pc, row) == 0)
+          reinterpret_cast<bf16*>(a.v_first)[(int64_t)row * Hkv * 64 + g * 64 + lane] = v;
+        bf16* vc = reinterpret_cast<bf16*>(const_cast<void*>(a.kl.v));
+        const int64_t vo = a.is_local
+            ? (((int64_t)un.seq * Hkv + g) * kHeadDim + lane) * a.kl.lcap + pos % a.kl.lcap
+            : (((int64_t)fpg[i] * Hkv + g) * kHeadDim + lane) * kPage + pos % kPage;
+        vc[vo] = v;
+      }
+    }
+  };
+  __syncthreads();
   int qlo[NQT], qhi[NQT];
   attn_bf16x8 qb[NQT][2];
 #pragma unroll
@@ -692,11 +866,10 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
     const int qpos = un.pos0 + z;
     qlo[t] = a.is_local ? max(0, qpos - a.window + 1) : 0;
     qhi[t] = qrow < 0 ? -1 : qpos;
-    const bf16* qp = reinterpret_cast<const bf16*>(a.qkv) + (int64_t)(qrow < 0 ? 0 : qrow) * a.ldq +
-                     (g * 4 + (c & 3)) * 64 + kq * 8;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      qb[t][ks] = qrow >= 0 ? *reinterpret_cast<const attn_bf16x8*>(qp + ks * 32) : zero;
+      qb[t][ks] = c < COLS ? *reinterpret_cast<const attn_bf16x8*>(&qs[c < COLS ? c : 0][ks * 32 + kq * 8])
+                           : zero;
   }
   float mrun[NQT], lrun[NQT];
   attn_f32x4 o[NQT][4];
@@ -712,10 +885,12 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
   // keys every row of the unit sees: [lo of the last row, position of the first row]
   const int full_lo = a.is_local ? max(0, uhi - a.window + 1) : 0;
   const int full_hi = un.pos0;
-  const int kb0 = s_lo + wv * 64;
+  const int f_lo = un.pos0 + zlo, f_hi = un.pos0 + zhi;  // this split's fresh positions
   for (int kb = kb0; kb <= s_hi; kb += kStride) {
-    attn_load_block(Kc, Vc, kv_block_layer(a.kl, a.is_local, a.Hkv, un.seq, g, kb), m16, kq,
-                    cur);
+    if (kb != kb0)
+      attn_load_block(Kc, Vc, kv_block_layer(a.kl, a.is_local, a.Hkv, un.seq, g, kb), m16, kq,
+                      cur);
+    if (kb <= f_hi && kb + 63 >= f_lo) attn_patch_fresh(cur, kb, f_lo, f_hi, un.pos0, m16, kq, fk, fv);
     const auto& kk = cur.k;
     const auto& vl = cur.vl;
     const auto& vh = cur.vh;
@@ -833,7 +1008,10 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
       }
     }
   }
-  if (nsplit == 1) return;
+  if (nsplit == 1) {
+    store_fresh();
+    return;
+  }
   // Hand-off to the merging block without a release/acquire pair. Every partial is written
   // and read with agent-scope atomics, which gfx950 issues as `global_store ... sc1` /
   // `global_load ... sc1`: coherent at device scope on their own (written through and read
@@ -855,6 +1033,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves) attn_decode_unit_kernel(AttnA
     if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
+  store_fresh();
   if (!s_last) return;
   attn_merge_splits<COLS>(a, u, g, un, nsplit);
 }
@@ -1613,6 +1792,8 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     int zs = (a.max_ctx + split - 1) / split;
     if (a.is_local) zs = std::min(zs, (a.window + a.unit_rows - 1 + split - 1) / split + 1);
     const dim3 grid(a.max_units, a.Hkv, zs);
+    if (!a.post || !a.q_norm || !a.k_norm || !a.v_lambda || !a.v_first || !a.cos || !a.sin)
+      return fail(PULSAR_ERR_INVALID, "decode attention: bf16 takes the q/k/v post operands");
     AttnArgs b = a;
     b.kl.k = a.kv.k[a.layer];
     b.kl.v = a.kv.v[a.layer];
