@@ -245,15 +245,25 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   const int passes = g0 ? KMUL0 : 1;
   const int kb = wv * (KITER * 32) + kq * 8;
   const bf16x8_t zero = {};
-  bf16x8_t bw[KITER], bu[KITER], xa[KITER];
+  // every pass's weights stay in registers (the all-rows group of a KMUL0 launch loads its
+  // second K half with the first, not one round trip after the first half's products)
+  bf16x8_t bw[KITER * KMUL0], bu[KITER], xa[KITER];
   // k tile of step i of this wave in pass p: p * (K / 32 per pass) + wv * KITER + i
 #define PULSAR_LOAD_W(pass)                                                              \
   do {                                                                                   \
     _Pragma("unroll") for (int i = 0; i < KITER; ++i) {                                  \
       const int64_t kt = (int64_t)(pass) * (kKPass / 32) + wv * KITER + i;               \
-      bw[i] = XCD ? load_bf16x8(w0 + kt * 512) : load_bf16x8_nt(w0 + kt * 512);         \
+      bw[(pass) * KITER + i] = XCD ? load_bf16x8(w0 + kt * 512) : load_bf16x8_nt(w0 + kt * 512); \
       if constexpr (kPair)                                                               \
         bu[i] = XCD ? load_bf16x8(w1 + kt * 512) : load_bf16x8_nt(w1 + kt * 512);        \
+    }                                                                                    \
+  } while (0)
+#define PULSAR_LOAD_W_REST()                                                             \
+  do {                                                                                   \
+    if constexpr (KMUL0 > 1) {                                                           \
+      if (g0) {                                                                          \
+        _Pragma("unroll") for (int p = 1; p < KMUL0; ++p) PULSAR_LOAD_W(p);              \
+      }                                                                                  \
     }                                                                                    \
   } while (0)
 
@@ -292,6 +302,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
     l0 = entry_load<MODE>(g, group, i0);
     l1 = entry_load<MODE>(g, group, i1);
     PULSAR_LOAD_W(0);
+    PULSAR_LOAD_W_REST();
   }
   while (true) {
     __builtin_amdgcn_sched_barrier(0);
@@ -311,14 +322,15 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
     const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * lda;
     const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * lda;
     f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
-    for (int pass = 0; pass < passes; ++pass) {
-      if (pass > 0) PULSAR_LOAD_W(pass);
+#pragma unroll
+    for (int pass = 0; pass < KMUL0; ++pass) {
+      if (pass >= passes) break;
 #pragma unroll
       for (int i = 0; i < KITER; ++i)
         xa[i] = (EAGER || ar0 >= 0) ? load_bf16x8(a0 + pass * kKPass + kb + 32 * i) : zero;
 #pragma unroll
       for (int i = 0; i < KITER; ++i) {
-        c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[i], c00, 0, 0, 0);
+        c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[pass * KITER + i], c00, 0, 0, 0);
         if constexpr (kPair) c01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bu[i], c01, 0, 0, 0);
       }
       if (two) {  // the second 16-row block reuses the A registers (fewer VGPRs, more waves)
@@ -327,7 +339,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
           xa[i] = ar1 >= 0 ? load_bf16x8(a1 + pass * kKPass + kb + 32 * i) : zero;
 #pragma unroll
         for (int i = 0; i < KITER; ++i) {
-          c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[i], c10, 0, 0, 0);
+          c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[pass * KITER + i], c10, 0, 0, 0);
           if constexpr (kPair) c11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bu[i], c11, 0, 0, 0);
         }
       }
@@ -370,9 +382,9 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
     i1 = tile0 + min(m + 16, n - 1);
     l0 = entry_load<MODE>(g, group, i0);
     l1 = entry_load<MODE>(g, group, i1);
-    if (passes > 1) PULSAR_LOAD_W(0);
   }
 #undef PULSAR_LOAD_W
+#undef PULSAR_LOAD_W_REST
 }
 
 // fp32: 4 waves per workgroup, one output column per wave, 32-row tile.

@@ -1347,14 +1347,25 @@ __global__ void __launch_bounds__(256) norm_router_kernel(RouterArgs a) {
   constexpr int EW = E / 4;
   __shared__ float lg[E];
   const int r = blockIdx.x;
-  if (r >= a.ctl->n_rows) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int pulse = a.rows[r].pulse;
   const int D = a.D, i0 = lane * EPL;
+  // No early exit (the compiler would hold every load behind the row-count test): each
+  // block computes its row, in bounds for every block since the grid is the engine's row
+  // capacity, and only the stores test the count. The step's row count and pulse ranges
+  // come in one scalar read of the control block, so the pulse-indexed weights wait one
+  // round trip, not two.
   const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)r * D;
-  const float* W = a.w + ((int64_t)pulse * E + wv * EW) * D;
   float xv[EPL], nw[EPL], wt[EW][EPL];
   ldv<EPL>(x + i0, xv);
+  int ps[kMaxPulses], pc[kMaxPulses];
+#pragma unroll
+  for (int q = 0; q < kMaxPulses; ++q) {
+    ps[q] = a.ctl->pulse_start[q];
+    pc[q] = a.ctl->pulse_count[q];
+  }
+  const bool live = r < a.ctl->n_rows;
+  const int pulse = step_row_pulse(ps, pc, r);
+  const float* W = a.w + ((int64_t)pulse * E + wv * EW) * D;
   ldv<EPL>(a.norm_w + (int64_t)pulse * D + i0, nw);
 #pragma unroll
   for (int q = 0; q < EW; ++q) ldv<EPL>(W + (int64_t)q * D + i0, wt[q]);
@@ -1365,7 +1376,7 @@ __global__ void __launch_bounds__(256) norm_router_kernel(RouterArgs a) {
   float y[EPL];
 #pragma unroll
   for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(nw[c] * (xv[c] * inv));
-  if (wv == 0) stv<EPL>(reinterpret_cast<T*>(a.xn) + (int64_t)r * D + i0, y);
+  if (wv == 0 && live) stv<EPL>(reinterpret_cast<T*>(a.xn) + (int64_t)r * D + i0, y);
 #pragma unroll
   for (int q = 0; q < EW; ++q) {
     float acc = 0.f;
@@ -1375,7 +1386,7 @@ __global__ void __launch_bounds__(256) norm_router_kernel(RouterArgs a) {
     if (lane == 0) lg[wv * EW + q] = acc;
   }
   __syncthreads();
-  if (wv != 0) return;
+  if (wv != 0 || !live) return;
   // sigmoid of mean-centred logits, + bias; rank = #experts ahead (value desc, index asc)
   const bool act = lane < E;
   const float l = act ? lg[lane] : 0.f;
@@ -1629,27 +1640,48 @@ template <typename T, int EPL, int KT>
 __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
   // one wave per row; lane owns elements [lane*EPL, lane*EPL + EPL)
   const int r = blockIdx.x;
-  const int n = a.ctl ? a.ctl->n_rows : a.m_fixed;
-  if (r >= n) return;
   const int K = a.K, D = a.D, lane = threadIdx.x, i0 = lane * EPL;
-  const int pulse = a.ctl ? a.rows[r].pulse : a.pulse;
+  // The row's operands go out before the row-count test (every block's row is in bounds:
+  // the grid is the row capacity), the routing weights as plain loads without a branch; the
+  // step's row count and pulse ranges come in one scalar read of the control block, so only
+  // the pulse-indexed scale waits for it.
   const T* shp = reinterpret_cast<const T*>(a.shared) + (int64_t)r * D + i0;
   const T* rop = reinterpret_cast<const T*>(a.routed) + (int64_t)r * K * D + i0;
-  const T* rsp = reinterpret_cast<const T*>(a.routed_scale) + (int64_t)pulse * D + i0;
   T* h = reinterpret_cast<T*>(a.h) + (int64_t)r * D + i0;
   float hv[EPL], sh[EPL], rs[EPL], ro[KT][EPL];
   ldv<EPL>(h, hv);
   ldv<EPL>(shp, sh);
-  ldv<EPL>(rsp, rs);
 #pragma unroll
   for (int k = 0; k < KT; ++k) ldv<EPL>(rop + (int64_t)(k < K ? k : 0) * D, ro[k]);
+  // routing weight k from lane k of one vector load (a per-slot scalar load would sit in a
+  // block of its own behind a wait)
+  const float wl = a.topk_w[(int64_t)r * K + min(lane, K - 1)];
   float w[KT];
+#pragma unroll
+  for (int k = 0; k < KT; ++k) w[k] = __shfl(wl, k < K ? k : 0, 64);
+  int n = a.m_fixed, pulse = a.pulse;
+  if (a.ctl) {
+    int ps[kMaxPulses], pc[kMaxPulses];
+#pragma unroll
+    for (int q = 0; q < kMaxPulses; ++q) {
+      ps[q] = a.ctl->pulse_start[q];
+      pc[q] = a.ctl->pulse_count[q];
+    }
+    n = a.ctl->n_rows;
+    pulse = step_row_pulse(ps, pc, r);
+  }
+  // no early exit (loads would wait behind the test): only the stores test the row count
+  const bool live = r < n;
+  ldv<EPL>(reinterpret_cast<const T*>(a.routed_scale) + (int64_t)pulse * D + i0, rs);
+  float nwn[EPL];
+  if (a.next_norm) ldv<EPL>(a.next_norm + (int64_t)pulse * D + i0, nwn);
   bool kept[KT];
 #pragma unroll
-  for (int k = 0; k < KT; ++k) {
-    const int kk = k < K ? k : 0;
-    w[k] = a.topk_w[(int64_t)r * K + kk];
-    kept[k] = a.keep ? a.keep[(int64_t)r * K + kk] != 0 : true;
+  for (int k = 0; k < KT; ++k) kept[k] = true;
+  if (a.keep) {
+    const int kl = a.keep[(int64_t)r * K + min(lane, K - 1)];
+#pragma unroll
+    for (int k = 0; k < KT; ++k) kept[k] = __shfl(kl, k < K ? k : 0, 64) != 0;
   }
   // K is uniform: one branch per top-k slot, the element loops inside
   float routed[EPL];
@@ -1678,15 +1710,15 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
 #pragma unroll
     for (int c = 0; c < EPL; ++c) hv[c] = rnd<T>(hv[c] + rnd<T>(sh[c] + routed[c]));
   }
+  if (!live) return;
   stv<EPL>(h, hv);
   if (a.next_norm) {
-    float ss = 0.f, nw[EPL], y[EPL];
+    float ss = 0.f, y[EPL];
 #pragma unroll
     for (int c = 0; c < EPL; ++c) ss += hv[c] * hv[c];
-    ldv<EPL>(a.next_norm + (int64_t)pulse * D + i0, nw);
     const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
 #pragma unroll
-    for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(nw[c] * (hv[c] * inv));
+    for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(nwn[c] * (hv[c] * inv));
     stv<EPL>(reinterpret_cast<T*>(a.xn) + (int64_t)r * D + i0, y);
   }
 }
