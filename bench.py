@@ -43,7 +43,6 @@ CLASS_KERNELS = {
     "lm_head": ["gemm_bf16_kernel<4, 4, 3, 1, false, false>"],
     "router": ["norm_router_kernel<bf16, 16, 16>"],
     "moe_combine": ["moe_combine_rows_kernel<bf16, 16, 4>"],
-    "qk_post": ["qk_post_kernel<bf16>"],
     "sample": ["sample_kernel<bf16, 32, 1024>"],
     "pulse_input": ["pulse_input_kernel<bf16, 16, 8, true>"],
     "pulse_output": ["pulse_output_kernel<bf16>"],

@@ -20,8 +20,16 @@ CLASSES = (
 )
 
 
-def step_bytes(cfg: PulsarConfig, es: int, rows, expert_counts, n_lrows: int) -> dict:
-    """rows: iterable of (seq, pulse, pos); expert_counts: [layers][E] rows per expert."""
+def step_bytes(cfg: PulsarConfig, es: int, rows, expert_counts, n_lrows: int,
+               fused_post: bool | None = None) -> dict:
+    """rows: iterable of (seq, pulse, pos); expert_counts: [layers][E] rows per expert.
+
+    fused_post (default: es == 2, the bf16 engine): the q/k/v post-processing runs inside
+    the decode attention, which then also reads each row's raw keys and values and writes
+    them to the cache (queries are finished in registers, not written back); no qk_post
+    class."""
+    if fused_post is None:
+        fused_post = es == 2
     D, H, Hk, hd = cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
     E, K, de, ds, V = cfg.n_routed_experts, cfg.top_k, cfg.d_expert, cfg.d_shared, cfg.vocab_size
     q_dim, qkv = cfg.q_dim, cfg.qkv_dim
@@ -48,8 +56,11 @@ def step_bytes(cfg: PulsarConfig, es: int, rows, expert_counts, n_lrows: int) ->
         assigned = int(sum(expert_counts[L]))
         out["rmsnorm"] += 2 * (n * D * es * 2 + npul * D * 4)
         out["qkv_gate_gemm"] += npul * (qkv + H) * D * es + n * (D + qkv + H) * es
-        out["qk_post"] += n * (qkv * es * 2 + 2 * Hk * hd * es)
         out["attention"] += ctx * Hk * hd * 2 * es + n * (q_dim + H + q_dim) * es
+        if fused_post:
+            out["attention"] += n * 4 * Hk * hd * es
+        else:
+            out["qk_post"] += n * (qkv * es * 2 + 2 * Hk * hd * es)
         out["wo_gemm"] += npul * D * q_dim * es + n * (q_dim + 2 * D) * es
         out["router"] += npul * E * D * 4 + n * D * es
         out["shared_gate_up"] += 2 * ds * D * es + n * (D + ds) * es

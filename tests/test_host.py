@@ -33,13 +33,19 @@ def test_attention_bytes_count_a_sequences_key_blocks_once():
     n_local = sum(cfg.is_local(L) for L in range(cfg.n_core))
     n_global = cfg.n_core - n_local
     kv = lambda keys: keys * hk * hd * 2 * es  # noqa: E731
-    act = cfg.q_dim + cfg.n_heads + cfg.q_dim
-    assert one == n_local * kv(W) + n_global * kv(pos + 1) + cfg.n_core * act * es
+    # per row: query in, output and gate; bf16 (fused post-processing): raw key and value
+    # in, key and value to the cache
+    act = (cfg.q_dim + cfg.n_heads + cfg.q_dim) * es + 4 * hk * hd * es
+    assert one == n_local * kv(W) + n_global * kv(pos + 1) + cfg.n_core * act
     # the speculative row adds one key per layer and its own activations, not a second cache read
-    assert two - one == n_local * kv(1) + n_global * kv(1) + cfg.n_core * act * es
+    assert two - one == n_local * kv(1) + n_global * kv(1) + cfg.n_core * act
     # two different sequences read two caches
     other = traffic.step_bytes(cfg, es, [(0, 2, pos), (1, 0, pos + 1)], counts, 2)["attention"]
-    assert other - one == n_local * kv(W) + n_global * kv(pos + 2) + cfg.n_core * act * es
+    assert other - one == n_local * kv(W) + n_global * kv(pos + 2) + cfg.n_core * act
+    # with a separate post-processing kernel its bytes are a class of their own
+    sep = traffic.step_bytes(cfg, es, [(0, 2, pos)], counts, 1, fused_post=False)
+    assert one - sep["attention"] == cfg.n_core * 4 * hk * hd * es
+    assert sep["qk_post"] == cfg.n_core * (cfg.qkv_dim * es * 2 + 2 * hk * hd * es)
 
 
 def test_weight_bytes_follow_pulses_and_touched_experts():
