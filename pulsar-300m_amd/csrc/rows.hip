@@ -1349,26 +1349,34 @@ __global__ void __launch_bounds__(256) norm_router_kernel(RouterArgs a) {
   const int r = blockIdx.x;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int D = a.D, i0 = lane * EPL;
-  // No early exit (the compiler would hold every load behind the row-count test): each
-  // block computes its row, in bounds for every block since the grid is the engine's row
-  // capacity, and only the stores test the count. The step's row count and pulse ranges
-  // come in one scalar read of the control block, so the pulse-indexed weights wait one
-  // round trip, not two.
-  const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)r * D;
-  float xv[EPL], nw[EPL], wt[EW][EPL];
-  ldv<EPL>(x + i0, xv);
+  // The row goes out first (in bounds for every block: the grid is the engine's row
+  // capacity), with the control block's row count and pulse ranges in one scalar read; the
+  // empty asm (a memory clobber, no operand) keeps the row's loads ahead of the row-count
+  // test without waiting for them. Blocks past the step's rows leave before their weight
+  // loads; the pulse-indexed weights of live rows wait one scalar round trip.
   int ps[kMaxPulses], pc[kMaxPulses];
 #pragma unroll
   for (int q = 0; q < kMaxPulses; ++q) {
     ps[q] = a.ctl->pulse_start[q];
     pc[q] = a.ctl->pulse_count[q];
   }
-  const bool live = r < a.ctl->n_rows;
+  const int n_rows = a.ctl->n_rows;
+  const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)r * D;
+  float xv[EPL], nw[EPL], wt[EW][EPL];
+  ldv<EPL>(x + i0, xv);
+  // (the weight pointers are read here too, so the weights do not wait for them)
+  const float* wbase = a.w;
+  const float* nbase = a.norm_w;
+  asm volatile("" ::"s"(wbase), "s"(nbase) : "memory");
+  if (r >= n_rows) return;
+  const bool live = true;
   const int pulse = step_row_pulse(ps, pc, r);
-  const float* W = a.w + ((int64_t)pulse * E + wv * EW) * D;
-  ldv<EPL>(a.norm_w + (int64_t)pulse * D + i0, nw);
+  const float* W = wbase + ((int64_t)pulse * E + wv * EW) * D;
+  ldv<EPL>(nbase + (int64_t)pulse * D + i0, nw);
 #pragma unroll
   for (int q = 0; q < EW; ++q) ldv<EPL>(W + (int64_t)q * D + i0, wt[q]);
+  // the weight loads go out before the row's arithmetic, which waits for the row
+  __builtin_amdgcn_sched_barrier(0);
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < EPL; ++c) ss += xv[c] * xv[c];
@@ -1641,10 +1649,12 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
   // one wave per row; lane owns elements [lane*EPL, lane*EPL + EPL)
   const int r = blockIdx.x;
   const int K = a.K, D = a.D, lane = threadIdx.x, i0 = lane * EPL;
-  // The row's operands go out before the row-count test (every block's row is in bounds:
-  // the grid is the row capacity), the routing weights as plain loads without a branch; the
-  // step's row count and pulse ranges come in one scalar read of the control block, so only
-  // the pulse-indexed scale waits for it.
+  // The row's operands go out first (every block's row is in bounds: the grid is the row
+  // capacity), the routing weights as one vector load (lane k holds slot k: per-slot scalar
+  // loads would each sit in a block of their own behind a wait), then the control block's
+  // row count and pulse ranges in one scalar read; the empty asm (a memory clobber, no
+  // operand) keeps the loads ahead of the row-count test without waiting for them, and
+  // blocks past the step's rows leave before the pulse-indexed loads.
   const T* shp = reinterpret_cast<const T*>(a.shared) + (int64_t)r * D + i0;
   const T* rop = reinterpret_cast<const T*>(a.routed) + (int64_t)r * K * D + i0;
   T* h = reinterpret_cast<T*>(a.h) + (int64_t)r * D + i0;
@@ -1653,12 +1663,7 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
   ldv<EPL>(shp, sh);
 #pragma unroll
   for (int k = 0; k < KT; ++k) ldv<EPL>(rop + (int64_t)(k < K ? k : 0) * D, ro[k]);
-  // routing weight k from lane k of one vector load (a per-slot scalar load would sit in a
-  // block of its own behind a wait)
   const float wl = a.topk_w[(int64_t)r * K + min(lane, K - 1)];
-  float w[KT];
-#pragma unroll
-  for (int k = 0; k < KT; ++k) w[k] = __shfl(wl, k < K ? k : 0, 64);
   int n = a.m_fixed, pulse = a.pulse;
   if (a.ctl) {
     int ps[kMaxPulses], pc[kMaxPulses];
@@ -1670,8 +1675,12 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
     n = a.ctl->n_rows;
     pulse = step_row_pulse(ps, pc, r);
   }
-  // no early exit (loads would wait behind the test): only the stores test the row count
-  const bool live = r < n;
+  asm volatile("" ::: "memory");
+  if (r >= n) return;
+  const bool live = true;
+  float w[KT];
+#pragma unroll
+  for (int k = 0; k < KT; ++k) w[k] = __shfl(wl, k < K ? k : 0, 64);
   ldv<EPL>(reinterpret_cast<const T*>(a.routed_scale) + (int64_t)pulse * D + i0, rs);
   float nwn[EPL];
   if (a.next_norm) ldv<EPL>(a.next_norm + (int64_t)pulse * D + i0, nwn);
