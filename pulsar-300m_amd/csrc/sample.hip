@@ -174,10 +174,17 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
     }
     return;
   }
+  // x / temperature for every score: the quotient by the correctly rounded reciprocal and
+  // one fma correction (Markstein's theorem: RN(q + (x - q t) r) = RN(x / t) when r =
+  // RN(1 / t) and no intermediate over- or underflows), three instructions in place of the
+  // full-precision divide; a non-finite product is kept as it is
+  const float tmp = a.temperature, rtmp = 1.0f / tmp;
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    l[i] = rnd<T>(l[i] / a.temperature);
+    const float q = l[i] * rtmp;
+    const float q2 = fmaf(fmaf(-q, tmp, l[i]), rtmp, q);
+    l[i] = rnd<T>(__builtin_isfinite(q) ? q2 : q);
     mx = fmaxf(mx, l[i]);
   }
   mx = block_max(mx, red);
@@ -194,9 +201,12 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
   for (int i = 0; i < PER / kPack; ++i) kw[i] = 0u;
   float zl = 0.f, at_max = 0.f;
   const uint32_t kmax = order_key(mx) >> kLow;
+  // exp(l - mx) as the hardware base-2 exponential of the scaled difference (a few ulps;
+  // the same values feed Z, the threshold search and the draws)
+  constexpr float kLog2e = 1.4426950408889634f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    pr[i] = expf(l[i] - mx);
+    pr[i] = __builtin_amdgcn_exp2f((l[i] - mx) * kLog2e);
     const uint32_t k = order_key(l[i]) >> kLow;
     kw[i / kPack] |= kPack == 2 ? k << (16 * (i & 1)) : k;
     zl += pr[i];
