@@ -4,7 +4,11 @@
 Workload (default): random-init Pulsar-283M in bf16 (weights N(0, 0.02), reference constant
 init elsewhere), batch 16, 2048-token uniform-random prompts, sampled self-speculative decode
 with temperature 0.8, top-p 0.95, repetition penalty 1.15 (the reference default), 256 new
-tokens per sequence, stop ids disabled so every sequence produces exactly 256 tokens.
+tokens per sequence, draft length 4, stop ids disabled so every sequence produces exactly
+256 tokens. Draft length 4 is the draft-block schedule: up to 4 pulse-0 drafts per round, one
+all-pulse verify of the block, drafts accepted down the block by the reference's equal-draw
+rule. The reference's own schedule (draft length 1, src/infer.py:623-731) is timed beside it
+(`exact_schedule`); `--draft-len 0` makes it the headline.
 
 A step = one generation of the whole batch from the prefilled KV cache: rewind (redraw the
 first token from the saved prefill logits with a new seed) and decode until every sequence
@@ -51,6 +55,23 @@ CLASS_KERNELS = {
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_c2_b16_t2048.md")
+BLOCK_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_c2_draft4_b16_t2048.md")
+# kernel classes by the short names of their templates (gemm EPI: 0 store, 1 qkv + gate,
+# 2 residual add, 3 SwiGLU, 4 logits), for class averages over every template of a class
+CLASS_PREFIXES = {
+    "attention": ("attn_decode_unit_kernel<",),
+    "routed_gate_up": ("gemm_bf16_kernel<3,", "gemm_bf16_lds_kernel<3,"),
+    "routed_down": ("gemm_bf16_kernel<0,", "gemm_bf16_lds_kernel<0,"),
+    "qkv_gate_gemm": ("gemm_bf16_kernel<1,", "gemm_bf16_lds_kernel<1,"),
+    "wo_gemm": ("gemm_bf16_kernel<2,", "gemm_bf16_lds_kernel<2,"),
+    "lm_head": ("gemm_bf16_kernel<4,", "gemm_bf16_lds_kernel<4,"),
+    "router": ("norm_router_kernel<",),
+    "moe_combine": ("moe_combine_rows_kernel<",),
+    "sample": ("sample_kernel<",),
+    "pulse_input": ("pulse_input_kernel<",),
+    "pulse_output": ("pulse_output_kernel<",),
+    "controller": ("controller_kernel", "controller_block_kernel"),
+}
 VERIFY_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_verify_b64_ctx8192.md")
 
 
@@ -65,7 +86,7 @@ def _phase_rows(rows: list, phase: str) -> list:
     from just after the controller launch that precedes its last prefill kernel up to the
     controller launch that ends it (drawing the first tokens); decode is everything after."""
     names = [r["Kernel_Name"] for r in rows]
-    ctl = [i for i, n in enumerate(names) if "controller_kernel" in n]
+    ctl = [i for i, n in enumerate(names) if "controller_kernel" in n or "controller_block" in n]
     pre = [i for i, n in enumerate(names) if "prefill" in n]
     if not pre:
         end = ctl[0] if ctl else -1
@@ -138,9 +159,22 @@ def pmc_summary(fetch_dir: str, write_dir: str, fetch_copy: str, write_copy: str
             agg[_short_kernel(r["Kernel_Name"])].append(float(r["Counter_Value"]))
         for k, v in agg.items():
             res.setdefault(k, {})[ctr] = round(sum(v) / len(v) * factor * 1024)
+        # class averages over every dispatch of the class's templates ("class:<name>")
+        for cls, pre in CLASS_PREFIXES.items():
+            v = [x for k, vals in agg.items() if k.startswith(pre) for x in vals]
+            if v:
+                res.setdefault("class:" + cls, {})[ctr] = round(sum(v) / len(v) * factor * 1024)
     out = lines + ["", "| kernel | fetch MB / dispatch | write MB / dispatch |", "|---|---|---|"]
     for k, v in sorted(res.items(), key=lambda kv: -kv[1].get("FETCH_SIZE", 0)):
+        if k.startswith("class:"):
+            continue
         out.append(f"| `{k}` | {v.get('FETCH_SIZE', 0) / 1e6:.3f} | {v.get('WRITE_SIZE', 0) / 1e6:.3f} |")
+    out += ["", "Class averages over every dispatch of the class's templates:", "",
+            "| class | fetch MB / dispatch | write MB / dispatch |", "|---|---|---|"]
+    for k, v in sorted(res.items(), key=lambda kv: -kv[1].get("FETCH_SIZE", 0)):
+        if k.startswith("class:"):
+            out.append(f"| {k[6:]} | {v.get('FETCH_SIZE', 0) / 1e6:.3f} | "
+                       f"{v.get('WRITE_SIZE', 0) / 1e6:.3f} |")
     out += ["", "```json", json.dumps(res, sort_keys=True), "```"]
     return "\n".join(out)
 
@@ -297,7 +331,7 @@ def verify_microbench(model, cfg, es, args):
 
 def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warmup, es=2,
                  profile=True, draft_len=0, label="", speculative=True,
-                 early_exit_threshold=None):
+                 early_exit_threshold=None, traffic_path=None):
     """Timed generations of a batch from one prefill: each generation rewinds (redraws the
     first tokens from the saved prefill logits with a new seed) and decodes until every
     sequence has n_new tokens (no stop ids). Returns accepted tokens/s, acceptance, the
@@ -348,6 +382,8 @@ def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warm
            "prefill_ms_first_call": round(prefill_s * 1e3, 1)}
     if early_exit_threshold is not None:
         out["exits_per_pulse"] = exits.tolist()
+    if draft_len > 0 and produced > accepted:
+        out["tokens_per_round"] = round(produced / (produced - accepted), 3)
     log(f"{label}: {steps} timed generations, {produced} tokens in {elapsed:.3f}s, "
         f"acceptance {accepted}/{tests}")
     if profile:
@@ -365,7 +401,14 @@ def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warm
                            "achieved": round(per_launch / avg_s / 1e9, 1), "peak": 8000.0,
                            "unit": "GB/s", "frac": round(per_launch / avg_s / HBM_PEAK, 4),
                            "bytes_per_launch": int(per_launch),
-                           "avg_launch_us": round(avg_s * 1e6, 2)}
+                           "avg_launch_us": round(avg_s * 1e6, 2),
+                           "empty_event_pair_us": round(pair_ms / max(pair_n, 1) * 1e3, 2)}
+        if traffic_path:
+            tb = recorded_traffic(["class:" + dom], traffic_path)
+            out["roofline"]["traffic"] = round(tb / 1e6, 3) if tb else None
+            out["roofline"]["traffic_unit"] = ("MB per launch (rocprofv3 FETCH_SIZE + "
+                                               "WRITE_SIZE, copy-calibrated, averaged over "
+                                               "every launch of the class)")
         out["kernel_profile"] = {
             k: {"ms": round(v[0], 3), "launches": v[1], "us_per_launch": round(v[0] / v[1] * 1e3, 2),
                 "GB_per_s": round(bytes_by_class[k] / max(v[0], 1e-9) / 1e6, 1)}
@@ -399,53 +442,6 @@ def early_exit_run(model, cfg, prompts, args) -> dict:
             "self_speculative_early_exit": {k: spec_ee[k] for k in (
                 "value", "unit", "pulse_steps_per_generation", "acceptance_rate",
                 "exits_per_pulse")}}
-
-
-def draft_block_run(model, cfg, prompts, args):
-    """The bench workload in draft-block mode (draft length args.draft_len): accepted
-    tokens/s over timed generations from the prefilled cache, acceptance rate."""
-    import torch
-
-    from pulsar_engine.engine import HipEngine
-
-    B, T = prompts.shape
-    N = args.new_tokens
-    eng = HipEngine(model, batch=B, max_prompt=T, max_new=N, temperature=args.temperature,
-                    top_p=args.top_p, repetition_penalty=args.repetition_penalty, stop_ids=[],
-                    seed=1, draft_len=args.draft_len)
-    eng.prefill(prompts)
-
-    def generation(seed):
-        eng.rewind(seed)
-        steps = eng.run(check_every=16)
-        st = eng.state()
-        return steps, int(st[:, 1].sum()), int(st[:, 11].sum()), int(st[:, 12].sum())
-
-    for w in range(args.warmup):
-        generation(4000 + w)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    produced = tests = accepted = steps = 0
-    for k in range(args.steps):
-        s_, p, t, a = generation(5000 + k)
-        steps += s_
-        produced += p
-        tests += t
-        accepted += a
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    eng.close()
-    return {
-        "schedule": f"draft-block (no reference counterpart): up to {args.draft_len} pulse-0 "
-                    "drafts per round, one all-pulse verify of the block, drafts accepted down "
-                    "the block by the reference's equal-draw rule",
-        "draft_len": args.draft_len,
-        "value": round(produced / el, 1), "unit": "tokens/s",
-        "ms_per_step": round(el / args.steps * 1e3, 2),
-        "acceptance_rate": round(accepted / tests, 4) if tests else None,
-        "tokens_per_round": round(produced / max(1, produced - accepted), 3),
-        "pulse_steps_per_generation": round(steps / args.steps, 1),
-    }
 
 
 def _cpu_model_name() -> str:
@@ -696,7 +692,7 @@ def main() -> int:
     ap.add_argument("--no-ops", action="store_true", help="skip the op-surface figures")
     ap.add_argument("--no-early-exit", action="store_true", help="skip the early-exit runs")
     ap.add_argument("--early-exit-threshold", type=float, default=0.99)
-    ap.add_argument("--only", choices=("c4", "c5", "c5d6"),
+    ap.add_argument("--only", choices=("c4", "c5", "c5d6", "c2d4"),
                     help="run only that workload, unprofiled (kernel traces)")
     ap.add_argument("--verify-only", action="store_true",
                     help="run only the verify microbenchmark (profiling)")
@@ -769,6 +765,12 @@ def main() -> int:
               flush=True)
         return 0
     prompts = np.stack([W.uniform_ids(0, f"bench_prompt_{b}", T, cfg.vocab_size) for b in range(B)])
+    if args.only == "c2d4":
+        print(json.dumps({"c2_draft_block": run_workload(
+            model, cfg, prompts, N, args.temperature, args.top_p, args.repetition_penalty,
+            args.steps, args.warmup, es, profile=False, draft_len=max(args.draft_len, 1),
+            label="c2 draft-block")}), flush=True)
+        return 0
     eng = HipEngine(model, batch=B, max_prompt=T, max_new=N, speculative=not args.plain,
                     temperature=args.temperature, top_p=args.top_p,
                     repetition_penalty=args.repetition_penalty, stop_ids=[], seed=1)
@@ -855,10 +857,28 @@ def main() -> int:
             f"pair {pair * 1e3:.2f} us), dominant {dom} {ms:.1f} ms")
         log("per-class: " + json.dumps(prof_detail))
 
+    exact = {"schedule": "exact self-speculative: the reference's draft length 1 (one pulse-0 "
+                         "draft per token, tested against the token's pulse-2 draw), the "
+                         "next token's pulse-0 draft pipelined with the verify pulse",
+             "value": round(value, 1), "unit": "tokens/s",
+             "ms_per_generation": round(elapsed / args.steps * 1e3, 2),
+             "pulse_steps_per_generation": round(graph_steps / args.steps, 1),
+             "acceptance_rate": round(accepted / tests, 4) if tests else None,
+             "hbm_roofline_frac_generation": round(step_frac, 4) if step_frac is not None else None,
+             "roofline": roofline, "kernel_profile": prof_detail}
     block = None
-    if args.draft_len > 0:
-        block = draft_block_run(model, cfg, prompts, args)
-        log(f"draft-block run: {json.dumps(block)}")
+    if args.draft_len > 0 and not args.plain:
+        block = run_workload(model, cfg, prompts, N, args.temperature, args.top_p,
+                             args.repetition_penalty, args.steps, args.warmup, es,
+                             profile=not args.no_profile, draft_len=args.draft_len,
+                             label=f"c2 draft-block {args.draft_len}",
+                             traffic_path=BLOCK_TRAFFIC_PROFILE)
+        block["schedule"] = (f"draft-block, draft length {args.draft_len}: up to "
+                             f"{args.draft_len} pulse-0 drafts per round, one all-pulse verify "
+                             "of the block, drafts accepted down the block by the reference's "
+                             "equal-draw rule (each emitted token is the full model's draw)")
+        log(f"draft-block run: {json.dumps({k: v for k, v in block.items() if k != 'kernel_profile'})}")
+    head = block if block is not None else exact
     early = None
     if not args.no_early_exit:
         early = early_exit_run(model, cfg, prompts, args)
@@ -909,12 +929,12 @@ def main() -> int:
         log(f"cpu baseline: {json.dumps({k: v for k, v in cpu.items() if k != 'c1'})}")
     line = {
         "metric": METRIC,
-        "value": round(value, 1),
+        "value": head["value"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(elapsed / args.steps * 1e3, 2),
+        "ms_per_step": head["ms_per_generation"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -925,17 +945,18 @@ def main() -> int:
                         f"{'plain' if args.plain else 'self-speculative'} decode of {N} tokens",
             "batch": B, "prompt_len": T, "new_tokens": N, "temperature": args.temperature,
             "top_p": args.top_p, "repetition_penalty": args.repetition_penalty,
-            "schedule": "plain" if args.plain else
-                        "exact self-speculative (pulse-0 draft pipelined with the verify pulse)",
+            "draft_len": args.draft_len if block is not None else (0 if args.plain else 1),
+            "schedule": "plain" if args.plain else head["schedule"],
             "stop_ids": "disabled",
         },
-        "acceptance_rate": round(accepted / tests, 4) if tests else None,
+        "acceptance_rate": head["acceptance_rate"],
+        "tokens_per_round": head.get("tokens_per_round"),
         "prefill": prefill,
-        "hbm_roofline_frac_generation": round(step_frac, 4) if step_frac is not None else None,
-        "roofline": roofline,
+        "hbm_roofline_frac_generation": head.get("hbm_roofline_frac_generation"),
+        "roofline": head.get("roofline"),
         "cpu_baseline": cpu,
-        "kernel_profile": prof_detail,
-        "draft_block": block,
+        "kernel_profile": head.get("kernel_profile"),
+        "exact_schedule": exact if block is not None else None,
         "verify": verify,
         "c1": c1,
         "c4": c4,

@@ -109,6 +109,8 @@ struct GemmArgs {
   int eager_w;
   int a_rows, a_rows0;  // rows of A and A0 (eager_w clamps speculative row indices into them)
   int grid_x, grid_y, grid_z;  // decode bf16 launches: (column block, group, row tile) extents
+  int g0_split;  // decode bf16 launches with group 0: grid.y rows of group 0 (its row tiles
+                 // spread over g0_split x grid_z workgroups per column block)
 };
 
 int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,

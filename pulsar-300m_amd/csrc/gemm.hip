@@ -215,16 +215,31 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   __shared__ float red[kGemmWaves][64][kPair ? 16 : 8];
   const GemmBlock blk = gemm_block<XCD>(g);
   if (!blk.valid) return;
-  // grid.y == 0 is the optional all-rows group (group -1) when has_g0 is set
-  const int group = blk.y + g.group_offset - (g.has_g0 ? 1 : 0);
-  const bool g0 = group < 0;
+  // grid.y < g0_split: the optional all-rows group (group -1) when has_g0 is set. Its row
+  // tiles go to g0_split x Z workgroups per column block (tile y Z + z, stride g0_split Z),
+  // those of a list group to Z (tile z, stride Z): the all-rows group holds about K / E
+  // times the rows of a routed expert, and one workgroup walking all of them would be the
+  // launch's longest chain of dependent tiles.
+  const int s0 = g.has_g0 ? g.g0_split : 0;
+  const bool g0 = blk.y < s0;
+  const int group = g0 ? -1 : blk.y - s0 + g.group_offset;
   const int N = g0 ? g.N0 : g.N;
   const int col0 = blk.x * 16;
   if (col0 >= N) return;
+  const int zs = XCD ? g.grid_z : (int)gridDim.z;
+  const int tstep = (g0 ? s0 * zs : zs) * 32;
+  int tile0 = (g0 ? blk.y * zs + blk.z : blk.z) * 32;
   int cnt = 0;
   if constexpr (!EAGER) {
     cnt = group_rows<MODE>(g, group);  // uniform per workgroup
-    if (blk.z * 32 >= cnt) return;
+    if (tile0 >= cnt) return;
+  } else {
+    // the all-rows group's later tiles exist for parallelism at large steps: they check
+    // the step's row count before streaming weights (the first tile never waits for it)
+    if (g0 && tile0 > 0) {
+      cnt = group_rows<MODE>(g, group);
+      if (tile0 >= cnt) return;
+    }
   }
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -271,7 +286,6 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   // barrier) the A rows: vector loads retire in issue order, so waiting for the few entry
   // loads leaves every weight load in flight. Lanes past the last row re-read the last
   // entry (always in bounds) and use a zero A operand.
-  int tile0 = blk.z * 32;
   int n, i0, i1, l0, l1;
   if constexpr (EAGER) {
     // Most experts have rows (the host decides from the batch size): the first tile's
@@ -374,7 +388,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
       const int row = blk * 16 + kq * 4 + j;
       if (vc && row < n) epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, col0 + m, acc, accu);
     }
-    tile0 += (XCD ? g.grid_z : (int)gridDim.z) * 32;
+    tile0 += tstep;
     if (tile0 >= cnt) break;
     __syncthreads();  // the partial sums in LDS are consumed before the next tile's writes
     n = min(32, cnt - tile0);
@@ -651,12 +665,13 @@ void launch_bf16_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
 // in parallel, and the re-read weight slices come from the XCD's L2 (XCD-aware order
 // below). The output head (64 MiB) measured slower that way at 320 rows (61 -> 75 us).
 constexpr int kTilesPerWorkgroup = 4;
+constexpr int kG0Split = 4;
 
 template <int EPI>
 int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream_t s) {
   const int tiles = (max_rows + 31) / 32;
   if (tiles <= 0 || groups <= 0) return PULSAR_OK;
-  const int gy = groups + (a.has_g0 ? 1 : 0);
+  int gy = groups + (a.has_g0 ? 1 : 0);
   const int nmax = a.has_g0 ? std::max(a.N, a.N0) : a.N;
   const int k0 = a.has_g0 ? a.K0 : a.K;
   if (dtype == PULSAR_BF16) {
@@ -669,8 +684,12 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
       return fail(PULSAR_ERR_UNSUPPORTED, "gemm: the all-rows group needs K0 = K or 2K");
     const int per_wg = a.row_mode == ROWS_PULSE ? 1 : kTilesPerWorkgroup;
     const int gz = (tiles + per_wg - 1) / per_wg;
+    // the all-rows group: one row tile per workgroup, up to kG0Split rows of the grid
+    const int s0 = a.has_g0 ? std::min(kG0Split, (tiles + gz - 1) / gz) : 0;
+    gy = groups + s0;
     dim3 grid((unsigned)((nmax + 15) / 16), (unsigned)gy, (unsigned)gz);
     GemmArgs ga = a;
+    ga.g0_split = s0;
     ga.grid_x = (int)grid.x;
     ga.grid_y = (int)grid.y;
     ga.grid_z = (int)grid.z;

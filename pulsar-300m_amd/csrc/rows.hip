@@ -764,9 +764,14 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
   // block and does not use it; in global layers its page read waits with the post operands,
   // all in flight together).
   const int kbf = min(kb0, s_hi / 64 * 64);
+  // Query column c = wv + 4 i of this wave is unit row z = i; in the 16- and 32-column
+  // launches rows past the unit's (a unit of a draft step holds one row) issue no loads (a
+  // uniform branch; the 8-column launch measured faster without it)
   float qx[NQ], qw[NQ], qcs[NQ], qsn[NQ];
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
+    qx[i] = qw[i] = qcs[i] = qsn[i] = 0.f;
+    if (NQ > 2 && ((wv + kUnitWaves * i) >> 2) >= un.n) continue;
     const int c = wv + kUnitWaves * i, z = c >> 2, head = g * 4 + (c & 3);
     const int row = max(unit_row<NZ>(un, z), 0);
     const int pos = z < un.n ? un.pos0 + z : un.pos0, pulse = step_row_pulse(ps, pc, row);
@@ -779,6 +784,9 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
   int fpg[NF];  // global layers: pool page of the fresh position
 #pragma unroll
   for (int i = 0; i < NF; ++i) {
+    fx[i] = fw[i] = fcs[i] = fsn[i] = fvf[i] = 0.f;
+    fpg[i] = 0;
+    if (NF > 1 && zlo + ((wv + kUnitWaves * i) >> 1) > zhi) continue;
     const int t = wv + kUnitWaves * i, z = min(zlo + (t >> 1), max(zhi, 0));
     const int row = max(unit_row<NZ>(un, z), 0), pos = un.pos0 + z;
     const int pulse = step_row_pulse(ps, pc, row);
@@ -896,6 +904,7 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
     const auto& vh = cur.vh;
 #pragma unroll
     for (int t = 0; t < NQT; ++t) {
+      if (t > 0 && 4 * t >= un.n) break;  // query tile t holds unit rows 4 t .. 4 t + 3
       attn_f32x4 sv[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
