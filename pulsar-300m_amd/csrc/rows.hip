@@ -1835,7 +1835,11 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     // engines of few sequences keep 256-key splits in the sliding-window layers: 1024-key
     // splits would leave most CUs idle there (two workgroups per unit and kv head)
     const bool few = a.max_units < kManyUnits;
-    const int bpw = !lng ? 1 : (a.is_local ? (few ? 1 : 4) : 8);
+    // 32-column units (draft blocks of 5-8 rows) hold two workgroups per CU (212 registers
+    // a lane): in global layers 512-key splits keep a batch-16 engine's workgroups
+    // resident in one round
+    const bool wide_units = a.unit_rows > 4;
+    const int bpw = !lng ? (wide_units && !a.is_local ? 2 : 1) : (a.is_local ? (few ? 1 : 4) : 8);
     const int split = kUnitSplit * bpw;
     // a unit's keys [lo, hi] lie in the splits from lo's to hi's: at most max_ctx keys, and in
     // sliding-window layers window + rows - 1 keys, which can straddle one more split
@@ -1858,6 +1862,8 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
       attn_decode_unit_kernel<C, 8><<<grid, 64 * kUnitWaves, 0, s>>>(b);            \
     else if (bpw == 4)                                                              \
       attn_decode_unit_kernel<C, 4><<<grid, 64 * kUnitWaves, 0, s>>>(b);            \
+    else if (bpw == 2)                                                              \
+      attn_decode_unit_kernel<C, 2><<<grid, 64 * kUnitWaves, 0, s>>>(b);            \
     else                                                                            \
       attn_decode_unit_kernel<C, 1><<<grid, 64 * kUnitWaves, 0, s>>>(b);            \
   } while (0)
