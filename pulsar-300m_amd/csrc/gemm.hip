@@ -209,7 +209,10 @@ __device__ __forceinline__ GemmBlock gemm_block(const GemmArgs& g) {
 
 template <int EPI, int KITER, int MODE, int KMUL0, bool EAGER, bool XCD>
 __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) {
-  constexpr bool kPair = (EPI == EPI_SWIGLU);
+  // two weight column tiles share each A operand: SwiGLU's gate and up columns, and the
+  // output head's columns c and N + c (the host halves N: the head's A rows are then read
+  // once per 32 vocabulary columns, not per 16)
+  constexpr bool kPair = (EPI == EPI_SWIGLU || EPI == EPI_LOGITS);
   constexpr int kKPass = KITER * 32 * kGemmWaves;  // K covered by one pass of the waves
   static_assert(!EAGER || MODE == ROWS_LIST, "eager weight loads are for expert lists");
   __shared__ float red[kGemmWaves][64][kPair ? 16 : 8];
@@ -386,7 +389,11 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
       // of tile row r is the entry held by lane r % 16 (rows 0-15: e0, 16-31: e1).
       const int crow = __shfl(blk ? e1 : e0, kq * 4 + j, 64);
       const int row = blk * 16 + kq * 4 + j;
-      if (vc && row < n) epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, col0 + m, acc, accu);
+      if (vc && row < n) {
+        epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, col0 + m, acc, accu);
+        if constexpr (EPI == EPI_LOGITS)
+          epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, N + col0 + m, accu, 0.f);
+      }
     }
     tile0 += tstep;
     if (tile0 >= cnt) break;
@@ -773,7 +780,15 @@ int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
     case EPI_QKVG: return launch_one<EPI_QKVG>(a, dtype, groups, max_rows, s);
     case EPI_RESID: return launch_one<EPI_RESID>(a, dtype, groups, max_rows, s);
     case EPI_SWIGLU: return launch_one<EPI_SWIGLU>(a, dtype, groups, max_rows, s);
-    case EPI_LOGITS: return launch_one<EPI_LOGITS>(a, dtype, groups, max_rows, s);
+    case EPI_LOGITS:
+      if (dtype == PULSAR_BF16) {
+        // column pairs (c, N/2 + c) per workgroup
+        if (a.N % 32 != 0) return fail(PULSAR_ERR_UNSUPPORTED, "gemm: logits N % 32 != 0");
+        GemmArgs h = a;
+        h.N = a.N / 2;
+        return launch_one<EPI_LOGITS>(h, dtype, groups, max_rows, s);
+      }
+      return launch_one<EPI_LOGITS>(a, dtype, groups, max_rows, s);
     case EPI_LOGITS_RAW: return launch_one<EPI_LOGITS_RAW>(a, dtype, groups, max_rows, s);
     case EPI_SCALE: return launch_one<EPI_SCALE>(a, dtype, groups, max_rows, s);
   }
