@@ -546,51 +546,79 @@ __device__ __forceinline__ int unit_row(const AttnUnit& un, int z) {
 
 // Last split block of (unit u, kv head g): merge the split partials (device-coherent loads),
 // normalise, round as the SDPA output and apply the head gate. Query column c = 4 z + h
-// (unit row z, head h of the group); a thread takes two dims of one column at a time.
-constexpr int kMergeChunk = 16;  // split partials loaded per round trip
+// (unit row z, head h of the group); element t = 32 c + e0 / 2 (two dims of one column).
+// A thread takes elements t, t + 256, ... of the unit's columns and issues the partial loads
+// of all of them (kMergeChunk splits at a time) before the first use: one round trip per
+// chunk however many rows the unit holds. Per element the splits are summed in order, so
+// a row's result does not depend on the unit's other rows.
 template <int COLS>
 __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int g,
                                                   const AttnUnit& un, int nsplit) {
-  for (int t = threadIdx.x; t < COLS * 32; t += blockDim.x) {
-    const int c = t >> 5, e0 = (t & 31) * 2;
-    const int row = unit_row<COLS / 4>(un, c >> 2);
-    if (row < 0) continue;
-    const float* p0 = a.part + ((((int64_t)u * a.Hkv + g) * a.max_splits) * COLS + c) * 66;
-    float Mx = -INFINITY, Ls = 0.f, Oa = 0.f, Ob = 0.f;
-    for (int c0 = 0; c0 < nsplit; c0 += kMergeChunk) {
-      float pm[kMergeChunk], pl[kMergeChunk], pa[kMergeChunk], pb[kMergeChunk];
+  constexpr int NT = 64 * kUnitWaves;
+  constexpr int EPT = (COLS * 32 + NT - 1) / NT;  // elements per thread
+  constexpr int CH = EPT > 2 ? 8 : 16;            // splits loaded per round trip
+  const int nel = min(un.n, COLS / 4) * 4 * 32;  // a multiple of 128: whole waves drop out
+  const int wbase = threadIdx.x & ~63;
+  const float* part = a.part + (((int64_t)u * a.Hkv + g) * a.max_splits) * COLS * 66;
+  float Mx[EPT], Ls[EPT], Oa[EPT], Ob[EPT], gate[EPT];
+  int off[EPT];
 #pragma unroll
-      for (int k = 0; k < kMergeChunk; ++k) {
-        const float* p = p0 + (int64_t)min(c0 + k, nsplit - 1) * COLS * 66;
-        pm[k] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        pl[k] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        pa[k] = __hip_atomic_load(p + 2 + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        pb[k] = __hip_atomic_load(p + 3 + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int e = 0; e < EPT; ++e) {
+    const int t = min((int)threadIdx.x + NT * e, nel - 1), c = t >> 5;
+    off[e] = c * 66 + (t & 31) * 2;
+    gate[e] = 0.f;
+    if (NT * e + wbase < nel)
+      gate[e] = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)unit_row<COLS / 4>(un, c >> 2) *
+                                                           a.H + g * 4 + (c & 3)]);
+    Mx[e] = -INFINITY;
+    Ls[e] = Oa[e] = Ob[e] = 0.f;
+  }
+  for (int c0 = 0; c0 < nsplit; c0 += CH) {
+    float pm[EPT][CH], pl[EPT][CH], pa[EPT][CH], pb[EPT][CH];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      if (NT * e + wbase >= nel) continue;
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        const float* p = part + (int64_t)min(c0 + k, nsplit - 1) * COLS * 66;
+        pm[e][k] = __hip_atomic_load(p + off[e] - (off[e] % 66), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pl[e][k] = __hip_atomic_load(p + off[e] - (off[e] % 66) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pa[e][k] = __hip_atomic_load(p + off[e] + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pb[e][k] = __hip_atomic_load(p + off[e] + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      float cm = Mx;
+    }
 #pragma unroll
-      for (int k = 0; k < kMergeChunk; ++k)
-        if (c0 + k < nsplit) cm = fmaxf(cm, pm[k]);
-      const float f0 = Mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(Mx - cm);
-      Ls *= f0;
-      Oa *= f0;
-      Ob *= f0;
+    for (int e = 0; e < EPT; ++e) {
+      if (NT * e + wbase >= nel) continue;
+      float cm = Mx[e];
 #pragma unroll
-      for (int k = 0; k < kMergeChunk; ++k) {
-        if (c0 + k < nsplit && pm[k] != -INFINITY) {
-          const float f = __builtin_amdgcn_exp2f(pm[k] - cm);
-          Ls += pl[k] * f;
-          Oa += pa[k] * f;
-          Ob += pb[k] * f;
+      for (int k = 0; k < CH; ++k)
+        if (c0 + k < nsplit) cm = fmaxf(cm, pm[e][k]);
+      const float f0 = Mx[e] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(Mx[e] - cm);
+      Ls[e] *= f0;
+      Oa[e] *= f0;
+      Ob[e] *= f0;
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        if (c0 + k < nsplit && pm[e][k] != -INFINITY) {
+          const float f = __builtin_amdgcn_exp2f(pm[e][k] - cm);
+          Ls[e] += pl[e][k] * f;
+          Oa[e] += pa[e][k] * f;
+          Ob[e] += pb[e][k] * f;
         }
       }
-      Mx = cm;
+      Mx[e] = cm;
     }
-    const int head = g * 4 + (c & 3);
-    const float gate = to_f(reinterpret_cast<const bf16*>(a.gate)[(int64_t)row * a.H + head]);
-    bf16* dst = reinterpret_cast<bf16*>(a.out) + (int64_t)row * a.H * 64 + head * 64 + e0;
-    dst[0] = f2bf(rnd<bf16>(Oa / Ls) * gate);
-    dst[1] = f2bf(rnd<bf16>(Ob / Ls) * gate);
+  }
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int t = threadIdx.x + NT * e;
+    if (t >= nel) continue;
+    const int c = t >> 5, e0 = (t & 31) * 2;
+    const int row = unit_row<COLS / 4>(un, c >> 2);
+    bf16* dst = reinterpret_cast<bf16*>(a.out) + (int64_t)row * a.H * 64 + (g * 4 + (c & 3)) * 64 + e0;
+    dst[0] = f2bf(rnd<bf16>(Oa[e] / Ls[e]) * gate[e]);
+    dst[1] = f2bf(rnd<bf16>(Ob[e] / Ls[e]) * gate[e]);
   }
 }
 
@@ -985,11 +1013,11 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
   }
   __syncthreads();
   // merge the waves: element t -> query column hr, dim d; the block's threads cover the
-  // COLS x 64 elements whatever its size
-  for (int t = threadIdx.x; t < COLS * 64; t += blockDim.x) {
+  // unit's columns (hr < 4 n) x 64 elements whatever its size
+  const int ncol = min(un.n, NZ) * 4;
+  for (int t = threadIdx.x; t < ncol * 64; t += blockDim.x) {
     const int hr = t >> 6, d = t & 63;
     const int row = unit_row<NZ>(un, hr >> 2);
-    if (row < 0) continue;
     float M = -INFINITY, L = 0.f, O = 0.f;
 #pragma unroll
     for (int w = 0; w < kUnitWaves; ++w) M = fmaxf(M, wm[w][hr]);
