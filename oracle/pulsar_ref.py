@@ -760,7 +760,12 @@ class RefEngine:
             stats.setdefault("accepted", 0)
             stats.setdefault("rounds", 0)
             stats.setdefault("p_accept", [])
+            stats.setdefault("kinds", [])  # per emitted token: 1 accepted draft, 0 drawn
         stops = self.stop_ids
+
+        def kind(k):
+            if stats is not None:
+                stats["kinds"].append(k)
 
         def smp(lg, extra):
             return self.sample(lg, seen + list(extra), temperature, top_p, repetition_penalty,
@@ -773,6 +778,7 @@ class RefEngine:
             return
         seen.append(t)
         produced += 1
+        kind(0)
         yield t
         while produced < max_new_tokens:
             g = min(draft_len, max_new_tokens - produced - 1)
@@ -807,6 +813,7 @@ class RefEngine:
                         acc = i + 1
                         seen.append(blk[i + 1])
                         produced += 1
+                        kind(1)
                         yield blk[i + 1]
                         if produced >= max_new_tokens:
                             done = True
@@ -820,8 +827,64 @@ class RefEngine:
                 return
             seen.append(nxt)
             produced += 1
+            kind(0)
             yield nxt
             t = nxt
+
+
+def replay_block_acceptance(engine: "RefEngine", prompt_ids, emitted, kinds, temperature: float,
+                            top_p: float, repetition_penalty: float, draft_len: int,
+                            max_new: Optional[int] = None) -> list:
+    """``RefEngine.block_speculative_ids`` driven along a given emitted stream instead of its
+    own draws (no stop ids): emitted[i] is the i-th output token, kinds[i] is 1 for an
+    accepted draft and 0 for a drawn token. A round starts at a drawn token t; the accepted
+    drafts d1..da that follow it were tested and accepted, and the round ran
+    min(a + 1, G) tests (G = min(draft_len, tokens still wanted - 1)): the last one
+    failed unless a == G. Test i depends on block rows 0..i only (t, d1..di, all emitted),
+    so the oracle's verify over those rows gives P(accept) = sum_x p_draft(x) p_verify(x)
+    from its pulse-0 (the draft's logits: the draft pass of row i sees the block's pulse-0
+    keys, as the verify's pulse 0 does) and last-pulse logits. `emitted` may be the start
+    of a longer generation of max_new tokens (default: its own length); a round cut off by
+    its end is left out. Returns (P(accept), accepted) per test."""
+    cfg = engine.cfg
+    ids = torch.as_tensor(prompt_ids, dtype=torch.long).view(1, -1)
+    cache = RefKVCache(cfg)
+    engine.prefill(ids, cache)
+    seen = ids[0].tolist()
+    pos = len(seen)
+    n = len(emitted)
+    total = n if max_new is None else max_new
+    out = []
+    i = 0
+    while i < n:
+        if kinds[i] != 0:
+            raise ValueError(f"token {i} marked as an accepted draft at the start of a round")
+        t = int(emitted[i])
+        seen.append(t)
+        produced = i + 1
+        if produced >= total:
+            break
+        a = 0
+        while i + 1 + a < n and kinds[i + 1 + a] == 1:
+            a += 1
+        if i + 1 + a >= n and produced + a < total:
+            break  # the round's last test lies past the given stream
+        g = min(draft_len, total - produced - 1)
+        if a > g:
+            raise ValueError(f"round at token {i}: {a} accepted drafts, at most {g} drafted")
+        blk = [t] + [int(x) for x in emitted[i + 1:i + 1 + a]]
+        _, per_pulse, kv = engine.block_verify(blk, pos, cache)
+        tests = min(a + 1, g)
+        for j in range(tests):
+            extra = blk[1:j + 1]
+            out.append((accept_probability(per_pulse[0][j:j + 1], per_pulse[-1][j:j + 1],
+                                           seen + extra, temperature, top_p,
+                                           repetition_penalty), j < a))
+        seen.extend(blk[1:])
+        engine.commit_block(cache, kv, a + 1)
+        pos += a + 1
+        i += 1 + a
+    return out
 
 
 def replay_acceptance(engine: "RefEngine", prompt_ids, emitted, kinds, temperature: float,

@@ -154,3 +154,41 @@ def test_block_acceptance_bookkeeping_hand_worked():
     # a rejection whose fresh draw is a stop id ends the stream
     eng = _Rigged([[0, 1]], stop_ids={0})
     assert list(eng.block_speculative_ids([1, 2], 10, 0.0, 1.0, 1.0, 1)) == [3]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_block_acceptance_replay_follows_the_generator(tiny_state, dtype):
+    """replay_block_acceptance driven along the generator's own sampled stream (its kinds
+    recorded in stats) gives the generator's tests: the same acceptance probabilities bit
+    for bit, in order, and the same accepted flags."""
+    cfg, st = tiny_state
+    g = golden("tiny_fp32.npz")
+    eng = R.load_ref(cfg, st, dtype, stop_ids=set())
+    # low temperature: the tiny model's drafts are then accepted now and then (both
+    # outcomes of a test, and rounds of several accepted drafts, are exercised)
+    for G, temp in ((3, 0.2), (4, 0.2)):
+        stats = {}
+        out = list(eng.block_speculative_ids(g["prompt"], 30, temp, 0.95, 1.15, G,
+                                             torch.Generator().manual_seed(11 + G), stats=stats))
+        assert len(out) == 30 and len(stats["kinds"]) == 30
+        rep = R.replay_block_acceptance(eng, g["prompt"], out, stats["kinds"], temp, 0.95, 1.15,
+                                        G)
+        assert [p for p, _ in rep] == stats["p_accept"]
+        assert sum(a for _, a in rep) == stats["accepted"] and len(rep) == stats["tests"]
+        assert 0 < stats["accepted"] < stats["tests"]
+
+
+def test_block_acceptance_replay_of_a_stream_prefix(tiny_state):
+    """A prefix of a longer generation replays the complete rounds it holds: the first
+    tests of the whole stream's replay, none from a round cut off by the prefix's end."""
+    cfg, st = tiny_state
+    g = golden("tiny_fp32.npz")
+    eng = R.load_ref(cfg, st, torch.float32, stop_ids=set())
+    stats = {}
+    out = list(eng.block_speculative_ids(g["prompt"], 30, 0.2, 0.95, 1.15, 4,
+                                         torch.Generator().manual_seed(15), stats=stats))
+    full = R.replay_block_acceptance(eng, g["prompt"], out, stats["kinds"], 0.2, 0.95, 1.15, 4)
+    for cut in (7, 13, 20):
+        part = R.replay_block_acceptance(eng, g["prompt"], out[:cut], stats["kinds"][:cut], 0.2,
+                                         0.95, 1.15, 4, max_new=30)
+        assert part == full[:len(part)] and len(part) <= len(full)
