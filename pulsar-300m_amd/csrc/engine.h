@@ -13,13 +13,13 @@ constexpr int kPage = 64;  // positions per KV page
 // One (token, pulse) evaluation inside a step. Rows of a step are sorted by pulse.
 struct RowDesc {
   int32_t seq;    // sequence index
-  int32_t slot;   // token-state slot of the sequence (0 or 1)
+  int32_t slot;   // the row's slot: c/s token (0 or 1, exact mode), block row (draft-block)
   int32_t pulse;  // 0..n_pulses-1
   int32_t pos;    // absolute position of the token
   int32_t token;  // token id
   int32_t lrow;   // logits row, or -1 when this pass needs no logits
   int32_t extra_seen;  // token counted as seen when sampling this row (-1 = none)
-  int32_t pad;
+  int32_t sslot;  // token-state slot the pulse kernels read and write (seq * slots + sslot)
 };
 
 // Step control block, written by the controller (or the host for prefill).

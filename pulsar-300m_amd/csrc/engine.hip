@@ -1305,7 +1305,7 @@ int verify(Engine& e, const int32_t* host_tokens, int n, int use_graph, hipStrea
         for (int i = 0; i < n; ++i) {
           const int r = b * n + i;
           rows[(size_t)k * MR + r] =
-              RowDesc{b, i, k, pos + i, host_tokens[r], k == P - 1 ? r : -1, -1, 0};
+              RowDesc{b, i, k, pos + i, host_tokens[r], k == P - 1 ? r : -1, -1, i};
         }
         units[(size_t)k * B + b] = un;
       }

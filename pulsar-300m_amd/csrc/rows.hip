@@ -67,7 +67,7 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
   if (r >= a.ctl->n_rows) return;
   const RowDesc rd = a.rows[r];
   const int D = a.D, i0 = lane * EPL;
-  const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * a.slots + rd.slot;
+  const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * a.slots + rd.sslot;
   T* e = reinterpret_cast<T*>(a.e_state) + (int64_t)st * D;
   const T* step = reinterpret_cast<const T*>(a.step_emb) + (int64_t)rd.pulse * D;
   float hv[EPL], stp[EPL];
@@ -1779,7 +1779,7 @@ __global__ void __launch_bounds__(256) pulse_output_kernel(PulseOutputArgs a) {
   if (r >= a.ctl->n_rows) return;
   const RowDesc rd = a.rows[r];
   const int D = a.D;
-  const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * a.slots + rd.slot;
+  const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * a.slots + rd.sslot;
   const T* hi = reinterpret_cast<const T*>(a.h_in) + (int64_t)r * D;
   const T* h = reinterpret_cast<const T*>(a.h) + (int64_t)r * D;
   const T* rs = reinterpret_cast<const T*>(a.res_scale) + (int64_t)rd.pulse * D;

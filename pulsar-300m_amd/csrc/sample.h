@@ -29,7 +29,7 @@ struct SeqState {
   int32_t row_c, row_s, lrow_c, lrow_s;
   uint32_t ctr;
   int32_t tail;  // plain mode with early exit: the last emitted token runs for its exit count
-  int32_t pad;
+  int32_t blk_base;  // draft-block mode: token-state slot of block row 0 (rotates per round)
   // draft-block mode: block tokens (blk[0] = the round's emitted token at position c_pos),
   // tokens known, phase (0 draft, 1 verify), step within the phase (draft index or verify
   // pulse), drafts wanted this round

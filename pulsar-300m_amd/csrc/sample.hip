@@ -583,7 +583,7 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
     s.lrow_s = lr++;
     a.lrow_seq[s.lrow_s] = b;
     a.lrow_extra[s.lrow_s] = s.s_tok;
-    a.rows[idx] = RowDesc{b, 1 - s.c_slot, 0, s.c_pos + 1, s.s_tok, s.lrow_s, s.s_tok, 0};
+    a.rows[idx] = RowDesc{b, 1 - s.c_slot, 0, s.c_pos + 1, s.s_tok, s.lrow_s, s.s_tok, 1 - s.c_slot};
     s.row_s = idx;
   }
   if (crow) {
@@ -594,7 +594,7 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
       a.lrow_seq[s.lrow_c] = b;
       a.lrow_extra[s.lrow_c] = -1;
     }
-    a.rows[idx] = RowDesc{b, s.c_slot, p, s.c_pos, s.c_tok, s.lrow_c, -1, 0};
+    a.rows[idx] = RowDesc{b, s.c_slot, p, s.c_pos, s.c_tok, s.lrow_c, -1, s.c_slot};
     s.row_c = idx;
     AttnUnit un{};
     un.seq = b;
@@ -644,6 +644,11 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
 namespace {
 
 __device__ void new_round(const ControllerArgs& a, SeqState& s, int tok) {
+  // block row i keeps its token state in slot (blk_base + i) % S; the base steps back one
+  // slot per round, so the row the previous round's last verify step ran one slot past its
+  // block (slot base - 1) is this round's row 0
+  const int S = engine_slots(a.draft_len);
+  s.blk_base = (s.blk_base + S - 1) % S;
   s.blk[0] = tok;
   for (int i = 1; i < kMaxBlock; ++i) s.blk[i] = -1;
   s.blk_n = 1;
@@ -655,21 +660,38 @@ __device__ void new_round(const ControllerArgs& a, SeqState& s, int tok) {
   s.blk_step = 0;
 }
 
+// The verify's pulse 0 runs only rows whose pulse 0 no draft step ran: a draft step ran
+// pulse 0 of its row over the committed cache and the block's earlier pulse-0 keys, which is
+// the verify's rule, so that row's keys, values and token state are the verify's pulse 0
+// already (the kernels' results do not depend on the other rows of a step). That leaves
+// the block's last row when a draft was drawn from the row before it, and none when a stop
+// id ended the block: the verify then starts at pulse 1, and the pipelined round's guess is
+// the stopping draft row's own penalised argmax.
+__device__ void enter_verify(const ControllerArgs& a, SeqState& s, bool last_ran, int lrow) {
+  s.blk_phase = 1;
+  s.blk_step = 0;
+  if (last_ran && a.n_pulses > 1) {
+    s.blk_step = 1;
+    if (block_pipelined(a.draft_len)) {
+      s.s_tok = a.argmax[lrow];
+      s.s_valid = !is_stop(a, s.s_tok);
+    }
+  }
+}
+
 __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
   const int P = a.n_pulses;
   if (s.blk_phase == 0) {
     const int j = s.blk_step;
     const int d = a.draw[s.lrow_c * 2];
     if (is_stop(a, d)) {
-      s.blk_phase = 1;
-      s.blk_step = 0;
+      enter_verify(a, s, true, s.lrow_c);
       return;
     }
     s.blk[j + 1] = d;
     s.blk_n = j + 2;
     if (j + 1 >= s.blk_g) {
-      s.blk_phase = 1;
-      s.blk_step = 0;
+      enter_verify(a, s, false, -1);
     } else {
       s.blk_step = j + 1;
     }
@@ -717,11 +739,11 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
     // the speculative row was this round's first draft step
     const int d = a.draw[spec_lrow * 2];
     if (is_stop(a, d)) {
-      s.blk_phase = 1;
+      enter_verify(a, s, true, spec_lrow);
     } else {
       s.blk[1] = d;
       s.blk_n = 2;
-      if (s.blk_g <= 1) s.blk_phase = 1;
+      if (s.blk_g <= 1) enter_verify(a, s, false, -1);
       else s.blk_step = 1;
     }
   }
@@ -769,6 +791,10 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
     } else {
       nrow = s.blk_n;
       pulse = s.blk_step;
+      if (pulse == 0 && P > 1) {  // the verify's pulse 0: the block's last row alone
+        slot0 = s.blk_n - 1;
+        nrow = 1;
+      }
       lrows = (pulse == P - 1 || a.all_logits) ? nrow : 0;
       // pulse 0 of a verify: the last row's logits give the guess
       guess_row = pipe && pulse == 0 && P > 1;
@@ -799,6 +825,7 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
     const int lr0 = v[3];
     s.row_c = r0;
     s.lrow_c = lrows ? lr0 : -1;
+    const int S = engine_slots(a.draft_len);
     AttnUnit un{};
     un.seq = b;
     un.n = nrow + (spec ? 1 : 0);
@@ -808,7 +835,7 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
     for (int i = 0; i < nrow; ++i) {
       const int slot = slot0 + i;
       const int lr = lrows == nrow ? lr0 + i : (lrows && i == nrow - 1 ? lr0 : -1);
-      a.rows[r0 + i] = RowDesc{b, slot, pulse, pos0 + i, s.blk[slot], lr, -1, 0};
+      a.rows[r0 + i] = RowDesc{b, slot, pulse, pos0 + i, s.blk[slot], lr, -1, (s.blk_base + slot) % S};
       if (lr >= 0) {
         a.lrow_seq[lr] = b;
         for (int x = 0; x < kMaxExtra; ++x)
@@ -823,7 +850,7 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
       // round's drafts and the guess)
       const int r = base[0] + v[0] + (pulse == 0 ? nrow : 0);
       const int lr = lr0 + lrows;
-      a.rows[r] = RowDesc{b, engine_slots(a.draft_len) - 1, 0, s.c_pos + nrow, s.s_tok, lr, -1, 0};
+      a.rows[r] = RowDesc{b, S - 1, 0, s.c_pos + nrow, s.s_tok, lr, -1, (s.blk_base + S - 1) % S};
       un.row[nrow] = r;
       s.row_s = r;
       s.lrow_s = lr;

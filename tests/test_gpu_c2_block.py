@@ -3,9 +3,10 @@ Pulsar-283M, 16 sequences of 2048 uniform-random prompt tokens, sampled (tempera
 top-p 0.95, repetition penalty 1.15, no stop ids), 256 new tokens, draft length 4.
 
 * Sequence 0's first round against the oracle's block restatement
-  (RefEngine.block_verify over the engine's own block [t, d1..d4] at the prompt's end):
-  the four draft rows' pulse-0 logits and the verify's pulse 0/1/2 logits of all five rows
-  within max|diff| / max|ref| <= 2e-2.
+  (RefEngine.block_verify over the engine's own block [t, d1..d4] at the prompt's end): the
+  pulse-0 logits of the five rows (four draft steps, and the verify's pulse 0, which runs
+  the last row alone: the draft steps ran the others' pulse 0 under the verify's rule) and
+  the verify's pulse 1/2 logits of all five rows within max|diff| / max|ref| <= 2e-2.
 * Every sequence emits 256 tokens; sequences 0 and 15 of the batch equal the same prompts
   decoded alone with the same random stream (a single run reproduces slot b with
   seed + b * 0x9E3779B97F4A7C15).
@@ -52,38 +53,32 @@ def test_c2_draft_block_parity_and_acceptance(models, full_state, c2_prompts):
               repetition_penalty=RP, stop_ids=[], draft_len=G)
     with HipEngine(model, batch=B, seed=SEED, all_logits=True, **kw) as eng:
         eng.prefill(c2_prompts)
-        drafts, verify = {}, {}
+        first = {}  # (pulse, block row) -> (token, logits) of the first round's rows
         for _ in range(2 * (G + P)):
             eng.step(1)
             rows = eng.rows(last=True)
             lg = eng.logits(len(rows))
-            mine = [r for r in rows if int(r[0]) == 0]
-            if len(mine) == 1 and int(mine[0][2]) == 0 and not verify:
-                drafts[int(mine[0][3]) - T] = lg[int(mine[0][5])].copy()
-            elif len(mine) > 1:
-                for r in mine:
-                    if T <= int(r[3]) <= T + G:  # the first round's block rows
-                        verify[(int(r[2]), int(r[3]) - T)] = (int(r[4]), lg[int(r[5])].copy())
-            if len(verify) == P * (G + 1):
+            for r in rows:
+                key = (int(r[2]), int(r[3]) - T)
+                if int(r[0]) == 0 and 0 <= key[1] <= G and key not in first:
+                    first[key] = (int(r[4]), lg[int(r[5])].copy())
+            if len(first) == P * (G + 1):
                 break
         eng.run()
         toks, kinds = eng.tokens(), eng.token_kinds()
         tests, accepted = eng.acceptance()
     print(f"[c2 draft 4] tests {tests} accepted {accepted}", flush=True)
     assert all(len(t) == N_NEW for t in toks)
-    assert sorted(drafts) == list(range(G)) and len(verify) == P * (G + 1)
-    blk = [verify[(0, i)][0] for i in range(G + 1)]
-    assert blk[0] == toks[0][0]
+    assert sorted(first) == [(k, i) for k in range(P) for i in range(G + 1)]
+    blk = [first[(0, i)][0] for i in range(G + 1)]
+    assert blk[0] == toks[0][0] and all(first[(k, i)][0] == blk[i] for k, i in first)
 
     ref = R.load_ref(cfg, st, torch.bfloat16, stop_ids=set())
     cache = R.RefKVCache(cfg)
     ref.prefill(torch.as_tensor(c2_prompts[0]).view(1, -1), cache)
     _, per_pulse, _ = ref.block_verify(blk, T, cache)
-    err = {}
-    for j, got in drafts.items():
-        err[("draft", j)] = max_abs_rel(got, per_pulse[0][j].float().numpy())
-    for (k, i), (_, got) in verify.items():
-        err[("verify", k, i)] = max_abs_rel(got, per_pulse[k][i].float().numpy())
+    err = {(k, i): max_abs_rel(got, per_pulse[k][i].float().numpy())
+           for (k, i), (_, got) in first.items()}
     worst = max(err, key=err.get)
     print(f"[c2 draft 4] sequence 0 first round: worst {worst} {err[worst]:.2e}", flush=True)
     assert err[worst] <= 2e-2
