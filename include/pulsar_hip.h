@@ -326,7 +326,10 @@ typedef struct PulsarEngineConfig {
                                   [11]=tests [12]=accepted */
 #define PULSAR_BUF_LOGITS 2    /* fp32 [n_lrows][V] logits of the last step */
 #define PULSAR_BUF_ROWS 3      /* int32 [n_rows][8] rows of the next step
-                                  (seq, slot, pulse, pos, token, lrow, extra, 0) */
+                                  (seq, slot, pulse, pos, token, lrow, extra, state slot):
+                                  slot = c/s token or block row, state slot = the token
+                                  state the row reads and writes (draft-block mode: rotates
+                                  per round) */
 #define PULSAR_BUF_CTL 4       /* int32 [16] n_rows, n_lrows, pulse_start[4],
                                   pulse_count[4], active, step, n_units */
 #define PULSAR_BUF_LAST_ROWS 5 /* int32 [n_rows][8] rows of the last executed step */
