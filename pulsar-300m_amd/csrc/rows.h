@@ -16,6 +16,9 @@ constexpr int kLongCacheSplits = 16;
 // engines of at least this many sequences (units) take 1024-key splits in the long
 // engines' sliding-window layers, fewer keep 256-key splits
 constexpr int kManyUnits = 16;
+// 64-key blocks per wave and split for units of more than 4 rows in engines below the
+// long-cache threshold (4 and fewer rows: 1)
+constexpr int kWideUnitBlocks = 2;
 static_assert(kUnitSplit >= kSplitLen, "split partial slots are sized for kSplitLen");
 constexpr int kMaxRank = 16;    // re-injection gate rank bound
 
