@@ -651,21 +651,32 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     ca.next_norm = l + 1 < e.L ? m.attn_norm[l + 1] : nullptr;
     ca.xn = e.xn;
     ca.eps = m.rms_eps;
+    if (fuse_post && l + 1 == e.L) {
+      // bf16: the last layer's combine also does the pulse output (no separate launch)
+      ca.h_in = e.h_in;
+      ca.res_scale = m.res_scale;
+      ca.hout_state = e.hout_state;
+      ca.slots = e.S;
+      ca.final_norm = m.final_norm;
+      ca.xn_final = e.xn_final;
+    }
     PULSAR_TIMED(PC_COMBINE, launch_moe_combine(ca, dt, MR, s));
   }
-  PulseOutputArgs po{};
-  po.ctl = ctl;
-  po.rows = rows;
-  po.D = D;
-  po.slots = e.S;
-  po.eps = m.rms_eps;
-  po.h_in = e.h_in;
-  po.h = e.h;
-  po.res_scale = m.res_scale;
-  po.hout_state = e.hout_state;
-  po.final_norm = m.final_norm;
-  po.xn_final = e.xn_final;
-  PULSAR_TIMED(PC_OUTPUT, launch_pulse_output(po, dt, MR, s));
+  if (!fuse_post) {
+    PulseOutputArgs po{};
+    po.ctl = ctl;
+    po.rows = rows;
+    po.D = D;
+    po.slots = e.S;
+    po.eps = m.rms_eps;
+    po.h_in = e.h_in;
+    po.h = e.h;
+    po.res_scale = m.res_scale;
+    po.hout_state = e.hout_state;
+    po.final_norm = m.final_norm;
+    po.xn_final = e.xn_final;
+    PULSAR_TIMED(PC_OUTPUT, launch_pulse_output(po, dt, MR, s));
+  }
   if (!head) return PULSAR_OK;
   GemmArgs g = gemm_base(e);
   g.A = e.xn_final;

@@ -236,6 +236,15 @@ struct CombineArgs {
   const float* next_norm;    // [P][D] attn_norm of the next layer (nullable)
   void* xn;                  // normed h output when next_norm is set
   float eps;
+  // decode, last layer (nullable hout_state: no pulse output here): the pulse output of
+  // pulse_output_kernel folded in — harmonic residual into the row's token state and, for
+  // logits rows, the final norm
+  const void* h_in;          // [rows][D] pulse input
+  const void* res_scale;     // [P][D] T
+  void* hout_state;          // [B * slots][D]
+  int slots;
+  const float* final_norm;   // [D]
+  void* xn_final;            // [lrows][D]
 };
 
 struct PulseOutputArgs {

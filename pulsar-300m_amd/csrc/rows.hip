@@ -1701,6 +1701,15 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
 #pragma unroll
   for (int k = 0; k < KT; ++k) ldv<EPL>(rop + (int64_t)(k < K ? k : 0) * D, ro[k]);
   const float wl = a.topk_w[(int64_t)r * K + min(lane, K - 1)];
+  // the folded pulse output's row operands go out with the rest (a uniform branch on a
+  // kernel argument)
+  const bool pout = a.hout_state != nullptr;
+  float hin[EPL];
+  RowDesc rd{};
+  if (pout) {
+    ldv<EPL>(reinterpret_cast<const T*>(a.h_in) + (int64_t)r * D + i0, hin);
+    rd = a.rows[r];
+  }
   int n = a.m_fixed, pulse = a.pulse;
   if (a.ctl) {
     int ps[kMaxPulses], pc[kMaxPulses];
@@ -1721,6 +1730,11 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
   ldv<EPL>(reinterpret_cast<const T*>(a.routed_scale) + (int64_t)pulse * D + i0, rs);
   float nwn[EPL];
   if (a.next_norm) ldv<EPL>(a.next_norm + (int64_t)pulse * D + i0, nwn);
+  float rso[EPL], fn[EPL];
+  if (pout) {
+    ldv<EPL>(reinterpret_cast<const T*>(a.res_scale) + (int64_t)pulse * D + i0, rso);
+    ldv<EPL>(a.final_norm + i0, fn);
+  }
   bool kept[KT];
 #pragma unroll
   for (int k = 0; k < KT; ++k) kept[k] = true;
@@ -1758,6 +1772,23 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
   }
   if (!live) return;
   stv<EPL>(h, hv);
+  if (pout) {
+    // pulse_output_kernel's arithmetic: out = h_in + (h - h_in) * res_scale, each step
+    // rounded to T; logits rows also get final_norm(out)
+    float o[EPL];
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) o[c] = rnd<T>(hin[c] + rnd<T>(rnd<T>(hv[c] - hin[c]) * rso[c]));
+    stv<EPL>(reinterpret_cast<T*>(a.hout_state) + ((int64_t)rd.seq * a.slots + rd.sslot) * D + i0, o);
+    if (rd.lrow >= 0) {
+      float ss = 0.f, y[EPL];
+#pragma unroll
+      for (int c = 0; c < EPL; ++c) ss += o[c] * o[c];
+      const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
+#pragma unroll
+      for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(fn[c] * (o[c] * inv));
+      stv<EPL>(reinterpret_cast<T*>(a.xn_final) + (int64_t)rd.lrow * D + i0, y);
+    }
+  }
   if (a.next_norm) {
     float ss = 0.f, y[EPL];
 #pragma unroll
