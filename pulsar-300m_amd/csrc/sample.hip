@@ -121,13 +121,6 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
 #pragma unroll
   for (int x = 0; x < kMaxExtra; ++x)
     xt[x] = x < a.n_extra ? a.lrow_extra[(int64_t)lr * a.extra_stride + x] : -1;
-#pragma unroll
-  for (int x = 0; x < kMaxExtra; ++x) {
-    if (xt[x] < 0) continue;
-    has_extra = true;
-    const int off = xt[x] - base;
-    if (off >= 0 && off < PER) xmask |= 1ull << off;
-  }
   float l[PER];
 #pragma unroll
   for (int i = 0; i < PER; i += 4) {
@@ -136,6 +129,13 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
     l[i + 1] = v.y;
     l[i + 2] = v.z;
     l[i + 3] = v.w;
+  }
+#pragma unroll
+  for (int x = 0; x < kMaxExtra; ++x) {
+    if (xt[x] < 0) continue;
+    has_extra = true;
+    const int off = xt[x] - base;
+    if (off >= 0 && off < PER) xmask |= 1ull << off;
   }
   if (a.out_maxprob) {
     // early-exit test (src/infer.py:540-541): max of softmax(logits) = 1 / sum exp(l - max),
@@ -177,17 +177,18 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
   // x / temperature for every score: the quotient by the correctly rounded reciprocal and
   // one fma correction (Markstein's theorem: RN(q + (x - q t) r) = RN(x / t) when r =
   // RN(1 / t) and no intermediate over- or underflows), three instructions in place of the
-  // full-precision divide; a non-finite product is kept as it is
+  // full-precision divide; a non-finite product is kept as it is. The map (this quotient,
+  // then the rounding to T) is monotone, so the largest scaled score is the scaled maximum:
+  // no reduction of its own.
   const float tmp = a.temperature, rtmp = 1.0f / tmp;
-  float mx = -INFINITY;
+  auto scaled = [&](float x) {
+    const float q = x * rtmp;
+    const float q2 = fmaf(fmaf(-q, tmp, x), rtmp, q);
+    return rnd<T>(__builtin_isfinite(q) ? q2 : q);
+  };
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const float q = l[i] * rtmp;
-    const float q2 = fmaf(fmaf(-q, tmp, l[i]), rtmp, q);
-    l[i] = rnd<T>(__builtin_isfinite(q) ? q2 : q);
-    mx = fmaxf(mx, l[i]);
-  }
-  mx = block_max(mx, red);
+  for (int i = 0; i < PER; ++i) l[i] = scaled(l[i]);
+  const float mx = scaled(am.v);
   // Unnormalised probabilities and order keys, computed once. bf16-rounded scores carry
   // no information in the low 16 key bits (all zero for positive, all one for negative
   // values, so equal high halves mean equal keys): the threshold search runs on the high
