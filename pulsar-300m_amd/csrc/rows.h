@@ -6,8 +6,9 @@
 namespace pulsar {
 
 constexpr int kSplitLen = 256;  // keys per decode-attention block (fp32 path)
-// bf16 decode attention: waves per workgroup and keys per split workgroup (one 64-key
-// block per wave: more, shorter splits measured faster than fewer, longer ones)
+// bf16 decode attention: waves per workgroup, and keys per split workgroup at one 64-key
+// block per wave (the unit in which split counts and partial slots are sized; launches
+// take 2-8 blocks per wave)
 constexpr int kUnitWaves = 4;
 constexpr int kUnitSplit = kUnitWaves * 64;
 // engines whose context needs more 256-key splits than this use 2048-key splits in the
@@ -16,9 +17,8 @@ constexpr int kLongCacheSplits = 16;
 // engines of at least this many sequences (units) take 1024-key splits in the long
 // engines' sliding-window layers, fewer keep 256-key splits
 constexpr int kManyUnits = 16;
-// 64-key blocks per wave and split for units of more than 4 rows in engines below the
-// long-cache threshold (4 and fewer rows: 1)
-constexpr int kWideUnitBlocks = 2;
+// 64-key blocks per wave and split in engines below the long-cache threshold
+constexpr int kShortCacheBlocks = 2;
 static_assert(kUnitSplit >= kSplitLen, "split partial slots are sized for kSplitLen");
 constexpr int kMaxRank = 16;    // re-injection gate rank bound
 

@@ -639,7 +639,7 @@ __device__ __forceinline__ void attn_merge_splits(const AttnArgs& a, int u, int 
 // to the caches at the end (the arithmetic of qk_post_kernel, bit for bit).
 // COLS = 8 serves units of up to 2 rows (exact mode), 16 up to 4, 32 up to 8. BPW = 64-key
 // blocks per wave and split: long caches take BPW = 8 (2048-key splits) in the global
-// layers and 4 in the sliding-window layers. Holding the next block in registers while
+// layers and 4 in the sliding-window layers, shorter ones 2 (512-key splits). Holding the next block in registers while
 // computing the current one (64 more registers: one wave per SIMD) and touching the next
 // blocks' lines ahead of their loads were both measured slower at 64 x 8192 positions, and
 // so was staging the blocks through LDS with direct global-to-LDS loads (2-stage rings of
@@ -1888,17 +1888,16 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     // the batch). Engines whose context needs more than kLongCacheSplits 256-key splits
     // take 2048-key splits (8 blocks per wave) in the global layers, which spread each
     // workgroup's fixed start and merge costs over 8x the keys, and 1024-key splits in the
-    // sliding-window layers (at most window + unit rows keys: two splits); shorter engines
-    // take 256-key splits (one block per wave, many workgroups in parallel).
+    // sliding-window layers (at most window + unit rows keys: two splits).
     const bool lng = a.max_splits_unit > kLongCacheSplits;
     // engines of few sequences keep 256-key splits in the sliding-window layers: 1024-key
     // splits would leave most CUs idle there (two workgroups per unit and kv head)
     const bool few = a.max_units < kManyUnits;
-    // 32-column units (draft blocks of 5-8 rows) hold two workgroups per CU (212 registers
-    // a lane) and repeat the unit's query post-processing in every split: 512-key splits
-    // (c2 draft-block: 25.4k -> 25.9k tokens/s with them in the sliding-window layers too)
-    const bool wide_units = a.unit_rows > 4;
-    const int bpw = !lng ? (wide_units ? kWideUnitBlocks : 1) : (a.is_local ? (few ? 1 : 4) : 8);
+    // shorter engines: 512-key splits (two blocks per wave). Every split repeats the unit's
+    // query post-processing and adds a partial to merge; against 256-key splits: c2
+    // draft-block 25.4k -> 25.9k tokens/s, c2 reference schedule 18.5k -> 18.9k, c5 85.3k
+    // -> 87.1k (1024-key splits for draft blocks: 24.8k)
+    const int bpw = !lng ? kShortCacheBlocks : (a.is_local ? (few ? 1 : 4) : 8);
     const int split = kUnitSplit * bpw;
     // a unit's keys [lo, hi] lie in the splits from lo's to hi's: at most max_ctx keys, and in
     // sliding-window layers window + rows - 1 keys, which can straddle one more split
