@@ -623,7 +623,8 @@ def kv_footprint(cfg) -> dict:
 
 def run_c4(model, cfg, args, profile: bool = True) -> dict:
     """4 sequences of 32768 uniform-random prompt tokens, 512 new tokens, greedy (the
-    configuration names no temperature), reference schedule."""
+    configuration names no temperature): reference schedule, and the draft-block mode at
+    the configuration's draft length 4 beside it."""
     import numpy as np
 
     from pulsar_engine import weights as W
@@ -632,6 +633,9 @@ def run_c4(model, cfg, args, profile: bool = True) -> dict:
                       warmup=1, label="c4", profile=profile)
     c4["workload"] = ("Pulsar-283M bf16, batch 4, 32768-token uniform prompts, greedy "
                       "self-speculative decode of 512 tokens (reference schedule)")
+    c4["draft_block_4"] = run_workload(model, cfg, p4, 512, 0.0, 1.0, args.repetition_penalty,
+                                       steps=1, warmup=1, profile=False, draft_len=4,
+                                       label="c4 draft-block 4")
     log(f"c4: {json.dumps({k: v for k, v in c4.items() if k != 'kernel_profile'})}")
     return c4
 
