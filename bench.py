@@ -37,23 +37,6 @@ for _p in (ROOT, PKG):
 METRIC = "accepted tokens/s at 1 GPU (batch 16, ctx 2k); % HBM roofline; acceptance rate"
 HBM_PEAK = 8.0e12
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 matrix-core peak (no sparsity)
-# kernels behind each timed class (names as rocprofv3 lists them), bf16 decode
-CLASS_KERNELS = {
-    "attention": ["attn_decode_unit_kernel<8, 1>"],
-    "routed_gate_up": ["gemm_bf16_kernel<3, 4, 1, 1, true, false>"],
-    "routed_down": ["gemm_bf16_kernel<0, 2, 1, 2, false, false>"],
-    "qkv_gate_gemm": ["gemm_bf16_kernel<1, 4, 0, 1, false, false>"],
-    "wo_gemm": ["gemm_bf16_kernel<2, 4, 0, 1, false, false>"],
-    "lm_head": ["gemm_bf16_kernel<4, 4, 3, 1, false, false>"],
-    "router": ["norm_router_kernel<bf16, 16, 16>"],
-    "moe_combine": ["moe_combine_rows_kernel<bf16, 16, 4>"],
-    "sample": ["sample_kernel<bf16, 32, 1024>"],
-    "pulse_input": ["pulse_input_kernel<bf16, 16, 8, true>"],
-    "pulse_output": ["pulse_output_kernel<bf16>"],
-    "controller": ["controller_kernel"],
-}
-
-
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_c2_b16_t2048.md")
 BLOCK_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_c2_draft4_b16_t2048.md")
 # kernel classes by the short names of their templates (gemm EPI: 0 store, 1 qkv + gate,
@@ -621,7 +604,7 @@ def kv_footprint(cfg) -> dict:
     return out
 
 
-def run_c4(model, cfg, args, profile: bool = True) -> dict:
+def run_c4(model, cfg, args, profile: bool = True, draft_block: bool = True) -> dict:
     """4 sequences of 32768 uniform-random prompt tokens, 512 new tokens, greedy (the
     configuration names no temperature): reference schedule, and the draft-block mode at
     the configuration's draft length 4 beside it."""
@@ -633,9 +616,10 @@ def run_c4(model, cfg, args, profile: bool = True) -> dict:
                       warmup=1, label="c4", profile=profile)
     c4["workload"] = ("Pulsar-283M bf16, batch 4, 32768-token uniform prompts, greedy "
                       "self-speculative decode of 512 tokens (reference schedule)")
-    c4["draft_block_4"] = run_workload(model, cfg, p4, 512, 0.0, 1.0, args.repetition_penalty,
-                                       steps=1, warmup=1, profile=False, draft_len=4,
-                                       label="c4 draft-block 4")
+    if draft_block:
+        c4["draft_block_4"] = run_workload(model, cfg, p4, 512, 0.0, 1.0,
+                                           args.repetition_penalty, steps=1, warmup=1,
+                                           profile=False, draft_len=4, label="c4 draft-block 4")
     log(f"c4: {json.dumps({k: v for k, v in c4.items() if k != 'kernel_profile'})}")
     return c4
 
@@ -758,7 +742,8 @@ def main() -> int:
         print(json.dumps({"verify": vr}), flush=True)
         return 0
     if args.only == "c4":
-        print(json.dumps({"c4": run_c4(model, cfg, args, profile=False)}), flush=True)
+        print(json.dumps({"c4": run_c4(model, cfg, args, profile=False, draft_block=False)}),
+              flush=True)
         return 0
     if args.only == "c5":
         print(json.dumps({"c5": run_c5(cfg, state, args, profile=False, draft_block=False)}),
@@ -841,13 +826,14 @@ def main() -> int:
         per_launch = bytes_by_class[dom] / max(n, 1)
         avg_s = ms / max(n, 1) / 1e3
         achieved = per_launch / avg_s
-        traffic_b = recorded_traffic(CLASS_KERNELS.get(dom, [dom]))
+        traffic_b = recorded_traffic(["class:" + dom])
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
                     "traffic": round(traffic_b / 1e6, 3) if traffic_b else None,
                     "traffic_unit": "MB per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
-                                    "copy-calibrated)",
-                    "kernel": dom, "kernels": CLASS_KERNELS.get(dom, [dom]),
+                                    "copy-calibrated, averaged over every launch of the "
+                                    "class)",
+                    "kernel": dom,
                     "bytes_per_launch": int(per_launch), "avg_launch_us": round(avg_s * 1e6, 2),
                     "empty_event_pair_us": round(pair * 1e3, 2)}
         all_bytes = sum(bytes_by_class.values())
