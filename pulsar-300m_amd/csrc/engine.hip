@@ -84,8 +84,15 @@ struct Engine {
   hipGraphExec_t exec_multi = nullptr;  // kGraphSteps steps in one graph
   hipGraph_t graph_multi = nullptr;
   hipStream_t capture_stream = nullptr;  // graphs are captured here (never the legacy stream)
+  // pulsar_engine_generate: two pinned readback slots (control block + every sequence's
+  // state) and their completion events
+  void* host_rb = nullptr;
+  hipEvent_t rb_ev[2] = {nullptr, nullptr};
 
   ~Engine() {
+    for (hipEvent_t ev : rb_ev)
+      if (ev) hipEventDestroy(ev);
+    if (host_rb) hipHostFree(host_rb);
     if (exec) hipGraphExecDestroy(exec);
     if (graph) hipGraphDestroy(graph);
     if (exec_multi) hipGraphExecDestroy(exec_multi);
@@ -1455,17 +1462,59 @@ int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
                            hipStream_t stream, int32_t* steps_run) {
   PULSAR_REQUIRE(handle && check_every >= 1, "engine_generate: bad argument");
   Engine& e = *reinterpret_cast<Engine*>(handle);
-  int done = 0;
-  StepCtl c{};
-  while (done < max_steps) {
-    const int n = std::min(check_every, max_steps - done);
-    PULSAR_TRY(step(e, n, 1, stream));
-    done += n;
-    PULSAR_CHECK_HIP(hipMemcpyAsync(&c, e.ctl, sizeof(StepCtl), hipMemcpyDeviceToHost, stream));
-    PULSAR_CHECK_HIP(hipStreamSynchronize(stream));
-    if (c.active == 0) break;
+  // Steps go out in batches of check_every. Each batch is followed by a copy of the control
+  // block and the sequences' states into pinned host memory and an event. While the host
+  // waits for one batch's readback, the next batch is already queued whenever that wait's
+  // predecessor proved the work outlasts it, so the GPU does not idle between batches: with
+  // no stop ids a live sequence still owes max_new - produced tokens, and it takes at least
+  // one step per token in the draft-block mode (a round of g drafts is g + 2 steps for at
+  // most g + 1 tokens) and one step per two tokens otherwise. Near the end, and with stop
+  // ids, each batch is checked before the next one goes out, so no step runs past the last
+  // live sequence's batch.
+  const size_t rb = sizeof(StepCtl) + sizeof(SeqState) * (size_t)e.B;
+  if (!e.host_rb) {
+    PULSAR_CHECK_HIP(hipHostMalloc(&e.host_rb, 2 * rb));
+    for (hipEvent_t& ev : e.rb_ev) PULSAR_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   }
-  if (steps_run) *steps_run = done;
+  const int per_token = e.cfg.draft_len > 0 ? 1 : 2;  // tokens per step, at most (see above)
+  int launched = 0, checked = 0, bound = 0;
+  int q_n = 0, q_head = 0, q_steps[2] = {0, 0};  // queued readbacks, oldest first
+  auto launch = [&](int n) -> int {
+    PULSAR_TRY(step(e, n, 1, stream));
+    launched += n;
+    const int k = (q_head + q_n) & 1;
+    char* dst = reinterpret_cast<char*>(e.host_rb) + k * rb;
+    PULSAR_CHECK_HIP(hipMemcpyAsync(dst, e.ctl, sizeof(StepCtl), hipMemcpyDeviceToHost, stream));
+    PULSAR_CHECK_HIP(hipMemcpyAsync(dst + sizeof(StepCtl), e.state, sizeof(SeqState) * e.B,
+                                    hipMemcpyDeviceToHost, stream));
+    PULSAR_CHECK_HIP(hipEventRecord(e.rb_ev[k], stream));
+    q_steps[k] = launched;
+    ++q_n;
+    return PULSAR_OK;
+  };
+  if (max_steps > 0) PULSAR_TRY(launch(std::min(check_every, max_steps)));
+  while (q_n > 0) {
+    const int n = std::min(check_every, max_steps - launched);
+    if (n > 0 && q_n < 2 && launched - checked + n <= bound) PULSAR_TRY(launch(n));
+    const int k = q_head;
+    PULSAR_CHECK_HIP(hipEventSynchronize(e.rb_ev[k]));
+    q_head ^= 1;
+    --q_n;
+    checked = q_steps[k];
+    const char* src = reinterpret_cast<const char*>(e.host_rb) + k * rb;
+    const StepCtl* c = reinterpret_cast<const StepCtl*>(src);
+    const SeqState* st = reinterpret_cast<const SeqState*>(src + sizeof(StepCtl));
+    if (c->active == 0) break;
+    int rem = 0;
+    if (e.cfg.n_stop == 0)
+      for (int b = 0; b < e.B; ++b)
+        if (!st[b].done) rem = std::max(rem, st[b].max_new - st[b].produced);
+    bound = rem / per_token;
+    if (q_n == 0 && launched < max_steps) PULSAR_TRY(launch(std::min(check_every, max_steps - launched)));
+  }
+  // a batch queued behind the last readback (never, when the bound holds) finishes first
+  if (q_n > 0) PULSAR_CHECK_HIP(hipEventSynchronize(e.rb_ev[(q_head + q_n - 1) & 1]));
+  if (steps_run) *steps_run = launched;
   return PULSAR_OK;
 }
 
