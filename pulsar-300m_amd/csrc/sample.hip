@@ -526,14 +526,16 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
   const int b = threadIdx.x;
   StepCtl* ctl = a.ctl;
   const int P = a.n_pulses;
+  // the sequence's state is read with the snapshot of the last step's rows and control
+  // block (one round trip for both, before the barrier that retires the snapshot)
+  const bool act = b < a.B;
+  SeqState s{};
+  if (act) s = a.state[b];
   const int n_prev = ctl->n_rows;
   for (int i = b; i < n_prev; i += blockDim.x) a.last_rows[i] = a.rows[i];
   if (b == 0) *a.last_ctl = *ctl;
   __syncthreads();
-  const bool act = b < a.B;
-  SeqState s{};
   if (act) {
-    s = a.state[b];
     if (a.init) {
       s = SeqState{};
       s.max_new = a.max_new;
@@ -710,10 +712,22 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
   const bool spec_ran = s.row_s >= 0;
   const int spec_lrow = s.lrow_s, guess = s.s_tok;
   const int n = s.blk_n, lr0 = s.lrow_c;
+  // every draw the round's end may read, loaded together (rows past the block re-read its
+  // last row; the speculative row's first draw too)
+  int dv[kMaxBlock], dw[kMaxBlock];
+#pragma unroll
+  for (int i = 0; i < kMaxBlock; ++i) {
+    const int r = lr0 + min(i, n - 1);
+    dv[i] = a.draw[r * 2];
+    dw[i] = a.draw[r * 2 + 1];
+  }
+  const int d_spec = a.draw[max(spec_lrow, 0) * 2];
   int acc = 0, nxt = -1;
-  for (int i = 0; i < n; ++i) {
+#pragma unroll
+  for (int i = 0; i < kMaxBlock; ++i) {
+    if (i >= n) break;
     if (i < n - 1) {
-      const int v = a.draw[(lr0 + i) * 2];
+      const int v = dv[i];
       s.tests += 1;
       if (v == s.blk[i + 1] && !is_stop(a, v)) {
         s.accepted += 1;
@@ -722,9 +736,9 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
         if (s.done) return;
         continue;
       }
-      nxt = a.draw[(lr0 + i) * 2 + 1];
+      nxt = dw[i];
     } else {
-      nxt = a.draw[(lr0 + i) * 2];
+      nxt = dv[i];
     }
     break;
   }
@@ -738,7 +752,7 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
   new_round(a, s, nxt);
   if (spec_ran && acc == n - 1 && nxt == guess && s.blk_phase == 0) {
     // the speculative row was this round's first draft step
-    const int d = a.draw[spec_lrow * 2];
+    const int d = d_spec;
     if (is_stop(a, d)) {
       enter_verify(a, s, true, spec_lrow);
     } else {
@@ -757,14 +771,16 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
   const int b = threadIdx.x;
   StepCtl* ctl = a.ctl;
   const int P = a.n_pulses;
+  // the sequence's state is read with the snapshot of the last step's rows and control
+  // block (one round trip for both, before the barrier that retires the snapshot)
+  const bool act = b < a.B;
+  SeqState s{};
+  if (act) s = a.state[b];
   const int n_prev = ctl->n_rows;
   for (int i = b; i < n_prev; i += blockDim.x) a.last_rows[i] = a.rows[i];
   if (b == 0) *a.last_ctl = *ctl;
   __syncthreads();
-  const bool act = b < a.B;
-  SeqState s{};
   if (act) {
-    s = a.state[b];
     if (a.init) {
       s = SeqState{};
       s.max_new = a.max_new;
