@@ -50,6 +50,31 @@ def test_fp32_block_greedy_streams_equal_oracle(models, full_state, G):
     assert got == want
 
 
+@pytest.mark.parametrize("k", [3, 6, 11])
+def test_fp32_block_stop_id_drafted_mid_block(models, full_state, k):
+    """A stop id among the drafts ends the block early; the verify then starts at pulse 1
+    (every block row's pulse 0 ran in a draft step) and the stop id is never emitted. The
+    stop is the k-th token of the stream without stop ids: greedy drafts are accepted here,
+    so the run with that stop drafts it mid-block. Streams equal the oracle's."""
+    from oracle import pulsar_ref as R
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import PulsarInferenceEngine
+
+    cfg, st = full_state
+    prompt = W.uniform_ids(64, "block_prompt", 40, cfg.vocab_size).tolist()
+    free = list(_oracle(full_state, torch.float32).block_speculative_ids(prompt, 20, 0.0, 1.0,
+                                                                        10.0, 4))
+    stop = free[k]
+    assert stop not in free[:k]
+    ref = R.load_ref(cfg, st, torch.float32, rope_tables_fp32=True, stop_ids={stop})
+    want = list(ref.block_speculative_ids(prompt, 20, 0.0, 1.0, 10.0, 4))
+    eng = PulsarInferenceEngine(models[torch.float32])
+    got = eng.generate_ids([prompt], max_new_tokens=20, temperature=0.0,
+                           repetition_penalty=10.0, stop_ids=[stop], draft_len=4)[0]
+    print(f"k={k} stop {stop}: gpu {got}\n                ref {want}")
+    assert want == free[:k] and got == want
+
+
 def _compare_block_passes(models, full_state, dtype, G, tol, prompt=None, n_new=12):
     from oracle import pulsar_ref as R
     from pulsar_engine import weights as W
