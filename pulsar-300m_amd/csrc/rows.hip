@@ -64,14 +64,19 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
     for (int i = lane; i < a.n_zero; i += 64) a.zero_counts[i] = 0;
   }
   const int r = blockIdx.x;
-  if (r >= a.ctl->n_rows) return;
+  // the row descriptor is read with the row count (the rows buffer holds a descriptor for
+  // every block of the grid; the empty asm keeps the load ahead of the count test), and the
+  // pulse-indexed vectors, the next layer norm's included, right after it
   const RowDesc rd = a.rows[r];
+  asm volatile("" ::: "memory");
+  if (r >= a.ctl->n_rows) return;
   const int D = a.D, i0 = lane * EPL;
   const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * a.slots + rd.sslot;
   T* e = reinterpret_cast<T*>(a.e_state) + (int64_t)st * D;
   const T* step = reinterpret_cast<const T*>(a.step_emb) + (int64_t)rd.pulse * D;
-  float hv[EPL], stp[EPL];
+  float hv[EPL], stp[EPL], nw[EPL];
   ldv<EPL>(step + i0, stp);
+  if (a.norm_w) ldv<EPL>(a.norm_w + (int64_t)rd.pulse * D + i0, nw);
   if (rd.pulse == 0) {
     if (!a.prefill) {
       const T* x0 = reinterpret_cast<const T*>(a.tok_emb) + (int64_t)rd.token * D;
@@ -216,13 +221,12 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
   stv<EPL>(h_in + i0, hv);
   stv<EPL>(h + i0, hv);
   if (a.norm_w) {
-    float ss = 0.f, w[EPL], y[EPL];
+    float ss = 0.f, y[EPL];
 #pragma unroll
     for (int c = 0; c < EPL; ++c) ss += hv[c] * hv[c];
-    ldv<EPL>(a.norm_w + (int64_t)rd.pulse * D + i0, w);
     const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + a.eps);
 #pragma unroll
-    for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(w[c] * (hv[c] * inv));
+    for (int c = 0; c < EPL; ++c) y[c] = rnd<T>(nw[c] * (hv[c] * inv));
     stv<EPL>(reinterpret_cast<T*>(a.xn) + (int64_t)r * D + i0, y);
   }
 }
