@@ -103,8 +103,16 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
   __shared__ float red[32];
   __shared__ ArgMax ared[16];
   const int lr = blockIdx.x;
-  if (lr >= a.ctl->n_lrows) return;
+  // the row's sequence and extra seen tokens are read with the row count (their buffers
+  // hold an entry for every block of the grid; the empty asm keeps the loads ahead of the
+  // count test), so the logits and the seen bits go out one round trip later, together
   const int seq = a.lrow_seq[lr];
+  int xt[kMaxExtra];
+#pragma unroll
+  for (int x = 0; x < kMaxExtra; ++x)
+    xt[x] = x < a.n_extra ? a.lrow_extra[(int64_t)lr * a.extra_stride + x] : -1;
+  asm volatile("" ::: "memory");
+  if (lr >= a.ctl->n_lrows) return;
   if (a.n_seq > 0 && (seq < 0 || seq >= a.n_seq)) {
     if (threadIdx.x < 3) (threadIdx.x == 0 ? a.out_argmax[lr] : a.out_draw[lr * 2 + threadIdx.x - 1]) = -1;
     return;
@@ -114,13 +122,8 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
   const int base = threadIdx.x * PER;
   // tokens counted as seen for this row beyond the sequence's bitmap, as a mask over this
   // thread's PER logits
-  // (all loads issued before the first use)
   uint64_t xmask = 0;
   bool has_extra = false;
-  int xt[kMaxExtra];
-#pragma unroll
-  for (int x = 0; x < kMaxExtra; ++x)
-    xt[x] = x < a.n_extra ? a.lrow_extra[(int64_t)lr * a.extra_stride + x] : -1;
   float l[PER];
 #pragma unroll
   for (int i = 0; i < PER; i += 4) {
