@@ -314,13 +314,14 @@ def verify_microbench(model, cfg, es, args):
 
 def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warmup, es=2,
                  profile=True, draft_len=0, label="", speculative=True,
-                 early_exit_threshold=None, traffic_path=None):
+                 early_exit_threshold=None, traffic_path=None, keep_seq0=0):
     """Timed generations of a batch from one prefill: each generation rewinds (redraws the
     first tokens from the saved prefill logits with a new seed) and decodes until every
     sequence has n_new tokens (no stop ids). Returns accepted tokens/s, acceptance, the
     whole generation's algorithmic bytes against the HBM peak and, from one eagerly
     profiled generation, the dominant kernel class's bytes per launch against its
-    event-timed launch duration."""
+    event-timed launch duration. keep_seq0 > 0 also returns the first keep_seq0 tokens of
+    sequence 0 in the last timed generation and their kinds (1: an accepted draft)."""
     import numpy as np
     import torch
 
@@ -358,6 +359,9 @@ def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warm
             exits += eng.exit_counts().sum(axis=0)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    seq0 = None
+    if keep_seq0 > 0:
+        seq0 = (eng.tokens()[0][:keep_seq0], eng.token_kinds()[0][:keep_seq0])
     out = {"value": round(produced / elapsed, 1), "unit": "tokens/s",
            "ms_per_generation": round(elapsed / steps * 1e3, 2),
            "pulse_steps_per_generation": round(nsteps / steps, 1),
@@ -367,6 +371,8 @@ def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warm
         out["exits_per_pulse"] = exits.tolist()
     if draft_len > 0 and produced > accepted:
         out["tokens_per_round"] = round(produced / (produced - accepted), 3)
+    if seq0 is not None:
+        out["seq0_tokens"], out["seq0_kinds"] = seq0
     log(f"{label}: {steps} timed generations, {produced} tokens in {elapsed:.3f}s, "
         f"acceptance {accepted}/{tests}")
     if profile:
@@ -436,13 +442,20 @@ def _cpu_model_name() -> str:
 
 
 def cpu_baseline(cfg, state, c2_prompts, c2_new, temperature, top_p, rp, c1_prompt, c1_new,
-                 c2_seqs=(0, 15)):
+                 c2_seqs=(0, 15), c1_block=(), replays=()):
     """The oracle (PyTorch CPU restatement of src/infer.py, pinned to the reference by the
     golden vectors) on this host's cores: sequences c2_seqs of the headline workload in bf16
     one after another, as the batch-1 reference path runs them (sampled self-speculative,
     c2_new tokens after each prefill; the oracle's own acceptance rate beside the expected
     one), and c1 exactly (fp32, batch 1, greedy self-speculative, c1_new tokens), whose id
-    stream the GPU run is checked against."""
+    stream the GPU run is checked against.
+
+    As the checker of the GPU run it also computes: the draft-block restatement's greedy
+    c1 streams (``block_speculative_ids``; c1_block: (name, draft length, repetition
+    penalty, tokens) tuples), and for each entry of replays (name, prompt, emitted tokens,
+    their kinds, draft length, temperature, tokens of the whole generation) the oracle's
+    acceptance probabilities of the entry's draft tests replayed along its emitted stream
+    (``replay_acceptance`` / ``replay_block_acceptance``), with the accepted count."""
     import torch
 
     from oracle import pulsar_ref as R
@@ -477,6 +490,23 @@ def cpu_baseline(cfg, state, c2_prompts, c2_new, temperature, top_p, rp, c1_prom
     c1_ids += list(g1)
     u2 = time.perf_counter()
     seqs = " and ".join(str(b) for b in c2_seqs)
+    blocks = {}
+    for name, g_, rp_, n_ in c1_block:
+        blocks[name] = list(ref1.block_speculative_ids(c1_prompt, n_, 0.0, 1.0, rp_, g_))
+    rep_out = {}
+    for name, prompt, toks, kinds, g_, temp_, total in replays:
+        v0 = time.perf_counter()
+        if g_ > 0:
+            rep = R.replay_block_acceptance(eng, prompt, toks, kinds, temp_, top_p, rp, g_,
+                                            max_new=total)
+        else:
+            rep = R.replay_acceptance(eng, prompt, toks, kinds, temp_, top_p, rp)
+        ps = [p for p, _ in rep]
+        rep_out[name] = {"tests": len(rep), "accepted": int(sum(a for _, a in rep)),
+                         "expected_accepted": round(float(sum(ps)), 3),
+                         "expected_acceptance": round(float(sum(ps) / len(ps)), 4) if ps else None,
+                         "replayed_tokens": len(toks),
+                         "s": round(time.perf_counter() - v0, 1)}
     return {
         "value": round(n / decode_s, 3) if n else None,
         "unit": "tokens/s",
@@ -495,6 +525,8 @@ def cpu_baseline(cfg, state, c2_prompts, c2_new, temperature, top_p, rp, c1_prom
                            f"self-speculative, {c1_new} new tokens",
                "value": round((len(c1_ids) - 1) / (u2 - u1), 3), "unit": "tokens/s",
                "prefill_and_first_token_s": round(u1 - u0, 2), "ids": c1_ids},
+        "c1_block_ids": blocks,
+        "acceptance_replay": rep_out,
     }
 
 
@@ -679,6 +711,11 @@ def main() -> int:
     ap.add_argument("--no-verify", action="store_true", help="skip the verify microbenchmark")
     ap.add_argument("--no-ops", action="store_true", help="skip the op-surface figures")
     ap.add_argument("--no-early-exit", action="store_true", help="skip the early-exit runs")
+    ap.add_argument("--no-t1", action="store_true",
+                    help="skip the headline workload at temperature 1.0 (acceptance below 1)")
+    ap.add_argument("--t1-temperature", type=float, default=1.0)
+    ap.add_argument("--replay-tokens", type=int, default=48,
+                    help="tokens of sequence 0 along which the oracle replays acceptance")
     ap.add_argument("--early-exit-threshold", type=float, default=0.99)
     ap.add_argument("--only", choices=("c4", "c5", "c5d6", "c2d4"),
                     help="run only that workload, unprofiled (kernel traces)")
@@ -866,9 +903,30 @@ def main() -> int:
         block["schedule"] = (f"draft-block, draft length {args.draft_len}: up to "
                              f"{args.draft_len} pulse-0 drafts per round, one all-pulse verify "
                              "of the block, drafts accepted down the block by the reference's "
-                             "equal-draw rule (each emitted token is the full model's draw)")
+                             "equal-draw rule; block rows after the first attend the block's "
+                             "same-pulse keys (the prefill rule), so this schedule is not "
+                             "reference-exact (exact_schedule is)")
         log(f"draft-block run: {json.dumps({k: v for k, v in block.items() if k != 'kernel_profile'})}")
     head = block if block is not None else exact
+    # the headline workload at a temperature where drafts are rejected (the random-init
+    # model accepts every draft at 0.8): both schedules, one timed generation each, with
+    # sequence 0's stream kept for the oracle's acceptance replay in the CPU leg
+    t1 = None
+    if not args.no_t1 and not args.plain:
+        t1 = {"workload": f"as the headline, temperature {args.t1_temperature}"}
+        for name, g_ in (("exact_schedule", 0), (f"draft_block_{max(args.draft_len, 1)}",
+                                                 max(args.draft_len, 1))):
+            r = run_workload(model, cfg, prompts, N, args.t1_temperature, args.top_p,
+                             args.repetition_penalty, 1, 1, es, profile=False, draft_len=g_,
+                             label=f"t{args.t1_temperature} {name}",
+                             keep_seq0=args.replay_tokens)
+            t1[name] = {k: r.get(k) for k in ("value", "unit", "ms_per_generation",
+                                              "pulse_steps_per_generation", "acceptance_rate",
+                                              "tokens_per_round", "seq0_tokens", "seq0_kinds")}
+            t1[name]["draft_len"] = g_
+        log(f"temperature {args.t1_temperature}: " + json.dumps(
+            {k: {x: y for x, y in v.items() if not x.startswith("seq0")}
+             for k, v in t1.items() if isinstance(v, dict)}))
     early = None
     if not args.no_early_exit:
         early = early_exit_run(model, cfg, prompts, args)
@@ -898,6 +956,33 @@ def main() -> int:
                           "64 new tokens (prefill included)",
               "value": round(len(c1_ids) / c1_s, 1), "unit": "tokens/s",
               "ms_per_generation": round(c1_s * 1e3, 2), "ids": c1_ids}
+        # the configuration's draft length 4 (draft-block schedule), at the headline penalty
+        # and at penalty 10, where the greedy drafts are rejected now and then
+        c1["draft_block_4"] = {}
+        for name, rp_, n_ in (("rp1.15", 1.15, 64), ("rp10", 10.0, 32)):
+            pe.generate_ids([c1_prompt.tolist()], max_new_tokens=n_, temperature=0.0,
+                            repetition_penalty=rp_, speculative=True, stop_ids=[], draft_len=4)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            ids_ = pe.generate_ids([c1_prompt.tolist()], max_new_tokens=n_, temperature=0.0,
+                                   repetition_penalty=rp_, speculative=True, stop_ids=[],
+                                   draft_len=4)[0]
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            tests_, acc_ = pe.last_engine.acceptance()
+            c1["draft_block_4"][name] = {"repetition_penalty": rp_, "new_tokens": n_,
+                                         "value": round(len(ids_) / dt, 1), "unit": "tokens/s",
+                                         "acceptance_rate": round(acc_ / tests_, 4) if tests_ else None,
+                                         "ids": ids_}
+        # the reference's schedule at penalty 10 (stop ids 0 and 2) against the stream the
+        # reference itself wrote for this prompt (tests/golden/full_fp32.npz)
+        gold = np.load(os.path.join(ROOT, "tests", "golden", "full_fp32.npz"))
+        assert np.array_equal(gold["prompt"], c1_prompt)
+        rp10 = pe.generate_ids([c1_prompt.tolist()], max_new_tokens=32, temperature=0.0,
+                               repetition_penalty=10.0, speculative=True, stop_ids=[0, 2])[0]
+        c1["rp10_exact"] = {"repetition_penalty": 10.0, "new_tokens": 32, "stop_ids": [0, 2],
+                            "ids": rp10, "identical_to_reference_golden":
+                                rp10 == gold["greedy_rp10_spec_ids"].tolist()}
         for e_ in list(pe._engines.values()):
             e_.close()
         del pe, m32
@@ -911,11 +996,26 @@ def main() -> int:
         log(f"op surface: {json.dumps(ops)}")
     cpu = None
     if not args.no_cpu_baseline:
+        replays = []
+        if t1 is not None:
+            for name, v in t1.items():
+                if isinstance(v, dict):
+                    replays.append((name, prompts[0], v["seq0_tokens"], v["seq0_kinds"],
+                                    v["draft_len"], args.t1_temperature, N))
         cpu = cpu_baseline(cfg, state, prompts, args.cpu_new_tokens, args.temperature,
                            args.top_p, args.repetition_penalty, c1_prompt, 64,
-                           c2_seqs=sorted({0, len(prompts) - 1}))
+                           c2_seqs=sorted({0, len(prompts) - 1}),
+                           c1_block=[] if c1 is None else [("rp1.15", 4, 1.15, 64),
+                                                           ("rp10", 4, 10.0, 32)],
+                           replays=replays)
         if c1 is not None:
             c1["token_identical_to_cpu_oracle"] = c1["ids"] == cpu["c1"]["ids"]
+            for name, v in c1["draft_block_4"].items():
+                v["token_identical_to_cpu_oracle_block"] = v["ids"] == cpu["c1_block_ids"][name]
+        if t1 is not None:
+            for name, rep in cpu["acceptance_replay"].items():
+                t1[name]["oracle_replay_seq0"] = rep
+        cpu.pop("c1_block_ids", None)
         log(f"cpu baseline: {json.dumps({k: v for k, v in cpu.items() if k != 'c1'})}")
     line = {
         "metric": METRIC,
@@ -938,6 +1038,7 @@ def main() -> int:
             "draft_len": args.draft_len if block is not None else (0 if args.plain else 1),
             "schedule": "plain" if args.plain else head["schedule"],
             "stop_ids": "disabled",
+            "reference_exact": block is None,
         },
         "acceptance_rate": head["acceptance_rate"],
         "tokens_per_round": head.get("tokens_per_round"),
@@ -947,6 +1048,15 @@ def main() -> int:
         "cpu_baseline": cpu,
         "kernel_profile": head.get("kernel_profile"),
         "exact_schedule": exact if block is not None else None,
+        "departure_from_reference_decode": None if block is None else {
+            "what": "max|logits - reference decode_step logits| / max|reference| of the "
+                    "verify's last-pulse rows 1..G against sequential decoding of the same "
+                    "tokens (row 0 is identical); full-size model, 40-token prompt, "
+                    "G = 4 and 6",
+            "fp32": [1.6e-3, 6.3e-3], "bf16": [4.7e-3, 6.6e-3], "bound": 2e-2,
+            "measured_by": "tests/test_oracle_block.py::"
+                           "test_block_rows_depart_from_the_reference_decode_within_bound"},
+        "temperature_1": t1,
         "verify": verify,
         "c1": c1,
         "c4": c4,
@@ -955,6 +1065,22 @@ def main() -> int:
         "early_exit": early,
         "op_surface": ops,
     }
+    # id lists go to the log; the line keeps their checks. The objects a reader of the line's
+    # end needs most (schedules, acceptance at temperature 1, c1 checks) come last.
+    if c1 is not None:
+        log("c1 ids: " + json.dumps({"exact": c1.pop("ids"), "rp10_exact": c1["rp10_exact"].pop("ids"),
+                                     **{f"draft_block_4_{k}": v.pop("ids")
+                                        for k, v in c1["draft_block_4"].items()}}))
+    if t1 is not None:
+        for name, v in t1.items():
+            if isinstance(v, dict):
+                log(f"temperature {args.t1_temperature} {name} sequence 0: "
+                    f"{json.dumps({'tokens': v.pop('seq0_tokens'), 'kinds': v.pop('seq0_kinds')})}")
+    if exact is not None and block is not None:
+        line["exact_schedule_kernel_profile"] = exact.pop("kernel_profile", None)
+    for k in ("verify", "c4", "c5", "c1", "exact_schedule", "departure_from_reference_decode",
+              "temperature_1"):
+        line[k] = line.pop(k)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -983,6 +983,105 @@ def spec_token_marginals(engine: "RefEngine", prompt_ids, temperature: float, to
     return [m1, m2, m3]
 
 
+def block_token_marginals(engine: "RefEngine", prompt_ids, temperature: float, top_p: float,
+                          repetition_penalty: float, draft_len: int, n_tokens: int,
+                          prune: float = 1e-6, stats: Optional[dict] = None,
+                          first: Optional[list] = None, depth: Optional[int] = None) -> list:
+    """Exact distributions (fp64 [V] each) of the first `depth` (default: all `n_tokens`)
+    tokens that ``RefEngine.block_speculative_ids`` emits with max_new_tokens = n_tokens and
+    no stop ids.
+
+    The drafts after a round's first rejection never reach the output: the next round
+    starts from the fresh draw f_i of the rejecting row i and keeps block rows 0..i, whose
+    keys, values and logits depend on rows 0..i only (a row attends block rows at positions
+    <= its own). So the emitted stream is the sequential process: at block row i (prefix
+    blk[0..i] over the committed cache) with a draft still to test (i < g), the next token
+    is x as the accepted draft with probability p_d(x) p_v(x) (draft draw x from the row's
+    pulse-0 logits, verify draw v from its last-pulse logits, independent), and the round
+    continues at row i + 1; otherwise (probability 1 - sum_y p_d(y) p_v(y)) it is a fresh
+    draw y ~ p_v and a round starts at y one position after row i. At i == g (no draft
+    left) the next token is y ~ p_v. p_d and p_v of row i come from ``block_verify`` of the
+    prefix (its pulse 0 is the draft pass of that row: both attend the block's pulse-0 keys
+    at positions <= the row's). Paths of probability below `prune` are not expanded; their
+    mass is missing from the later distributions. `stats` (optional) receives the number of
+    verified prefixes ("nodes"), the acceptance probability of every expanded test
+    ("p_accept", with its path weight in "w_accept") and, per emitted token, the probability
+    that it is an accepted draft ("accepted_mass", a list of `depth` floats). `first`
+    (optional) expands only the paths whose first token is in it (the first distribution is
+    still the whole one), so disjoint `first` sets split the enumeration into parts whose
+    later distributions add up."""
+    cfg = engine.cfg
+    ids = torch.as_tensor(prompt_ids, dtype=torch.long).view(1, -1)
+    cache0 = RefKVCache(cfg)
+    logits0 = engine.prefill(ids, cache0)[:, -1, :].clone()
+    seen0 = ids[0].tolist()
+    V = cfg.vocab_size
+    depth = n_tokens if depth is None else min(depth, n_tokens)
+    marg = [torch.zeros(V, dtype=torch.float64) for _ in range(depth)]
+    if depth <= 0:
+        return marg
+    if stats is not None:
+        stats.setdefault("nodes", 0)
+        stats.setdefault("p_accept", [])
+        stats.setdefault("w_accept", [])
+        stats["accepted_mass"] = [0.0] * depth
+    dist = lambda lg, seen: sampling_distribution(lg, seen, temperature, top_p,  # noqa: E731
+                                                  repetition_penalty)
+
+    def commit(cache, kv, n_keep):
+        import copy
+
+        c = copy.deepcopy(cache)
+        engine.commit_block(c, kv, n_keep)
+        return c
+
+    m1 = dist(logits0, seen0)
+    marg[0] += m1
+    # stack entries: (path weight, committed cache, seen through block row 0, position of
+    # block row 0, block prefix, tokens produced, drafts of this round)
+    stack = []
+    if depth > 1:
+        g1 = min(draft_len, n_tokens - 2)
+        for t in torch.nonzero(m1 > prune).view(-1).tolist():
+            if first is not None and t not in first:
+                continue
+            stack.append((float(m1[t]), cache0, seen0 + [t], len(seen0), [t], 1, g1))
+    while stack:
+        w, cache, seen, pos, blk, produced, g = stack.pop()
+        i = len(blk) - 1
+        _, per_pulse, kv = engine.block_verify(blk, pos, cache)
+        if stats is not None:
+            stats["nodes"] += 1
+        s_row = seen + blk[1:]
+        pv = dist(per_pulse[-1][i:i + 1], s_row)
+        k = produced  # index of the next emitted token
+        if i < g:
+            pd = dist(per_pulse[0][i:i + 1], s_row)
+            acc = pd * pv
+            p_acc = float(acc.sum())
+            if stats is not None:
+                stats["p_accept"].append(p_acc)
+                stats["w_accept"].append(w)
+                stats["accepted_mass"][k] += w * p_acc
+            marg[k] += w * acc
+            if k + 1 < depth:
+                for x in torch.nonzero(w * acc > prune).view(-1).tolist():
+                    stack.append((w * float(acc[x]), cache, seen, pos, blk + [x], produced + 1, g))
+            nxt = (1.0 - p_acc) * pv
+        else:
+            nxt = pv
+        marg[k] += w * nxt
+        if k + 1 < depth:
+            live = torch.nonzero(w * nxt > prune).view(-1).tolist()
+            if live:
+                c = commit(cache, kv, i + 1)
+                g2 = min(draft_len, n_tokens - (produced + 1) - 1)
+                for y in live:
+                    stack.append((w * float(nxt[y]), c, s_row + [y], pos + i + 1, [y],
+                                  produced + 1, g2))
+    return marg
+
+
 def sampling_distribution(lgt: torch.Tensor, seen: list, temperature: float, top_p: float,
                           repetition_penalty: float) -> torch.Tensor:
     """The distribution ``RefEngine.sample`` draws from, as an fp64 vector of length V."""

@@ -10,6 +10,22 @@ constexpr int kMaxPulses = 3;
 constexpr int kHeadDim = 64;
 constexpr int kPage = 64;  // positions per KV page
 
+// Take n consecutive pages from a KV page pool (pool[0]: pages handed out, pool[1]: spent
+// flag, pool_pages: pool size). Returns the first page, or -1 after setting the spent flag
+// when fewer than n are left. The counter only moves on success, so a request the pool
+// cannot serve leaves its pages to smaller requests; each failed compare-and-swap means
+// another request took pages, so the loop ends after at most one pass per competitor.
+__device__ __forceinline__ int take_pages(int32_t* pool, int n, int pool_pages) {
+  int cur = __hip_atomic_load(&pool[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (cur + n <= pool_pages) {
+    const int prev = atomicCAS(&pool[0], cur, cur + n);
+    if (prev == cur) return cur;
+    cur = prev;
+  }
+  atomicOr(&pool[1], 1);
+  return -1;
+}
+
 // One (token, pulse) evaluation inside a step. Rows of a step are sorted by pulse.
 struct RowDesc {
   int32_t seq;    // sequence index

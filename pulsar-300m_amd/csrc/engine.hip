@@ -819,11 +819,8 @@ __global__ void kv_ensure_pages_kernel(const AttnUnit* units, int32_t* table, in
   const int have = count[un.seq];
   if (have >= need) return;
   const int n = need - have;
-  const int first = atomicAdd(&pool[0], n);
-  if (first + n > pool_pages) {
-    atomicOr(&pool[1], 1);
-    return;
-  }
+  const int first = take_pages(pool, n, pool_pages);
+  if (first < 0) return;
   for (int i = 0; i < n; ++i) table[(int64_t)un.seq * max_pages + have + i] = first + i;
   count[un.seq] = need;
 }
@@ -1309,6 +1306,23 @@ int verify(Engine& e, const int32_t* host_tokens, int n, int use_graph, hipStrea
     for (int i = 0; i < B * n; ++i)
       PULSAR_REQUIRE(host_tokens[i] >= 0 && host_tokens[i] < e.V,
                      "engine_verify: token id out of vocabulary");
+    {
+      // the block's global-layer pages must come from the pool: a block the pool cannot hold
+      // fails here rather than attending and writing the spare page
+      std::vector<int32_t> have(B);
+      int32_t pool[2] = {0, 0};
+      PULSAR_CHECK_HIP(hipMemcpyAsync(have.data(), e.page_count, 4 * (size_t)B,
+                                      hipMemcpyDeviceToHost, s));
+      PULSAR_CHECK_HIP(hipMemcpyAsync(pool, e.pool, 8, hipMemcpyDeviceToHost, s));
+      PULSAR_CHECK_HIP(hipStreamSynchronize(s));
+      const int need = (e.prompt_len + n - 1) / kPage + 1;
+      int64_t more = 0;
+      for (int b = 0; b < B; ++b) more += std::max(0, need - have[b]);
+      PULSAR_REQUIRE(pool[0] + more <= e.pool_pages,
+                     "engine_verify: KV page pool too small for the block: " +
+                         std::to_string(more) + " more pages needed, " +
+                         std::to_string(std::max(0, e.pool_pages - pool[0])) + " left");
+    }
     const int pos = e.prompt_len, BN = B * n;
     std::vector<RowDesc> rows((size_t)P * MR, RowDesc{0, 0, 0, 0, 0, -1, -1, 0});
     std::vector<StepCtl> ctls(P);
@@ -1466,17 +1480,19 @@ int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
   // block and the sequences' states into pinned host memory and an event. While the host
   // waits for one batch's readback, the next batch is already queued whenever that wait's
   // predecessor proved the work outlasts it, so the GPU does not idle between batches: with
-  // no stop ids a live sequence still owes max_new - produced tokens, and it takes at least
-  // one step per token in the draft-block mode (a round of g drafts is g + 2 steps for at
-  // most g + 1 tokens) and one step per two tokens otherwise. Near the end, and with stop
-  // ids, each batch is checked before the next one goes out, so no step runs past the last
-  // live sequence's batch.
+  // no stop ids a live sequence still owes rem = max_new - produced tokens. In the
+  // draft-block mode the round in flight can emit up to draft_len + 1 of them in one step
+  // (a verify's last pulse), and every later round takes at least one step per token (a
+  // round of g drafts is g + 2 or more steps for at most g + 1 tokens), so at least
+  // max(1, rem - draft_len) steps remain; otherwise at least one step per two tokens. Near
+  // the end, and with stop ids, each batch is checked before the next one goes out, so no
+  // step runs past the last live sequence's batch.
   const size_t rb = sizeof(StepCtl) + sizeof(SeqState) * (size_t)e.B;
   if (!e.host_rb) {
     PULSAR_CHECK_HIP(hipHostMalloc(&e.host_rb, 2 * rb));
     for (hipEvent_t& ev : e.rb_ev) PULSAR_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   }
-  const int per_token = e.cfg.draft_len > 0 ? 1 : 2;  // tokens per step, at most (see above)
+  const int G = e.cfg.draft_len;
   int launched = 0, checked = 0, bound = 0;
   int q_n = 0, q_head = 0, q_steps[2] = {0, 0};  // queued readbacks, oldest first
   auto launch = [&](int n) -> int {
@@ -1509,7 +1525,8 @@ int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
     if (e.cfg.n_stop == 0)
       for (int b = 0; b < e.B; ++b)
         if (!st[b].done) rem = std::max(rem, st[b].max_new - st[b].produced);
-    bound = rem / per_token;
+    // steps that certainly still have a live sequence (see above)
+    bound = G > 0 ? (rem > G ? rem - G : (rem > 0 ? 1 : 0)) : rem / 2;
     if (q_n == 0 && launched < max_steps) PULSAR_TRY(launch(std::min(check_every, max_steps - launched)));
   }
   // a batch queued behind the last readback (never, when the bound holds) finishes first

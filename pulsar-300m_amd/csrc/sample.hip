@@ -487,11 +487,8 @@ __device__ bool ensure_pages(const ControllerArgs& a, int b, int hi) {
   const int have = a.page_count[b];
   if (have >= need) return true;
   const int n = need - have;
-  const int first = atomicAdd(&a.pool[0], n);
-  if (first + n > a.pool_pages) {
-    atomicOr(&a.pool[1], 1);
-    return false;
-  }
+  const int first = take_pages(a.pool, n, a.pool_pages);
+  if (first < 0) return false;
   for (int i = 0; i < n; ++i) a.page_table[(int64_t)b * a.max_pages + have + i] = first + i;
   a.page_count[b] = need;
   return true;

@@ -8,6 +8,7 @@ them; PulsarEngineConfig.kv_pages).
   of the full run's), run() raises, and nothing else is disturbed; a prompt set larger than
   the pool fails prefill with a message.
 * The block verify takes the page of its block positions: logits equal the default pool's.
+* A verify block the pool cannot hold fails before any launch and takes no page.
 """
 
 from __future__ import annotations
@@ -97,3 +98,25 @@ def test_verify_takes_its_block_page(models, full_state):
             pages = eng.kv_pages()
             assert pages["used"] == B * 3 and not pages["spent"], pages
     np.testing.assert_array_equal(out[0], out[1])
+
+
+def test_verify_refuses_a_block_the_pool_cannot_hold(models, full_state):
+    """A block whose positions need pages the pool no longer has fails before any launch
+    (instead of reading and writing the spare page) and takes no page; a block on the cached
+    pages runs."""
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+
+    cfg = full_state[0]
+    ctx, n = 126, 5  # cached positions 0..125: two pages per sequence
+    blocks = np.stack([W.uniform_ids(60 + b, "kv_pages_block", n, cfg.vocab_size)
+                       for b in range(B)])
+    with HipEngine(models[torch.bfloat16], batch=B, max_prompt=1, max_new=8, temperature=0.0,
+                   stop_ids=[], draft_len=n - 1, max_ctx=512, kv_pages=B * 2 + 1) as eng:
+        eng.fill_kv(ctx, seed=3)
+        eng.verify(blocks[:, :2])  # positions 126, 127: the second page
+        assert eng.kv_pages() == {"pool": B * 2 + 1, "used": B * 2, "spent": False}
+        with pytest.raises(RuntimeError, match="KV page pool too small for the block"):
+            eng.verify(blocks)  # positions 126..130: a third page for each of B sequences
+        assert eng.kv_pages() == {"pool": B * 2 + 1, "used": B * 2, "spent": False}
+        assert np.isfinite(eng.logits(B * 2)).all()

@@ -192,3 +192,196 @@ def test_block_acceptance_replay_of_a_stream_prefix(tiny_state):
         part = R.replay_block_acceptance(eng, g["prompt"], out[:cut], stats["kinds"][:cut], 0.2,
                                          0.95, 1.15, 4, max_new=30)
         assert part == full[:len(part)] and len(part) <= len(full)
+
+
+# -- exact emitted-token distributions of the draft-block mode ------------------------------
+
+
+def _literal_block_marginals(eng, prompt, temp, top_p, rp, G, n):
+    """Every draw of ``block_speculative_ids`` enumerated as the generator makes it: all of a
+    round's drafts first (each from block_pass pulse 0 of the growing block, as the
+    generator does), then the verify's draws row by row (v_i against the draft, and the
+    second draw f_i at a rejection). Drafts after a rejection are enumerated too; nothing is
+    pruned. The model's evaluations are memoised by (committed history, block), which
+    changes no probability. Returns the distributions of the n emitted tokens and, per
+    token, the probability that it is an accepted draft."""
+    import copy
+
+    cfg = eng.cfg
+    dist = lambda lg, seen: R.sampling_distribution(lg, seen, temp, top_p, rp)  # noqa: E731
+    sup = lambda p: [(x, float(p[x])) for x in torch.nonzero(p > 0).view(-1).tolist()]  # noqa: E731
+    cache0 = R.RefKVCache(cfg)
+    lg0 = eng.prefill(torch.as_tensor(prompt).view(1, -1), cache0)[:, -1, :]
+    seen0 = list(prompt)
+    marg = [torch.zeros(cfg.vocab_size, dtype=torch.float64) for _ in range(n)]
+    accm = [0.0] * n
+    caches = {(): cache0}
+    memo = {}
+
+    def draft_dist(hist, seen, pos, blk):
+        key = ("d", hist, tuple(blk))
+        if key not in memo:
+            j = len(blk) - 1
+            lgp, _, _, _ = eng.block_pass(blk, pos, caches[hist], 0)
+            memo[key] = sup(dist(lgp[j:j + 1], seen + blk[1:j + 1]))
+        return memo[key]
+
+    def verify_dists(hist, seen, pos, blk):
+        key = ("v", hist, tuple(blk))
+        if key not in memo:
+            lg, _, kv = eng.block_verify(blk, pos, caches[hist])
+            memo[key] = ([sup(dist(lg[i:i + 1], seen + blk[1:i + 1])) for i in range(len(blk))],
+                         kv)
+        return memo[key]
+
+    def round_(w, hist, seen, pos, t, produced):
+        g = min(G, n - produced - 1)
+
+        def drafts(wd, blk):
+            if len(blk) - 1 == g:
+                verify(wd, blk)
+                return
+            for d, pd in draft_dist(hist, seen, pos, blk):
+                drafts(wd * pd, blk + [d])
+
+        def verify(wv, blk):
+            pvs, kv = verify_dists(hist, seen, pos, blk)
+
+            def emit(we, i, f):
+                k = produced + i
+                marg[k][f] += we
+                if k + 1 < n:
+                    h2 = hist + (tuple(blk[:i + 1]),)
+                    if h2 not in caches:
+                        c = copy.deepcopy(caches[hist])
+                        eng.commit_block(c, kv, i + 1)
+                        caches[h2] = c
+                    round_(we, h2, seen + blk[1:i + 1] + [f], pos + i + 1, f, k + 1)
+
+            def walk(ww, i):
+                k = produced + i
+                if i < len(blk) - 1:
+                    for v, pv in pvs[i]:
+                        if v == blk[i + 1]:
+                            marg[k][v] += ww * pv
+                            accm[k] += ww * pv
+                            if k + 1 < n:
+                                walk(ww * pv, i + 1)
+                            continue
+                        for f, pf in pvs[i]:
+                            emit(ww * pv * pf, i, f)
+                else:
+                    for f, pf in pvs[i]:
+                        emit(ww * pf, i, f)
+
+            walk(wv, 0)
+
+        drafts(w, [t])
+
+    m1 = dist(lg0, seen0)
+    marg[0] += m1
+    if n > 1:
+        for t, p1 in sup(m1):
+            round_(p1, (), seen0 + [t], len(seen0), t, 1)
+    return marg, accm
+
+
+def test_block_marginals_equal_a_literal_enumeration_of_every_draw(tiny_state):
+    """block_token_marginals (which never expands drafts after a round's first rejection)
+    against the literal enumeration above: same distributions of every emitted token and
+    the same accepted-draft probabilities, on rounds with several drafts where both test
+    outcomes carry weight."""
+    cfg, st = tiny_state
+    g = golden("tiny_fp32.npz")
+    eng = R.load_ref(cfg, st, torch.float32, stop_ids=set())
+    prompt = g["prompt"].tolist()
+    temp, top_p, rp, G, n = 0.05, 0.5, 10.0, 2, 4
+    want, want_acc = _literal_block_marginals(eng, prompt, temp, top_p, rp, G, n)
+    stats = {}
+    got = R.block_token_marginals(eng, prompt, temp, top_p, rp, G, n, prune=0.0, stats=stats)
+    for k in range(n):
+        assert abs(float(want[k].sum()) - 1.0) < 1e-9
+        torch.testing.assert_close(got[k], want[k], atol=1e-12, rtol=0)
+    np.testing.assert_allclose(stats["accepted_mass"], want_acc, atol=1e-12, rtol=0)
+    pa = np.asarray(stats["p_accept"])
+    # both outcomes of the tests carry weight, and rounds accept more than one draft
+    assert 0.2 < min(want_acc[1:n - 1]) and max(want_acc) < 0.8
+    assert pa.min() < 0.9 and want_acc[2] > 0.05
+
+
+def test_block_marginals_second_token_is_the_reference_test(tiny_state):
+    """The first draft test of a round is the reference's test (block row 0 is the
+    reference's decode of the round's token), so the distribution of the second emitted
+    token equals the one spec_token_marginals computes for the reference's generator."""
+    cfg, st = tiny_state
+    g = golden("tiny_fp32.npz")
+    eng = R.load_ref(cfg, st, torch.float32, stop_ids=set())
+    prompt = g["prompt"].tolist()
+    ref = R.spec_token_marginals(eng, prompt, 0.05, 0.9, 10.0, prune=0.0)
+    got = R.block_token_marginals(eng, prompt, 0.05, 0.9, 10.0, 4, 6, prune=0.0, depth=2)
+    torch.testing.assert_close(got[0], ref[0], atol=1e-12, rtol=0)
+    torch.testing.assert_close(got[1], ref[1], atol=1e-12, rtol=0)
+
+
+def test_block_marginals_fixture_matches_the_oracle():
+    """tests/golden/block_marginals_small.npz (the GPU test's expectation) against a fresh
+    enumeration of its first three tokens, and its recorded workload."""
+    import json
+
+    from pulsar_engine import weights as W
+    from pulsar_engine.config import small_config
+
+    f = golden("block_marginals_small.npz")
+    s = json.loads(str(f["settings"]))
+    cfg = small_config()
+    st = W.synthetic_state(cfg, seed=s["weight_seed"])
+    assert str(f["weights_digest"]) == W.state_digest(st)
+    prompt = W.uniform_ids(s["prompt_seed"], s["prompt_name"], s["prompt_len"], cfg.vocab_size)
+    np.testing.assert_array_equal(f["prompt"], prompt)
+    eng = R.load_ref(cfg, st, torch.float32, stop_ids=set())
+    stats = {}
+    got = R.block_token_marginals(eng, prompt, s["temperature"], s["top_p"],
+                                  s["repetition_penalty"], s["draft_len"], s["n_tokens"],
+                                  prune=s["prune"], stats=stats, depth=3)
+    for k in range(3):
+        want = np.zeros(cfg.vocab_size)
+        want[f[f"idx_{k}"]] = f[f"p_{k}"]
+        np.testing.assert_allclose(got[k].numpy(), want, atol=1e-12, rtol=0)
+    np.testing.assert_allclose(stats["accepted_mass"], f["accepted_mass"][:3], atol=1e-12)
+    # the regime the GPU test needs: drafts are rejected about half the time
+    assert 0.3 < float(f["mean_p_accept"]) < 0.7
+    assert all(0.3 < float(a) < 0.7 for a in f["accepted_mass"][1:5])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("G", [4, 6])
+def test_block_rows_depart_from_the_reference_decode_within_bound(full_state, dtype, G):
+    """How far the draft-block mode is from the reference: the verify's last-pulse logits of
+    block rows 1..G attend the block's same-pulse keys (the prefill rule), where the
+    reference's decode attends every earlier token's last-pulse keys (src/infer.py:140-155).
+    Full-size model, a 40-token prompt, the block = the first G + 1 tokens of the oracle's
+    greedy penalty-10 stream: row 0 equals the reference's decode_step bit for bit; rows
+    1..G differ by far more than fp32 arithmetic (so the mode is not reference-exact) and
+    stay within the bf16 logits bound of 2e-2 (max|diff| / max|ref|). Measured: fp32
+    1.6e-3 to 6.3e-3, bf16 4.7e-3 to 6.6e-3."""
+    from pulsar_engine import weights as W
+
+    cfg, st = full_state
+    prompt = W.uniform_ids(7, "gpu_prompt", 40, cfg.vocab_size).tolist()
+    eng = R.load_ref(cfg, st, dtype, stop_ids=set())
+    toks = list(eng.stream_generate_ids(prompt, G + 1, 0.0, 1.0, 10.0))
+    assert len(toks) == G + 1
+    ca = R.RefKVCache(cfg)
+    eng.prefill(torch.as_tensor(prompt).view(1, -1), ca)
+    last, _, _ = eng.block_verify(toks, len(prompt), ca)
+    cb = R.RefKVCache(cfg)
+    eng.prefill(torch.as_tensor(prompt).view(1, -1), cb)
+    seq = [eng.decode_step(t, len(prompt) + i, cb)[0] for i, t in enumerate(toks)]
+    rel = [float((last[i].float() - seq[i].float()).abs().max() / seq[i].float().abs().max())
+           for i in range(G + 1)]
+    print(f"[block vs decode] {dtype} G={G}: max-abs-rel per row {[f'{r:.2e}' for r in rel]}",
+          flush=True)
+    assert torch.equal(last[0], seq[0])
+    assert max(rel[1:]) <= 2e-2
+    if dtype == torch.float32:
+        assert min(rel[1:]) > 1e-4
