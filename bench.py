@@ -179,6 +179,47 @@ def recorded_traffic(kernels: list, path: str = None):
     return total
 
 
+DECODE_TRACE_PROFILE = os.path.join(ROOT, "profiles", "decode_kernels_c2_b16_t2048.md")
+BLOCK_TRACE_PROFILE = os.path.join(ROOT, "profiles", "decode_kernels_c2_draft4_b16_t2048.md")
+
+
+def recorded_kernel_us(cls: str, path: str):
+    """Average kernel-trace duration (us) of a kernel class from a committed rocprofv3
+    summary table (`| kernel | dispatches | avg us | ...`), weighted by dispatches over every
+    template of the class (CLASS_PREFIXES), or None."""
+    try:
+        with open(path) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return None
+    n = tot = 0.0
+    for line in lines:
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) < 3 or not cells[0].startswith("`"):
+            continue
+        name = cells[0].strip("`")
+        if not name.startswith(CLASS_PREFIXES.get(cls, (cls,))):
+            continue
+        try:
+            d, us = float(cells[1]), float(cells[2])
+        except ValueError:
+            continue
+        n += d
+        tot += d * us
+    return tot / n if n else None
+
+
+def trace_fraction(roof: dict, cls: str, path: str) -> None:
+    """Add to a roofline object the class's kernel-trace average from the committed summary
+    at `path` and the fraction of the HBM peak that follows from it (the event span also
+    holds the command processor's dispatch, so the event-timed `frac` is the lower one)."""
+    us = recorded_kernel_us(cls, path)
+    roof["kernel_trace_us"] = round(us, 2) if us else None
+    roof["frac_kernel_trace"] = (round(roof["bytes_per_launch"] / (us * 1e-6) / HBM_PEAK, 4)
+                                 if us else None)
+    roof["kernel_trace_profile"] = os.path.relpath(path, ROOT)
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -314,7 +355,7 @@ def verify_microbench(model, cfg, es, args):
 
 def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warmup, es=2,
                  profile=True, draft_len=0, label="", speculative=True,
-                 early_exit_threshold=None, traffic_path=None, keep_seq0=0):
+                 early_exit_threshold=None, traffic_path=None, keep_seq0=0, trace_path=None):
     """Timed generations of a batch from one prefill: each generation rewinds (redraws the
     first tokens from the saved prefill logits with a new seed) and decodes until every
     sequence has n_new tokens (no stop ids). Returns accepted tokens/s, acceptance, the
@@ -392,6 +433,8 @@ def run_workload(model, cfg, prompts, n_new, temperature, top_p, rp, steps, warm
                            "bytes_per_launch": int(per_launch),
                            "avg_launch_us": round(avg_s * 1e6, 2),
                            "empty_event_pair_us": round(pair_ms / max(pair_n, 1) * 1e3, 2)}
+        if trace_path:
+            trace_fraction(out["roofline"], dom, trace_path)
         if traffic_path:
             tb = recorded_traffic(["class:" + dom], traffic_path)
             out["roofline"]["traffic"] = round(tb / 1e6, 3) if tb else None
@@ -873,6 +916,7 @@ def main() -> int:
                     "kernel": dom,
                     "bytes_per_launch": int(per_launch), "avg_launch_us": round(avg_s * 1e6, 2),
                     "empty_event_pair_us": round(pair * 1e3, 2)}
+        trace_fraction(roofline, dom, DECODE_TRACE_PROFILE)
         all_bytes = sum(bytes_by_class.values())
         # whole-generation algorithmic bytes against the graph-replayed generation time
         step_frac = (all_bytes / (elapsed / args.steps)) / HBM_PEAK
@@ -899,7 +943,8 @@ def main() -> int:
                              args.repetition_penalty, args.steps, args.warmup, es,
                              profile=not args.no_profile, draft_len=args.draft_len,
                              label=f"c2 draft-block {args.draft_len}",
-                             traffic_path=BLOCK_TRAFFIC_PROFILE)
+                             traffic_path=BLOCK_TRAFFIC_PROFILE,
+                             trace_path=BLOCK_TRACE_PROFILE if args.draft_len == 4 else None)
         block["schedule"] = (f"draft-block, draft length {args.draft_len}: up to "
                              f"{args.draft_len} pulse-0 drafts per round, one all-pulse verify "
                              "of the block, drafts accepted down the block by the reference's "

@@ -377,7 +377,9 @@ int pulsar_engine_generate(void* handle, int32_t max_steps, int32_t check_every,
  * PULSAR_BUF_LOGITS. n <= draft_len + 1 (<= 2 in exact mode). The decode state is not
  * touched; the block positions' keys/values are overwritten. host_tokens == NULL re-runs
  * the last uploaded block without a host synchronisation (timing); otherwise the upload
- * synchronises the stream. use_graph=1 replays a captured HIP graph of the passes.
+ * synchronises the stream; an upload whose positions need more global-layer KV pages
+ * than the pool has left fails with PULSAR_ERR_INVALID before any launch. use_graph=1
+ * replays a captured HIP graph of the passes.
  * No reference counterpart: it is the verify step of the draft-block mode, and of the
  * verify microbenchmark (a 5-token verify over pre-filled caches). */
 int pulsar_engine_verify(void* handle, const int32_t* host_tokens, int32_t n, int32_t use_graph,

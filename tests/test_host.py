@@ -123,6 +123,29 @@ def test_pmc_summary_calibrates_and_feeds_traffic(tmp_path, monkeypatch):
     assert b.recorded_traffic(["not_profiled"]) is None
 
 
+def test_kernel_trace_fraction_follows_the_committed_table(tmp_path):
+    """The roofline's kernel-trace fraction: a class's dispatch-weighted average over every
+    template of the class in a committed summary table, against the class's bytes per
+    launch."""
+    b = _bench()
+    table = tmp_path / "trace.md"
+    table.write_text("\n".join([
+        "| kernel | dispatches | avg us | total ms | share | busy dispatches | busy avg us |",
+        "|---|---|---|---|---|---|---|",
+        "| `attn_decode_unit_kernel<32, 2>` | 30 | 10.00 | 0.30 | 50% | 30 | 10.00 |",
+        "| `attn_decode_unit_kernel<8, 2>` | 10 | 20.00 | 0.20 | 30% | 10 | 20.00 |",
+        "| `moe_combine_rows_kernel<bf16, 16, 4>` | 40 | 4.00 | 0.16 | 20% | 40 | 4.00 |"]))
+    assert b.recorded_kernel_us("attention", str(table)) == pytest.approx(12.5)
+    assert b.recorded_kernel_us("moe_combine", str(table)) == pytest.approx(4.0)
+    assert b.recorded_kernel_us("router", str(table)) is None
+    roof = {"bytes_per_launch": 10_000_000}
+    b.trace_fraction(roof, "attention", str(table))
+    assert roof["kernel_trace_us"] == 12.5
+    assert roof["frac_kernel_trace"] == pytest.approx(10e6 / 12.5e-6 / 8e12, abs=1e-4)
+    # the committed headline summary exists and names the dominant class
+    assert b.recorded_kernel_us("attention", b.BLOCK_TRACE_PROFILE) is not None
+
+
 def test_config_from_dict_keeps_reference_names():
     cfg = PulsarConfig.from_dict({"d_model": 512, "n_heads": 8, "n_kv_heads": 2})
     assert (cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim) == (512, 8, 2, 64)
