@@ -137,5 +137,11 @@ int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
 // independent of batch composition picks one by a per-sequence property (prompt length).
 int launch_gemm_wide(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
                      hipStream_t s);
+// Same contract and identical results as launch_gemm (the same summation order), for row
+// sets of tens to hundreds of rows per group: 64-row x 64-column tiles with the weights
+// staged through LDS, so that weights are read once per 64 rows. bf16 with the store,
+// qkv + gate, residual and SwiGLU epilogues; other launches go to launch_gemm.
+int launch_gemm_mid(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
+                    hipStream_t s);
 
 }  // namespace pulsar

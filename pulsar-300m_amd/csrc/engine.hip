@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <array>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -20,6 +21,7 @@ struct Engine {
   int D = 0, H = 0, Hkv = 0, qkv = 0, qkvg = 0, E = 0, K = 0, de = 0, ds = 0, L = 0, P = 0, V = 0;
   int B = 0, max_rows = 0, R = 0, max_pages = 0, lcap = 0, max_splits = 0, max_splits_unit = 0;
   int G = 0;  // drafts per round (draft-block mode), 0 = exact mode
+  int mid_rows = 0;  // steps of this many rows or more run the mid-size projection GEMMs
   int S = 2;  // token-state slots per sequence: rows of one sequence in a step
   std::vector<void*> allocs;
 
@@ -232,6 +234,12 @@ enum ProfClass {
   PC_CONTROL, PC_EVENT_PAIR
 };
 
+// From kMidRows rows up to kWideRows the projections run in the mid-size tiles of
+// launch_gemm_mid (64 rows x 64 columns, weights staged through LDS). They give results
+// identical to the row-tile kernel's, so the threshold is a matter of speed only; the
+// environment variable PULSAR_GEMM_MID_ROWS (read when an engine is created) overrides it.
+constexpr int kMidRows = 128;
+
 int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) {
   PULSAR_TRY(validate(m, c));
   Engine* e = new Engine();
@@ -256,6 +264,13 @@ int create(const PulsarModelDesc& m, const PulsarEngineConfig& c, Engine** out) 
   e->G = c.draft_len;
   e->S = engine_slots(c.draft_len);
   e->max_rows = e->S * c.max_batch;
+  e->mid_rows = kMidRows;
+  if (const char* v = std::getenv("PULSAR_GEMM_MID_ROWS")) {
+    char* end = nullptr;
+    const long r = std::strtol(v, &end, 10);
+    PULSAR_REQUIRE(end != v && *end == 0 && r >= 0, "PULSAR_GEMM_MID_ROWS must be a row count");
+    e->mid_rows = (int)std::min<long>(r, 1L << 30);
+  }
   e->R = std::max(e->max_rows, c.max_batch * c.max_prompt);
   e->max_pages = (c.max_ctx + kPage - 1) / kPage;
   // ring capacity: the window plus the rows one step writes (at most kMaxBlock), so that a
@@ -386,10 +401,11 @@ GemmArgs gemm_base(const Engine& e) {
 // Engines whose steps hold kWideHeadRows rows or more (verify blocks, batches of 64+) run
 // the output head in the 128 x 256 LDS tiles of the prefill GEMMs (its 64 MiB of weights
 // read once per 128 rows instead of once per 32); from kWideRows rows (the draft-block
-// mode at batch 256) the decode projections too. Below that the row-tile GEMMs are faster:
-// 128 x 256 tiles leave most CUs idle at a few hundred rows (320-row verify: 3.78 against
-// 5.35 ms with every projection in wide tiles). The two kinds sum K in different orders,
-// so an engine's logits can differ from an engine's on the other side of a threshold by
+// mode at batch 256) the decode projections too. Below that the row-tile and mid-size
+// GEMMs are faster: 128 x 256 tiles leave most CUs idle at a few hundred rows (320-row
+// verify: 3.78 against 5.35 ms with every projection in wide tiles). The wide tiles sum K
+// in another order than the row-tile and mid-size kernels (which agree exactly), so an
+// engine's logits can differ from an engine's on the other side of a wide threshold by
 // bf16 rounding; engines on the same side agree exactly.
 constexpr int kWideHeadRows = 128;
 constexpr int kWideRows = 1024;
@@ -411,6 +427,11 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
   const int eager_experts = (int64_t)MR * e.K >= 2 * (int64_t)e.E ? 1 : 0;
   const bool wide = dt == PULSAR_BF16 && MR >= kWideRows;
   const bool wide_head = dt == PULSAR_BF16 && MR >= kWideHeadRows;
+  const bool mid = dt == PULSAR_BF16 && !wide && e.mid_rows > 0 && MR >= e.mid_rows;
+  // projection GEMMs below the wide-tile threshold
+  auto gemm = [&](const GemmArgs& g, int epi, int groups) {
+    return mid ? launch_gemm_mid(g, dt, epi, groups, MR, s) : launch_gemm(g, dt, epi, groups, MR, s);
+  };
   // bf16: the decode attention finishes q, k and v itself (no qk_post launch)
   const bool fuse_post = dt == PULSAR_BF16;
   if (e.prof_on) {
@@ -464,7 +485,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     g.bias = m.gate_bias[l];
     g.bias_group_stride = e.H;
     PULSAR_TIMED(PC_QKVG, wide ? launch_gemm_wide(g, dt, EPI_QKVG, e.P, MR, s)
-                               : launch_gemm(g, dt, EPI_QKVG, e.P, MR, s));
+                               : gemm(g, EPI_QKVG, e.P));
     QKPostArgs qa{};
     qa.ctl = ctl;
     qa.rows = rows;
@@ -532,7 +553,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
     g.row_mode = ROWS_PULSE;
     g.ctl = ctl;
     PULSAR_TIMED(PC_WO, wide ? launch_gemm_wide(g, dt, EPI_RESID, e.P, MR, s)
-                             : launch_gemm(g, dt, EPI_RESID, e.P, MR, s));
+                             : gemm(g, EPI_RESID, e.P));
     RouterArgs ra{};
     ra.ctl = ctl;
     ra.rows = rows;
@@ -596,7 +617,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
       g.C0 = e.act_s;
       g.ldc0 = e.ds;
       g.N0 = e.ds;
-      PULSAR_TIMED(PC_ROUTED_GU, launch_gemm(g, dt, EPI_SWIGLU, e.E, MR, s));
+      PULSAR_TIMED(PC_ROUTED_GU, gemm(g, EPI_SWIGLU, e.E));
     }
     // shared + routed down projections
     g = gemm_base(e);
@@ -625,12 +646,12 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
       g.C0 = e.out_s;
       g.ldc0 = D;
       g.N0 = D;
-      PULSAR_TIMED(PC_ROUTED_DOWN, launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
+      PULSAR_TIMED(PC_ROUTED_DOWN, gemm(g, EPI_STORE, e.E));
     } else {
       // the fused launch takes K0 = K or 2K for the shared group; other widths and wide
       // tiles: two launches
       PULSAR_TIMED(PC_ROUTED_DOWN, wide ? launch_gemm_wide(g, dt, EPI_STORE, e.E, MR, s)
-                                        : launch_gemm(g, dt, EPI_STORE, e.E, MR, s));
+                                        : gemm(g, EPI_STORE, e.E));
       GemmArgs gs = gemm_base(e);
       gs.A = e.act_s;
       gs.lda = e.ds;
@@ -643,7 +664,7 @@ int enqueue_pass(Engine& e, const StepCtl* ctl, const RowDesc* rows, const AttnU
       gs.row_mode = ROWS_ALL;
       gs.ctl = ctl;
       PULSAR_TIMED(PC_SHARED_DOWN, wide ? launch_gemm_wide(gs, dt, EPI_STORE, 1, MR, s)
-                                        : launch_gemm(gs, dt, EPI_STORE, 1, MR, s));
+                                        : gemm(gs, EPI_STORE, 1));
     }
     CombineArgs ca{};
     ca.ctl = ctl;

@@ -526,20 +526,66 @@ __device__ __forceinline__ void epilogue4(const GemmArgs& g, int epi, int group,
 constexpr int kTileRows = 128;
 constexpr int kWideStages = 3;
 
+// Row-set launches of the wide kernel are 1-D grids. The tiles that hold rows, in the order
+// (group, row tile, column block) with column blocks fastest, are cut into 8 equal
+// contiguous ranges, one per XCD (workgroup L runs on XCD L % 8, as slot L / 8 of its
+// range). The column blocks of a row tile then follow one another on one XCD, which
+// fetches the tile's rows into its L2 once for all of them, and a group's weights are read
+// by the one or two XCDs whose ranges hold its tiles. Row counts are read on the device, so
+// every XCD gets an equal share of the tiles that exist; workgroups past the end exit.
+template <int MODE>
+__device__ __forceinline__ bool wide_tile(const GemmArgs& g, int& bx, int& group, int& bz) {
+  const int L = (int)blockIdx.x, xcd = L % kXcds, slot = L / kXcds;
+  const int lane = (int)threadIdx.x & 63;
+  // row tiles of each group, 64 groups per pass (one per lane)
+  int total = 0;
+  for (int y0 = 0; y0 < g.grid_y; y0 += 64) {
+    const int y = y0 + lane;
+    const int nt = y < g.grid_y
+        ? min((group_rows<MODE>(g, y + g.group_offset) + kTileRows - 1) / kTileRows, g.grid_z)
+        : 0;
+    for (int j = 0; j < 64 && y0 + j < g.grid_y; ++j) total += __builtin_amdgcn_readlane(nt, j);
+  }
+  total *= g.grid_x;
+  const int per = (total + kXcds - 1) / kXcds;
+  int item = xcd * per + slot;
+  if (slot >= per || item >= total) return false;
+  bx = item % g.grid_x;
+  int t = item / g.grid_x;
+  for (int y0 = 0; y0 < g.grid_y; y0 += 64) {
+    const int y = y0 + lane;
+    const int nt = y < g.grid_y
+        ? min((group_rows<MODE>(g, y + g.group_offset) + kTileRows - 1) / kTileRows, g.grid_z)
+        : 0;
+    for (int j = 0; j < 64 && y0 + j < g.grid_y; ++j) {
+      const int ntj = __builtin_amdgcn_readlane(nt, j);
+      if (t < ntj) {
+        group = y0 + j + g.group_offset;
+        bz = t;
+        return true;
+      }
+      t -= ntj;
+    }
+  }
+  return false;
+}
+
 template <int EPI, int MODE>
 __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
   constexpr int S = kWideStages;
   __shared__ bf16x8_t sA[S][8][64];   // [buffer][row tile][lane]
   __shared__ bf16x8_t sW[S][16][64];  // [buffer][column tile][lane]
-  const int group = (int)blockIdx.y + g.group_offset;
+  int bx = (int)blockIdx.x, group = (int)blockIdx.y + g.group_offset, bz = (int)blockIdx.z;
+  if constexpr (MODE != ROWS_LOGITS) {
+    if (!wide_tile<MODE>(g, bx, group, bz)) return;
+  }
   const int N = g.N;
   const int KT = g.K / 32;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wr = wv >> 1, wc = wv & 1;
   const int m16 = lane & 15, kq = lane >> 4;
   const int cnt = group_rows<MODE>(g, group);
-  int bx = (int)blockIdx.x, bz = (int)blockIdx.z;
   if constexpr (MODE == ROWS_LOGITS) {
     // output head (one group): workgroup L runs on XCD L % 8; give each XCD a contiguous
     // range of column tiles with their row tiles one after another, so the row tiles of a
@@ -644,6 +690,192 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   }
 }
 
+// Mid-size row sets (tens to a few hundred rows per group: block verifies, large decode
+// batches). A workgroup of 4 waves owns R = 64 RB rows of one group (RB = kMidRowBlocks)
+// and 4 weight column tiles (64 output columns; SwiGLU: 32 gate columns and their 32 up
+// twins); wave w computes rows 16 RB w .. 16 RB (w + 1) - 1 against all 4 tiles. The weight tiles of each
+// k step go through a ring of S LDS buffers with direct global-to-LDS loads (each wave
+// fetches one 1 KB tile, all 4 waves read all 4); the wave's own rows go to registers.
+// Every weight byte is read once per row tile instead of once per 32 rows, every row once
+// per 64 columns instead of once per 16, and S - 1 k steps are in flight. 64-row tiles
+// measured faster than 128-row ones (more workgroups for the attention projections of a
+// 320-row verify: qkv 16.0 -> 11.6 us), and rings of 4 to 10 buffers alike.
+//
+// Summation order: K is cut into the 8 chunks of gemm_bf16_kernel (wave w of that kernel
+// takes k tiles p K/32 + w KITER + i, pass p, i < KITER), each chunk summed by one chain
+// of matrix-core products from zero and the chunks added in order 0..7 to a zero start,
+// as that kernel's LDS reduction does: the two kernels give identical results, so a
+// caller picks either one by speed alone.
+constexpr int kMidWaves = 4;
+
+// Tile of a 1-D mid-size launch: the tiles that hold rows, ordered (group, row tile,
+// column block) with column blocks fastest and the fused all-rows group (has_g0) first,
+// are cut into 8 contiguous ranges, one per XCD, as in wide_tile.
+template <int MODE, int CW, int R>
+__device__ __forceinline__ bool mid_tile(const GemmArgs& g, int& cb, int& group, int& rt,
+                                         int& cnt) {
+  const int L = (int)blockIdx.x, xcd = L % kXcds, slot = L / kXcds;
+  const int lane = (int)threadIdx.x & 63;
+  const int s0 = g.has_g0 ? 1 : 0;
+  const int ng = g.grid_y + s0;  // at most 64 (host check)
+  int rows = 0, nx = 0, items = 0;
+  if (lane < ng) {
+    const int grp = lane < s0 ? -1 : lane - s0 + g.group_offset;
+    rows = group_rows<MODE>(g, grp);
+    nx = ((lane < s0 ? g.N0 : g.N) + CW - 1) / CW;
+    items = min((rows + R - 1) / R, g.grid_z) * nx;
+  }
+  int total = 0;
+  for (int j = 0; j < ng; ++j) total += __builtin_amdgcn_readlane(items, j);
+  const int per = (total + kXcds - 1) / kXcds;
+  int it = xcd * per + slot;
+  if (slot >= per || it >= total) return false;
+  for (int j = 0; j < ng; ++j) {
+    const int ij = __builtin_amdgcn_readlane(items, j);
+    if (it < ij) {
+      const int nxj = __builtin_amdgcn_readlane(nx, j);
+      group = j < s0 ? -1 : j - s0 + g.group_offset;
+      rt = it / nxj;
+      cb = it % nxj;
+      cnt = __builtin_amdgcn_readlane(rows, j);
+      return true;
+    }
+    it -= ij;
+  }
+  return false;
+}
+
+// The k loop of one mid-size tile: PASSES passes of 8 KITER k tiles, visited chunk by chunk
+// (chunk w: tiles p 8 KITER + w KITER + i, p < PASSES, i < KITER). wsrc: this wave's weight
+// tile at k tile 0 (lane offset included); arow: the wave's A rows at k 0 (lane offset
+// included). tot: the chunk sums added in chunk order.
+template <int KITER, int PASSES, int RB, int SR>
+__device__ __forceinline__ void mid_kloop(const bf16* wsrc, const bf16* const (&arow)[RB],
+                                          bf16x8_t (*sW)[4][64], int wv, int lane,
+                                          f32x4_t (&tot)[RB][4]) {
+  constexpr int CK = KITER * PASSES, STEPS = 8 * CK, KB = 8 * KITER;
+  constexpr int S = SR < STEPS ? SR : STEPS;  // ring buffers in use (at most sW's SR)
+  static_assert(S >= 3, "ring of at least 3 buffers");
+  auto ktile = [](int s) { return ((s % CK) / KITER) * KB + (s / CK) * KITER + (s % CK) % KITER; };
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  bf16x8_t xa[S][RB];
+  f32x4_t acc[RB][4];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) tot[rb][c] = zero;
+#pragma unroll
+  for (int j = 0; j < S - 1; ++j) {
+    load_lds16(wsrc + (int64_t)ktile(j) * 512, &sW[j][wv][0]);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) xa[j][rb] = load_bf16x8(arow[rb] + ktile(j) * 32);
+  }
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    // steps stay in program order (the scheduler would otherwise keep several chunks'
+    // accumulators live at once)
+    __builtin_amdgcn_sched_barrier(0);
+    // step s's loads are done once at most the S - 2 younger steps' loads (1 + RB each)
+    // are outstanding; the barrier publishes every wave's weight tile of step s and
+    // retires step s - 1, whose buffer the next fetch fills
+    if (s + S - 2 < STEPS)
+      wait_vmcnt<(S - 2) * (1 + RB)>();
+    else
+      wait_vmcnt<0>();
+    lds_barrier();
+    if (s + S - 1 < STEPS) {
+      const int j = s + S - 1;
+      load_lds16(wsrc + (int64_t)ktile(j) * 512, &sW[j % S][wv][0]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) xa[j % S][rb] = load_bf16x8(arow[rb] + ktile(j) * 32);
+    }
+    bf16x8_t fw[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) fw[c] = sW[s % S][c][lane];
+    // a chunk's chain starts from zero
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s % S][rb], fw[c],
+                                                            s % CK == 0 ? zero : acc[rb][c], 0, 0, 0);
+    if ((s + 1) % CK == 0) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) tot[rb][c] += acc[rb][c];
+    }
+  }
+}
+
+template <int EPI, int MODE, int KITER, int KMUL0, int RB, int S>
+__global__ void __launch_bounds__(64 * kMidWaves, 2) gemm_bf16_mid_kernel(GemmArgs g) {
+  constexpr bool kPair = (EPI == EPI_SWIGLU);
+  constexpr int CW = kPair ? 32 : 64;  // output columns per column block
+  constexpr int R = kMidWaves * RB * 16;
+  __shared__ bf16x8_t sW[S][4][64];
+  int cb, group, rt, cnt;
+  if (!mid_tile<MODE, CW, R>(g, cb, group, rt, cnt)) return;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int m = lane & 15, kq = lane >> 4;
+  const bool g0 = group < 0;
+  const int N = g0 ? g.N0 : g.N;
+  const int KT = (g0 ? g.K0 : g.K) / 32;
+  const bf16* W = g0 ? reinterpret_cast<const bf16*>(g.W0)
+                     : reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
+  const bf16* A = reinterpret_cast<const bf16*>(g0 ? g.A0 : g.A);
+  const int64_t lda = g0 ? g.lda0 : g.lda;
+  void* Cout = g0 ? g.C0 : g.C;
+  const int64_t ldc = g0 ? g.ldc0 : g.ldc;
+  // this wave's weight tile: SwiGLU gate tiles 2 cb, 2 cb + 1 and their up twins N/16 on;
+  // otherwise tiles 4 cb .. 4 cb + 3 (tiles past N re-read the last one, never stored)
+  int ct;
+  if constexpr (kPair)
+    ct = (wv & 2 ? N / 16 : 0) + cb * 2 + (wv & 1);
+  else
+    ct = min(cb * 4 + wv, N / 16 - 1);
+  const bf16* wsrc = W + ((int64_t)ct * KT * 64 + lane) * 8;
+  // rows of the wave: 16-row block rb holds tile rows 16 (RB wv + rb) + 0..15; lanes past
+  // the count re-read the last row (computed, never stored)
+  const int r0 = rt * R + wv * RB * 16;
+  int ent[RB];
+  const bf16* arow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int i = min(r0 + rb * 16 + m, cnt - 1);
+    ent[rb] = entry_fix<MODE>(group, i, entry_load<MODE>(g, group, i));
+    arow[rb] = A + (int64_t)a_row_of<MODE>(g, group, ent[rb]) * lda + kq * 8;
+  }
+  f32x4_t tot[RB][4];
+  if (g0 && KMUL0 > 1)
+    mid_kloop<KITER, KMUL0, RB, S>(wsrc, arow, sW, wv, lane, tot);
+  else
+    mid_kloop<KITER, 1, RB, S>(wsrc, arow, sW, wv, lane, tot);
+  // D layout of 16x16 MFMA: lane holds rows 4 kq + j of its block, column m; the C row of
+  // block row r is the entry held by lane r
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int crow = __shfl(ent[rb], kq * 4 + j, 64);
+      if (r0 + rb * 16 + kq * 4 + j >= cnt) continue;
+      if constexpr (kPair) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, (cb * 2 + c) * 16 + m,
+                         tot[rb][c][j], tot[rb][c + 2][j]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int col = (cb * 4 + c) * 16 + m;
+          if (col < N)
+            epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, col, tot[rb][c][j], 0.f);
+        }
+      }
+    }
+  }
+}
+
 template <int EPI, int MODE, int KMUL0, bool EAGER, bool XCD>
 void launch_bf16_kx(const GemmArgs& a, dim3 grid, hipStream_t s) {
   constexpr int T = 64 * kGemmWaves;
@@ -729,15 +961,77 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
   return PULSAR_OK;
 }
 
+template <int EPI, int MODE, int KMUL0, int RB, int S>
+void launch_mid_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  switch (a.K) {
+    case 256: gemm_bf16_mid_kernel<EPI, MODE, 1, KMUL0, RB, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
+    case 512: gemm_bf16_mid_kernel<EPI, MODE, 2, KMUL0, RB, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
+    case 1024: gemm_bf16_mid_kernel<EPI, MODE, 4, KMUL0, RB, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
+    default: gemm_bf16_mid_kernel<EPI, MODE, 8, KMUL0, RB, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
+  }
+}
+
+constexpr int kMidRowBlocks = 1;  // 16-row blocks per wave: 64-row tiles
+constexpr int kMidStages = 6;
+
+template <int EPI>
+int launch_mid(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
+  constexpr int RB = kMidRowBlocks, S = kMidStages;
+  constexpr int R = kMidWaves * RB * 16;
+  constexpr int CW = EPI == EPI_SWIGLU ? 32 : 64;
+  if (groups <= 0 || max_rows <= 0) return PULSAR_OK;
+  if (a.K != 256 && a.K != 512 && a.K != 1024 && a.K != 2048)
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: K must be 256, 512, 1024 or 2048");
+  const int ncol = EPI == EPI_SWIGLU ? 32 : 16;
+  if (a.N % ncol != 0 || (a.has_g0 && a.N0 % ncol != 0))
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: mid-size tiles need N % 16 == 0 (SwiGLU: 32)");
+  if (a.has_g0 && (a.row_mode != ROWS_LIST || a.ctl == nullptr))
+    return fail(PULSAR_ERR_INVALID,
+                "gemm: the all-rows group fuses into list launches with a control block only");
+  if (a.has_g0 && a.K0 != a.K && a.K0 != 2 * a.K)
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: the all-rows group needs K0 = K or 2K");
+  if (groups + (a.has_g0 ? 1 : 0) > 64)
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: mid-size tiles take at most 64 groups");
+  GemmArgs ga = a;
+  ga.grid_y = groups;
+  ga.grid_z = (max_rows + R - 1) / R;
+  int64_t items = (int64_t)groups * ga.grid_z * ((a.N + CW - 1) / CW);
+  if (a.has_g0) items += (int64_t)ga.grid_z * ((a.N0 + CW - 1) / CW);
+  if (items > (int64_t)1 << 30) return fail(PULSAR_ERR_INVALID, "gemm: mid-size launch too large");
+  const dim3 grid((unsigned)((items + kXcds - 1) / kXcds * kXcds));
+  const bool k2 = a.has_g0 && a.K0 == 2 * a.K;
+  switch (a.row_mode) {
+    case ROWS_PULSE: launch_mid_k<EPI, ROWS_PULSE, 1, RB, S>(ga, grid, s); break;
+    case ROWS_ALL: launch_mid_k<EPI, ROWS_ALL, 1, RB, S>(ga, grid, s); break;
+    case ROWS_LIST:
+      if (k2)
+        launch_mid_k<EPI, ROWS_LIST, 2, RB, S>(ga, grid, s);
+      else
+        launch_mid_k<EPI, ROWS_LIST, 1, RB, S>(ga, grid, s);
+      break;
+    default: return fail(PULSAR_ERR_INVALID, "gemm: row mode of a mid-size launch");
+  }
+  PULSAR_LAUNCH_CHECK();
+  return PULSAR_OK;
+}
+
 template <int EPI>
 int launch_wide(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
   const int colw = EPI == EPI_SWIGLU ? 128 : 256;
   dim3 grid((unsigned)((a.N + colw - 1) / colw), (unsigned)groups,
             (unsigned)((max_rows + kTileRows - 1) / kTileRows));
+  // row-set modes: a 1-D grid over (column block, group, row tile), split by wide_tile
+  GemmArgs ga = a;
+  ga.grid_x = (int)grid.x;
+  ga.grid_y = (int)grid.y;
+  ga.grid_z = (int)grid.z;
+  const int64_t tiles = (int64_t)ga.grid_x * ga.grid_y * ga.grid_z;
+  if (tiles > (int64_t)1 << 30) return fail(PULSAR_ERR_INVALID, "gemm: wide launch too large");
+  const dim3 g1((unsigned)((tiles + kXcds - 1) / kXcds * kXcds));
   switch (a.row_mode) {
-    case ROWS_PULSE: gemm_bf16_lds_kernel<EPI, ROWS_PULSE><<<grid, 256, 0, s>>>(a); break;
-    case ROWS_LIST: gemm_bf16_lds_kernel<EPI, ROWS_LIST><<<grid, 256, 0, s>>>(a); break;
-    case ROWS_ALL: gemm_bf16_lds_kernel<EPI, ROWS_ALL><<<grid, 256, 0, s>>>(a); break;
+    case ROWS_PULSE: gemm_bf16_lds_kernel<EPI, ROWS_PULSE><<<g1, 256, 0, s>>>(ga); break;
+    case ROWS_LIST: gemm_bf16_lds_kernel<EPI, ROWS_LIST><<<g1, 256, 0, s>>>(ga); break;
+    case ROWS_ALL: gemm_bf16_lds_kernel<EPI, ROWS_ALL><<<g1, 256, 0, s>>>(ga); break;
     case ROWS_LOGITS:
       if constexpr (EPI == EPI_LOGITS || EPI == EPI_LOGITS_RAW) {
         gemm_bf16_lds_kernel<EPI, ROWS_LOGITS><<<grid, 256, 0, s>>>(a);
@@ -768,6 +1062,18 @@ int launch_gemm_wide(const GemmArgs& a, int dtype, int epi, int groups, int max_
     case EPI_SCALE: return launch_wide<EPI_SCALE>(a, groups, max_rows, s);
     case EPI_LOGITS: return launch_wide<EPI_LOGITS>(a, groups, max_rows, s);
     case EPI_LOGITS_RAW: return launch_wide<EPI_LOGITS_RAW>(a, groups, max_rows, s);
+  }
+  return launch_gemm(a, dtype, epi, groups, max_rows, s);
+}
+
+int launch_gemm_mid(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
+                    hipStream_t s) {
+  if (dtype != PULSAR_BF16) return launch_gemm(a, dtype, epi, groups, max_rows, s);
+  switch (epi) {
+    case EPI_STORE: return launch_mid<EPI_STORE>(a, groups, max_rows, s);
+    case EPI_QKVG: return launch_mid<EPI_QKVG>(a, groups, max_rows, s);
+    case EPI_RESID: return launch_mid<EPI_RESID>(a, groups, max_rows, s);
+    case EPI_SWIGLU: return launch_mid<EPI_SWIGLU>(a, groups, max_rows, s);
   }
   return launch_gemm(a, dtype, epi, groups, max_rows, s);
 }
