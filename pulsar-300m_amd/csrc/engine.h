@@ -132,15 +132,16 @@ struct GemmArgs {
 int launch_gemm(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
                 hipStream_t s);
 // Same contract, for row sets of hundreds to tens of thousands of rows (prefill): bf16
-// launches without a fused all-rows group use 128 x 128 output tiles; others fall back to
+// launches without a fused all-rows group use 128 x 256 output tiles; others fall back to
 // launch_gemm. The two kernels sum K in different orders, so a caller that wants results
 // independent of batch composition picks one by a per-sequence property (prompt length).
 int launch_gemm_wide(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
                      hipStream_t s);
 // Same contract and identical results as launch_gemm (the same summation order), for row
-// sets of tens to hundreds of rows per group: 64-row x 64-column tiles with the weights
-// staged through LDS, so that weights are read once per 64 rows. bf16 with the store,
-// qkv + gate, residual and SwiGLU epilogues; other launches go to launch_gemm.
+// sets of tens to hundreds of rows per group: 64-row tiles of 64 (rows of a pulse, all
+// rows) or 128 (expert lists) weight columns staged through LDS, so that weights are read
+// once per 64 rows. bf16 with the store, qkv + gate, residual and SwiGLU epilogues; other
+// launches go to launch_gemm.
 int launch_gemm_mid(const GemmArgs& a, int dtype, int epi, int groups, int max_rows,
                     hipStream_t s);
 

@@ -235,7 +235,7 @@ enum ProfClass {
 };
 
 // From kMidRows rows up to kWideRows the projections run in the mid-size tiles of
-// launch_gemm_mid (64 rows x 64 columns, weights staged through LDS). They give results
+// launch_gemm_mid (64-row tiles, weights staged through LDS). They give results
 // identical to the row-tile kernel's, so the threshold is a matter of speed only; the
 // environment variable PULSAR_GEMM_MID_ROWS (read when an engine is created) overrides it.
 constexpr int kMidRows = 128;

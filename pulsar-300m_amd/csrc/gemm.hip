@@ -691,15 +691,20 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
 }
 
 // Mid-size row sets (tens to a few hundred rows per group: block verifies, large decode
-// batches). A workgroup of 4 waves owns R = 64 RB rows of one group (RB = kMidRowBlocks)
-// and 4 weight column tiles (64 output columns; SwiGLU: 32 gate columns and their 32 up
-// twins); wave w computes rows 16 RB w .. 16 RB (w + 1) - 1 against all 4 tiles. The weight tiles of each
-// k step go through a ring of S LDS buffers with direct global-to-LDS loads (each wave
-// fetches one 1 KB tile, all 4 waves read all 4); the wave's own rows go to registers.
-// Every weight byte is read once per row tile instead of once per 32 rows, every row once
-// per 64 columns instead of once per 16, and S - 1 k steps are in flight. 64-row tiles
-// measured faster than 128-row ones (more workgroups for the attention projections of a
-// 320-row verify: qkv 16.0 -> 11.6 us), and rings of 4 to 10 buffers alike.
+// batches). A workgroup of 4 waves owns R = 64 RB rows of one group and CT weight column
+// tiles of 16 (CT = 4: 64 output columns, SwiGLU 32 gate columns and their 32 up twins;
+// CT = 8: twice that); wave w computes rows 16 RB w .. 16 RB (w + 1) - 1 against all CT
+// tiles. The weight tiles of each 32-wide k step go through a ring of S LDS buffers with
+// direct global-to-LDS loads (each wave fetches CT / 4 of the 1 KB tiles, all 4 waves read
+// all CT); the wave's own rows go to registers. The launch moves rows x (weight rows) x K x 2 (1/(16 CT) + 1/R) bytes from L2 to
+// the CUs, which bounds it (about 10 TB/s measured: timing copies without the k loop or
+// without the products put the 320-row verify's routed gate/up at 6.2 and 22.9 of its
+// 22.7 us, and rings of 4 to 10 buffers or 2 to 4 k tiles per stage ran alike; lanes past
+// the row count re-read the last row, whose lines their wave's load fetches once). The
+// expert launches take 64 x 128 tiles (RB = 1, CT = 8; 320-row verify: routed gate/up 22.8
+// us in 64 x 64 tiles, 21.1 in 64 x 128, 21.8 in 128 x 128 at one wave per SIMD, 24.4 in
+// 128 x 64) and the attention projections, whose few hundred dense rows need the
+// workgroups, 64 x 64 (RB = 1, CT = 4).
 //
 // Summation order: K is cut into the 8 chunks of gemm_bf16_kernel (wave w of that kernel
 // takes k tiles p K/32 + w KITER + i, pass p, i < KITER), each chunk summed by one chain
@@ -746,74 +751,78 @@ __device__ __forceinline__ bool mid_tile(const GemmArgs& g, int& cb, int& group,
 }
 
 // The k loop of one mid-size tile: PASSES passes of 8 KITER k tiles, visited chunk by chunk
-// (chunk w: tiles p 8 KITER + w KITER + i, p < PASSES, i < KITER). wsrc: this wave's weight
-// tile at k tile 0 (lane offset included); arow: the wave's A rows at k 0 (lane offset
-// included). tot: the chunk sums added in chunk order.
-template <int KITER, int PASSES, int RB, int SR>
-__device__ __forceinline__ void mid_kloop(const bf16* wsrc, const bf16* const (&arow)[RB],
-                                          bf16x8_t (*sW)[4][64], int wv, int lane,
-                                          f32x4_t (&tot)[RB][4]) {
+// (chunk w: tiles p 8 KITER + w KITER + i, p < PASSES, i < KITER). wsrc[h]: the wave's
+// weight tile h (tile wv + 4 h of the block) at k tile 0, lane offset included; arow: the
+// wave's A rows at k 0 (lane offset included). tot: the chunk sums added in chunk
+// order.
+template <int KITER, int PASSES, int RB, int CT, int SR>
+__device__ __forceinline__ void mid_kloop(const bf16* const (&wsrc)[CT / 4],
+                                          const bf16* const (&arow)[RB], bf16x8_t (*sW)[CT][64],
+                                          int wv, int lane, f32x4_t (&tot)[RB][CT]) {
   constexpr int CK = KITER * PASSES, STEPS = 8 * CK, KB = 8 * KITER;
   constexpr int S = SR < STEPS ? SR : STEPS;  // ring buffers in use (at most sW's SR)
-  static_assert(S >= 3, "ring of at least 3 buffers");
-  auto ktile = [](int s) { return ((s % CK) / KITER) * KB + (s / CK) * KITER + (s % CK) % KITER; };
+  static_assert(S >= 2, "ring of at least 2 buffers");
+  constexpr int LOADS = CT / 4 + RB;  // vector loads of one wave per step
+  static_assert((S - 2) * LOADS <= 63, "vmcnt range");
+  // k tile of step t of the chunk-ordered sequence
+  auto ktile = [](int t) { return ((t % CK) / KITER) * KB + (t / CK) * KITER + (t % CK) % KITER; };
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
   bf16x8_t xa[S][RB];
-  f32x4_t acc[RB][4];
+  f32x4_t acc[RB][CT];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) tot[rb][c] = zero;
+    for (int c = 0; c < CT; ++c) tot[rb][c] = zero;
+  auto fetch = [&](int j) {
+    const int kt = ktile(j);
 #pragma unroll
-  for (int j = 0; j < S - 1; ++j) {
-    load_lds16(wsrc + (int64_t)ktile(j) * 512, &sW[j][wv][0]);
+    for (int h = 0; h < CT / 4; ++h)
+      load_lds16(wsrc[h] + (int64_t)kt * 512, &sW[j % S][wv + 4 * h][0]);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) xa[j][rb] = load_bf16x8(arow[rb] + ktile(j) * 32);
-  }
+    for (int rb = 0; rb < RB; ++rb) xa[j % S][rb] = load_bf16x8(arow[rb] + kt * 32);
+  };
+#pragma unroll
+  for (int j = 0; j < S - 1; ++j) fetch(j);
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     // steps stay in program order (the scheduler would otherwise keep several chunks'
     // accumulators live at once)
     __builtin_amdgcn_sched_barrier(0);
-    // step s's loads are done once at most the S - 2 younger steps' loads (1 + RB each)
-    // are outstanding; the barrier publishes every wave's weight tile of step s and
-    // retires step s - 1, whose buffer the next fetch fills
+    // step s's loads are done once at most the S - 2 younger steps' loads are
+    // outstanding; the barrier publishes every wave's weight tiles of step s and retires
+    // step s - 1, whose buffer the next fetch fills
     if (s + S - 2 < STEPS)
-      wait_vmcnt<(S - 2) * (1 + RB)>();
+      wait_vmcnt<(S - 2) * LOADS>();
     else
       wait_vmcnt<0>();
     lds_barrier();
-    if (s + S - 1 < STEPS) {
-      const int j = s + S - 1;
-      load_lds16(wsrc + (int64_t)ktile(j) * 512, &sW[j % S][wv][0]);
+    if (s + S - 1 < STEPS) fetch(s + S - 1);
+    bf16x8_t fw[CT];
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) xa[j % S][rb] = load_bf16x8(arow[rb] + ktile(j) * 32);
-    }
-    bf16x8_t fw[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) fw[c] = sW[s % S][c][lane];
+    for (int c = 0; c < CT; ++c) fw[c] = sW[s % S][c][lane];
     // a chunk's chain starts from zero
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < CT; ++c)
         acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s % S][rb], fw[c],
                                                             s % CK == 0 ? zero : acc[rb][c], 0, 0, 0);
     if ((s + 1) % CK == 0) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) tot[rb][c] += acc[rb][c];
+        for (int c = 0; c < CT; ++c) tot[rb][c] += acc[rb][c];
     }
   }
 }
 
-template <int EPI, int MODE, int KITER, int KMUL0, int RB, int S>
+template <int EPI, int MODE, int KITER, int KMUL0, int RB, int CT, int S>
 __global__ void __launch_bounds__(64 * kMidWaves, 2) gemm_bf16_mid_kernel(GemmArgs g) {
   constexpr bool kPair = (EPI == EPI_SWIGLU);
-  constexpr int CW = kPair ? 32 : 64;  // output columns per column block
+  constexpr int CW = kPair ? CT * 8 : CT * 16;  // output columns per column block
   constexpr int R = kMidWaves * RB * 16;
-  __shared__ bf16x8_t sW[S][4][64];
+  static_assert(CT == 4 || CT == 8, "4 or 8 weight tiles per workgroup");
+  __shared__ bf16x8_t sW[S][CT][64];
   int cb, group, rt, cnt;
   if (!mid_tile<MODE, CW, R>(g, cb, group, rt, cnt)) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -827,14 +836,20 @@ __global__ void __launch_bounds__(64 * kMidWaves, 2) gemm_bf16_mid_kernel(GemmAr
   const int64_t lda = g0 ? g.lda0 : g.lda;
   void* Cout = g0 ? g.C0 : g.C;
   const int64_t ldc = g0 ? g.ldc0 : g.ldc;
-  // this wave's weight tile: SwiGLU gate tiles 2 cb, 2 cb + 1 and their up twins N/16 on;
-  // otherwise tiles 4 cb .. 4 cb + 3 (tiles past N re-read the last one, never stored)
-  int ct;
-  if constexpr (kPair)
-    ct = (wv & 2 ? N / 16 : 0) + cb * 2 + (wv & 1);
-  else
-    ct = min(cb * 4 + wv, N / 16 - 1);
-  const bf16* wsrc = W + ((int64_t)ct * KT * 64 + lane) * 8;
+  // weight tile c of the block: SwiGLU gate tiles (CT/2) cb + c for c < CT/2 and their up
+  // twins N/16 on; otherwise tiles CT cb + c (tiles past N re-read the last one, never
+  // stored). Wave wv fetches tiles wv + 4 h.
+  const bf16* wsrc[CT / 4];
+#pragma unroll
+  for (int h = 0; h < CT / 4; ++h) {
+    const int c = wv + 4 * h;
+    int ct;
+    if constexpr (kPair)
+      ct = (c < CT / 2 ? 0 : N / 16 - CT / 2) + cb * (CT / 2) + c;
+    else
+      ct = min(cb * CT + c, N / 16 - 1);
+    wsrc[h] = W + ((int64_t)ct * KT * 64 + lane) * 8;
+  }
   // rows of the wave: 16-row block rb holds tile rows 16 (RB wv + rb) + 0..15; lanes past
   // the count re-read the last row (computed, never stored)
   const int r0 = rt * R + wv * RB * 16;
@@ -846,11 +861,11 @@ __global__ void __launch_bounds__(64 * kMidWaves, 2) gemm_bf16_mid_kernel(GemmAr
     ent[rb] = entry_fix<MODE>(group, i, entry_load<MODE>(g, group, i));
     arow[rb] = A + (int64_t)a_row_of<MODE>(g, group, ent[rb]) * lda + kq * 8;
   }
-  f32x4_t tot[RB][4];
+  f32x4_t tot[RB][CT];
   if (g0 && KMUL0 > 1)
-    mid_kloop<KITER, KMUL0, RB, S>(wsrc, arow, sW, wv, lane, tot);
+    mid_kloop<KITER, KMUL0, RB, CT, S>(wsrc, arow, sW, wv, lane, tot);
   else
-    mid_kloop<KITER, 1, RB, S>(wsrc, arow, sW, wv, lane, tot);
+    mid_kloop<KITER, 1, RB, CT, S>(wsrc, arow, sW, wv, lane, tot);
   // D layout of 16x16 MFMA: lane holds rows 4 kq + j of its block, column m; the C row of
   // block row r is the entry held by lane r
 #pragma unroll
@@ -861,13 +876,13 @@ __global__ void __launch_bounds__(64 * kMidWaves, 2) gemm_bf16_mid_kernel(GemmAr
       if (r0 + rb * 16 + kq * 4 + j >= cnt) continue;
       if constexpr (kPair) {
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
-          epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, (cb * 2 + c) * 16 + m,
-                         tot[rb][c][j], tot[rb][c + 2][j]);
+        for (int c = 0; c < CT / 2; ++c)
+          epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset,
+                         (cb * (CT / 2) + c) * 16 + m, tot[rb][c][j], tot[rb][c + CT / 2][j]);
       } else {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int col = (cb * 4 + c) * 16 + m;
+        for (int c = 0; c < CT; ++c) {
+          const int col = (cb * CT + c) * 16 + m;
           if (col < N)
             epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, col, tot[rb][c][j], 0.f);
         }
@@ -961,37 +976,26 @@ int launch_one(const GemmArgs& a, int dtype, int groups, int max_rows, hipStream
   return PULSAR_OK;
 }
 
-template <int EPI, int MODE, int KMUL0, int RB, int S>
+template <int EPI, int MODE, int KMUL0, int RB, int CT, int S>
 void launch_mid_k(const GemmArgs& a, dim3 grid, hipStream_t s) {
   switch (a.K) {
-    case 256: gemm_bf16_mid_kernel<EPI, MODE, 1, KMUL0, RB, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
-    case 512: gemm_bf16_mid_kernel<EPI, MODE, 2, KMUL0, RB, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
-    case 1024: gemm_bf16_mid_kernel<EPI, MODE, 4, KMUL0, RB, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
-    default: gemm_bf16_mid_kernel<EPI, MODE, 8, KMUL0, RB, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
+    case 256: gemm_bf16_mid_kernel<EPI, MODE, 1, KMUL0, RB, CT, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
+    case 512: gemm_bf16_mid_kernel<EPI, MODE, 2, KMUL0, RB, CT, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
+    case 1024: gemm_bf16_mid_kernel<EPI, MODE, 4, KMUL0, RB, CT, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
+    default: gemm_bf16_mid_kernel<EPI, MODE, 8, KMUL0, RB, CT, S><<<grid, 64 * kMidWaves, 0, s>>>(a); break;
   }
 }
 
-constexpr int kMidRowBlocks = 1;  // 16-row blocks per wave: 64-row tiles
-constexpr int kMidStages = 6;
-
-template <int EPI>
-int launch_mid(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
-  constexpr int RB = kMidRowBlocks, S = kMidStages;
+// Tile shape of a mid-size launch: expert lists in 64 x 128 tiles, rows of a pulse or all
+// rows (one dense group) in 64 x 64 tiles; rings of 6 buffers.
+template <int EPI, int RB, int CT, int S>
+int launch_mid_shape(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
   constexpr int R = kMidWaves * RB * 16;
-  constexpr int CW = EPI == EPI_SWIGLU ? 32 : 64;
-  if (groups <= 0 || max_rows <= 0) return PULSAR_OK;
-  if (a.K != 256 && a.K != 512 && a.K != 1024 && a.K != 2048)
-    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: K must be 256, 512, 1024 or 2048");
-  const int ncol = EPI == EPI_SWIGLU ? 32 : 16;
+  constexpr int CW = EPI == EPI_SWIGLU ? CT * 8 : CT * 16;
+  const int ncol = EPI == EPI_SWIGLU ? CT * 8 : 16;
   if (a.N % ncol != 0 || (a.has_g0 && a.N0 % ncol != 0))
-    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: mid-size tiles need N % 16 == 0 (SwiGLU: 32)");
-  if (a.has_g0 && (a.row_mode != ROWS_LIST || a.ctl == nullptr))
-    return fail(PULSAR_ERR_INVALID,
-                "gemm: the all-rows group fuses into list launches with a control block only");
-  if (a.has_g0 && a.K0 != a.K && a.K0 != 2 * a.K)
-    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: the all-rows group needs K0 = K or 2K");
-  if (groups + (a.has_g0 ? 1 : 0) > 64)
-    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: mid-size tiles take at most 64 groups");
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: mid-size tiles need N % 16 == 0 (SwiGLU: a "
+                                        "multiple of the column block)");
   GemmArgs ga = a;
   ga.grid_y = groups;
   ga.grid_z = (max_rows + R - 1) / R;
@@ -1001,18 +1005,34 @@ int launch_mid(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
   const dim3 grid((unsigned)((items + kXcds - 1) / kXcds * kXcds));
   const bool k2 = a.has_g0 && a.K0 == 2 * a.K;
   switch (a.row_mode) {
-    case ROWS_PULSE: launch_mid_k<EPI, ROWS_PULSE, 1, RB, S>(ga, grid, s); break;
-    case ROWS_ALL: launch_mid_k<EPI, ROWS_ALL, 1, RB, S>(ga, grid, s); break;
+    case ROWS_PULSE: launch_mid_k<EPI, ROWS_PULSE, 1, RB, CT, S>(ga, grid, s); break;
+    case ROWS_ALL: launch_mid_k<EPI, ROWS_ALL, 1, RB, CT, S>(ga, grid, s); break;
     case ROWS_LIST:
       if (k2)
-        launch_mid_k<EPI, ROWS_LIST, 2, RB, S>(ga, grid, s);
+        launch_mid_k<EPI, ROWS_LIST, 2, RB, CT, S>(ga, grid, s);
       else
-        launch_mid_k<EPI, ROWS_LIST, 1, RB, S>(ga, grid, s);
+        launch_mid_k<EPI, ROWS_LIST, 1, RB, CT, S>(ga, grid, s);
       break;
     default: return fail(PULSAR_ERR_INVALID, "gemm: row mode of a mid-size launch");
   }
   PULSAR_LAUNCH_CHECK();
   return PULSAR_OK;
+}
+
+template <int EPI>
+int launch_mid(const GemmArgs& a, int groups, int max_rows, hipStream_t s) {
+  if (groups <= 0 || max_rows <= 0) return PULSAR_OK;
+  if (a.K != 256 && a.K != 512 && a.K != 1024 && a.K != 2048)
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: K must be 256, 512, 1024 or 2048");
+  if (a.has_g0 && (a.row_mode != ROWS_LIST || a.ctl == nullptr))
+    return fail(PULSAR_ERR_INVALID,
+                "gemm: the all-rows group fuses into list launches with a control block only");
+  if (a.has_g0 && a.K0 != a.K && a.K0 != 2 * a.K)
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: the all-rows group needs K0 = K or 2K");
+  if (groups + (a.has_g0 ? 1 : 0) > 64)
+    return fail(PULSAR_ERR_UNSUPPORTED, "gemm: mid-size tiles take at most 64 groups");
+  if (a.row_mode == ROWS_LIST) return launch_mid_shape<EPI, 1, 8, 6>(a, groups, max_rows, s);
+  return launch_mid_shape<EPI, 1, 4, 6>(a, groups, max_rows, s);
 }
 
 template <int EPI>
