@@ -785,6 +785,7 @@ int enqueue_step(Engine& e, hipStream_t s) {
   co.pool = e.pool;
   co.pool_pages = e.pool_pages;
   co.max_pages = e.max_pages;
+  co.max_lrows = e.max_rows;
   PULSAR_TRY(launch_controller(co, s));
   prof_span(e, PC_CONTROL, _pc, prof_mark(e, s));
   return PULSAR_OK;
@@ -930,6 +931,7 @@ int first_token(Engine& e, uint64_t seed, hipStream_t s) {
   co.pool = e.pool;
   co.pool_pages = e.pool_pages;
   co.max_pages = e.max_pages;
+  co.max_lrows = e.max_rows;
   PULSAR_TRY(launch_controller(co, s));
   // host vectors above are read by the async copies: finish before they go out of scope
   PULSAR_CHECK_HIP(hipStreamSynchronize(s));

@@ -86,6 +86,7 @@ struct ControllerArgs {
   int32_t* page_count;
   int32_t* pool;
   int pool_pages, max_pages;
+  int max_lrows;  // logits rows of the largest step (sizes the LDS copy of argmax / draw)
 };
 
 int launch_sample(const SampleArgs& a, int dtype, int max_lrows, hipStream_t s);

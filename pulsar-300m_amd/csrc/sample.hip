@@ -328,23 +328,36 @@ __global__ void __launch_bounds__(NT) sample_kernel(SampleArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-__device__ bool is_stop(const ControllerArgs& a, int tok) {
+// LDS copies of what the step's controller reads by an index it learns from the state (the
+// last step's argmax and draws) and of the stop ids, loaded by the whole block together
+// with the state, so that the state's round trip is the only one before the layout.
+constexpr int kCtlMaxLrows = 2048;
+struct CtlShared {
+  int draw[2 * kCtlMaxLrows];
+  int argmax[kCtlMaxLrows];
+  int stop[8];
+};
+__shared__ CtlShared ctl_lds;
+
+__device__ __forceinline__ bool is_stop(const ControllerArgs& a, int tok) {
   for (int i = 0; i < a.n_stop; ++i)
-    if (a.stop_ids[i] == tok) return true;
+    if (ctl_lds.stop[i] == tok) return true;
   return false;
 }
 
 // Append tok to the sequence's output; kind 1 marks an accepted draft, 0 a drawn token.
-__device__ void emit(const ControllerArgs& a, SeqState& s, int b, int tok, int kind = 0) {
+__device__ __forceinline__ void emit(const ControllerArgs& a, SeqState& s, int b, int tok, int kind = 0) {
   a.out_tokens[(int64_t)b * a.max_new + s.produced] = tok;
   if (a.out_kinds) a.out_kinds[(int64_t)b * a.max_new + s.produced] = kind;
   s.produced += 1;
-  a.seen[(int64_t)b * (a.V / 32) + (tok >> 5)] |= 1u << (tok & 31);
+  // only this thread writes the sequence's row: a no-return atomic sets the bit without
+  // reading the word back first (one round trip less)
+  atomicOr(&a.seen[(int64_t)b * (a.V / 32) + (tok >> 5)], 1u << (tok & 31));
   if (s.produced >= s.max_new) s.done = 1;
 }
 
 // c <- s (whose pulse 0 ran this step). kind = kind of the new current token.
-__device__ void promote(const ControllerArgs& a, SeqState& s, int kind) {
+__device__ __forceinline__ void promote(const ControllerArgs& a, SeqState& s, int kind) {
   s.c_tok = s.s_tok;
   s.c_pos = s.c_pos + 1;
   s.c_slot = 1 - s.c_slot;
@@ -354,17 +367,17 @@ __device__ void promote(const ControllerArgs& a, SeqState& s, int kind) {
   // the new current token's pulse-0 logits are those of the s row
   const int lr = s.lrow_s;
   if (kind == KIND_TESTED) {
-    s.d_tok = a.draw[lr * 2];
+    s.d_tok = ctl_lds.draw[lr * 2];
     s.s_valid = !is_stop(a, s.d_tok);
     s.s_tok = s.d_tok;
   } else {
-    const int g = a.argmax[lr];
+    const int g = ctl_lds.argmax[lr];
     s.s_valid = !is_stop(a, g);
     s.s_tok = g;
   }
 }
 
-__device__ void fresh(SeqState& s, int tok) {
+__device__ __forceinline__ void fresh(SeqState& s, int tok) {
   s.c_tok = tok;
   s.c_pos = s.c_pos + 1;
   s.c_slot = 1 - s.c_slot;
@@ -378,14 +391,14 @@ __device__ void fresh(SeqState& s, int tok) {
 // Tokens whose pulses the reference runs through decode_step, the only place its early
 // exit applies: every decoded token in plain mode (src/infer.py:620), an accepted draft in
 // speculative mode (:728); the tested tokens' draft/verify passes never exit (:700-714).
-__device__ bool exit_eligible(const ControllerArgs& a, const SeqState& s) {
+__device__ __forceinline__ bool exit_eligible(const ControllerArgs& a, const SeqState& s) {
   return a.early_exit && (!a.speculative || s.c_kind == KIND_PLAIN);
 }
 
 // Plain decode with early exit: the reference's loop runs decode_step on the last emitted
 // token as well (src/infer.py:619-620), and counts its exit; keep the sequence running for
 // that token's pulses (it emits nothing after them).
-__device__ void keep_for_tail(const ControllerArgs& a, SeqState& s) {
+__device__ __forceinline__ void keep_for_tail(const ControllerArgs& a, SeqState& s) {
   if (s.done && a.early_exit && !a.speculative) {
     s.done = 0;
     s.tail = 1;
@@ -395,8 +408,8 @@ __device__ void keep_for_tail(const ControllerArgs& a, SeqState& s) {
 // The current token is done without a draft test (plain mode, an accepted draft, or an
 // early exit): the next token is a draw from logits row lr; a speculative row that ran
 // with that very token is kept.
-__device__ void finish_untested(const ControllerArgs& a, SeqState& s, int b, int lr, bool s_ran) {
-  const int t = a.draw[lr * 2];
+__device__ __forceinline__ void finish_untested(const ControllerArgs& a, SeqState& s, int b, int lr, bool s_ran) {
+  const int t = ctl_lds.draw[lr * 2];
   if (is_stop(a, t)) {
     s.done = 1;
     return;
@@ -411,7 +424,7 @@ __device__ void finish_untested(const ControllerArgs& a, SeqState& s, int b, int
 }
 
 // Advance one sequence's state after the step whose rows it ran.
-__device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
+__device__ __forceinline__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
   const int P = a.n_pulses;
   s.ctr += 1;
   const int pulse_ran = s.c_pulse;
@@ -430,11 +443,11 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
     if (pulse_ran == 0 && a.speculative) {
       const int lr = s.lrow_c;
       if (s.c_kind == KIND_TESTED) {
-        s.d_tok = a.draw[lr * 2];
+        s.d_tok = ctl_lds.draw[lr * 2];
         s.s_valid = !is_stop(a, s.d_tok);
         s.s_tok = s.d_tok;
       } else {
-        const int g = a.argmax[lr];
+        const int g = ctl_lds.argmax[lr];
         s.s_valid = !is_stop(a, g);
         s.s_tok = g;
       }
@@ -445,7 +458,7 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
   const int lr = s.lrow_c;
   const bool s_ran = s.row_s >= 0;
   if (a.speculative && s.c_kind == KIND_TESTED) {
-    const int v = a.draw[lr * 2];
+    const int v = ctl_lds.draw[lr * 2];
     s.tests += 1;
     if (s.d_tok == v && !is_stop(a, s.d_tok)) {
       s.accepted += 1;
@@ -461,7 +474,7 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
         }
       }
     } else {
-      const int t = a.draw[lr * 2 + 1];
+      const int t = ctl_lds.draw[lr * 2 + 1];
       if (is_stop(a, t)) {
         s.done = 1;
       } else {
@@ -480,11 +493,11 @@ __device__ void update_seq(const ControllerArgs& a, SeqState& s, int b) {
 }
 
 // Global-layer KV pages for sequence b's positions up to hi, taken from the pool in order
-// of request; false (and the pool's spent flag set) when the pool cannot cover them.
-__device__ bool ensure_pages(const ControllerArgs& a, int b, int hi) {
+// of request; false (and the pool's spent flag set) when the pool cannot cover them. have:
+// the sequence's page count, read at the kernel's start.
+__device__ __forceinline__ bool ensure_pages(const ControllerArgs& a, int b, int hi, int have) {
   if (!a.page_table) return true;
   const int need = hi / kPage + 1;
-  const int have = a.page_count[b];
   if (have >= need) return true;
   const int n = need - have;
   const int first = take_pages(a.pool, n, a.pool_pages);
@@ -494,43 +507,79 @@ __device__ bool ensure_pages(const ControllerArgs& a, int b, int hi) {
   return true;
 }
 
-// Exclusive scan of N counters over the block (blockDim 256) in LDS.
+// Exclusive scan of N counters over the block (blockDim 256): wave prefix sums by lane
+// shifts, then the 4 wave totals through LDS (two barriers).
 template <int N>
 __device__ void scan_counts(int* v, int* sh, int* total) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int k = 0; k < N; ++k) sh[k * 256 + t] = v[k];
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
-    int add[N];
-#pragma unroll
-    for (int k = 0; k < N; ++k) add[k] = t >= off ? sh[k * 256 + t - off] : 0;
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < N; ++k) sh[k * 256 + t] += add[k];
-    __syncthreads();
-  }
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int inc[N];
 #pragma unroll
   for (int k = 0; k < N; ++k) {
-    total[k] = sh[k * 256 + 255];
-    v[k] = sh[k * 256 + t] - v[k];
+    int x = v[k];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    inc[k] = x;
+    if (lane == 63) sh[k * 4 + w] = x;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int wt = sh[k * 4 + i];
+      if (i < w) pre += wt;
+      tot += wt;
+    }
+    total[k] = tot;
+    v[k] = pre + inc[k] - v[k];
   }
   __syncthreads();
 }
 
+// NL loads of draws per thread (2 max_lrows <= 256 NL), issued before any store.
+template <int NL>
+__device__ void ctl_preload(const ControllerArgs& a) {
+  CtlShared& c = ctl_lds;
+  constexpr int NA = (NL + 1) / 2;
+  const int t = threadIdx.x;
+  const int nd = 2 * a.max_lrows, na = a.max_lrows;
+  int d[NL], m[NA];
+#pragma unroll
+  for (int k = 0; k < NL; ++k) d[k] = a.draw[min(t + 256 * k, nd - 1)];
+#pragma unroll
+  for (int k = 0; k < NA; ++k) m[k] = a.argmax[min(t + 256 * k, na - 1)];
+  const int st = a.stop_ids[min(t, 7)];
+#pragma unroll
+  for (int k = 0; k < NL; ++k)
+    if (t + 256 * k < nd) c.draw[t + 256 * k] = d[k];
+#pragma unroll
+  for (int k = 0; k < NA; ++k)
+    if (t + 256 * k < na) c.argmax[t + 256 * k] = m[k];
+  if (t < a.n_stop) c.stop[t] = st;
+}
+
+
 // One thread per sequence: advance the state, then lay out the next step's rows grouped by
 // pulse (sequence order within a pulse) and its logits rows. Also snapshots the rows and
 // control block of the step that just ran (readable for testing).
+template <int NL>
 __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
-  __shared__ int sh[5 * 256];
+  __shared__ int sh[5 * 4];
   const int b = threadIdx.x;
   StepCtl* ctl = a.ctl;
   const int P = a.n_pulses;
-  // the sequence's state is read with the snapshot of the last step's rows and control
-  // block (one round trip for both, before the barrier that retires the snapshot)
+  // the sequence's state and page count are read with the snapshot of the last step's rows
+  // and control block and the LDS copies (one round trip for all, before the barrier that
+  // retires the snapshot)
   const bool act = b < a.B;
   SeqState s{};
   if (act) s = a.state[b];
+  const int have = act && a.page_table ? a.page_count[b] : 0;
+  ctl_preload<NL>(a);
   const int n_prev = ctl->n_rows;
   for (int i = b; i < n_prev; i += blockDim.x) a.last_rows[i] = a.rows[i];
   if (b == 0) *a.last_ctl = *ctl;
@@ -545,7 +594,7 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
       // draws use counters 2 * ctr (+1 for the speculative row), so ctr starts at 1 and no
       // later draw reuses the first token's uniform
       s.ctr = 1;
-      const int t = a.draw[b * 2];
+      const int t = ctl_lds.draw[b * 2];
       if (is_stop(a, t) || s.max_new <= 0) {
         s.done = 1;
       } else {
@@ -559,7 +608,7 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
     // pages for the next step's positions: the current token's, and the speculative row's
     // one position later; a sequence the pool cannot serve stops here
     if (!s.done && !ensure_pages(a, b, s.c_pos + (a.speculative && s.c_pulse == P - 1 &&
-                                                  s.s_valid ? 1 : 0)))
+                                                  s.s_valid ? 1 : 0), have))
       s.done = 1;
   }
   // rows of the next step
@@ -646,7 +695,7 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-__device__ void new_round(const ControllerArgs& a, SeqState& s, int tok) {
+__device__ __forceinline__ void new_round(const ControllerArgs& a, SeqState& s, int tok) {
   // block row i keeps its token state in slot (blk_base + i) % S; the base steps back one
   // slot per round, so the row the previous round's last verify step ran one slot past its
   // block (slot base - 1) is this round's row 0
@@ -670,23 +719,23 @@ __device__ void new_round(const ControllerArgs& a, SeqState& s, int tok) {
 // the block's last row when a draft was drawn from the row before it, and none when a stop
 // id ended the block: the verify then starts at pulse 1, and the pipelined round's guess is
 // the stopping draft row's own penalised argmax.
-__device__ void enter_verify(const ControllerArgs& a, SeqState& s, bool last_ran, int lrow) {
+__device__ __forceinline__ void enter_verify(const ControllerArgs& a, SeqState& s, bool last_ran, int lrow) {
   s.blk_phase = 1;
   s.blk_step = 0;
   if (last_ran && a.n_pulses > 1) {
     s.blk_step = 1;
     if (block_pipelined(a.draft_len)) {
-      s.s_tok = a.argmax[lrow];
+      s.s_tok = ctl_lds.argmax[lrow];
       s.s_valid = !is_stop(a, s.s_tok);
     }
   }
 }
 
-__device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
+__device__ __forceinline__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
   const int P = a.n_pulses;
   if (s.blk_phase == 0) {
     const int j = s.blk_step;
-    const int d = a.draw[s.lrow_c * 2];
+    const int d = ctl_lds.draw[s.lrow_c * 2];
     if (is_stop(a, d)) {
       enter_verify(a, s, true, s.lrow_c);
       return;
@@ -703,7 +752,7 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
   if (s.blk_step < P - 1) {
     if (s.blk_step == 0 && s.lrow_s >= 0) {
       // guess of the next round's first token (pipelined rounds)
-      s.s_tok = a.argmax[s.lrow_s];
+      s.s_tok = ctl_lds.argmax[s.lrow_s];
       s.s_valid = !is_stop(a, s.s_tok);
     }
     s.blk_step += 1;
@@ -718,10 +767,10 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
 #pragma unroll
   for (int i = 0; i < kMaxBlock; ++i) {
     const int r = lr0 + min(i, n - 1);
-    dv[i] = a.draw[r * 2];
-    dw[i] = a.draw[r * 2 + 1];
+    dv[i] = ctl_lds.draw[r * 2];
+    dw[i] = ctl_lds.draw[r * 2 + 1];
   }
-  const int d_spec = a.draw[max(spec_lrow, 0) * 2];
+  const int d_spec = ctl_lds.draw[max(spec_lrow, 0) * 2];
   int acc = 0, nxt = -1;
 #pragma unroll
   for (int i = 0; i < kMaxBlock; ++i) {
@@ -766,16 +815,20 @@ __device__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
 
 }  // namespace
 
+template <int NL>
 __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a) {
-  __shared__ int sh[5 * 256];
+  __shared__ int sh[5 * 4];
   const int b = threadIdx.x;
   StepCtl* ctl = a.ctl;
   const int P = a.n_pulses;
-  // the sequence's state is read with the snapshot of the last step's rows and control
-  // block (one round trip for both, before the barrier that retires the snapshot)
+  // the sequence's state and page count are read with the snapshot of the last step's rows
+  // and control block and the LDS copies (one round trip for all, before the barrier that
+  // retires the snapshot)
   const bool act = b < a.B;
   SeqState s{};
   if (act) s = a.state[b];
+  const int have = act && a.page_table ? a.page_count[b] : 0;
+  ctl_preload<NL>(a);
   const int n_prev = ctl->n_rows;
   for (int i = b; i < n_prev; i += blockDim.x) a.last_rows[i] = a.rows[i];
   if (b == 0) *a.last_ctl = *ctl;
@@ -785,7 +838,7 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
       s = SeqState{};
       s.max_new = a.max_new;
       s.c_pos = a.prompt_len;
-      const int t = a.draw[b * 2];
+      const int t = ctl_lds.draw[b * 2];
       if (is_stop(a, t) || s.max_new <= 0) {
         s.done = 1;
       } else {
@@ -821,7 +874,7 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
     }
     pos0 = s.c_pos + slot0;
     // pages for the step's positions; a sequence the pool cannot serve stops here
-    if (!ensure_pages(a, b, spec ? s.c_pos + nrow : pos0 + nrow - 1)) {
+    if (!ensure_pages(a, b, spec ? s.c_pos + nrow : pos0 + nrow - 1, have)) {
       s.done = 1;
       live = false;
       nrow = lrows = 0;
@@ -975,15 +1028,28 @@ int launch_sample_rows(const float* logits, int n_rows, int V, int dtype, const 
   return launch_sample(a, dtype, n_rows, s);
 }
 
+template <int NL>
+void launch_controller_nl(const ControllerArgs& a, hipStream_t s) {
+  if (a.draft_len > 0)
+    controller_block_kernel<NL><<<1, 256, 0, s>>>(a);
+  else
+    controller_kernel<NL><<<1, 256, 0, s>>>(a);
+}
+
 int launch_controller(const ControllerArgs& a, hipStream_t s) {
   if (a.B > 256) return fail(PULSAR_ERR_UNSUPPORTED, "controller: at most 256 sequences");
-  if (a.draft_len > 0) {
-    if (a.draft_len >= kMaxBlock || a.n_pulses > 3 || !a.lrow_ctr)
-      return fail(PULSAR_ERR_INVALID, "controller: draft-block mode arguments");
-    controller_block_kernel<<<1, 256, 0, s>>>(a);
-  } else {
-    controller_kernel<<<1, 256, 0, s>>>(a);
-  }
+  if (a.max_lrows < a.B || a.max_lrows > kCtlMaxLrows)
+    return fail(PULSAR_ERR_INVALID, "controller: max_lrows must be in [B, 2048]");
+  if (a.n_stop < 0 || a.n_stop > 8) return fail(PULSAR_ERR_INVALID, "controller: n_stop");
+  if (a.draft_len > 0 && (a.draft_len >= kMaxBlock || a.n_pulses > 3 || !a.lrow_ctr))
+    return fail(PULSAR_ERR_INVALID, "controller: draft-block mode arguments");
+  // draws per thread of the LDS copy: 2 max_lrows over 256 threads
+  const int nl = (2 * a.max_lrows + 255) / 256;
+  if (nl <= 1) launch_controller_nl<1>(a, s);
+  else if (nl <= 2) launch_controller_nl<2>(a, s);
+  else if (nl <= 4) launch_controller_nl<4>(a, s);
+  else if (nl <= 8) launch_controller_nl<8>(a, s);
+  else launch_controller_nl<16>(a, s);
   PULSAR_LAUNCH_CHECK();
   return PULSAR_OK;
 }
