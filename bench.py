@@ -43,10 +43,10 @@ BLOCK_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_c2_draft4_b1
 # 2 residual add, 3 SwiGLU, 4 logits), for class averages over every template of a class
 CLASS_PREFIXES = {
     "attention": ("attn_decode_unit_kernel<",),
-    "routed_gate_up": ("gemm_bf16_kernel<3,", "gemm_bf16_lds_kernel<3,"),
-    "routed_down": ("gemm_bf16_kernel<0,", "gemm_bf16_lds_kernel<0,"),
-    "qkv_gate_gemm": ("gemm_bf16_kernel<1,", "gemm_bf16_lds_kernel<1,"),
-    "wo_gemm": ("gemm_bf16_kernel<2,", "gemm_bf16_lds_kernel<2,"),
+    "routed_gate_up": ("gemm_bf16_kernel<3,", "gemm_bf16_lds_kernel<3,", "gemm_bf16_mid_kernel<3,"),
+    "routed_down": ("gemm_bf16_kernel<0,", "gemm_bf16_lds_kernel<0,", "gemm_bf16_mid_kernel<0,"),
+    "qkv_gate_gemm": ("gemm_bf16_kernel<1,", "gemm_bf16_lds_kernel<1,", "gemm_bf16_mid_kernel<1,"),
+    "wo_gemm": ("gemm_bf16_kernel<2,", "gemm_bf16_lds_kernel<2,", "gemm_bf16_mid_kernel<2,"),
     "lm_head": ("gemm_bf16_kernel<4,", "gemm_bf16_lds_kernel<4,"),
     "router": ("norm_router_kernel<",),
     "moe_combine": ("moe_combine_rows_kernel<",),
