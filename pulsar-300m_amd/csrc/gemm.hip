@@ -605,16 +605,20 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
   const bf16* A = reinterpret_cast<const bf16*>(g.A);
   const bf16* W = reinterpret_cast<const bf16*>(g.W) + (int64_t)group * g.w_group_stride;
 
-  // staging: wave wv fills row tiles wv + 4 h (h < 2) and weight tiles wv + 4 h (h < 4);
-  // lane l of a row tile's load carries row 16 t + (l & 15), k chunk l >> 4
+  // staging: wave wv fills row tiles wv + 4 h (h < 2) and weight tiles wv + 4 h (h < 4).
+  // A row tile's 64 16-byte chunks sit in LDS as (row m, k chunk q) at slot
+  // 4 m + (q ^ (m >> 2 & 3)): the load's lane l carries row 16 t + (l >> 2), so 16 lanes
+  // fetch the 64 contiguous bytes of 4 rows, and the XOR puts the 16 rows of one k chunk
+  // that a fragment read takes on 16 different 16-byte bank groups
   const bf16* ga[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int r = (wv + 4 * h) * 16 + m16;
+    const int r = (wv + 4 * h) * 16 + (lane >> 2);
     const int i = min(r_wg + r, cnt - 1);
     const int e = entry_load<MODE>(g, group, i);
-    ga[h] = A + (int64_t)a_row_of<MODE>(g, group, e) * g.lda + kq * 8;
+    ga[h] = A + (int64_t)a_row_of<MODE>(g, group, e) * g.lda + ((lane & 3) ^ (lane >> 4 & 3)) * 8;
   }
+  const int aslot = m16 * 4 + (kq ^ (m16 >> 2 & 3));  // this lane's fragment chunk
   const bf16* gw[4];
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
@@ -659,7 +663,7 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
     if (kt + S - 1 < KT) fetch(kt + S - 1, buf == 0 ? S - 1 : buf - 1);
     bf16x8_t fa[4], fw[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = sA[buf][wr * 4 + i][lane];
+    for (int i = 0; i < 4; ++i) fa[i] = sA[buf][wr * 4 + i][aslot];
 #pragma unroll
     for (int j = 0; j < 8; ++j) fw[j] = sW[buf][wcol[j]][lane];
 #pragma unroll
