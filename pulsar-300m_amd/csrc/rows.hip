@@ -1274,7 +1274,9 @@ __global__ void __launch_bounds__(256 * (4 / NQ)) attn_prefill_mfma_kernel(AttnA
   const bool stager = threadIdx.x < 512;
   constexpr int kLd = 72;  // LDS row stride in bf16: 16 bytes of padding against bank conflicts
   __shared__ __attribute__((aligned(16))) __bf16 Ks[64][kLd];  // [key][dim]
-  __shared__ __attribute__((aligned(16))) __bf16 Vs[64][kLd];  // [dim][key]
+  // [dim][key slot]: within each 32-key half, lane kq's 8 keys of the second product (keys
+  // 4 kq .. 4 kq + 3 of both 16-key tiles) sit in slots 8 kq .. 8 kq + 7
+  __shared__ __attribute__((aligned(16))) __bf16 Vs[64][kLd];
   const int T_ = a.prefill_T;
   const int ntile = (T_ + 63) / 64;
   const int b = (int)blockIdx.x / ntile;
@@ -1340,7 +1342,14 @@ __global__ void __launch_bounds__(256 * (4 / NQ)) attn_prefill_mfma_kernel(AttnA
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         *reinterpret_cast<attn_bf16x8*>(&Ks[sr][sc16 + 8 * c]) = kr[c];
-        *reinterpret_cast<attn_bf16x8*>(&Vs[sr][sc16 + 8 * c]) = vr[c];
+        // keys k0 .. k0 + 7 of the block: the two 4-key halves go to the slots of lanes
+        // kq and kq + 1 of the same key-tile parity
+        const int k0 = sc16 + 8 * c, w0 = k0 & 31, kqa = (w0 >> 2) & 3;
+        bf16* vrow = reinterpret_cast<bf16*>(&Vs[sr][(k0 & 32) + (w0 >> 4) * 4]);
+        *reinterpret_cast<attn_bf16x4*>(vrow + kqa * 8) =
+            __builtin_shufflevector(vr[c], vr[c], 0, 1, 2, 3);
+        *reinterpret_cast<attn_bf16x4*>(vrow + (kqa + 1) * 8) =
+            __builtin_shufflevector(vr[c], vr[c], 4, 5, 6, 7);
       }
     }
     __syncthreads();
@@ -1398,9 +1407,7 @@ __global__ void __launch_bounds__(256 * (4 / NQ)) attn_prefill_mfma_kernel(AttnA
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const attn_bf16x4 lo4 = *reinterpret_cast<const attn_bf16x4*>(&Vs[mt * 16 + m16][ks * 32 + kq * 4]);
-        const attn_bf16x4 hi4 = *reinterpret_cast<const attn_bf16x4*>(&Vs[mt * 16 + m16][ks * 32 + 16 + kq * 4]);
-        const attn_bf16x8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+        const attn_bf16x8 av = *reinterpret_cast<const attn_bf16x8*>(&Vs[mt * 16 + m16][ks * 32 + kq * 8]);
 #pragma unroll
         for (int nt = 0; nt < NQ; ++nt)
           o[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[nt][ks], o[mt][nt], 0, 0, 0);
