@@ -1259,13 +1259,16 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
 // In this orientation P never leaves the registers: the D tile of S^T gives lane l keys
 // 4*(l/16) + j (j < 4) of query l % 16, and the B operand of the second product takes 8
 // keys of query l % 16 -- here the 4 keys of key tile 2s and the 4 of tile 2s + 1, a
-// permutation of the reduction index that the V^T operand (two 8-byte LDS reads) repeats.
+// permutation of the reduction index that the V^T operand repeats (V^T is staged with those
+// 8 keys in consecutive slots: one 16-byte LDS read per fragment).
 // Scores use exp2 with log2(e) folded into the scale; P is rounded to bf16 for the second
 // product, the running max, sum and output accumulate in fp32.
 // ---------------------------------------------------------------------------
 
+// At least 4 waves per SIMD (at most 128 registers per lane): with NQ = 2 two workgroups of
+// 8 waves share a CU, so one computes while the other waits at its barriers.
 template <int NQ>
-__global__ void __launch_bounds__(256 * (4 / NQ)) attn_prefill_mfma_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256 * (4 / NQ), 4) attn_prefill_mfma_kernel(AttnArgs a) {
   // NQ 16-query tiles per wave: the 64 queries of the block are split over 4 / NQ waves
   // per head, so the block has 4 heads x (4 / NQ) waves
   constexpr int kThreads = 256 * (4 / NQ);
@@ -2091,9 +2094,10 @@ int launch_attn_prefill(const AttnArgs& a, int dtype, int B, hipStream_t s) {
   if (a.H != 4 * a.Hkv)
     return fail(PULSAR_ERR_UNSUPPORTED, "prefill attention: four query heads per kv head");
   if (dtype == PULSAR_BF16) {
-    // one 16-query tile per wave: 16 waves of about 95 registers each hide the MFMA, LDS
-    // and exp latencies better than 4 waves of 4 tiles (measured 1.5x on 16 x 2048 tokens)
-    attn_prefill_mfma_kernel<1><<<dim3(B * ntile, a.Hkv), 1024, 0, s>>>(a);
+    // two 16-query tiles per wave: each K and V fragment read from LDS feeds two products
+    // (16 x 2048 tokens: 289 -> 260 us per launch against one tile per wave at 16 waves;
+    // 352 us with two tiles at 136 registers, where one workgroup fills a CU)
+    attn_prefill_mfma_kernel<2><<<dim3(B * ntile, a.Hkv), 512, 0, s>>>(a);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   }
