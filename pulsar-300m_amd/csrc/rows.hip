@@ -32,6 +32,19 @@ __device__ __forceinline__ void load8(const float* p, float* o) {
   o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
+__device__ __forceinline__ void store8(bf16* p, const float* v) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)f2bf(v[2 * i]).u |
+           ((uint32_t)f2bf(v[2 * i + 1]).u << 16);
+  *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+__device__ __forceinline__ void store8(float* p, const float* v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+
 // Row-wise sum of squares of a D-vector held by the block (256 threads).
 template <typename T>
 __device__ float row_inv_rms(const T* x, int D, float eps, float* red) {
@@ -399,8 +412,10 @@ __global__ void __launch_bounds__(256) qk_post_kernel(QKPostArgs a) {
     cs[i] = a.cos[(int64_t)rd[i].pos * 32 + j];
     sn[i] = a.sin[(int64_t)rd[i].pos * 32 + j];
   }
+  bool keep[RPW];  // row stored (exists and not before a prefill's window)
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
+    keep[i] = false;
     if (r0 + i >= n) break;
     const int r = r0 + i;
     const int pulse = rd[i].pulse, pos = rd[i].pos;
@@ -414,12 +429,32 @@ __global__ void __launch_bounds__(256) qk_post_kernel(QKPostArgs a) {
         vv = rnd<T>(rnd<T>(rnd<T>(1.0f - lv) * vv) + rnd<T>(lv * vf0[i]));
       }
     }
+    v[i] = vv;
     const float k = norm_rope(x[i], a.k_norm + ((int64_t)pulse * Hk + g) * 64, cs[i], sn[i]);
     if (a.prefill && a.is_local && pos < a.prefill_T - a.window) continue;
+    keep[i] = true;
     reinterpret_cast<T*>(a.kv.k[a.layer])[kv_offset(a.kv, a.layer, rd[i].seq, g, pos) + lane] =
         from_f<T>(k);
-    reinterpret_cast<T*>(a.kv.v[a.layer])[kv_offset_v(a.kv, a.layer, rd[i].seq, g, pos, lane)] =
-        from_f<T>(vv);
+  }
+  // V is stored dimension-major: 8 stored rows of one sequence at consecutive positions from
+  // a multiple of 8 are 8 adjacent elements of the lane's dimension row, written as one
+  // vector; other row sets go element by element
+  T* Vc = reinterpret_cast<T*>(a.kv.v[a.layer]);
+  bool vec = RPW % 8 == 0 && (rd[0].pos & 7) == 0 &&
+             (!kv_is_local(a.kv, a.layer) || (a.kv.lcap & 7) == 0);
+#pragma unroll
+  for (int i = 0; i < (RPW % 8 == 0 ? 8 : 0); ++i)
+    vec = vec && keep[i] && rd[i].seq == rd[0].seq && rd[i].pos == rd[0].pos + i;
+  if (vec) {
+    T* vp = Vc + kv_offset_v(a.kv, a.layer, rd[0].seq, g, rd[0].pos, lane);
+    store8(vp, v);
+#pragma unroll
+    for (int i = 8; i < RPW; ++i)
+      if (keep[i]) Vc[kv_offset_v(a.kv, a.layer, rd[i].seq, g, rd[i].pos, lane)] = from_f<T>(v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+      if (keep[i]) Vc[kv_offset_v(a.kv, a.layer, rd[i].seq, g, rd[i].pos, lane)] = from_f<T>(v[i]);
   }
 }
 
@@ -1986,7 +2021,7 @@ int launch_pulse_input(const PulseInputArgs& a, int dtype, int max_rows, hipStre
 // Row sets of this many rows or more (prefill) take several rows per block / wave.
 constexpr int kManyRows = 1024;
 constexpr int kNormRowsPerBlock = 8;
-constexpr int kPostRowsPerWave = 2;
+constexpr int kPostRowsPerWave = 8;
 
 template <typename T, int RPB>
 void launch_norm_rows_t(const NormArgs& a, int max_rows, hipStream_t s) {
