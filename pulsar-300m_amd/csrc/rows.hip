@@ -346,10 +346,12 @@ __global__ void __launch_bounds__(256) norm_rows_kernel(NormArgs a) {
 // QK-norm + RoPE (+YaRN) on q heads, value residual + K-norm + RoPE on kv heads and the
 // cache write. One wave per head vector (lane = element, rotate-half partner = lane^32);
 // a wave takes head hh of RPW consecutive rows, their loads issued before the first
-// reduction (prefill: 2 rows, 117 -> 104 us per launch at 16 x 2048 tokens; 4 rows 106, 8
-// rows 112; decode: 1). The value cache is dimension-major, so each lane's value store
-// lands in its own line. Prefill and fp32 decode; bf16 decode does the same arithmetic
-// inside attn_decode_unit_kernel.
+// reduction (prefill: 8 rows; decode: 1). The value cache is dimension-major: 8 rows of one
+// sequence at consecutive positions from a multiple of 8 leave each lane 8 adjacent values
+// of its dimension row, stored as one vector (16 x 2048 tokens: 117 us per launch with one
+// row per wave and element stores, 104 with 2 rows, 95 with 8 rows and vector stores).
+// Prefill and fp32 decode; bf16 decode does the same arithmetic inside
+// attn_decode_unit_kernel.
 // ---------------------------------------------------------------------------
 template <typename T, int RPW>
 __global__ void __launch_bounds__(256) qk_post_kernel(QKPostArgs a) {
