@@ -889,7 +889,12 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
   const int s_lo = base + s * SPLIT;
   const int s_hi = min(uhi, s_lo + SPLIT - 1);
   constexpr int kStride = kUnitWaves * 64;
-  const int kb0 = s_lo + wv * 64;
+  // the wave's first block: blocks wholly before the unit's first key (sliding-window
+  // layers: the first row's window start) are masked for every row and would leave the
+  // wave's running max, sum and output at their initial values, so the wave skips them
+  const int lo_blk = (a.is_local ? max(0, un.pos0 - a.window + 1) : 0) & ~63;
+  const int kbw = s_lo + wv * 64;
+  const int kb0 = kbw + (lo_blk > kbw ? (lo_blk - kbw + kStride - 1) / kStride * kStride : 0);
   // Post-processing of the step's projections (what qk_post_kernel does, fused): every split
   // finishes the unit's query columns (wave per column, lane = dimension: RMSNorm over the
   // head, RoPE, YaRN query scale); the split whose keys hold a unit row's own position
