@@ -261,10 +261,79 @@ struct PulseOutputArgs {
   void* xn_final;         // [lrows][D]
 };
 
-// Shared top-k routine of the two router kernels (single thread).
+// route_topk for compile-time E and K: every loop unrolled and every array index a
+// constant, so the arrays stay in registers (with runtime bounds the selected experts'
+// scores are read with lane-dependent indices). The same operations in the same order as
+// the generic form below, so the results are identical.
+template <typename T, int E, int K>
+__device__ __forceinline__ void route_topk_fixed(const float* lg, const float* bias, int r,
+                                                 const RouterArgs& a) {
+  float sum = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) sum += lg[e];
+  const float mean = sum / (float)E;
+  float s[E], b[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float c = lg[e] - mean;
+    s[e] = 1.0f / (1.0f + expf(-c));
+    b[e] = s[e] + bias[e];
+  }
+  // sorted (descending) selection with its experts' scores; the initial entries name
+  // expert 0, as the generic form's do
+  int bi[K];
+  float bv[K], bs[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    bi[k] = 0;
+    bv[k] = -INFINITY;
+    bs[k] = s[0];
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float v = b[e];
+    if (v > bv[K - 1]) {
+      int p = K - 1;
+#pragma unroll
+      for (int q = K - 1; q > 0; --q)
+        if (p == q && v > bv[q - 1]) {
+          bv[q] = bv[q - 1];
+          bi[q] = bi[q - 1];
+          bs[q] = bs[q - 1];
+          p = q - 1;
+        }
+#pragma unroll
+      for (int q = 0; q < K; ++q)
+        if (p == q) {
+          bv[q] = v;
+          bi[q] = e;
+          bs[q] = s[e];
+        }
+    }
+  }
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) tot += bs[k];
+  tot += 1e-6f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    a.topk_idx[(int64_t)r * K + k] = bi[k];
+    a.topk_w[(int64_t)r * K + k] = rnd<T>(bs[k] / tot);
+    if (a.lists) {
+      const int p = atomicAdd(&a.list_count[bi[k]], 1);
+      a.lists[(int64_t)bi[k] * a.list_stride + p] = r * K + k;
+    }
+  }
+}
+
+// Shared top-k routine of the router kernels (single thread).
 template <typename T>
 __device__ __forceinline__ void route_topk(const float* lg, int E, int K, const float* bias, int r,
                                            const RouterArgs& a) {
+  if (E == 16 && K == 4) {
+    route_topk_fixed<T, 16, 4>(lg, bias, r, a);
+    return;
+  }
   float sum = 0.f;
   for (int e = 0; e < E; ++e) sum += lg[e];
   const float mean = sum / (float)E;
