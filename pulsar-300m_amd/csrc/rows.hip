@@ -1667,10 +1667,12 @@ __global__ void __launch_bounds__(256) router_prefill_mfma_kernel(RouterArgs a) 
 // ---------------------------------------------------------------------------
 // One block per (sequence, expert). A first pass counts the sequence's assignments to the
 // expert and stages up to kCapStage of them in LDS (loads batched ahead of their tests, one
-// LDS atomic per wave; prefill of 16 x 2048 tokens: 97 -> 84 us per launch). Under capacity every one is kept; over
-// capacity each is ranked against the others by (key asc, flat index asc), in LDS when
-// staged, else against the sequence's assignments in memory. The block then reserves its
-// kept count in the expert's list with one atomic and writes its entries there.
+// LDS atomic per wave; prefill of 16 x 2048 tokens: 97 -> 84 us per launch). Under
+// capacity every one is kept; over capacity the C first in (key asc, flat index asc) order
+// are: the C-th smallest key found by bisection over the keys' ordered bits, in LDS when
+// staged, else over the sequence's assignments in memory, and the assignments on that key
+// ranked by flat index. The block then reserves its kept count in the expert's list with
+// one atomic and writes its entries there.
 __device__ int block_excl_scan_int(int v, int* scratch, int* total) {
   const int tid = threadIdx.x, nt = blockDim.x;
   __syncthreads();  // previous users of the scratch are done
@@ -1697,13 +1699,26 @@ __device__ int block_sum_int(int v, int* scratch) {
   block_excl_scan_int(v, scratch, &tot);
   return tot;
 }
+// Sum of one small count per thread over a block of 256 threads (exact: counts stay far
+// below 2^24); every thread returns the same total.
+__device__ __forceinline__ int block_count(int v, float* red4) {
+  const float f = wave_sum((float)v);
+  __syncthreads();  // the previous call's readers are done
+  if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = f;
+  __syncthreads();
+  return (int)(red4[0] + red4[1] + red4[2] + red4[3]);
+}
 constexpr int kCapStage = 4096;
+constexpr int kTieBits = 32768;  // flat indices of a sequence's assignments the tie bitmap holds
 __global__ void __launch_bounds__(256) prefill_select_kernel(
     const int32_t* __restrict__ idx, const float* __restrict__ w, int32_t* __restrict__ keep,
     int32_t* __restrict__ lists, int32_t* __restrict__ lcount, int64_t list_stride, int T_, int K,
     int E, int C) {
   __shared__ int s_n, s_base;
   __shared__ int s_off[256];
+  __shared__ float s_red[4];
+  __shared__ uint32_t tbits[kTieBits / 32];  // assignments on the threshold key, by flat index
+  __shared__ int tpre[kTieBits / 32];        // set bits in the words before each word
   __shared__ int sidx[kCapStage];
   __shared__ float skey[kCapStage];
   __shared__ uint8_t skept[kCapStage];
@@ -1754,17 +1769,77 @@ __global__ void __launch_bounds__(256) prefill_select_kernel(
   const bool staged = n <= kCapStage;
   int mine = 0;
   if (staged) {
+    // Over capacity, an assignment is kept when fewer than C others precede it in (key,
+    // flat index) order: the C-th smallest key uc by bisection over the staged keys' ordered
+    // bits (one counting pass per step), then keys below uc are kept, keys above dropped,
+    // and those on uc ranked by flat index among themselves. The keys are e - 0.5 w/(1+w)
+    // with w >= 0 (never -0 or NaN), so the ordered bits compare as the floats do.
+    uint32_t uc = 0xffffffffu;
+    int below = 0;
+    bool tie_bits = false, lone_tie = false;
+    if (n > C) {
+      uint32_t lo = 0u, hi = 0xffffffffu;
+      while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        int c = 0;
+        for (int q = tid; q < n; q += nt) c += ordered_bits(skey[q]) <= mid ? 1 : 0;
+        if (block_count(c, s_red) >= C)
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      uc = lo;
+      int c = 0, ct = 0;
+      for (int q = tid; q < n; q += nt) {
+        const uint32_t uk = ordered_bits(skey[q]);
+        c += uk < uc ? 1 : 0;
+        ct += uk == uc ? 1 : 0;
+      }
+      below = block_count(c, s_red);
+      // the assignments on uc as a bitmap of flat indices with per-word prefix counts, so
+      // each one's rank among them is one lookup (saturated routing scores make ties
+      // common; ranking each against every staged key was up to 150 us per launch)
+      const int nties = block_count(ct, s_red);  // at least one: uc is a staged key
+      lone_tie = nties == 1;
+      tie_bits = nties > 1 && per <= kTieBits;
+      if (tie_bits) {
+        const int nw = (int)((per + 31) / 32);
+        for (int w = tid; w < nw; w += nt) tbits[w] = 0u;
+        __syncthreads();
+        for (int q = tid; q < n; q += nt)
+          if (ordered_bits(skey[q]) == uc) atomicOr(&tbits[sidx[q] >> 5], 1u << (sidx[q] & 31));
+        __syncthreads();
+        const int wpt = (nw + nt - 1) / nt, w0 = tid * wpt, w1 = min(nw, w0 + wpt);
+        int cnt = 0;
+        for (int w = w0; w < w1; ++w) cnt += __popc(tbits[w]);
+        int tot_ties;
+        int run = block_excl_scan_int(cnt, s_off, &tot_ties);
+        for (int w = w0; w < w1; ++w) {
+          tpre[w] = run;
+          run += __popc(tbits[w]);
+        }
+        __syncthreads();
+      }
+    }
     for (int q = tid; q < n; q += nt) {
       bool kept = true;
       if (n > C) {
-        const int iq = sidx[q];
-        const float kq = skey[q];
-        int rank = 0;
-        for (int u = 0; u < n; ++u) {
-          const float ku = skey[u];
-          rank += (ku < kq || (ku == kq && sidx[u] < iq)) ? 1 : 0;
+        const uint32_t uk = ordered_bits(skey[q]);
+        if (uk == uc) {
+          const int iq = sidx[q];
+          int ties = 0;
+          if (lone_tie) {
+            ties = 0;
+          } else if (tie_bits) {
+            ties = tpre[iq >> 5] + __popc(tbits[iq >> 5] & ((1u << (iq & 31)) - 1u));
+          } else {
+            for (int u = 0; u < n; ++u)
+              ties += (ordered_bits(skey[u]) == uc && sidx[u] < iq) ? 1 : 0;
+          }
+          kept = below + ties < C;
+        } else {
+          kept = uk < uc;
         }
-        kept = rank < C;
       }
       keep[s0 + sidx[q]] = kept ? 1 : 0;
       skept[q] = kept ? 1 : 0;

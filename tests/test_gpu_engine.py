@@ -216,6 +216,40 @@ def test_prefill_capacity_drops_match_oracle(full_state, dtype, tol):
     eng.close()
 
 
+@pytest.mark.parametrize("T_", [200, 1100])
+def test_prefill_capacity_ties_rank_by_flat_index(full_state, T_):
+    """Zero router weights give every token the same sigmoid scores, and the expert biases
+    send all of them to experts 0-3 with equal routing weights: every assignment of an
+    expert sits on one key, so the kept set is the first C assignments in flat-index order
+    (C = 64 of 200 and 352 of 1100 per expert). fp32 prefill logits against the oracle."""
+    from oracle import pulsar_ref as R
+    from pulsar_engine import weights as W
+    from pulsar_engine.engine import HipEngine
+    from pulsar_engine.model import DeviceModel
+
+    cfg, st = full_state
+    bias = np.zeros(cfg.n_routed_experts, np.float32)
+    bias[:4] = 1.0
+    st2 = dict(st)
+    for i in range(cfg.n_core):
+        st2[f"core.{i}.mlp.expert_bias"] = np.tile(bias, (cfg.max_pulses, 1))
+        st2[f"core.{i}.mlp.router_weight"] = np.zeros_like(st[f"core.{i}.mlp.router_weight"])
+    C = R.moe_capacity(T_, cfg)
+    assert C < T_
+    prompt = W.uniform_ids(90, "tie_prompt", T_, cfg.vocab_size)
+    model = DeviceModel(cfg, st2, torch.float32)
+    eng = HipEngine(model, batch=1, max_prompt=T_, max_new=4, speculative=False,
+                    temperature=0.0, repetition_penalty=1.0, stop_ids=[])
+    eng.prefill(prompt[None])
+    got = eng.logits(1)[0]
+    ref_eng = R.load_ref(cfg, st2, torch.float32, rope_tables_fp32=True, stop_ids=set())
+    ref = ref_eng.prefill(torch.as_tensor(prompt).view(1, -1), R.RefKVCache(cfg))
+    err = max_abs_rel(got, ref.float().numpy().reshape(-1))
+    print(f"capacity ties T={T_} C={C}: {err:.3e}")
+    assert err <= 1e-4
+    eng.close()
+
+
 @pytest.mark.parametrize("draft_len", [0, 4])
 def test_multi_step_graphs_equal_single_steps_and_eager(models, full_state, draft_len):
     """Runs of steps launch four steps per graph: the same sampled decode stepped one graph
