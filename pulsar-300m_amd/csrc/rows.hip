@@ -1623,34 +1623,49 @@ __global__ void __launch_bounds__(256) router_prefill_kernel(RouterArgs a) {
 
 // Prefill router in bf16 on the matrix cores: logits[rows][E] = X . bf16(W)^T with fp32
 // accumulation, E <= 16 experts as the 16 columns of one v_mfma_f32_16x16x32_bf16 tile;
-// a wave owns 16 rows. The logits, rounded to bf16, go through LDS to the shared top-k
+// a wave owns 16 rows, a workgroup of 8 waves converts the weights into LDS once for its
+// 128 rows (16 x 2048 tokens: 28.1 -> 21.4 us per launch against every wave loading and
+// converting them itself). The logits, rounded to bf16, go through LDS to the shared top-k
 // routine (one lane per row), so routing is the same as router_prefill_kernel's.
-__global__ void __launch_bounds__(256) router_prefill_mfma_kernel(RouterArgs a) {
-  __shared__ float lg[4][16][17];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+constexpr int kRouterWaves = 8;     // 16-row tiles per workgroup
+constexpr int kRouterMaxD = 1024;   // model widths the staged weights cover
+__global__ void __launch_bounds__(64 * kRouterWaves) router_prefill_mfma_kernel(RouterArgs a) {
+  // the pulse's weights, rounded to bf16 once per workgroup, in B-operand order: k step t,
+  // lane (expert m16, k chunk kq) -> W[m16][32 t + 8 kq .. + 7] (zero for m16 >= E)
+  __shared__ attn_bf16x8 sw[kRouterMaxD / 32][64];
+  __shared__ float lg[kRouterWaves][16][17];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int m16 = lane & 15, kq = lane >> 4;
-  const int r0 = ((int)blockIdx.x * 4 + wv) * 16;
-  const int D = a.D, E = a.E;
+  const int r0 = ((int)blockIdx.x * kRouterWaves + wv) * 16;
+  const int D = a.D, E = a.E, KS = D / 32;
   const bf16* xp = reinterpret_cast<const bf16*>(a.x) +
                    (int64_t)min(r0 + m16, a.m_fixed - 1) * D + kq * 8;
-  const bool ev = m16 < E;
-  const float* wp = a.w + ((int64_t)a.pulse * E + (ev ? m16 : 0)) * D + kq * 8;
-  attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const attn_bf16x8 zero = {};
-  for (int k = 0; k < D; k += 256) {
-    attn_bf16x8 xa[8], wb[8];
+  // the first rows' loads go out ahead of the weight staging
+  attn_bf16x8 xa[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      xa[u] = *reinterpret_cast<const attn_bf16x8*>(xp + k + 32 * u);
-      const float4 w0 = *reinterpret_cast<const float4*>(wp + k + 32 * u);
-      const float4 w1 = *reinterpret_cast<const float4*>(wp + k + 32 * u + 4);
-      attn_bf16x8 t;
-      t[0] = (__bf16)w0.x; t[1] = (__bf16)w0.y; t[2] = (__bf16)w0.z; t[3] = (__bf16)w0.w;
-      t[4] = (__bf16)w1.x; t[5] = (__bf16)w1.y; t[6] = (__bf16)w1.z; t[7] = (__bf16)w1.w;
-      wb[u] = ev ? t : zero;
+  for (int u = 0; u < 8; ++u) xa[u] = *reinterpret_cast<const attn_bf16x8*>(xp + 32 * u);
+  const float* wbase = a.w + (int64_t)a.pulse * E * D;
+  for (int f = tid; f < KS * 64; f += 64 * kRouterWaves) {
+    const int t = f >> 6, l = f & 63, ex = l & 15;
+    const float* src = wbase + (int64_t)min(ex, E - 1) * D + t * 32 + (l >> 4) * 8;
+    const float4 w0 = *reinterpret_cast<const float4*>(src);
+    const float4 w1 = *reinterpret_cast<const float4*>(src + 4);
+    attn_bf16x8 v;
+    v[0] = (__bf16)w0.x; v[1] = (__bf16)w0.y; v[2] = (__bf16)w0.z; v[3] = (__bf16)w0.w;
+    v[4] = (__bf16)w1.x; v[5] = (__bf16)w1.y; v[6] = (__bf16)w1.z; v[7] = (__bf16)w1.w;
+    sw[t][l] = ex < E ? v : zero;
+  }
+  __syncthreads();
+  attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < D; k += 256) {
+    if (k > 0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) xa[u] = *reinterpret_cast<const attn_bf16x8*>(xp + k + 32 * u);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[u], wb[u], acc, 0, 0, 0);
+    for (int u = 0; u < 8; ++u)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[u], sw[(k >> 5) + u][lane], acc, 0, 0, 0);
   }
   // lane holds the logits of rows 4 kq + j for expert m16
 #pragma unroll
@@ -2250,8 +2265,10 @@ int launch_norm_router(const RouterArgs& a, int dtype, int max_rows, hipStream_t
 }
 int launch_router_prefill(const RouterArgs& a, int dtype, hipStream_t s) {
   if (a.E > 32) return fail(PULSAR_ERR_UNSUPPORTED, "router: at most 32 experts");
-  if (dtype == PULSAR_BF16 && a.E <= 16 && a.D % 256 == 0) {
-    router_prefill_mfma_kernel<<<dim3((unsigned)((a.m_fixed + 63) / 64)), 256, 0, s>>>(a);
+  if (dtype == PULSAR_BF16 && a.E <= 16 && a.D % 256 == 0 && a.D <= kRouterMaxD) {
+    const int rows = 16 * kRouterWaves;
+    router_prefill_mfma_kernel<<<dim3((unsigned)((a.m_fixed + rows - 1) / rows)), 64 * kRouterWaves,
+                                 0, s>>>(a);
     PULSAR_LAUNCH_CHECK();
     return PULSAR_OK;
   }
