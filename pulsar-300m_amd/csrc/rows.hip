@@ -297,19 +297,22 @@ __global__ void __launch_bounds__(256) norm_rows_kernel(NormArgs a) {
   const int r0 = blockIdx.x * RPB;
   if (r0 >= n) return;
   const int D = a.D, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  float xv[RPB][EPT], inv[RPB];
-  const float* w[RPB];
+  float xv[RPB][EPT], wt[RPB][EPT], inv[RPB];
   // loads branch-free (a load on one side of a branch makes the join wait for every load
-  // in flight): elements past D read element D - 1 and count as zero
+  // in flight): elements past D read element D - 1 and count as zero; the norm weights go
+  // out with the rows, ahead of the reduction
 #pragma unroll
   for (int j = 0; j < RPB; ++j) {
     const int r = min(r0 + j, n - 1);  // rows past n recompute the last row, never stored
     const int src = a.use_lrows ? a.lrow_src[r] : r;
     const int pulse = a.use_lrows ? 0 : a.rows[r].pulse;
     const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)src * a.ldx;
-    w[j] = a.w + (int64_t)pulse * a.w_pulse_stride;
+    const float* w = a.w + (int64_t)pulse * a.w_pulse_stride;
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) xv[j][k] = ld(x, min(t + 256 * k, D - 1));
+    for (int k = 0; k < EPT; ++k) {
+      xv[j][k] = ld(x, min(t + 256 * k, D - 1));
+      wt[j][k] = w[min(t + 256 * k, D - 1)];
+    }
   }
 #pragma unroll
   for (int j = 0; j < RPB; ++j) {
@@ -337,7 +340,7 @@ __global__ void __launch_bounds__(256) norm_rows_kernel(NormArgs a) {
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
       const int i = t + 256 * k;
-      if (i < D) y[i] = from_f<T>(w[j][i] * (xv[j][k] * inv[j]));
+      if (i < D) y[i] = from_f<T>(wt[j][k] * (xv[j][k] * inv[j]));
     }
   }
 }
