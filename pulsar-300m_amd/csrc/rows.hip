@@ -284,10 +284,11 @@ __global__ void prefill_conv_kernel(const T* __restrict__ a, const float* __rest
 // RMSNorm of step rows with per-pulse weights: out[r] = T(w[pulse] * (x * inv)).
 // A block of 256 threads normalises RPB rows; thread t holds elements t, t + 256, ... of
 // each (D <= 256 EPT), summed in that order, then the wave sums and the 4 wave partials in
-// wave order: each row's arithmetic is the same for every RPB. Every load of the block is
-// issued before the first reduction: with the loads behind a per-element bounds branch
-// each one waited for the last (prefill of 16 x 2048 tokens: 59.6 -> 38.8 us per launch;
-// 8 rows per block or 1 measured alike). Prefill takes 8 rows per block, decode steps and
+// wave order: each row's arithmetic is the same for every RPB. Every load of the block,
+// the norm weights included, is issued before the first reduction: with the loads behind a
+// per-element bounds branch each one waited for the last (prefill of 16 x 2048 tokens:
+// 59.6 -> 38.8 us per launch; the weights loaded up front 39.4 -> 35.7 us at 8 rows per
+// block, 27.7 us at 4, 28.9 us at 2). Prefill takes 4 rows per block, decode steps and
 // logits rows one.
 // ---------------------------------------------------------------------------
 template <typename T, int RPB, int EPT>
@@ -2120,7 +2121,7 @@ int launch_pulse_input(const PulseInputArgs& a, int dtype, int max_rows, hipStre
 }
 // Row sets of this many rows or more (prefill) take several rows per block / wave.
 constexpr int kManyRows = 1024;
-constexpr int kNormRowsPerBlock = 8;
+constexpr int kNormRowsPerBlock = 4;
 constexpr int kPostRowsPerWave = 8;
 
 template <typename T, int RPB>
