@@ -566,6 +566,28 @@ __device__ void ctl_preload(const ControllerArgs& a) {
 // One thread per sequence: advance the state, then lay out the next step's rows grouped by
 // pulse (sequence order within a pulse) and its logits rows. Also snapshots the rows and
 // control block of the step that just ran (readable for testing).
+// The sequence state moves between memory and registers as 16-byte words at constant
+// offsets: a struct copy leaves the fields a kernel never names in scratch memory.
+static_assert(sizeof(SeqState) % 16 == 0 && alignof(SeqState) <= 16, "SeqState words");
+__device__ __forceinline__ void state_load(SeqState& s, const SeqState* p) {
+  constexpr int W = (int)(sizeof(SeqState) / 16);
+  int4 v[W];
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    v[k] = reinterpret_cast<const int4*>(p)[k];
+    // the words pass through registers (no memory-to-memory copy of the fields this
+    // kernel never names)
+    asm volatile("" : "+v"(v[k].x), "+v"(v[k].y), "+v"(v[k].z), "+v"(v[k].w));
+  }
+#pragma unroll
+  for (int k = 0; k < W; ++k) reinterpret_cast<int4*>(&s)[k] = v[k];
+}
+__device__ __forceinline__ void state_store(SeqState* p, const SeqState& s) {
+  constexpr int W = (int)(sizeof(SeqState) / 16);
+#pragma unroll
+  for (int k = 0; k < W; ++k) reinterpret_cast<int4*>(p)[k] = reinterpret_cast<const int4*>(&s)[k];
+}
+
 template <int NL>
 __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
   __shared__ int sh[5 * 4];
@@ -576,8 +598,8 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
   // and control block and the LDS copies (one round trip for all, before the barrier that
   // retires the snapshot)
   const bool act = b < a.B;
-  SeqState s{};
-  if (act) s = a.state[b];
+  alignas(16) SeqState s{};
+  if (act) state_load(s, a.state + b);
   const int have = act && a.page_table ? a.page_count[b] : 0;
   ctl_preload<NL>(a);
   const int n_prev = ctl->n_rows;
@@ -657,7 +679,7 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
     for (int i = 2; i < kMaxBlock; ++i) un.row[i] = -1;
     a.units[v[4]] = un;
   }
-  if (act) a.state[b] = s;
+  if (act) state_store(a.state + b, s);
   if (b == 0) {
     for (int p = 0; p < 4; ++p) {
       ctl->pulse_start[p] = p < 3 ? base[p] : total[0] + total[1] + total[2];
@@ -695,14 +717,22 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-__device__ __forceinline__ void new_round(const ControllerArgs& a, SeqState& s, int tok) {
+// The block tokens while the controller works on them: a vector value, whose elements at
+// run-time indices are register selects. (Indexed at run time inside the state struct,
+// they kept the whole struct in scratch memory: 176 bytes per lane.) The struct's copy is
+// read and written only at constant offsets, at the kernel's start and end.
+typedef int32_t BlkVec __attribute__((ext_vector_type(kMaxBlock)));
+static_assert(kMaxBlock == 8, "BlkVec holds the block tokens");
+
+__device__ __forceinline__ void new_round(const ControllerArgs& a, SeqState& s, BlkVec& bk,
+                                          int tok) {
   // block row i keeps its token state in slot (blk_base + i) % S; the base steps back one
   // slot per round, so the row the previous round's last verify step ran one slot past its
   // block (slot base - 1) is this round's row 0
   const int S = engine_slots(a.draft_len);
   s.blk_base = (s.blk_base + S - 1) % S;
-  s.blk[0] = tok;
-  for (int i = 1; i < kMaxBlock; ++i) s.blk[i] = -1;
+#pragma unroll
+  for (int i = 0; i < kMaxBlock; ++i) bk[i] = i == 0 ? tok : -1;
   s.blk_n = 1;
   s.ctr += 1;
   s.s_valid = 0;
@@ -731,7 +761,8 @@ __device__ __forceinline__ void enter_verify(const ControllerArgs& a, SeqState& 
   }
 }
 
-__device__ __forceinline__ void update_block(const ControllerArgs& a, SeqState& s, int b) {
+__device__ __forceinline__ void update_block(const ControllerArgs& a, SeqState& s, BlkVec& bk,
+                                             int b) {
   const int P = a.n_pulses;
   if (s.blk_phase == 0) {
     const int j = s.blk_step;
@@ -740,7 +771,7 @@ __device__ __forceinline__ void update_block(const ControllerArgs& a, SeqState& 
       enter_verify(a, s, true, s.lrow_c);
       return;
     }
-    s.blk[j + 1] = d;
+    bk[j + 1] = d;
     s.blk_n = j + 2;
     if (j + 1 >= s.blk_g) {
       enter_verify(a, s, false, -1);
@@ -778,7 +809,7 @@ __device__ __forceinline__ void update_block(const ControllerArgs& a, SeqState& 
     if (i < n - 1) {
       const int v = dv[i];
       s.tests += 1;
-      if (v == s.blk[i + 1] && !is_stop(a, v)) {
+      if (v == bk[i + 1] && !is_stop(a, v)) {
         s.accepted += 1;
         emit(a, s, b, v, 1);
         acc = i + 1;
@@ -798,14 +829,14 @@ __device__ __forceinline__ void update_block(const ControllerArgs& a, SeqState& 
   }
   emit(a, s, b, nxt);
   if (s.done) return;
-  new_round(a, s, nxt);
+  new_round(a, s, bk, nxt);
   if (spec_ran && acc == n - 1 && nxt == guess && s.blk_phase == 0) {
     // the speculative row was this round's first draft step
     const int d = d_spec;
     if (is_stop(a, d)) {
       enter_verify(a, s, true, spec_lrow);
     } else {
-      s.blk[1] = d;
+      bk[1] = d;
       s.blk_n = 2;
       if (s.blk_g <= 1) enter_verify(a, s, false, -1);
       else s.blk_step = 1;
@@ -825,8 +856,11 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
   // and control block and the LDS copies (one round trip for all, before the barrier that
   // retires the snapshot)
   const bool act = b < a.B;
-  SeqState s{};
-  if (act) s = a.state[b];
+  alignas(16) SeqState s{};
+  if (act) state_load(s, a.state + b);
+  BlkVec bk;
+#pragma unroll
+  for (int i = 0; i < kMaxBlock; ++i) bk[i] = s.blk[i];
   const int have = act && a.page_table ? a.page_count[b] : 0;
   ctl_preload<NL>(a);
   const int n_prev = ctl->n_rows;
@@ -836,6 +870,7 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
   if (act) {
     if (a.init) {
       s = SeqState{};
+      bk = 0;
       s.max_new = a.max_new;
       s.c_pos = a.prompt_len;
       const int t = ctl_lds.draw[b * 2];
@@ -843,10 +878,10 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
         s.done = 1;
       } else {
         emit(a, s, b, t);
-        if (!s.done) new_round(a, s, t);
+        if (!s.done) new_round(a, s, bk, t);
       }
     } else if (!s.done) {
-      update_block(a, s, b);
+      update_block(a, s, bk, b);
     }
   }
   bool live = act && !s.done;
@@ -882,7 +917,9 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
     }
   }
   int v[5] = {0, 0, 0, 0, 0};  // rows of pulse 0, 1, 2; logits rows; attention units
-  v[pulse] = nrow;
+  v[0] = pulse == 0 ? nrow : 0;
+  v[1] = pulse == 1 ? nrow : 0;
+  v[2] = pulse == 2 ? nrow : 0;
   if (spec) v[0] += 1;
   v[3] = lrows + (spec ? 1 : 0);
   v[4] = live ? 1 : 0;
@@ -891,7 +928,7 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
   const int base[3] = {0, total[0], total[0] + total[1]};
   s.row_c = s.row_s = s.lrow_c = s.lrow_s = -1;
   if (live) {
-    const int r0 = base[pulse] + v[pulse];
+    const int r0 = pulse == 0 ? v[0] : pulse == 1 ? base[1] + v[1] : base[2] + v[2];
     const int lr0 = v[3];
     s.row_c = r0;
     s.lrow_c = lrows ? lr0 : -1;
@@ -900,16 +937,21 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
     un.seq = b;
     un.n = nrow + (spec ? 1 : 0);
     un.pos0 = pos0;
+#pragma unroll
     for (int i = 0; i < kMaxBlock; ++i) un.row[i] = i < nrow ? r0 + i : -1;
     if (guess_row) s.lrow_s = lrows == nrow ? lr0 + nrow - 1 : lr0;
-    for (int i = 0; i < nrow; ++i) {
+#pragma unroll
+    for (int i = 0; i < kMaxBlock; ++i) {
+      if (i >= nrow) break;
       const int slot = slot0 + i;
       const int lr = lrows == nrow ? lr0 + i : (lrows && i == nrow - 1 ? lr0 : -1);
-      a.rows[r0 + i] = RowDesc{b, slot, pulse, pos0 + i, s.blk[slot], lr, -1, (s.blk_base + slot) % S};
+      a.rows[r0 + i] = RowDesc{b, slot, pulse, pos0 + i, bk[slot], lr, -1,
+                               (s.blk_base + slot) % S};
       if (lr >= 0) {
         a.lrow_seq[lr] = b;
+#pragma unroll
         for (int x = 0; x < kMaxExtra; ++x)
-          a.lrow_extra[(int64_t)lr * kMaxExtra + x] = x < slot ? s.blk[1 + x] : -1;
+          a.lrow_extra[(int64_t)lr * kMaxExtra + x] = x < slot ? bk[1 + x] : -1;
         // distinct stream per (round, draft or verify, block row)
         a.lrow_ctr[lr] = (s.ctr * 2u + (s.blk_phase == 0 ? 0u : 1u)) * (uint32_t)kMaxBlock + slot;
       }
@@ -921,18 +963,22 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
       const int r = base[0] + v[0] + (pulse == 0 ? nrow : 0);
       const int lr = lr0 + lrows;
       a.rows[r] = RowDesc{b, S - 1, 0, s.c_pos + nrow, s.s_tok, lr, -1, (s.blk_base + S - 1) % S};
-      un.row[nrow] = r;
+#pragma unroll
+      for (int i = 0; i < kMaxBlock; ++i) un.row[i] = i == nrow ? r : un.row[i];
       s.row_s = r;
       s.lrow_s = lr;
       a.lrow_seq[lr] = b;
+#pragma unroll
       for (int x = 0; x < kMaxExtra; ++x)
         a.lrow_extra[(int64_t)lr * kMaxExtra + x] =
-            x < nrow - 1 ? s.blk[1 + x] : (x == nrow - 1 ? s.s_tok : -1);
+            x < nrow - 1 ? bk[1 + x] : (x == nrow - 1 ? s.s_tok : -1);
       a.lrow_ctr[lr] = ((s.ctr + 1u) * 2u) * (uint32_t)kMaxBlock;
     }
     a.units[v[4]] = un;
   }
-  if (act) a.state[b] = s;
+#pragma unroll
+  for (int i = 0; i < kMaxBlock; ++i) s.blk[i] = bk[i];
+  if (act) state_store(a.state + b, s);
   if (b == 0) {
     for (int p = 0; p < 4; ++p) {
       ctl->pulse_start[p] = p < 3 ? base[p] : total[0] + total[1] + total[2];
