@@ -215,7 +215,10 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   constexpr bool kPair = (EPI == EPI_SWIGLU || EPI == EPI_LOGITS);
   constexpr int kKPass = KITER * 32 * kGemmWaves;  // K covered by one pass of the waves
   static_assert(!EAGER || MODE == ROWS_LIST, "eager weight loads are for expert lists");
-  __shared__ float red[kGemmWaves][64][kPair ? 16 : 8];
+  // partial tiles [wave][tile value][lane]: the lanes of one value are consecutive words,
+  // so the writes and the reducing reads hit 64 different banks (lane-major rows of 16
+  // values put every 4th lane on the same bank: 16-way conflicts on the reads)
+  __shared__ float red[kGemmWaves][kPair ? 16 : 8][64];
   const GemmBlock blk = gemm_block<XCD>(g);
   if (!blk.valid) return;
   // grid.y < g0_split: the optional all-rows group (group -1) when has_g0 is set. Its row
@@ -363,16 +366,13 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
     }
     // Partial tiles to LDS; then wave w reduces and stores tile value w of every lane:
     // row block w / 4, accumulator element w % 4 (with its up-projection twin for SwiGLU).
-    {
-      float* r = red[wv][lane];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        r[j] = c00[j];
-        r[4 + j] = c10[j];
-        if constexpr (kPair) {
-          r[8 + j] = c01[j];
-          r[12 + j] = c11[j];
-        }
+    for (int j = 0; j < 4; ++j) {
+      red[wv][j][lane] = c00[j];
+      red[wv][4 + j][lane] = c10[j];
+      if constexpr (kPair) {
+        red[wv][8 + j][lane] = c01[j];
+        red[wv][12 + j][lane] = c11[j];
       }
     }
     __syncthreads();
@@ -382,8 +382,8 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
       float acc = 0.f, accu = 0.f;
 #pragma unroll
       for (int w = 0; w < kGemmWaves; ++w) {
-        acc += red[w][lane][blk * 4 + j];
-        if constexpr (kPair) accu += red[w][lane][8 + blk * 4 + j];
+        acc += red[w][blk * 4 + j][lane];
+        if constexpr (kPair) accu += red[w][8 + blk * 4 + j][lane];
       }
       // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16; the C row
       // of tile row r is the entry held by lane r % 16 (rows 0-15: e0, 16-31: e1).
