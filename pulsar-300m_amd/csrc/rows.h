@@ -17,8 +17,10 @@ constexpr int kLongCacheSplits = 16;
 // engines of at least this many sequences (units) take 1024-key splits in the long
 // engines' sliding-window layers, fewer keep 256-key splits
 constexpr int kManyUnits = 16;
-// 64-key blocks per wave and split in engines below the long-cache threshold
+// 64-key blocks per wave and split in engines below the long-cache threshold, and in
+// those of at least kWideSplitUnits sequences (many workgroups already: 1024-key splits)
 constexpr int kShortCacheBlocks = 2;
+constexpr int kWideSplitUnits = 128;
 static_assert(kUnitSplit >= kSplitLen, "split partial slots are sized for kSplitLen");
 constexpr int kMaxRank = 16;    // re-injection gate rank bound
 

@@ -2166,11 +2166,13 @@ int launch_qk_post(const QKPostArgs& a, int dtype, int max_rows, hipStream_t s) 
 }
 int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s) {
   if (dtype == PULSAR_BF16) {
-    // Key split per launch, from the layer type and the engine's context length only (never
-    // the batch). Engines whose context needs more than kLongCacheSplits 256-key splits
-    // take 2048-key splits (8 blocks per wave) in the global layers, which spread each
-    // workgroup's fixed start and merge costs over 8x the keys, and 1024-key splits in the
-    // sliding-window layers (at most window + unit rows keys: two splits).
+    // Key split per launch, from the layer type, the engine's context length and, for
+    // shorter contexts, whether the engine holds kWideSplitUnits sequences or more: results
+    // are the same for engines on the same side of each threshold. Engines whose context
+    // needs more than kLongCacheSplits 256-key splits take 2048-key splits (8 blocks per
+    // wave) in the global layers, which spread each workgroup's fixed start and merge costs
+    // over 8x the keys, and 1024-key splits in the sliding-window layers (at most window +
+    // unit rows keys: two splits).
     const bool lng = a.max_splits_unit > kLongCacheSplits;
     // engines of few sequences keep 256-key splits in the sliding-window layers: 1024-key
     // splits would leave most CUs idle there (two workgroups per unit and kv head)
@@ -2178,8 +2180,12 @@ int launch_attn_decode(const AttnArgs& a, int dtype, int max_rows, hipStream_t s
     // shorter engines: 512-key splits (two blocks per wave). Every split repeats the unit's
     // query post-processing and adds a partial to merge; against 256-key splits: c2
     // draft-block 25.4k -> 25.9k tokens/s, c2 reference schedule 18.5k -> 18.9k, c5 85.3k
-    // -> 87.1k (1024-key splits for draft blocks: 24.8k)
-    const int bpw = !lng ? kShortCacheBlocks : (a.is_local ? (few ? 1 : 4) : 8);
+    // -> 87.1k (1024-key splits for draft blocks: 24.8k). Engines of kWideSplitUnits
+    // sequences or more have workgroups enough at 1024-key splits, which leave most units
+    // one split and no merge: 256 x 1024 positions, reference schedule 116.8k -> 124.3k
+    // tokens/s, draft length 6 104.4k -> 111.5k.
+    const int short_bpw = a.max_units >= kWideSplitUnits ? 4 : kShortCacheBlocks;
+    const int bpw = !lng ? short_bpw : (a.is_local ? (few ? 1 : 4) : 8);
     const int split = kUnitSplit * bpw;
     // a unit's keys [lo, hi] lie in the splits from lo's to hi's: at most max_ctx keys, and in
     // sliding-window layers window + rows - 1 keys, which can straddle one more split

@@ -34,8 +34,9 @@ def _alone(eng, prompts, i, sub, **kw):
 def _spec_plain_single(model, prompts, n_new, singles, sub=1):
     """Greedy self-speculative == plain over the batch, and sequences `singles` decode the same
     in a sub-batch of `sub` prompts (1: alone). Batches of 64+ sequences hold 128+ rows per
-    step and run the output head in 128-row tiles (1024+ rows: the projections too), so
-    they are compared with sub-batches on the same side of those thresholds."""
+    step and run the output head in 128-row tiles (1024+ rows: the projections too), and
+    those of 128+ sequences take 1024-key attention splits below the long-cache threshold,
+    so they are compared with sub-batches on the same side of those thresholds."""
     from pulsar_engine.engine import PulsarInferenceEngine
 
     eng = PulsarInferenceEngine(model)
@@ -87,7 +88,7 @@ def test_c5_batch_256_spec_equals_plain_and_batch_equals_single(full_state, c5_m
 
     cfg = full_state[0]
     prompts = [W.zipf_ids(5, f"c5_prompt_{b}", 512, cfg.vocab_size).tolist() for b in range(256)]
-    spec = _spec_plain_single(c5_model[1], prompts, 512, singles=[0, 255], sub=64)
+    spec = _spec_plain_single(c5_model[1], prompts, 512, singles=[0, 255], sub=128)
     print("c5 first tokens", [s[:4] for s in spec[:4]], "lengths", sorted({len(s) for s in spec}))
 
 
