@@ -700,7 +700,9 @@ __global__ void __launch_bounds__(256, 2) gemm_bf16_lds_kernel(GemmArgs g) {
 // CT = 8: twice that); wave w computes rows 16 RB w .. 16 RB (w + 1) - 1 against all CT
 // tiles. The weight tiles of each 32-wide k step go through a ring of S LDS buffers with
 // direct global-to-LDS loads (each wave fetches CT / 4 of the 1 KB tiles, all 4 waves read
-// all CT); the wave's own rows go to registers. The launch moves rows x (weight rows) x K x 2 (1/(16 CT) + 1/R) bytes from L2 to
+// all CT); the wave's own rows go through the same ring (one 1 KB direct load per 16-row
+// block, read back by the wave alone: 320-row verify 3.15 -> 3.06 ms against loading them
+// into registers, whose 16 lanes of a load touched 16 rows). The launch moves rows x (weight rows) x K x 2 (1/(16 CT) + 1/R) bytes from L2 to
 // the CUs, which bounds it (about 10 TB/s measured: timing copies without the k loop or
 // without the products put the 320-row verify's routed gate/up at 6.2 and 22.9 of its
 // 22.7 us, and rings of 4 to 10 buffers or 2 to 4 k tiles per stage ran alike; lanes past
@@ -762,7 +764,8 @@ __device__ __forceinline__ bool mid_tile(const GemmArgs& g, int& cb, int& group,
 template <int KITER, int PASSES, int RB, int CT, int SR>
 __device__ __forceinline__ void mid_kloop(const bf16* const (&wsrc)[CT / 4],
                                           const bf16* const (&arow)[RB], bf16x8_t (*sW)[CT][64],
-                                          int wv, int lane, f32x4_t (&tot)[RB][CT]) {
+                                          bf16x8_t (*sA)[kMidWaves * RB][64], int aslot, int wv,
+                                          int lane, f32x4_t (&tot)[RB][CT]) {
   constexpr int CK = KITER * PASSES, STEPS = 8 * CK, KB = 8 * KITER;
   constexpr int S = SR < STEPS ? SR : STEPS;  // ring buffers in use (at most sW's SR)
   static_assert(S >= 2, "ring of at least 2 buffers");
@@ -771,7 +774,6 @@ __device__ __forceinline__ void mid_kloop(const bf16* const (&wsrc)[CT / 4],
   // k tile of step t of the chunk-ordered sequence
   auto ktile = [](int t) { return ((t % CK) / KITER) * KB + (t / CK) * KITER + (t % CK) % KITER; };
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  bf16x8_t xa[S][RB];
   f32x4_t acc[RB][CT];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
@@ -783,7 +785,7 @@ __device__ __forceinline__ void mid_kloop(const bf16* const (&wsrc)[CT / 4],
     for (int h = 0; h < CT / 4; ++h)
       load_lds16(wsrc[h] + (int64_t)kt * 512, &sW[j % S][wv + 4 * h][0]);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) xa[j % S][rb] = load_bf16x8(arow[rb] + kt * 32);
+    for (int rb = 0; rb < RB; ++rb) load_lds16(arow[rb] + kt * 32, &sA[j % S][wv * RB + rb][0]);
   };
 #pragma unroll
   for (int j = 0; j < S - 1; ++j) fetch(j);
@@ -801,15 +803,17 @@ __device__ __forceinline__ void mid_kloop(const bf16* const (&wsrc)[CT / 4],
       wait_vmcnt<0>();
     lds_barrier();
     if (s + S - 1 < STEPS) fetch(s + S - 1);
-    bf16x8_t fw[CT];
+    bf16x8_t fw[CT], xa[RB];
 #pragma unroll
     for (int c = 0; c < CT; ++c) fw[c] = sW[s % S][c][lane];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) xa[rb] = sA[s % S][wv * RB + rb][aslot];
     // a chunk's chain starts from zero
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int c = 0; c < CT; ++c)
-        acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[s % S][rb], fw[c],
+        acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[rb], fw[c],
                                                             s % CK == 0 ? zero : acc[rb][c], 0, 0, 0);
     if ((s + 1) % CK == 0) {
 #pragma unroll
@@ -827,6 +831,11 @@ __global__ void __launch_bounds__(64 * kMidWaves, 2) gemm_bf16_mid_kernel(GemmAr
   constexpr int R = kMidWaves * RB * 16;
   static_assert(CT == 4 || CT == 8, "4 or 8 weight tiles per workgroup");
   __shared__ bf16x8_t sW[S][CT][64];
+  // each wave's A rows of a k step go through the same ring: 16 rows x 32 k per row block,
+  // chunk (row m, k chunk q) at slot 4 m + (q ^ 2 (m >> 3)): the load's lanes 4 j .. 4 j + 3
+  // fetch row j's 64 contiguous bytes, and the fragment read (lane = row m, chunk kq) is
+  // free of LDS bank conflicts
+  __shared__ bf16x8_t sA[S][kMidWaves * RB][64];
   int cb, group, rt, cnt;
   if (!mid_tile<MODE, CW, R>(g, cb, group, rt, cnt)) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -855,7 +864,8 @@ __global__ void __launch_bounds__(64 * kMidWaves, 2) gemm_bf16_mid_kernel(GemmAr
     wsrc[h] = W + ((int64_t)ct * KT * 64 + lane) * 8;
   }
   // rows of the wave: 16-row block rb holds tile rows 16 (RB wv + rb) + 0..15; lanes past
-  // the count re-read the last row (computed, never stored)
+  // the count re-read the last row (computed, never stored). Lane l loads row l >> 2 of
+  // the block (its entry is lane (l >> 2)'s), chunk (l & 3) ^ 2 (l >> 5).
   const int r0 = rt * R + wv * RB * 16;
   int ent[RB];
   const bf16* arow[RB];
@@ -863,13 +873,15 @@ __global__ void __launch_bounds__(64 * kMidWaves, 2) gemm_bf16_mid_kernel(GemmAr
   for (int rb = 0; rb < RB; ++rb) {
     const int i = min(r0 + rb * 16 + m, cnt - 1);
     ent[rb] = entry_fix<MODE>(group, i, entry_load<MODE>(g, group, i));
-    arow[rb] = A + (int64_t)a_row_of<MODE>(g, group, ent[rb]) * lda + kq * 8;
+    const int el = __shfl(ent[rb], lane >> 2, 64);
+    arow[rb] = A + (int64_t)a_row_of<MODE>(g, group, el) * lda + ((lane & 3) ^ ((lane >> 5) << 1)) * 8;
   }
+  const int aslot = m * 4 + (kq ^ ((m >> 3) << 1));  // this lane's fragment chunk
   f32x4_t tot[RB][CT];
   if (g0 && KMUL0 > 1)
-    mid_kloop<KITER, KMUL0, RB, CT, S>(wsrc, arow, sW, wv, lane, tot);
+    mid_kloop<KITER, KMUL0, RB, CT, S>(wsrc, arow, sW, sA, aslot, wv, lane, tot);
   else
-    mid_kloop<KITER, 1, RB, CT, S>(wsrc, arow, sW, wv, lane, tot);
+    mid_kloop<KITER, 1, RB, CT, S>(wsrc, arow, sW, sA, aslot, wv, lane, tot);
   // D layout of 16x16 MFMA: lane holds rows 4 kq + j of its block, column m; the C row of
   // block row r is the entry held by lane r
 #pragma unroll
