@@ -215,10 +215,15 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   constexpr bool kPair = (EPI == EPI_SWIGLU || EPI == EPI_LOGITS);
   constexpr int kKPass = KITER * 32 * kGemmWaves;  // K covered by one pass of the waves
   static_assert(!EAGER || MODE == ROWS_LIST, "eager weight loads are for expert lists");
-  // partial tiles [wave][tile value][lane]: the lanes of one value are consecutive words,
-  // so the writes and the reducing reads hit 64 different banks (lane-major rows of 16
-  // values put every 4th lane on the same bank: 16-way conflicts on the reads)
-  __shared__ float red[kGemmWaves][kPair ? 16 : 8][64];
+  // One LDS slice per wave: first the wave's A rows of a 16-row block (one 1 KB tile per
+  // k tile and pass), then its partial tile values [value][lane] for the K-split sum (the
+  // lanes of one value are consecutive words: conflict-free writes and reducing reads;
+  // lane-major rows of 16 values put every 4th lane on one bank, 16-way conflicts). A wave
+  // only writes its own slice, so the A staging needs no barrier.
+  constexpr int kAFrags = KITER * KMUL0;
+  constexpr int kRedFloats = (kPair ? 16 : 8) * 64;
+  constexpr int kSliceFloats = kAFrags * 256 > kRedFloats ? kAFrags * 256 : kRedFloats;
+  __shared__ __attribute__((aligned(16))) float lds_slices[kGemmWaves * kSliceFloats];
   const GemmBlock blk = gemm_block<XCD>(g);
   if (!blk.valid) return;
   // grid.y < g0_split: the optional all-rows group (group -1) when has_g0 is set. Its row
@@ -339,24 +344,49 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
       ar0 = m < n ? a_row_of<MODE>(g, group, e0) : -1;
       ar1 = m + 16 < n ? a_row_of<MODE>(g, group, e1) : -1;
     }
-    const bf16* a0 = A + (int64_t)(ar0 < 0 ? 0 : ar0) * lda;
-    const bf16* a1 = A + (int64_t)(ar1 < 0 ? 0 : ar1) * lda;
+    // A rows through the wave's LDS slice: tile (pass p, k tile i) holds the block's 16
+    // rows x 32 k as (row r, k chunk q) at slot 4 r + (q ^ 2 (r >> 3)); the load's lanes
+    // 4 j .. 4 j + 3 fetch row j's 64 contiguous bytes (a register load's 16 lanes touched
+    // 16 rows), and the fragment read (lane = row m, chunk kq) is free of bank conflicts.
+    // Rows past the count load row 0 (computed, never stored).
+    bf16x8_t* astage = reinterpret_cast<bf16x8_t*>(lds_slices + wv * kSliceFloats);
+    const int acl = (lane & 3) ^ ((lane >> 5) << 1);
+    const int aslot = m * 4 + (kq ^ ((m >> 3) << 1));
+    auto stage_a = [&](int ar_lane) {  // ar_lane: A row of block row lane >> 2
+      const bf16* src = A + (int64_t)(ar_lane < 0 ? 0 : ar_lane) * lda + wv * (KITER * 32) + acl * 8;
+#pragma unroll
+      for (int pass = 0; pass < KMUL0; ++pass) {
+        if (pass >= passes) break;
+#pragma unroll
+        for (int i = 0; i < KITER; ++i)
+          load_lds16(src + pass * kKPass + 32 * i, astage + (pass * KITER + i) * 64);
+      }
+    };
     f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
+    stage_a(__shfl(ar0, lane >> 2, 64));
+    wait_vmcnt<0>();  // this wave's A tiles (and, issued before them, its weights) are in
 #pragma unroll
     for (int pass = 0; pass < KMUL0; ++pass) {
       if (pass >= passes) break;
 #pragma unroll
       for (int i = 0; i < KITER; ++i)
-        xa[i] = (EAGER || ar0 >= 0) ? load_bf16x8(a0 + pass * kKPass + kb + 32 * i) : zero;
+        xa[i] = (EAGER || ar0 >= 0) ? astage[(pass * KITER + i) * 64 + aslot] : zero;
 #pragma unroll
       for (int i = 0; i < KITER; ++i) {
         c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[pass * KITER + i], c00, 0, 0, 0);
         if constexpr (kPair) c01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bu[i], c01, 0, 0, 0);
       }
-      if (two) {  // the second 16-row block reuses the A registers (fewer VGPRs, more waves)
+    }
+    if (two) {  // the second 16-row block reuses the slice once the first block's reads are in
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      stage_a(__shfl(ar1, lane >> 2, 64));
+      wait_vmcnt<0>();
+#pragma unroll
+      for (int pass = 0; pass < KMUL0; ++pass) {
+        if (pass >= passes) break;
 #pragma unroll
         for (int i = 0; i < KITER; ++i)
-          xa[i] = ar1 >= 0 ? load_bf16x8(a1 + pass * kKPass + kb + 32 * i) : zero;
+          xa[i] = ar1 >= 0 ? astage[(pass * KITER + i) * 64 + aslot] : zero;
 #pragma unroll
         for (int i = 0; i < KITER; ++i) {
           c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[pass * KITER + i], c10, 0, 0, 0);
@@ -364,15 +394,18 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
         }
       }
     }
+    // the partial values overwrite the slice: its A reads are done
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // Partial tiles to LDS; then wave w reduces and stores tile value w of every lane:
     // row block w / 4, accumulator element w % 4 (with its up-projection twin for SwiGLU).
+    float* red_w = lds_slices + wv * kSliceFloats;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      red[wv][j][lane] = c00[j];
-      red[wv][4 + j][lane] = c10[j];
+      red_w[j * 64 + lane] = c00[j];
+      red_w[(4 + j) * 64 + lane] = c10[j];
       if constexpr (kPair) {
-        red[wv][8 + j][lane] = c01[j];
-        red[wv][12 + j][lane] = c11[j];
+        red_w[(8 + j) * 64 + lane] = c01[j];
+        red_w[(12 + j) * 64 + lane] = c11[j];
       }
     }
     __syncthreads();
@@ -382,8 +415,8 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
       float acc = 0.f, accu = 0.f;
 #pragma unroll
       for (int w = 0; w < kGemmWaves; ++w) {
-        acc += red[w][blk * 4 + j][lane];
-        if constexpr (kPair) accu += red[w][8 + blk * 4 + j][lane];
+        acc += lds_slices[w * kSliceFloats + (blk * 4 + j) * 64 + lane];
+        if constexpr (kPair) accu += lds_slices[w * kSliceFloats + (8 + blk * 4 + j) * 64 + lane];
       }
       // D layout of 16x16 MFMA: lane holds rows (lane/16)*4 + j, column lane%16; the C row
       // of tile row r is the entry held by lane r % 16 (rows 0-15: e0, 16-31: e1).
