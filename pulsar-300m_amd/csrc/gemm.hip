@@ -159,7 +159,16 @@ __device__ __forceinline__ int entry_fix(int group, int i, int v) {
 }
 template <int MODE>
 __device__ __forceinline__ int a_row_of(const GemmArgs& g, int group, int raw) {
-  if constexpr (MODE == ROWS_LIST) return group < 0 ? raw : raw / g.a_div;
+  if constexpr (MODE == ROWS_LIST) {
+    if (group < 0) return raw;
+    // a_div is 1 (expert output rows) or the top-k count (token rows). A power of two takes
+    // a shift instead of the ~30-instruction integer division; entries are non-negative
+    // (only the spare-capacity entries of eager launches may not be, and their rows are
+    // clamped, computed and never stored).
+    const int d = g.a_div;
+    if ((d & (d - 1)) == 0) return raw >> __builtin_ctz((unsigned)d);
+    return raw / d;
+  }
   return raw;
 }
 template <int MODE>
@@ -205,6 +214,21 @@ __device__ __forceinline__ GemmBlock gemm_block(const GemmArgs& g) {
   b.y = pair / g.grid_x;
   b.valid = b.y < g.grid_y;
   return b;
+}
+
+// s_waitcnt vmcnt(n) for an n that is a constant once the caller's loops are unrolled.
+__device__ __forceinline__ void wait_vmcnt_unrolled(int n) {
+  switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 4: wait_vmcnt<4>(); break;
+    case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;
+    case 7: wait_vmcnt<7>(); break;
+    default: wait_vmcnt<0>(); break;
+  }
 }
 
 template <int EPI, int KITER, int MODE, int KMUL0, bool EAGER, bool XCD>
@@ -296,8 +320,11 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
   // Row entries of the first tile first, then the weights, then (after a scheduling
   // barrier) the A rows: vector loads retire in issue order, so waiting for the few entry
   // loads leaves every weight load in flight. Lanes past the last row re-read the last
-  // entry (always in bounds) and use a zero A operand.
-  int n, i0, i1, l0, l1;
+  // entry (always in bounds) and use a zero A operand. Each lane loads two entries per
+  // block: that of its fragment row m (for the A operand's zero test and the stores) and
+  // that of the row sr = lane / 4 whose 16 bytes it stages into LDS.
+  const int sr = lane >> 2;
+  int n, i0, i1, l0, l1, si0, si1, ls0, ls1;
   if constexpr (EAGER) {
     // Most experts have rows (the host decides from the batch size): the first tile's
     // entries and the weights go out before the row count, whose scalar load retires apart
@@ -307,8 +334,12 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
     i0 = tile0 + m;
     i1 = tile0 + m + 16;
     const int32_t* lst = g.list + (int64_t)max(group, 0) * g.list_stride;
+    si0 = tile0 + sr;
+    si1 = tile0 + sr + 16;
     l0 = lst[min((int64_t)i0, cap)];
     l1 = lst[min((int64_t)i1, cap)];
+    ls0 = lst[min((int64_t)si0, cap)];
+    ls1 = lst[min((int64_t)si1, cap)];
     __builtin_amdgcn_sched_barrier(0);
     PULSAR_LOAD_W(0);
     // no early exit on the count: a branch on it would let the compiler test it before
@@ -318,42 +349,55 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
     // Use the entries here: the wait for them then leaves the weight loads behind them in
     // flight, and the compiler cannot merge these loads into the next tile's (which would
     // put them behind the weights and the count).
-    asm volatile("" ::"v"(l0), "v"(l1));
+    asm volatile("" ::"v"(l0), "v"(l1), "v"(ls0), "v"(ls1));
     n = max(0, min(32, cnt - tile0));
   } else {
     n = min(32, cnt - tile0);
     i0 = tile0 + min(m, n - 1);
     i1 = tile0 + min(m + 16, n - 1);
+    si0 = tile0 + min(sr, n - 1);
+    si1 = tile0 + min(sr + 16, n - 1);
     l0 = entry_load<MODE>(g, group, i0);
     l1 = entry_load<MODE>(g, group, i1);
+    ls0 = entry_load<MODE>(g, group, si0);
+    ls1 = entry_load<MODE>(g, group, si1);
     PULSAR_LOAD_W(0);
     PULSAR_LOAD_W_REST();
   }
-  while (true) {
+  // One row tile (32 rows) of the group. The first tile runs outside the loop: in a
+  // loop, the wait for the entries of a later tile (issued last) would also stand at the
+  // first tile's A loads and make them wait for the whole weight slice.
+  auto run_tile = [&]() {
     __builtin_amdgcn_sched_barrier(0);
     const bool two = n > 16;  // second 16-row block present (uniform per workgroup)
     const int e0 = entry_fix<MODE>(group, i0, l0), e1 = entry_fix<MODE>(group, i1, l1);
-    int ar0, ar1;
+    const int es0 = entry_fix<MODE>(group, si0, ls0), es1 = entry_fix<MODE>(group, si1, ls1);
+    int ar0, ar1, as0, as1;  // ar: fragment row's A row (-1: zero operand); as: staged row
     if constexpr (EAGER) {
       // every lane of the first row block loads a row (clamped into the A buffer): rows
       // past the count are computed and never stored, so no A load waits on the count
       const int lim = (g0 ? g.a_rows0 : g.a_rows) - 1;
       ar0 = min(max(a_row_of<MODE>(g, group, e0), 0), lim);
       ar1 = m + 16 < n ? min(max(a_row_of<MODE>(g, group, e1), 0), lim) : -1;
+      as0 = min(max(a_row_of<MODE>(g, group, es0), 0), lim);
+      as1 = min(max(a_row_of<MODE>(g, group, es1), 0), lim);
     } else {
       ar0 = m < n ? a_row_of<MODE>(g, group, e0) : -1;
       ar1 = m + 16 < n ? a_row_of<MODE>(g, group, e1) : -1;
+      as0 = a_row_of<MODE>(g, group, es0);  // rows past the count re-read the last row
+      as1 = a_row_of<MODE>(g, group, es1);
     }
     // A rows through the wave's LDS slice: tile (pass p, k tile i) holds the block's 16
     // rows x 32 k as (row r, k chunk q) at slot 4 r + (q ^ 2 (r >> 3)); the load's lanes
     // 4 j .. 4 j + 3 fetch row j's 64 contiguous bytes (a register load's 16 lanes touched
     // 16 rows), and the fragment read (lane = row m, chunk kq) is free of bank conflicts.
-    // Rows past the count load row 0 (computed, never stored).
+    // With one pass the fragment reads wait for their own tile only (the A loads retire in
+    // issue order, after the weights); a compiler barrier keeps each read behind its wait.
     bf16x8_t* astage = reinterpret_cast<bf16x8_t*>(lds_slices + wv * kSliceFloats);
     const int acl = (lane & 3) ^ ((lane >> 5) << 1);
     const int aslot = m * 4 + (kq ^ ((m >> 3) << 1));
-    auto stage_a = [&](int ar_lane) {  // ar_lane: A row of block row lane >> 2
-      const bf16* src = A + (int64_t)(ar_lane < 0 ? 0 : ar_lane) * lda + wv * (KITER * 32) + acl * 8;
+    auto stage_a = [&](int as) {  // as: A row of block row sr
+      const bf16* src = A + (int64_t)as * lda + wv * (KITER * 32) + acl * 8;
 #pragma unroll
       for (int pass = 0; pass < KMUL0; ++pass) {
         if (pass >= passes) break;
@@ -363,14 +407,24 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
       }
     };
     f32x4_t c00 = {0.f, 0.f, 0.f, 0.f}, c10 = c00, c01 = c00, c11 = c00;
-    stage_a(__shfl(ar0, lane >> 2, 64));
-    wait_vmcnt<0>();  // this wave's A tiles (and, issued before them, its weights) are in
+    auto wait_a = [&](int i) {  // before the fragment read of k tile i of the first pass
+      if constexpr (KMUL0 == 1) {
+        wait_vmcnt_unrolled(KITER - 1 - i);
+        asm volatile("" ::: "memory");
+      } else if (i == 0) {
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+      }
+    };
+    stage_a(as0);
 #pragma unroll
     for (int pass = 0; pass < KMUL0; ++pass) {
       if (pass >= passes) break;
 #pragma unroll
-      for (int i = 0; i < KITER; ++i)
+      for (int i = 0; i < KITER; ++i) {
+        if (pass == 0) wait_a(i);
         xa[i] = (EAGER || ar0 >= 0) ? astage[(pass * KITER + i) * 64 + aslot] : zero;
+      }
 #pragma unroll
       for (int i = 0; i < KITER; ++i) {
         c00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[pass * KITER + i], c00, 0, 0, 0);
@@ -379,14 +433,15 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
     }
     if (two) {  // the second 16-row block reuses the slice once the first block's reads are in
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      stage_a(__shfl(ar1, lane >> 2, 64));
-      wait_vmcnt<0>();
+      stage_a(as1);
 #pragma unroll
       for (int pass = 0; pass < KMUL0; ++pass) {
         if (pass >= passes) break;
 #pragma unroll
-        for (int i = 0; i < KITER; ++i)
+        for (int i = 0; i < KITER; ++i) {
+          if (pass == 0) wait_a(i);
           xa[i] = ar1 >= 0 ? astage[(pass * KITER + i) * 64 + aslot] : zero;
+        }
 #pragma unroll
         for (int i = 0; i < KITER; ++i) {
           c10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], bw[pass * KITER + i], c10, 0, 0, 0);
@@ -428,14 +483,22 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_bf16_kernel(GemmArgs g) 
           epilogue<bf16>(g, EPI, group, Cout, ldc, crow + g.c_row_offset, N + col0 + m, accu, 0.f);
       }
     }
-    tile0 += tstep;
-    if (tile0 >= cnt) break;
+  };
+  run_tile();
+  tile0 += tstep;
+  while (tile0 < cnt) {
     __syncthreads();  // the partial sums in LDS are consumed before the next tile's writes
     n = min(32, cnt - tile0);
     i0 = tile0 + min(m, n - 1);
     i1 = tile0 + min(m + 16, n - 1);
+    si0 = tile0 + min(sr, n - 1);
+    si1 = tile0 + min(sr + 16, n - 1);
     l0 = entry_load<MODE>(g, group, i0);
     l1 = entry_load<MODE>(g, group, i1);
+    ls0 = entry_load<MODE>(g, group, si0);
+    ls1 = entry_load<MODE>(g, group, si1);
+    run_tile();
+    tile0 += tstep;
   }
 #undef PULSAR_LOAD_W
 #undef PULSAR_LOAD_W_REST
