@@ -158,8 +158,10 @@ struct KVLayer {
   const int32_t* page_table;
 };
 
-__device__ __forceinline__ KVBlock kv_block_layer(const KVLayer& c, bool local, int Hkv, int b,
-                                                  int g, int kb) {
+// Block of key position kb of sequence b, KV head g; global layers take the pool page of
+// the block from the caller (`page`, read from the page table beforehand).
+__device__ __forceinline__ KVBlock kv_block_layer_page(const KVLayer& c, bool local, int Hkv,
+                                                       int b, int g, int kb, int64_t page) {
   KVBlock r;
   if (local) {
     const int64_t bg = (int64_t)b * Hkv + g;
@@ -168,12 +170,18 @@ __device__ __forceinline__ KVBlock kv_block_layer(const KVLayer& c, bool local, 
     r.v0 = bg * kHeadDim * c.lcap + ring;
     r.vstride = c.lcap;
   } else {
-    const int64_t pg = kv_page(c.page_table, c.max_pages, b, kb) * Hkv + g;
+    const int64_t pg = page * Hkv + g;
     r.k0 = pg * kPage * kHeadDim;
     r.v0 = pg * kHeadDim * kPage;
     r.vstride = kPage;
   }
   return r;
+}
+
+__device__ __forceinline__ KVBlock kv_block_layer(const KVLayer& c, bool local, int Hkv, int b,
+                                                  int g, int kb) {
+  return kv_block_layer_page(c, local, Hkv, b, g, kb,
+                             local ? 0 : kv_page(c.page_table, c.max_pages, b, kb));
 }
 
 struct AttnArgs {

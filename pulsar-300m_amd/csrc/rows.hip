@@ -899,6 +899,17 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
   const int lo_blk = (a.is_local ? max(0, un.pos0 - a.window + 1) : 0) & ~63;
   const int kbw = s_lo + wv * 64;
   const int kb0 = kbw + (lo_blk > kbw ? (lo_blk - kbw + kStride - 1) / kStride * kStride : 0);
+  // The wave's first block (a wave without blocks loads the split's last block and does not
+  // use it). Global layers: its pool page is a scalar load (the block index is uniform per
+  // wave) issued before the post operands below: the block's loads wait for it in the scalar
+  // counter, not for every operand load in flight (local layers read an in-bounds entry and
+  // ignore it: no branch around the load).
+  const int kbf = min(kb0, s_hi / 64 * 64);
+  const int pt_idx = __builtin_amdgcn_readfirstlane(
+      un.seq * a.kl.max_pages + min(kbf / kPage, a.kl.max_pages - 1));
+  const int pg_first =
+      ((const __attribute__((address_space(4))) int32_t*)(uintptr_t)a.kl.page_table)[pt_idx];
+  __builtin_amdgcn_sched_barrier(0);
   // Post-processing of the step's projections (what qk_post_kernel does, fused): every split
   // finishes the unit's query columns (wave per column, lane = dimension: RMSNorm over the
   // head, RoPE, YaRN query scale); the split whose keys hold a unit row's own position
@@ -914,46 +925,54 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
   const int H = a.H, Hkv = a.Hkv, jr = lane & 31;
   // Loads without branches (addresses clamped into range, results unused where invalid): a
   // load on one side of a branch makes the join wait for every load in flight. Order: the
-  // post operands, then the wave's first block (a wave without blocks loads the split's last
-  // block and does not use it; in global layers its page read waits with the post operands,
-  // all in flight together).
-  const int kbf = min(kb0, s_hi / 64 * 64);
+  // first block's page, the post operands, then the wave's first block.
   // Query column c = wv + 4 i of this wave is unit row z = i; in the 16- and 32-column
   // launches rows past the unit's (a unit of a draft step holds one row) issue no loads (a
   // uniform branch; the 8-column launch measured faster without it)
-  float qx[NQ], qw[NQ], qcs[NQ], qsn[NQ];
+  // bf16 inputs stay raw bits until their use: converted inside the branch of their load, a
+  // column's input made the next column's loads wait for it (one round trip per column).
+  // Skipped inputs start at a zero the compiler cannot see as a constant, which keeps it from
+  // folding the conversion back into the branch.
+  uint32_t opaque_zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(opaque_zero));
+  uint32_t qx[NQ];
+  float qw[NQ], qcs[NQ], qsn[NQ];
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
-    qx[i] = qw[i] = qcs[i] = qsn[i] = 0.f;
+    qx[i] = opaque_zero;
+    qw[i] = qcs[i] = qsn[i] = 0.f;
     if (NQ > 2 && ((wv + kUnitWaves * i) >> 2) >= un.n) continue;
     const int c = wv + kUnitWaves * i, z = c >> 2, head = g * 4 + (c & 3);
     const int row = max(unit_row<NZ>(un, z), 0);
     const int pos = z < un.n ? un.pos0 + z : un.pos0, pulse = step_row_pulse(ps, pc, row);
-    qx[i] = to_f(qkv[(int64_t)row * a.ldq + head * 64 + lane]);
+    qx[i] = qkv[(int64_t)row * a.ldq + head * 64 + lane].u;
     qw[i] = a.q_norm[((int64_t)pulse * H + head) * 64 + lane];
     qcs[i] = a.cos[(int64_t)pos * 32 + jr];
     qsn[i] = a.sin[(int64_t)pos * 32 + jr];
   }
-  float fx[NF], fw[NF], fcs[NF], fsn[NF], fvf[NF];
+  uint32_t fx[NF], fvf[NF];
+  float fw[NF], fcs[NF], fsn[NF];
   int fpg[NF];  // global layers: pool page of the fresh position
 #pragma unroll
   for (int i = 0; i < NF; ++i) {
-    fx[i] = fw[i] = fcs[i] = fsn[i] = fvf[i] = 0.f;
+    fx[i] = fvf[i] = opaque_zero;
+    fw[i] = fcs[i] = fsn[i] = 0.f;
     fpg[i] = 0;
     if (NF > 1 && zlo + ((wv + kUnitWaves * i) >> 1) > zhi) continue;
     const int t = wv + kUnitWaves * i, z = min(zlo + (t >> 1), max(zhi, 0));
     const int row = max(unit_row<NZ>(un, z), 0), pos = un.pos0 + z;
     const int pulse = step_row_pulse(ps, pc, row);
     const int col = (t & 1) == 0 ? (H + g) * 64 : (H + Hkv + g) * 64;
-    fx[i] = to_f(qkv[(int64_t)row * a.ldq + col + lane]);
+    fx[i] = qkv[(int64_t)row * a.ldq + col + lane].u;
     fw[i] = a.k_norm[((int64_t)pulse * Hkv + g) * 64 + lane];
     fcs[i] = a.cos[(int64_t)pos * 32 + jr];
     fsn[i] = a.sin[(int64_t)pos * 32 + jr];
-    fvf[i] = to_f(reinterpret_cast<const bf16*>(a.v_first)[(int64_t)row * Hkv * 64 + g * 64 + lane]);
+    fvf[i] = reinterpret_cast<const bf16*>(a.v_first)[(int64_t)row * Hkv * 64 + g * 64 + lane].u;
     fpg[i] = a.kl.page_table[(int64_t)un.seq * a.kl.max_pages + pos / kPage];
   }
   AttnKV cur;
-  attn_load_block(Kc, Vc, kv_block_layer(a.kl, a.is_local, Hkv, un.seq, g, kbf), m16, kq, cur);
+  attn_load_block(Kc, Vc, kv_block_layer_page(a.kl, a.is_local, Hkv, un.seq, g, kbf, pg_first),
+                  m16, kq, cur);
   auto norm_rope = [&](float x, float w, float cs, float sn) {
     const float ss = wave_sum(x * x);
     const float inv = 1.0f / sqrtf(ss / 64.0f + a.eps);
@@ -966,7 +985,7 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
     const int c = wv + kUnitWaves * i, z = c >> 2;
     float o = 0.f;
     if (unit_row<NZ>(un, z) >= 0) {
-      o = norm_rope(qx[i], qw[i], qcs[i], qsn[i]);
+      o = norm_rope(__uint_as_float(qx[i] << 16), qw[i], qcs[i], qsn[i]);
       const int pos = un.pos0 + z;
       if (!a.is_local && pos + 1 > a.base_seq_len) {
         const double b0 = (double)a.base_seq_len;
@@ -982,11 +1001,12 @@ __attribute__((amdgpu_waves_per_eu(COLS <= 16 ? 3 : 2))) attn_decode_unit_kernel
     const int t = wv + kUnitWaves * i, z = zlo + (t >> 1);
     if (z > zhi) continue;
     if ((t & 1) == 0) {
-      fk[z][lane] = f2bf(norm_rope(fx[i], fw[i], fcs[i], fsn[i])).u;
+      fk[z][lane] = f2bf(norm_rope(__uint_as_float(fx[i] << 16), fw[i], fcs[i], fsn[i])).u;
     } else {
-      float v = fx[i];
+      float v = __uint_as_float(fx[i] << 16);
       if (step_row_pulse(ps, pc, unit_row<NZ>(un, z)) == 0 && a.layer > 0)
-        v = rnd<bf16>(rnd<bf16>(rnd<bf16>(1.0f - lv0) * v) + rnd<bf16>(lv0 * fvf[i]));
+        v = rnd<bf16>(rnd<bf16>(rnd<bf16>(1.0f - lv0) * v) +
+                      rnd<bf16>(lv0 * __uint_as_float(fvf[i] << 16)));
       fv[z][lane] = f2bf(v).u;
     }
   }
