@@ -1568,6 +1568,9 @@ __global__ void __launch_bounds__(256) norm_router_kernel(RouterArgs a) {
   ldv<EPL>(nbase + (int64_t)pulse * D + i0, nw);
 #pragma unroll
   for (int q = 0; q < EW; ++q) ldv<EPL>(W + (int64_t)q * D + i0, wt[q]);
+  // the ranking wave's bias goes out with the weights (after the logits exchange it would be
+  // one more round trip); lanes past the experts read expert 0's and do not use it
+  const float bias_l = a.bias[(int64_t)pulse * E + (lane < E ? lane : 0)];
   // the weight loads go out before the row's arithmetic, which waits for the row
   __builtin_amdgcn_sched_barrier(0);
   float ss = 0.f;
@@ -1596,7 +1599,7 @@ __global__ void __launch_bounds__(256) norm_router_kernel(RouterArgs a) {
   for (int j = 0; j < E; ++j) sum += lane_bcast(l, j);
   const float cen = l - sum / (float)E;
   const float sc = 1.0f / (1.0f + expf(-cen));
-  const float bsc = sc + (act ? a.bias[(int64_t)pulse * E + lane] : 0.f);
+  const float bsc = sc + (act ? bias_l : 0.f);
   int rank = 0;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
@@ -1964,15 +1967,14 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
 #pragma unroll
   for (int k = 0; k < KT; ++k) ldv<EPL>(rop + (int64_t)(k < K ? k : 0) * D, ro[k]);
   const float wl = a.topk_w[(int64_t)r * K + min(lane, K - 1)];
-  // the folded pulse output's row operands go out with the rest (a uniform branch on a
-  // kernel argument)
+  // the folded pulse output's row operands go out with the rest; launches without it re-read
+  // the row's h instead (no branch around the load: converted inside one, the load made the
+  // control block's reads and the pulse-indexed loads wait for every row operand)
   const bool pout = a.hout_state != nullptr;
   float hin[EPL];
+  ldv<EPL>(pout ? reinterpret_cast<const T*>(a.h_in) + (int64_t)r * D + i0 : h, hin);
   RowDesc rd{};
-  if (pout) {
-    ldv<EPL>(reinterpret_cast<const T*>(a.h_in) + (int64_t)r * D + i0, hin);
-    rd = a.rows[r];
-  }
+  if (pout) rd = a.rows[r];
   int n = a.m_fixed, pulse = a.pulse;
   if (a.ctl) {
     int ps[kMaxPulses], pc[kMaxPulses];
@@ -1987,9 +1989,8 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
   asm volatile("" ::: "memory");
   if (r >= n) return;
   const bool live = true;
-  float w[KT];
-#pragma unroll
-  for (int k = 0; k < KT; ++k) w[k] = __shfl(wl, k < K ? k : 0, 64);
+  // the pulse-indexed operands go out before the routing weights' lane shuffles (which wait
+  // for the row operands issued ahead of them)
   ldv<EPL>(reinterpret_cast<const T*>(a.routed_scale) + (int64_t)pulse * D + i0, rs);
   float nwn[EPL];
   if (a.next_norm) ldv<EPL>(a.next_norm + (int64_t)pulse * D + i0, nwn);
@@ -1998,6 +1999,9 @@ __global__ void __launch_bounds__(64) moe_combine_rows_kernel(CombineArgs a) {
     ldv<EPL>(reinterpret_cast<const T*>(a.res_scale) + (int64_t)pulse * D + i0, rso);
     ldv<EPL>(a.final_norm + i0, fn);
   }
+  float w[KT];
+#pragma unroll
+  for (int k = 0; k < KT; ++k) w[k] = __shfl(wl, k < K ? k : 0, 64);
   bool kept[KT];
 #pragma unroll
   for (int k = 0; k < KT; ++k) kept[k] = true;
