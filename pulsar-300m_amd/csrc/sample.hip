@@ -569,18 +569,21 @@ __device__ void ctl_preload(const ControllerArgs& a) {
 // The sequence state moves between memory and registers as 16-byte words at constant
 // offsets: a struct copy leaves the fields a kernel never names in scratch memory.
 static_assert(sizeof(SeqState) % 16 == 0 && alignof(SeqState) <= 16, "SeqState words");
-__device__ __forceinline__ void state_load(SeqState& s, const SeqState* p) {
-  constexpr int W = (int)(sizeof(SeqState) / 16);
-  int4 v[W];
+constexpr int kStateWords = (int)(sizeof(SeqState) / 16);
+// The state's words go out as loads first (no wait); state_commit, after the kernel's other
+// loads are issued, passes them through registers into the state (no memory-to-memory copy
+// of the fields a kernel never names). Passed one by one right after their loads, each word
+// waited for its load before the next load went out: one round trip per word.
+__device__ __forceinline__ void state_issue(int4 (&v)[kStateWords], const SeqState* p) {
 #pragma unroll
-  for (int k = 0; k < W; ++k) {
-    v[k] = reinterpret_cast<const int4*>(p)[k];
-    // the words pass through registers (no memory-to-memory copy of the fields this
-    // kernel never names)
+  for (int k = 0; k < kStateWords; ++k) v[k] = reinterpret_cast<const int4*>(p)[k];
+}
+__device__ __forceinline__ void state_commit(SeqState& s, int4 (&v)[kStateWords]) {
+#pragma unroll
+  for (int k = 0; k < kStateWords; ++k)
     asm volatile("" : "+v"(v[k].x), "+v"(v[k].y), "+v"(v[k].z), "+v"(v[k].w));
-  }
 #pragma unroll
-  for (int k = 0; k < W; ++k) reinterpret_cast<int4*>(&s)[k] = v[k];
+  for (int k = 0; k < kStateWords; ++k) reinterpret_cast<int4*>(&s)[k] = v[k];
 }
 __device__ __forceinline__ void state_store(SeqState* p, const SeqState& s) {
   constexpr int W = (int)(sizeof(SeqState) / 16);
@@ -599,12 +602,14 @@ __global__ void __launch_bounds__(256) controller_kernel(ControllerArgs a) {
   // retires the snapshot)
   const bool act = b < a.B;
   alignas(16) SeqState s{};
-  if (act) state_load(s, a.state + b);
+  int4 sw[kStateWords];  // threads past the batch read the last sequence's and drop it
+  state_issue(sw, a.state + min(b, a.B - 1));
   const int have = act && a.page_table ? a.page_count[b] : 0;
   ctl_preload<NL>(a);
   const int n_prev = ctl->n_rows;
   for (int i = b; i < n_prev; i += blockDim.x) a.last_rows[i] = a.rows[i];
   if (b == 0) *a.last_ctl = *ctl;
+  if (act) state_commit(s, sw);
   __syncthreads();
   if (act) {
     if (a.init) {
@@ -857,15 +862,17 @@ __global__ void __launch_bounds__(256) controller_block_kernel(ControllerArgs a)
   // retires the snapshot)
   const bool act = b < a.B;
   alignas(16) SeqState s{};
-  if (act) state_load(s, a.state + b);
-  BlkVec bk;
-#pragma unroll
-  for (int i = 0; i < kMaxBlock; ++i) bk[i] = s.blk[i];
+  int4 sw[kStateWords];  // threads past the batch read the last sequence's and drop it
+  state_issue(sw, a.state + min(b, a.B - 1));
   const int have = act && a.page_table ? a.page_count[b] : 0;
   ctl_preload<NL>(a);
   const int n_prev = ctl->n_rows;
   for (int i = b; i < n_prev; i += blockDim.x) a.last_rows[i] = a.rows[i];
   if (b == 0) *a.last_ctl = *ctl;
+  if (act) state_commit(s, sw);
+  BlkVec bk;
+#pragma unroll
+  for (int i = 0; i < kMaxBlock; ++i) bk[i] = s.blk[i];
   __syncthreads();
   if (act) {
     if (a.init) {
