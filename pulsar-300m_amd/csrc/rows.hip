@@ -87,8 +87,19 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
   const int st = a.prefill ? rd.pos + rd.seq * a.prefill_T : rd.seq * a.slots + rd.sslot;
   T* e = reinterpret_cast<T*>(a.e_state) + (int64_t)st * D;
   const T* step = reinterpret_cast<const T*>(a.step_emb) + (int64_t)rd.pulse * D;
-  float hv[EPL], stp[EPL], nw[EPL];
-  ldv<EPL>(step + i0, stp);
+  float hv[EPL], nw[EPL];
+  // the step vector stays in its storage type until its use inside the branches below
+  // (converted here, its loads made the branches' loads wait for them)
+  T stp_raw[EPL];
+  if constexpr ((EPL * sizeof(T)) % 16 == 0) {
+#pragma unroll
+    for (int w = 0; w < (int)(EPL * sizeof(T) / 16); ++w)
+      reinterpret_cast<uint4*>(stp_raw)[w] = reinterpret_cast<const uint4*>(step + i0)[w];
+  } else {
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) stp_raw[c] = step[i0 + c];
+  }
+  auto stp = [&](int c) { return to_f(stp_raw[c]); };
   if (a.norm_w) ldv<EPL>(a.norm_w + (int64_t)rd.pulse * D + i0, nw);
   if (rd.pulse == 0) {
     if (!a.prefill) {
@@ -106,14 +117,14 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
         float v = rnd<T>(x[c] * inv * an[c]);
         if (a.conv_w) v = rnd<T>(v + a.conv_w[(i0 + c) * 4] * v);
         ev[c] = v;
-        hv[c] = rnd<T>(v + stp[c]);
+        hv[c] = rnd<T>(v + stp(c));
       }
       stv<EPL>(e + i0, ev);
     } else {
       float ev[EPL];
       ldv<EPL>(e + i0, ev);
 #pragma unroll
-      for (int c = 0; c < EPL; ++c) hv[c] = rnd<T>(ev[c] + stp[c]);
+      for (int c = 0; c < EPL; ++c) hv[c] = rnd<T>(ev[c] + stp(c));
     }
   } else if constexpr (EXACT && sizeof(T) == 2 && EPL % 8 == 0 && EPL <= 16) {
     // The same re-injection as the general branch below, with every load of the row (state,
@@ -175,7 +186,7 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
 #pragma unroll
       for (int j = 0; j < RT; ++j) acc += gh[j] * wv[j];
       const float mix = rnd<T>(sigmoidf_(rnd<T>(acc + bv[c])));
-      hv[c] = rnd<T>(rnd<T>(lerp_ref(rv[c], ev[c], mix)) + stp[c]);
+      hv[c] = rnd<T>(rnd<T>(lerp_ref(rv[c], ev[c], mix)) + stp(c));
     }
   } else {
     // rank-R re-injection: g = T(T(e . wd[j][:D]) + T(r . wd[j][D:])), mix = sigmoid(up g + b)
@@ -226,7 +237,7 @@ __global__ void __launch_bounds__(64) pulse_input_kernel(PulseInputArgs a) {
       for (int j = 0; j < RT; ++j)
         if (EXACT || j < R) acc += gh[j] * wv[j];
       const float mix = rnd<T>(sigmoidf_(rnd<T>(acc + bv[c])));
-      hv[c] = rnd<T>(rnd<T>(lerp_ref(rv[c], ev[c], mix)) + stp[c]);
+      hv[c] = rnd<T>(rnd<T>(lerp_ref(rv[c], ev[c], mix)) + stp(c));
     }
   }
   T* h_in = reinterpret_cast<T*>(a.h_in) + (int64_t)r * D;
